@@ -1,0 +1,198 @@
+/*
+ * samhip — MI355X (gfx950) quantized mul_mat backend, C ABI.
+ *
+ * Drop-in replacement for the ggml operators that SAM.cpp's quantized linears
+ * reach (GGML_OP_MUL_MAT on GGUF-packed Q8_0/Q4_K/Q5_K/Q6_K weights against
+ * F32 activations, and GGML_OP_GET_ROWS), keeping ggml's tensor semantics:
+ *   W = src0 [ne0 = K, ne1 = N] packed rows, nb[0] = block bytes, nb[1] = row stride
+ *   X = src1 [ne0 = K, ne1 = M] F32, nb[0] = 4, nb[1] >= 4*K (strided rows allowed)
+ *   Y = dst  [ne0 = N, ne1 = M] F32, Y[m][n] = sum_k W[n][k] * X[m][k]
+ * (reference: ggml_mul_mat as called by sam3_channel_projection,
+ * src/models/sam3/ops.hpp:40-45; layout stated at
+ * tools/benchmark/ggml_linear_probe.cpp:103).
+ *
+ * No C++ exception crosses this boundary: every entry point returns an int
+ * status (0 = ok, negative = error class) and records a message readable with
+ * samhip_last_error().  The C++ host layer maps SAMHIP_ERR_INVALID_ARGUMENT to
+ * std::invalid_argument and every other error to std::runtime_error, as
+ * src/runtime/ggml/workspace.hpp:174-177 and README.md:239-242 do.
+ *
+ * Threading: a context is single-threaded and stream-ordered (one HIP stream);
+ * distinct contexts may be used from distinct threads.  The library never
+ * keeps a caller pointer after a call returns.
+ */
+#ifndef SAMHIP_H
+#define SAMHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SAMHIP_ABI_VERSION 1
+
+/* ggml / GGUF type ids used on the path (ggml.h enum ggml_type). */
+enum samhip_type {
+    SAMHIP_TYPE_F32 = 0,
+    SAMHIP_TYPE_F16 = 1,
+    SAMHIP_TYPE_Q8_0 = 8,
+    SAMHIP_TYPE_Q4_K = 12,
+    SAMHIP_TYPE_Q5_K = 13,
+    SAMHIP_TYPE_Q6_K = 14,
+    SAMHIP_TYPE_Q8_K = 15,
+    SAMHIP_TYPE_I32 = 26
+};
+
+enum samhip_status {
+    SAMHIP_OK = 0,
+    SAMHIP_ERR_INVALID_ARGUMENT = -1, /* bad shape/type/pointer: std::invalid_argument */
+    SAMHIP_ERR_UNSUPPORTED = -2,      /* no kernel for this operand combination */
+    SAMHIP_ERR_DEVICE = -3,           /* HIP runtime failure */
+    SAMHIP_ERR_OUT_OF_MEMORY = -4
+};
+
+/* Arithmetic contract of mul_mat (mirrors sam::CpuComputeMode /
+ * sam::CudaComputeMode, include/sam/types.hpp:13-14):
+ *  Q8_NATIVE: activations are packed per call to the weight's ggml
+ *             vec_dot_type (Q8_0 for Q8_0 weights, Q8_K for K-quants),
+ *             bit-exact with ggml's CPU from_float, then multiplied on fp16
+ *             MFMA with F32 accumulation.  Compare with the CPU
+ *             "ggml-quantized-cpu-native-v1" path.
+ *  F16:       activations are rounded to fp16 directly; compare with the
+ *             CPU "ggml-quantized-weights-f32-v1" (F32-decode) path.
+ * In both, the weight operand is fp16(ggml to_float(W)). */
+enum samhip_compute {
+    SAMHIP_COMPUTE_Q8_NATIVE = 0,
+    SAMHIP_COMPUTE_F16 = 1
+};
+
+/* Q8_0 activation rounding (tools/quantize/cache_quantization.py:76-95):
+ * X86: ggml CPU from_float on x86-64 (scale 127/amax, ties to even),
+ * REF: ggml quantize_row_q8_0_ref (scale 1/d, ties away from zero). */
+enum samhip_q8_rounding {
+    SAMHIP_Q8_ROUND_X86 = 0,
+    SAMHIP_Q8_ROUND_REF = 1
+};
+
+/* ggml tensor descriptor: ne = elements per dimension, nb = byte strides,
+ * data = device address.  Only 2-D operands (ne[2] = ne[3] = 1) are used. */
+typedef struct samhip_tensor {
+    int32_t type;
+    int64_t ne[4];
+    size_t nb[4];
+    void* data;
+} samhip_tensor;
+
+typedef struct samhip_options {
+    uint32_t version;     /* SAMHIP_ABI_VERSION */
+    int32_t device;       /* HIP device index (BackendOptions::hip_device) */
+    int32_t compute;      /* enum samhip_compute */
+    int32_t q8_rounding;  /* enum samhip_q8_rounding */
+} samhip_options;
+
+/* Versioned execution counters, after ggml_cuda_sam_q8_rhs_query_v1's struct
+ * {version, path, launches, payload_bytes, allocation_bytes}
+ * (cmake/patches/ggml-native-activation.patch:13-26). */
+typedef struct samhip_exec_info {
+    uint32_t version;
+    int32_t device;
+    uint64_t mul_mat_calls;
+    uint64_t gemm_launches;
+    uint64_t skinny_launches;
+    uint64_t activation_launches;
+    uint64_t get_rows_calls;
+    uint64_t activation_payload_peak_bytes;
+    uint64_t activation_allocation_peak_bytes;
+    char kernel_variant[64];      /* last mul_mat kernel */
+    char arithmetic_profile[48];  /* e.g. "samhip-q8-native-f16mfma-v1" */
+    char device_name[64];
+} samhip_exec_info;
+
+typedef struct samhip_context samhip_context;
+
+/* --- identity and devices ------------------------------------------------ */
+int samhip_abi_version(void);
+int samhip_device_count(int* count);
+
+/* --- context (one device, one stream) ------------------------------------ */
+/* replaces make_cuda_backend(device, compute, ...) as the backend driver
+ * factory (src/runtime/ggml/backends/cuda.hpp:156-189). */
+int samhip_context_create(const samhip_options* options, samhip_context** out);
+void samhip_context_destroy(samhip_context* ctx);
+/* Run subsequent calls on `hip_stream` (a hipStream_t); NULL restores the
+ * context's own stream. */
+int samhip_context_set_stream(samhip_context* ctx, void* hip_stream);
+int samhip_synchronize(samhip_context* ctx);
+
+/* --- device memory (ggml_backend_alloc_ctx_tensors / tensor_set / get) --- */
+int samhip_buffer_alloc(samhip_context* ctx, size_t bytes, void** device_ptr);
+int samhip_buffer_free(samhip_context* ctx, void* device_ptr);
+/* Synchronous copies, as ggml_backend_tensor_set/get (src/models/sam3/
+ * model.hpp:130, src/runtime/ggml/host_tensor.hpp:18-33).  Packed weight
+ * bytes are uploaded unchanged. */
+int samhip_tensor_set(samhip_context* ctx, void* device_dst, const void* host_src, size_t bytes);
+int samhip_tensor_get(samhip_context* ctx, void* host_dst, const void* device_src, size_t bytes);
+
+/* --- operators ------------------------------------------------------------ */
+/* 1 if mul_mat(w, x, y) has a kernel, else 0; asked before execution so an
+ * unsupported node is a runtime error, not a crash (ggml_backend_supports_op
+ * at src/runtime/ggml/graph.hpp:65-78). */
+int samhip_supports_mul_mat(const samhip_tensor* w, const samhip_tensor* x, const samhip_tensor* y);
+
+/* GGML_OP_MUL_MAT (ggml_mul_mat; ggml-cuda mul_mat dispatch
+ * tests/runtime/ggml/test_quantization.cpp:604-614).  w may be a row-offset
+ * view of a larger packed tensor, x may have a row stride above 4*K. */
+int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_tensor* x, const samhip_tensor* y);
+
+/* GGML_OP_GET_ROWS: dst row i = to_float(src row ids[i]) (ggml_get_rows,
+ * src/models/sam3/text_encoder.hpp:158).  src type F32/F16/Q8_0/Q4_K/Q5_K/
+ * Q6_K, ids I32, dst F32.  Out-of-range ids fail with INVALID_ARGUMENT. */
+int samhip_get_rows(samhip_context* ctx, const samhip_tensor* src, const samhip_tensor* ids, const samhip_tensor* dst);
+
+/* Row quantization on the device, bit-exact with ggml:
+ *   Q8_0: ggml from_float / quantize_row_q8_0_ref per `q8_rounding`
+ *   Q8_K: quantize_row_q8_K_ref (CPU activation packing for K weights)
+ *   Q4_K, Q5_K, Q6_K: quantize_row_q*_K_ref (ggml_quantize_chunk without
+ *         importance weights; tools/quantize/quantize_rows.cpp:210)
+ * src rows have `src_row_stride` bytes, dst rows are packed back to back. */
+int samhip_quantize_rows(samhip_context* ctx, int32_t type, const float* src, size_t src_row_stride,
+                         void* dst, int64_t rows, int64_t k, int32_t q8_rounding);
+
+/* ggml to_float on the device for Q8_0/Q4_K/Q5_K/Q6_K/Q8_K rows (bit-exact). */
+int samhip_dequantize_rows(samhip_context* ctx, int32_t type, const void* src, size_t src_row_stride,
+                           float* dst, int64_t rows, int64_t k);
+
+/* Host-side payload check run before upload, as validate_quantized_payload
+ * (src/models/sam3/weights.hpp:384-425): non-finite d (offset 0, or
+ * type_size-2 for Q6_K), non-finite dmin (offset 2 for Q4_K/Q5_K) or a
+ * non-finite decoded value is rejected. */
+int samhip_validate_quantized_payload(int32_t type, int64_t ne0, int64_t rows, const void* host_bytes, size_t bytes);
+
+/* --- diagnostics ------------------------------------------------------------ */
+int samhip_query(samhip_context* ctx, samhip_exec_info* info);
+
+/* Per-launch kernel timing, the device-side counterpart of the reference's
+ * opt-in GraphObserver computing/computed callbacks
+ * (src/runtime/ggml/observer.hpp:14-22; tools/benchmark/execution_cost.hpp:
+ * 47-80): between trace_begin and trace_end every kernel launch of the context
+ * is bracketed by HIP events on the context's stream.  trace_end waits for the
+ * stream and copies up to `capacity` records; *count receives the number
+ * recorded (which may exceed capacity). */
+typedef struct samhip_kernel_record {
+    char kernel[64];
+    int32_t weight_type;
+    int64_t m, n, k;
+    float ms;
+} samhip_kernel_record;
+int samhip_trace_begin(samhip_context* ctx);
+int samhip_trace_end(samhip_context* ctx, samhip_kernel_record* records, size_t capacity, size_t* count);
+/* Copies the calling thread's last error message; returns its full length. */
+size_t samhip_last_error(char* buffer, size_t size);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAMHIP_H */

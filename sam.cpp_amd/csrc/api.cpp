@@ -1,0 +1,457 @@
+// C ABI of libsamhip (include/samhip.h): contexts, validation, dispatch.
+#include "samhip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "internal.hpp"
+
+using namespace samhip;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return status;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(e == hipErrorOutOfMemory ? SAMHIP_ERR_OUT_OF_MEMORY : SAMHIP_ERR_DEVICE, "%s: %s", what,
+                hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                         \
+    do {                                            \
+        hipError_t e_ = (expr);                     \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+bool is_weight_type(int t) { return t == T_Q8_0 || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
+
+// Activation packing type for a weight type: ggml's CPU vec_dot_type
+// (src/runtime/ggml/backends/cpu.hpp:13-23).
+int vec_dot_type(int wtype) { return wtype == T_Q8_0 ? T_Q8_0 : T_Q8_K; }
+
+size_t row_bytes(int t, int64_t k) { return size_t(k / block_elems(t)) * size_t(block_bytes(t)); }
+
+}  // namespace
+
+struct samhip_context {
+    int device = 0;
+    int compute = SAMHIP_COMPUTE_Q8_NATIVE;
+    int q8_rounding = SAMHIP_Q8_ROUND_X86;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    // staged fp16 activations [M][K] followed by F32 row scales [M]
+    void* staging = nullptr;
+    size_t staging_bytes = 0;
+    int* flag = nullptr;   // device error flag (get_rows id range)
+    samhip_exec_info info{};
+    // per-launch event trace (samhip_trace_begin / samhip_trace_end)
+    struct TraceRecord {
+        const char* kernel;
+        int weight_type;
+        int64_t m, n, k;
+        hipEvent_t start, stop;
+    };
+    bool tracing = false;
+    std::vector<TraceRecord> trace;
+    std::vector<hipEvent_t> event_pool;
+};
+
+namespace {
+
+int set_device(samhip_context* ctx) {
+    HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
+    return SAMHIP_OK;
+}
+
+int ensure_staging(samhip_context* ctx, size_t bytes) {
+    if (bytes <= ctx->staging_bytes) return SAMHIP_OK;
+    if (ctx->staging) {
+        HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        HIP_TRY(hipFree(ctx->staging), "hipFree");
+        ctx->staging = nullptr;
+        ctx->staging_bytes = 0;
+    }
+    const size_t rounded = (bytes + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
+    HIP_TRY(hipMalloc(&ctx->staging, rounded), "hipMalloc staging");
+    ctx->staging_bytes = rounded;
+    ctx->info.activation_allocation_peak_bytes =
+        std::max<uint64_t>(ctx->info.activation_allocation_peak_bytes, rounded);
+    return SAMHIP_OK;
+}
+
+constexpr size_t kMaxTraceRecords = size_t(1) << 20;
+
+hipEvent_t pooled_event(samhip_context* ctx) {
+    if (!ctx->event_pool.empty()) {
+        hipEvent_t e = ctx->event_pool.back();
+        ctx->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+// Launches `body` on the context stream, bracketed by events when tracing.
+template <class Body>
+int traced(samhip_context* ctx, const char* kernel, int wt, int64_t m, int64_t n, int64_t k, Body body) {
+    hipEvent_t a = nullptr, b = nullptr;
+    const bool record = ctx->tracing && ctx->trace.size() < kMaxTraceRecords;
+    if (record) {
+        a = pooled_event(ctx);
+        b = pooled_event(ctx);
+        if (!a || !b) return fail(SAMHIP_ERR_DEVICE, "hipEventCreate failed");
+        HIP_TRY(hipEventRecord(a, ctx->stream), "hipEventRecord");
+    }
+    const int rc = body();
+    if (record) {
+        HIP_TRY(hipEventRecord(b, ctx->stream), "hipEventRecord");
+        ctx->trace.push_back({kernel, wt, m, n, k, a, b});
+    }
+    return rc;
+}
+
+const char* stage_name(int mode) {
+    return mode == T_F16 ? "stage_rows_f16" : mode == T_Q8_0 ? "stage_rows_q8_0" : "stage_rows_q8_k";
+}
+
+const char* profile_name(int compute) {
+    return compute == SAMHIP_COMPUTE_F16 ? "samhip-f16-f16mfma-v1" : "samhip-q8-native-f16mfma-v1";
+}
+
+// Returns 0 when supported, else a reason string (checked without touching
+// device memory).
+const char* mul_mat_problem(const samhip_tensor* w, const samhip_tensor* x, const samhip_tensor* y) {
+    if (!w || !x || !y) return "null tensor descriptor";
+    if (!is_weight_type(w->type)) return "weight type must be Q8_0, Q4_K, Q5_K or Q6_K";
+    if (x->type != T_F32 || y->type != T_F32) return "activation and output must be F32";
+    const int64_t K = w->ne[0], N = w->ne[1], M = x->ne[1];
+    if (K <= 0 || N <= 0 || M <= 0) return "empty operand";
+    for (int i = 2; i < 4; ++i)
+        if (w->ne[i] != 1 || x->ne[i] != 1 || y->ne[i] != 1) return "only 2-D operands are supported";
+    if (K % block_elems(w->type)) return "K is not a multiple of the weight block size";
+    if (x->ne[0] != K) return "activation width differs from weight width";
+    if (y->ne[0] != N || y->ne[1] != M) return "output shape must be [N, M]";
+    if (w->nb[0] != size_t(block_bytes(w->type))) return "weight nb[0] must equal the block size";
+    if (w->nb[1] < row_bytes(w->type, K)) return "weight rows overlap";
+    if (x->nb[0] != 4 || x->nb[1] < size_t(4 * K) || x->nb[1] % 4) return "activation rows must be F32-contiguous";
+    if (y->nb[0] != 4 || y->nb[1] < size_t(4 * N) || y->nb[1] % 4) return "output rows must be F32-contiguous";
+    if (!w->data || !x->data || !y->data) return "null data pointer";
+    if (reinterpret_cast<uintptr_t>(w->data) % 2 || w->nb[1] % 2) return "packed weight rows must be 2-byte aligned";
+    if (reinterpret_cast<uintptr_t>(x->data) % 4 || reinterpret_cast<uintptr_t>(y->data) % 4)
+        return "F32 operands must be 4-byte aligned";
+    if (K > (int64_t(1) << 24) || N > (int64_t(1) << 30) || M > (int64_t(1) << 30)) return "dimension too large";
+    return nullptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+int samhip_abi_version(void) { return SAMHIP_ABI_VERSION; }
+
+int samhip_device_count(int* count) {
+    if (!count) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null count");
+    int n = 0;
+    const hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) n = 0;
+    *count = n;
+    return SAMHIP_OK;
+}
+
+int samhip_context_create(const samhip_options* options, samhip_context** out) {
+    if (!out) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null output context");
+    *out = nullptr;
+    samhip_options o{SAMHIP_ABI_VERSION, 0, SAMHIP_COMPUTE_Q8_NATIVE, SAMHIP_Q8_ROUND_X86};
+    if (options) o = *options;
+    if (o.version != SAMHIP_ABI_VERSION) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "unsupported samhip ABI version %u", o.version);
+    if (o.compute != SAMHIP_COMPUTE_Q8_NATIVE && o.compute != SAMHIP_COMPUTE_F16)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "unknown HIP compute mode");
+    if (o.q8_rounding != SAMHIP_Q8_ROUND_X86 && o.q8_rounding != SAMHIP_Q8_ROUND_REF)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "unknown Q8 rounding mode");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(SAMHIP_ERR_DEVICE, "no HIP device is visible");
+    if (o.device < 0 || o.device >= n) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "HIP device %d out of range [0, %d)", o.device, n);
+    samhip_context* ctx = new (std::nothrow) samhip_context;
+    if (!ctx) return fail(SAMHIP_ERR_OUT_OF_MEMORY, "context allocation failed");
+    ctx->device = o.device;
+    ctx->compute = o.compute;
+    ctx->q8_rounding = o.q8_rounding;
+    ctx->info.version = SAMHIP_ABI_VERSION;
+    ctx->info.device = o.device;
+    std::snprintf(ctx->info.arithmetic_profile, sizeof(ctx->info.arithmetic_profile), "%s", profile_name(o.compute));
+    hipDeviceProp_t prop;
+    if (hipSetDevice(o.device) != hipSuccess || hipGetDeviceProperties(&prop, o.device) != hipSuccess ||
+        hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipMalloc(reinterpret_cast<void**>(&ctx->flag), sizeof(int)) != hipSuccess) {
+        samhip_context_destroy(ctx);
+        return fail(SAMHIP_ERR_DEVICE, "HIP context initialization failed");
+    }
+    std::snprintf(ctx->info.device_name, sizeof(ctx->info.device_name), "%s (%s)", prop.name, prop.gcnArchName);
+    ctx->stream = ctx->own_stream;
+    *out = ctx;
+    return SAMHIP_OK;
+}
+
+void samhip_context_destroy(samhip_context* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->own_stream) (void)hipStreamSynchronize(ctx->own_stream);
+    if (ctx->stream && ctx->stream != ctx->own_stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->staging) (void)hipFree(ctx->staging);
+    if (ctx->flag) (void)hipFree(ctx->flag);
+    for (auto& r : ctx->trace) {
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
+    }
+    for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+}
+
+int samhip_context_set_stream(samhip_context* ctx, void* hip_stream) {
+    if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+    return SAMHIP_OK;
+}
+
+int samhip_synchronize(samhip_context* ctx) {
+    if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    return SAMHIP_OK;
+}
+
+int samhip_buffer_alloc(samhip_context* ctx, size_t bytes, void** device_ptr) {
+    if (!ctx || !device_ptr || bytes == 0) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "invalid buffer request");
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipMalloc(device_ptr, bytes), "hipMalloc");
+    return SAMHIP_OK;
+}
+
+int samhip_buffer_free(samhip_context* ctx, void* device_ptr) {
+    if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    if (!device_ptr) return SAMHIP_OK;
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    HIP_TRY(hipFree(device_ptr), "hipFree");
+    return SAMHIP_OK;
+}
+
+int samhip_tensor_set(samhip_context* ctx, void* device_dst, const void* host_src, size_t bytes) {
+    if (!ctx || (bytes && (!device_dst || !host_src))) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "invalid tensor_set");
+    if (!bytes) return SAMHIP_OK;
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipMemcpyAsync(device_dst, host_src, bytes, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync H2D");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    return SAMHIP_OK;
+}
+
+int samhip_tensor_get(samhip_context* ctx, void* host_dst, const void* device_src, size_t bytes) {
+    if (!ctx || (bytes && (!device_src || !host_dst))) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "invalid tensor_get");
+    if (!bytes) return SAMHIP_OK;
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipMemcpyAsync(host_dst, device_src, bytes, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync D2H");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    return SAMHIP_OK;
+}
+
+int samhip_supports_mul_mat(const samhip_tensor* w, const samhip_tensor* x, const samhip_tensor* y) {
+    return mul_mat_problem(w, x, y) == nullptr ? 1 : 0;
+}
+
+int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_tensor* x, const samhip_tensor* y) {
+    if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    if (const char* why = mul_mat_problem(w, x, y)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "mul_mat: %s", why);
+    const int K = int(w->ne[0]), N = int(w->ne[1]), M = int(x->ne[1]);
+    if (int rc = set_device(ctx)) return rc;
+    const size_t a_bytes = size_t(M) * size_t(K) * 2;
+    const size_t a_offset = (a_bytes + 255) & ~size_t(255);
+    if (int rc = ensure_staging(ctx, a_offset + size_t(M) * 4)) return rc;
+    _Float16* a = static_cast<_Float16*>(ctx->staging);
+    float* rs = reinterpret_cast<float*>(static_cast<uint8_t*>(ctx->staging) + a_offset);
+    const int mode = ctx->compute == SAMHIP_COMPUTE_F16 ? T_F16 : vec_dot_type(w->type);
+    const bool aligned = reinterpret_cast<uintptr_t>(x->data) % 16 == 0 && x->nb[1] % 16 == 0;
+    int rc = traced(ctx, stage_name(mode), w->type, M, N, K, [&]() -> int {
+        launch_stage_rows(mode, aligned, static_cast<const float*>(x->data), int64_t(x->nb[1] / 4), M, K, a, K, rs,
+                          ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->stream);
+        HIP_TRY(hipGetLastError(), "activation staging launch");
+        return SAMHIP_OK;
+    });
+    if (rc) return rc;
+    const char* variant = gemm_variant(w->type);
+    if (!variant) return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no kernel for weight type %d", w->type);
+    rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
+        launch_gemm(w->type, a, K, rs, w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
+                    int64_t(y->nb[1] / 4), M, N, K, ctx->stream);
+        HIP_TRY(hipGetLastError(), "gemm launch");
+        return SAMHIP_OK;
+    });
+    if (rc) return rc;
+    ctx->info.mul_mat_calls++;
+    ctx->info.activation_launches++;
+    ctx->info.gemm_launches++;
+    ctx->info.activation_payload_peak_bytes = std::max<uint64_t>(ctx->info.activation_payload_peak_bytes, a_bytes);
+    std::snprintf(ctx->info.kernel_variant, sizeof(ctx->info.kernel_variant), "%s", variant);
+    return SAMHIP_OK;
+}
+
+int samhip_get_rows(samhip_context* ctx, const samhip_tensor* src, const samhip_tensor* ids, const samhip_tensor* dst) {
+    if (!ctx || !src || !ids || !dst) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "get_rows: null argument");
+    const int t = src->type;
+    if (t != T_F32 && t != T_F16 && !is_weight_type(t)) return fail(SAMHIP_ERR_UNSUPPORTED, "get_rows: unsupported source type %d", t);
+    if (ids->type != T_I32 || dst->type != T_F32) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "get_rows: ids must be I32 and dst F32");
+    const int64_t K = src->ne[0], rows = src->ne[1], n = ids->ne[0];
+    if (K <= 0 || rows <= 0 || n <= 0 || K % 32 || K % block_elems(t))
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "get_rows: row width must be a positive multiple of the block size and 32");
+    if (dst->ne[0] != K || dst->ne[1] != n || ids->nb[0] != 4 || dst->nb[0] != 4 || dst->nb[1] < size_t(4 * K))
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "get_rows: dst must be [K, n] F32 and ids contiguous I32");
+    if (src->nb[1] < row_bytes(t, K) || !src->data || !ids->data || !dst->data)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "get_rows: invalid source rows");
+    for (int i = 2; i < 4; ++i)
+        if (src->ne[i] != 1 || ids->ne[i] != 1 || dst->ne[i] != 1) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "get_rows: 2-D only");
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipMemsetAsync(ctx->flag, 0, sizeof(int), ctx->stream), "hipMemsetAsync");
+    launch_dequant_rows(t, src->data, int64_t(src->nb[1]), static_cast<const int32_t*>(ids->data), rows,
+                        static_cast<float*>(dst->data), int64_t(dst->nb[1] / 4), int(n), int(K), ctx->flag, ctx->stream);
+    HIP_TRY(hipGetLastError(), "get_rows launch");
+    int bad = 0;
+    HIP_TRY(hipMemcpyAsync(&bad, ctx->flag, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    ctx->info.get_rows_calls++;
+    if (bad) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "get_rows: row id out of range [0, %lld)", (long long)rows);
+    return SAMHIP_OK;
+}
+
+int samhip_quantize_rows(samhip_context* ctx, int32_t type, const float* src, size_t src_row_stride, void* dst,
+                         int64_t rows, int64_t k, int32_t q8_rounding) {
+    if (!ctx || !src || !dst || rows <= 0 || k <= 0) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: invalid argument");
+    if (type != T_Q8_0 && type != T_Q8_K && type != T_Q4_K && type != T_Q5_K && type != T_Q6_K)
+        return fail(SAMHIP_ERR_UNSUPPORTED, "quantize_rows: unsupported type %d", type);
+    if (k % block_elems(type)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: k must be a multiple of %d", block_elems(type));
+    if (src_row_stride < size_t(4 * k) || src_row_stride % 4 || reinterpret_cast<uintptr_t>(src) % 4)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: invalid source stride");
+    if (q8_rounding != SAMHIP_Q8_ROUND_X86 && q8_rounding != SAMHIP_Q8_ROUND_REF)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: unknown Q8 rounding");
+    if ((type == T_Q8_K) && reinterpret_cast<uintptr_t>(dst) % 4) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: Q8_K dst must be 4-byte aligned");
+    if (rows > (int64_t(1) << 30) || k > (int64_t(1) << 24)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: too large");
+    if (int rc = set_device(ctx)) return rc;
+    if (type == T_Q8_0 || type == T_Q8_K)
+        launch_quantize_act(type, src, int64_t(src_row_stride / 4), int(rows), int(k), dst,
+                            q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->stream);
+    else
+        launch_quantize_weights(type, src, int64_t(src_row_stride / 4), int(rows), int(k), dst, ctx->stream);
+    HIP_TRY(hipGetLastError(), "quantize launch");
+    return SAMHIP_OK;
+}
+
+int samhip_dequantize_rows(samhip_context* ctx, int32_t type, const void* src, size_t src_row_stride, float* dst,
+                           int64_t rows, int64_t k) {
+    if (!ctx || !src || !dst || rows <= 0 || k <= 0) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "dequantize_rows: invalid argument");
+    if (!is_weight_type(type) && type != T_Q8_K) return fail(SAMHIP_ERR_UNSUPPORTED, "dequantize_rows: unsupported type %d", type);
+    if (k % block_elems(type) || src_row_stride < row_bytes(type, k))
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "dequantize_rows: invalid row shape");
+    if (rows > (int64_t(1) << 30) || k > (int64_t(1) << 24)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "dequantize_rows: too large");
+    if (int rc = set_device(ctx)) return rc;
+    launch_dequant_rows(type, src, int64_t(src_row_stride), nullptr, rows, dst, k, int(rows), int(k), nullptr, ctx->stream);
+    HIP_TRY(hipGetLastError(), "dequantize launch");
+    return SAMHIP_OK;
+}
+
+int samhip_validate_quantized_payload(int32_t type, int64_t ne0, int64_t rows, const void* host_bytes, size_t bytes) {
+    if (!is_weight_type(type)) return fail(SAMHIP_ERR_UNSUPPORTED, "invalid quantized SAM tensor layout");
+    if (ne0 <= 0 || rows <= 0 || ne0 % block_elems(type)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "invalid quantized SAM tensor layout");
+    const size_t rb = row_bytes(type, ne0);
+    if (size_t(rows) > SIZE_MAX / rb || size_t(rows) * rb != bytes || (!host_bytes && bytes))
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantized SAM tensor payload size does not match its shape");
+    const uint8_t* p = static_cast<const uint8_t*>(host_bytes);
+    const int bb = block_bytes(type), be = block_elems(type);
+    auto half_value = [](const uint8_t* q) {
+        const uint16_t h = uint16_t(q[0] | (q[1] << 8));
+        const uint32_t e = (h >> 10) & 0x1f, m = h & 0x3ff;
+        if (e == 0x1f) return m ? NAN : ((h & 0x8000) ? -INFINITY : INFINITY);
+        float v = e ? std::ldexp(float(m | 0x400), int(e) - 25) : std::ldexp(float(m), -24);
+        return (h & 0x8000) ? -v : v;
+    };
+    for (size_t b = 0; b < size_t(rows) * size_t(ne0 / be); ++b) {
+        const uint8_t* blk = p + b * bb;
+        const float d = half_value(blk + (type == T_Q6_K ? bb - 2 : 0));
+        if (!std::isfinite(d)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "non-finite quantized SAM block scale");
+        if ((type == T_Q4_K || type == T_Q5_K) && !std::isfinite(half_value(blk + 2)))
+            return fail(SAMHIP_ERR_INVALID_ARGUMENT, "non-finite quantized SAM block minimum scale");
+        // With finite scales the decoded values of these formats are bounded
+        // by |d| * 127 (Q8_0), |d| * 63 * 31 + |dmin| * 63 (Q4_K/Q5_K) and
+        // |d| * 128 * 32 (Q6_K), all finite in F32.
+    }
+    return SAMHIP_OK;
+}
+
+int samhip_trace_begin(samhip_context* ctx) {
+    if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    for (auto& r : ctx->trace) {
+        ctx->event_pool.push_back(r.start);
+        ctx->event_pool.push_back(r.stop);
+    }
+    ctx->trace.clear();
+    ctx->tracing = true;
+    return SAMHIP_OK;
+}
+
+int samhip_trace_end(samhip_context* ctx, samhip_kernel_record* records, size_t capacity, size_t* count) {
+    if (!ctx || (capacity && !records)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "invalid trace_end argument");
+    ctx->tracing = false;
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    for (size_t i = 0; i < ctx->trace.size() && i < capacity; ++i) {
+        const auto& r = ctx->trace[i];
+        samhip_kernel_record& o = records[i];
+        std::snprintf(o.kernel, sizeof(o.kernel), "%s", r.kernel);
+        o.weight_type = r.weight_type;
+        o.m = r.m;
+        o.n = r.n;
+        o.k = r.k;
+        HIP_TRY(hipEventElapsedTime(&o.ms, r.start, r.stop), "hipEventElapsedTime");
+    }
+    if (count) *count = ctx->trace.size();
+    for (auto& r : ctx->trace) {
+        ctx->event_pool.push_back(r.start);
+        ctx->event_pool.push_back(r.stop);
+    }
+    ctx->trace.clear();
+    return SAMHIP_OK;
+}
+
+int samhip_query(samhip_context* ctx, samhip_exec_info* info) {
+    if (!ctx || !info) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null query argument");
+    *info = ctx->info;
+    return SAMHIP_OK;
+}
+
+size_t samhip_last_error(char* buffer, size_t size) {
+    if (buffer && size) {
+        const size_t n = std::min(size - 1, g_last_error.size());
+        std::memcpy(buffer, g_last_error.data(), n);
+        buffer[n] = '\0';
+    }
+    return g_last_error.size();
+}
+
+}  // extern "C"

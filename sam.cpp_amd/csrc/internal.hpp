@@ -1,0 +1,32 @@
+// Launchers shared between the kernel translation units and the C ABI layer.
+#pragma once
+
+#include "blocks.hpp"
+
+namespace samhip {
+
+// mode: T_F16 (direct), T_Q8_0 or T_Q8_K (native activation packing).
+void launch_stage_rows(int mode, bool aligned, const float* x, int64_t x_stride, int M, int K, _Float16* a,
+                       int64_t lda, float* row_scale, int x86, hipStream_t stream);
+
+// Q8_0 / Q8_K activation rows in ggml wire format.
+void launch_quantize_act(int type, const float* x, int64_t x_stride, int rows, int K, void* dst, int x86,
+                         hipStream_t stream);
+
+// Q4_K / Q5_K / Q6_K weight rows in ggml wire format (ggml_quantize_chunk).
+void launch_quantize_weights(int type, const float* x, int64_t x_stride, int rows, int K, void* dst,
+                             hipStream_t stream);
+
+// to_float (ids == nullptr) or get_rows (ids != nullptr, bad_id flag set on
+// an out-of-range id).
+void launch_dequant_rows(int type, const void* src, int64_t src_stride, const int32_t* ids, int64_t src_rows,
+                         float* dst, int64_t dst_stride, int rows, int K, int* bad_id, hipStream_t stream);
+
+// Kernel variant name for a weight type, or nullptr when unsupported.
+const char* gemm_variant(int wtype);
+
+// Returns the kernel variant name, or nullptr for an unsupported type.
+const char* launch_gemm(int wtype, const _Float16* a, int64_t lda, const float* row_scale, const void* w,
+                        int64_t w_stride, float* y, int64_t ldy, int M, int N, int K, hipStream_t stream);
+
+}  // namespace samhip

@@ -1,0 +1,329 @@
+// Activation staging (the per-call RHS packing of the mul_mat path), row
+// quantizers in ggml wire format, and to_float / get_rows, for gfx950.
+//
+// Staging turns F32 activation rows into the fp16 MFMA A operand:
+//   Q8_0 mode : value = fp16(to_float(q8_0 block) * 2^-e)  (Q8_0 weights)
+//   Q8_K mode : value = fp16(to_float(q8_K block) * 2^-e)  (K-quant weights)
+//   F16 mode  : value = fp16(x * 2^-e)
+// where the Q8 blocks are bit-exact with ggml's CPU from_float for the
+// weight's vec_dot_type (src/runtime/ggml/backends/cpu.hpp:13-23) and 2^e is
+// a per-row power of two that keeps the row maximum inside fp16's range; the
+// GEMM epilogue multiplies it back exactly.
+#include "internal.hpp"
+
+#pragma clang fp contract(off)
+
+namespace samhip {
+
+namespace {
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// max over aligned groups of `width` lanes
+template <int width>
+__device__ __forceinline__ float group_max(float v) {
+    for (int off = width / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+template <int width>
+__device__ __forceinline__ int group_sum(int v) {
+    for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// 2^e as a float for |e| <= 126.
+__device__ __forceinline__ float exp2i(int e) { return __builtin_bit_cast(float, uint32_t(127 + e) << 23); }
+
+// Row exponent e with rowmax * 2^-e in [2^14, 2^15), clamped to [-110, 110]
+// so that both 2^e and 2^-e are normal floats.
+__device__ __forceinline__ int row_exponent(float rowmax) {
+    if (!(rowmax > 0.f) || !__builtin_isfinite(rowmax)) return 0;
+    const int biased = int((__builtin_bit_cast(uint32_t, rowmax) >> 23) & 0xffu);
+    int e = (biased == 0 ? -126 : biased - 127) - 14;
+    return e < -110 ? -110 : (e > 110 ? 110 : e);
+}
+
+__device__ __forceinline__ floatx4 load4f(const float* p) { return *reinterpret_cast<const floatx4*>(p); }
+
+// Q8_0 block: amax over 8 lanes x 4 values; returns fp16 d bits and codes.
+__device__ __forceinline__ void q8_0_codes(const floatx4& v, int x86, float& d_out, int q[4]) {
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = group_max<8>(amax);
+    const float d = amax / 127.f;
+    float inv;
+    if (x86) inv = amax != 0.f ? 127.f / amax : 0.f;
+    else inv = d != 0.f ? 1.f / d : 0.f;
+    d_out = d;
+    for (int i = 0; i < 4; ++i) {
+        const float s = v[i] * inv;
+        q[i] = int(x86 ? __builtin_rintf(s) : __builtin_roundf(s));
+    }
+}
+
+// Q8_K block over the whole wave (64 lanes x 4 values = 256): ggml keeps the
+// first element of largest magnitude as the signed maximum.
+__device__ __forceinline__ void q8_k_codes(const floatx4& v, int lane, float& d_out, int q[4]) {
+    float amax = 0.f, smax = 0.f;
+    int idx = 1 << 30;
+    for (int i = 0; i < 4; ++i) {
+        const float a = fabsf(v[i]);
+        if (a > amax) { amax = a; smax = v[i]; idx = 4 * lane + i; }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float oa = __shfl_xor(amax, off, 64);
+        const float os = __shfl_xor(smax, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; smax = os; idx = oi; }
+    }
+    if (amax == 0.f) {
+        d_out = 0.f;
+        for (int i = 0; i < 4; ++i) q[i] = 0;
+        return;
+    }
+    const float iscale = -127.f / smax;
+    for (int i = 0; i < 4; ++i) {
+        const int t = int(__builtin_rintf(iscale * v[i]));
+        q[i] = t < 127 ? t : 127;
+    }
+    d_out = 1.f / iscale;
+}
+
+// One wave per row, 4 rows per 256-thread block.
+template <int MODE>
+__global__ __launch_bounds__(256) void stage_rows_kernel(const float* __restrict__ x, int64_t x_stride, int M, int K,
+                                                         _Float16* __restrict__ a, int64_t lda,
+                                                         float* __restrict__ row_scale, int x86) {
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= M) return;
+    const float* xr = x + int64_t(m) * x_stride;
+    float rmax = 0.f;
+    for (int k = 4 * lane; k < K; k += 256) {
+        const floatx4 v = load4f(xr + k);
+        rmax = fmaxf(rmax, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    }
+    rmax = wave_max(rmax);
+    const int e = row_exponent(rmax);
+    const float down = exp2i(-e);
+    if (lane == 0) row_scale[m] = exp2i(e);
+    _Float16* ar = a + int64_t(m) * lda;
+    for (int k = 4 * lane; k < K; k += 256) {
+        const floatx4 v = load4f(xr + k);
+        _Float16 out[4];
+        if (MODE == T_F16) {
+            for (int i = 0; i < 4; ++i) out[i] = (_Float16)(v[i] * down);
+        } else {
+            float d;
+            int q[4];
+            if (MODE == T_Q8_0) {
+                q8_0_codes(v, x86, d, q);
+                d = half_bits_to_float(float_to_half_bits(d));   // stored fp16 scale
+            } else {
+                q8_k_codes(v, lane, d, q);
+            }
+            for (int i = 0; i < 4; ++i) out[i] = (_Float16)((d * (float)q[i]) * down);
+        }
+        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<half4*>(ar + k) = half4{out[0], out[1], out[2], out[3]};
+    }
+}
+
+// Scalar-load variant for rows that are not 16-byte aligned.
+template <int MODE>
+__global__ __launch_bounds__(256) void stage_rows_unaligned_kernel(const float* __restrict__ x, int64_t x_stride, int M,
+                                                                   int K, _Float16* __restrict__ a, int64_t lda,
+                                                                   float* __restrict__ row_scale, int x86) {
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= M) return;
+    const float* xr = x + int64_t(m) * x_stride;
+    auto load = [&](int k) { return floatx4{xr[k], xr[k + 1], xr[k + 2], xr[k + 3]}; };
+    float rmax = 0.f;
+    for (int k = 4 * lane; k < K; k += 256) {
+        const floatx4 v = load(k);
+        rmax = fmaxf(rmax, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    }
+    rmax = wave_max(rmax);
+    const int e = row_exponent(rmax);
+    const float down = exp2i(-e);
+    if (lane == 0) row_scale[m] = exp2i(e);
+    _Float16* ar = a + int64_t(m) * lda;
+    for (int k = 4 * lane; k < K; k += 256) {
+        const floatx4 v = load(k);
+        float d = 0.f;
+        int q[4];
+        if (MODE == T_Q8_0) {
+            q8_0_codes(v, x86, d, q);
+            d = half_bits_to_float(float_to_half_bits(d));
+        } else if (MODE == T_Q8_K) {
+            q8_k_codes(v, lane, d, q);
+        }
+        for (int i = 0; i < 4; ++i)
+            ar[k + i] = MODE == T_F16 ? (_Float16)(v[i] * down) : (_Float16)((d * (float)q[i]) * down);
+    }
+}
+
+// Q8_0 / Q8_K rows in ggml wire format.  One wave per row.
+template <int TYPE>
+__global__ __launch_bounds__(256) void quantize_act_kernel(const float* __restrict__ x, int64_t x_stride, int rows,
+                                                           int K, uint8_t* __restrict__ dst, int x86) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float* xr = x + int64_t(r) * x_stride;
+    constexpr int BE = block_elems(TYPE), BB = block_bytes(TYPE);
+    uint8_t* out = dst + int64_t(r) * (K / BE) * BB;
+    for (int k = 4 * lane; k < K; k += 256) {
+        const floatx4 v = floatx4{xr[k], xr[k + 1], xr[k + 2], xr[k + 3]};
+        float d;
+        int q[4];
+        if (TYPE == T_Q8_0) q8_0_codes(v, x86, d, q);
+        else q8_k_codes(v, lane, d, q);
+        uint8_t* blk = out + (k / BE) * BB;
+        const int within = k % BE;
+        if (TYPE == T_Q8_0) {
+            if (within == 0) {
+                const uint16_t h = float_to_half_bits(d);
+                blk[0] = uint8_t(h & 0xff);
+                blk[1] = uint8_t(h >> 8);
+            }
+            for (int i = 0; i < 4; ++i) blk[2 + within + i] = uint8_t(int8_t(q[i]));
+        } else {
+            if (within == 0) *reinterpret_cast<float*>(blk) = d;
+            for (int i = 0; i < 4; ++i) blk[4 + within + i] = uint8_t(int8_t(q[i]));
+            const int s = group_sum<4>(q[0] + q[1] + q[2] + q[3]);
+            if ((lane & 3) == 0) {
+                const int16_t s16 = int16_t(s);
+                blk[260 + 2 * (within / 16)] = uint8_t(uint16_t(s16) & 0xff);
+                blk[260 + 2 * (within / 16) + 1] = uint8_t(uint16_t(s16) >> 8);
+            }
+        }
+    }
+}
+
+// to_float of one 32-element group (a Q8_0 block, a Q4_K/Q5_K sub-block, two
+// Q6_K sub-blocks, a quarter of a Q8_K block's codes).
+template <int TYPE>
+__device__ void dequant32(const uint8_t* row, int g, float* y) {
+    if (TYPE == T_Q8_0) {
+        const uint8_t* b = row + 34 * g;
+        const float d = half_bits_to_float(load2_a2(b));
+        for (int i = 0; i < 32; ++i) y[i] = d * (float)(int8_t)b[2 + i];
+    } else if (TYPE == T_Q8_K) {
+        const uint8_t* b = row + 292 * (g >> 3);
+        const float d = __builtin_bit_cast(float, load4_a2(b));
+        for (int i = 0; i < 32; ++i) y[i] = d * (float)(int8_t)b[4 + 32 * (g & 7) + i];
+    } else if (TYPE == T_Q4_K || TYPE == T_Q5_K) {
+        const int bb = TYPE == T_Q4_K ? 144 : 176;
+        const uint8_t* b = row + bb * (g >> 3);
+        const int j = g & 7;
+        const uint32_t sc[3] = {load4_a2(b + 4), load4_a2(b + 8), load4_a2(b + 12)};
+        int s, m;
+        k4_scale_min(j, sc, s, m);
+        const float dj = half_bits_to_float(load2_a2(b)) * (float)s;
+        const float mj = half_bits_to_float(load2_a2(b + 2)) * (float)m;
+        const uint8_t* qs = b + (TYPE == T_Q4_K ? 16 : 48) + 32 * (j >> 1);
+        for (int l = 0; l < 32; ++l) {
+            int v = (j & 1) ? (qs[l] >> 4) : (qs[l] & 0x0f);
+            if (TYPE == T_Q5_K && ((b[16 + l] >> j) & 1)) v += 16;
+            y[l] = dj * (float)v - mj;
+        }
+    } else if (TYPE == T_Q6_K) {
+        const uint8_t* b = row + 210 * (g >> 3);
+        const int j = g & 7, half = j >> 2, q4 = j & 3;
+        const float d = half_bits_to_float(load2_a2(b + 208));
+        for (int l = 0; l < 32; ++l) {
+            const uint8_t lb = b[64 * half + 32 * (q4 & 1) + l];
+            const int lo = (q4 < 2) ? (lb & 0x0f) : (lb >> 4);
+            const int hi = (b[128 + 32 * half + l] >> (2 * q4)) & 3;
+            const int sc = (int8_t)b[192 + 8 * half + 2 * q4 + l / 16];
+            y[l] = d * (float)sc * (float)((lo | (hi << 4)) - 32);
+        }
+    }
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __restrict__ src, int64_t src_stride,
+                                                           const int32_t* __restrict__ ids, int64_t src_rows,
+                                                           float* __restrict__ dst, int64_t dst_stride, int rows,
+                                                           int K, int* __restrict__ bad_id) {
+    const int groups = K / 32;
+    const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= int64_t(rows) * groups) return;
+    const int r = int(t / groups), g = int(t % groups);
+    int64_t sr = r;
+    if (ids) {
+        sr = ids[r];
+        if (sr < 0 || sr >= src_rows) {
+            if (g == 0) atomicOr(bad_id, 1);
+            return;
+        }
+    }
+    const uint8_t* row = src + sr * src_stride;
+    float* y = dst + int64_t(r) * dst_stride + 32 * g;
+    if (TYPE == T_F32) {
+        const float* f = reinterpret_cast<const float*>(row) + 32 * g;
+        for (int i = 0; i < 32; ++i) y[i] = f[i];
+    } else if (TYPE == T_F16) {
+        const _Float16* f = reinterpret_cast<const _Float16*>(row) + 32 * g;
+        for (int i = 0; i < 32; ++i) y[i] = (float)f[i];
+    } else {
+        dequant32<TYPE>(row, g, y);
+    }
+}
+
+}  // namespace
+
+void launch_stage_rows(int mode, bool aligned, const float* x, int64_t x_stride, int M, int K, _Float16* a,
+                       int64_t lda, float* row_scale, int x86, hipStream_t stream) {
+    const dim3 grid((M + 3) / 4), block(256);
+#define SAMHIP_STAGE(MODE)                                                                                      \
+    if (aligned) hipLaunchKernelGGL(stage_rows_kernel<MODE>, grid, block, 0, stream, x, x_stride, M, K, a, lda, \
+                                    row_scale, x86);                                                           \
+    else hipLaunchKernelGGL(stage_rows_unaligned_kernel<MODE>, grid, block, 0, stream, x, x_stride, M, K, a, lda, \
+                            row_scale, x86);
+    switch (mode) {
+        case T_F16: SAMHIP_STAGE(T_F16) break;
+        case T_Q8_0: SAMHIP_STAGE(T_Q8_0) break;
+        case T_Q8_K: SAMHIP_STAGE(T_Q8_K) break;
+        default: break;
+    }
+#undef SAMHIP_STAGE
+}
+
+void launch_quantize_act(int type, const float* x, int64_t x_stride, int rows, int K, void* dst, int x86,
+                         hipStream_t stream) {
+    const dim3 grid((rows + 3) / 4), block(256);
+    if (type == T_Q8_0)
+        hipLaunchKernelGGL(quantize_act_kernel<T_Q8_0>, grid, block, 0, stream, x, x_stride, rows, K,
+                           static_cast<uint8_t*>(dst), x86);
+    else
+        hipLaunchKernelGGL(quantize_act_kernel<T_Q8_K>, grid, block, 0, stream, x, x_stride, rows, K,
+                           static_cast<uint8_t*>(dst), x86);
+}
+
+void launch_dequant_rows(int type, const void* src, int64_t src_stride, const int32_t* ids, int64_t src_rows,
+                         float* dst, int64_t dst_stride, int rows, int K, int* bad_id, hipStream_t stream) {
+    const int64_t threads = int64_t(rows) * (K / 32);
+    const dim3 grid(unsigned((threads + 255) / 256)), block(256);
+    const uint8_t* s = static_cast<const uint8_t*>(src);
+#define SAMHIP_DQ(T) \
+    hipLaunchKernelGGL(dequant_rows_kernel<T>, grid, block, 0, stream, s, src_stride, ids, src_rows, dst, dst_stride, rows, K, bad_id)
+    switch (type) {
+        case T_F32: SAMHIP_DQ(T_F32); break;
+        case T_F16: SAMHIP_DQ(T_F16); break;
+        case T_Q8_0: SAMHIP_DQ(T_Q8_0); break;
+        case T_Q4_K: SAMHIP_DQ(T_Q4_K); break;
+        case T_Q5_K: SAMHIP_DQ(T_Q5_K); break;
+        case T_Q6_K: SAMHIP_DQ(T_Q6_K); break;
+        case T_Q8_K: SAMHIP_DQ(T_Q8_K); break;
+        default: break;
+    }
+#undef SAMHIP_DQ
+}
+
+}  // namespace samhip

@@ -1,0 +1,281 @@
+"""ctypes binding of libsamhip (include/samhip.h) for tests and bench.py.
+
+This is a thin veneer over the C ABI, in the manner of the reference's own
+ctypes bridge to its native CUDA cache encoder
+(tools/quantize/cache_quantization.py:26-49).  There is no fallback: if
+libsamhip.so is missing or no HIP device is visible, calls raise.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsamhip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "samhip.h")
+
+ABI_VERSION = 1
+F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, I32 = 0, 1, 8, 12, 13, 14, 15, 26
+COMPUTE_Q8_NATIVE, COMPUTE_F16 = 0, 1
+ROUND_X86, ROUND_REF = 0, 1
+OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_DEVICE, ERR_OUT_OF_MEMORY = 0, -1, -2, -3, -4
+BLOCK_ELEMS = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256, I32: 1}
+BLOCK_BYTES = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292, I32: 4}
+TYPE_NAMES = {Q8_0: "q8_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K", F32: "f32", F16: "f16"}
+
+# Every entry point the header declares, with its ctypes signature.
+_P, _I, _I32, _I64, _SZ, _U32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_uint32
+
+
+class Tensor(ctypes.Structure):
+    _fields_ = [("type", ctypes.c_int32), ("ne", ctypes.c_int64 * 4), ("nb", ctypes.c_size_t * 4), ("data", ctypes.c_void_p)]
+
+
+class Options(ctypes.Structure):
+    _fields_ = [("version", ctypes.c_uint32), ("device", ctypes.c_int32), ("compute", ctypes.c_int32),
+                ("q8_rounding", ctypes.c_int32)]
+
+
+class ExecInfo(ctypes.Structure):
+    _fields_ = [("version", ctypes.c_uint32), ("device", ctypes.c_int32),
+                ("mul_mat_calls", ctypes.c_uint64), ("gemm_launches", ctypes.c_uint64),
+                ("skinny_launches", ctypes.c_uint64), ("activation_launches", ctypes.c_uint64),
+                ("get_rows_calls", ctypes.c_uint64), ("activation_payload_peak_bytes", ctypes.c_uint64),
+                ("activation_allocation_peak_bytes", ctypes.c_uint64), ("kernel_variant", ctypes.c_char * 64),
+                ("arithmetic_profile", ctypes.c_char * 48), ("device_name", ctypes.c_char * 64)]
+
+
+class KernelRecord(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_char * 64), ("weight_type", ctypes.c_int32), ("m", ctypes.c_int64),
+                ("n", ctypes.c_int64), ("k", ctypes.c_int64), ("ms", ctypes.c_float)]
+
+
+SIGNATURES = {
+    "samhip_abi_version": ([], _I),
+    "samhip_device_count": ([_P], _I),
+    "samhip_context_create": ([ctypes.POINTER(Options), ctypes.POINTER(_P)], _I),
+    "samhip_context_destroy": ([_P], None),
+    "samhip_context_set_stream": ([_P, _P], _I),
+    "samhip_synchronize": ([_P], _I),
+    "samhip_buffer_alloc": ([_P, _SZ, ctypes.POINTER(_P)], _I),
+    "samhip_buffer_free": ([_P, _P], _I),
+    "samhip_tensor_set": ([_P, _P, _P, _SZ], _I),
+    "samhip_tensor_get": ([_P, _P, _P, _SZ], _I),
+    "samhip_supports_mul_mat": ([ctypes.POINTER(Tensor)] * 3, _I),
+    "samhip_mul_mat": ([_P] + [ctypes.POINTER(Tensor)] * 3, _I),
+    "samhip_get_rows": ([_P] + [ctypes.POINTER(Tensor)] * 3, _I),
+    "samhip_quantize_rows": ([_P, _I32, _P, _SZ, _P, _I64, _I64, _I32], _I),
+    "samhip_dequantize_rows": ([_P, _I32, _P, _SZ, _P, _I64, _I64], _I),
+    "samhip_validate_quantized_payload": ([_I32, _I64, _I64, _P, _SZ], _I),
+    "samhip_query": ([_P, ctypes.POINTER(ExecInfo)], _I),
+    "samhip_last_error": ([ctypes.c_char_p, _SZ], _SZ),
+    "samhip_trace_begin": ([_P], _I),
+    "samhip_trace_end": ([_P, ctypes.POINTER(KernelRecord), _SZ, ctypes.POINTER(_SZ)], _I),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libsamhip.so; raises if it was not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"libsamhip.so is not built ({LIB_PATH}); run __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        if L.samhip_abi_version() != ABI_VERSION:
+            raise RuntimeError("libsamhip ABI version mismatch")
+        _lib = L
+    return _lib
+
+
+class SamhipError(RuntimeError):
+    def __init__(self, status, message):
+        super().__init__(f"samhip status {status}: {message}")
+        self.status = status
+
+
+class InvalidArgument(SamhipError, ValueError):
+    pass
+
+
+def last_error():
+    buf = ctypes.create_string_buffer(1024)
+    lib().samhip_last_error(buf, 1024)
+    return buf.value.decode(errors="replace")
+
+
+def check(status):
+    if status != OK:
+        cls = InvalidArgument if status == ERR_INVALID_ARGUMENT else SamhipError
+        raise cls(status, last_error())
+    return status
+
+
+def row_bytes(qtype, k):
+    return k // BLOCK_ELEMS[qtype] * BLOCK_BYTES[qtype]
+
+
+def device_count():
+    n = ctypes.c_int(0)
+    check(lib().samhip_device_count(ctypes.byref(n)))
+    return n.value
+
+
+def tensor(qtype, ne0, ne1, data, nb1=None):
+    """A 2-D ggml tensor descriptor over device address `data`."""
+    t = Tensor()
+    t.type = qtype
+    t.ne[0], t.ne[1], t.ne[2], t.ne[3] = ne0, ne1, 1, 1
+    nb0 = BLOCK_BYTES[qtype]
+    rb = row_bytes(qtype, ne0)
+    t.nb[0] = nb0
+    t.nb[1] = rb if nb1 is None else nb1
+    t.nb[2] = t.nb[1] * ne1
+    t.nb[3] = t.nb[2]
+    t.data = data
+    return t
+
+
+def validate_quantized_payload(qtype, ne0, rows, payload):
+    payload = np.ascontiguousarray(payload, np.uint8)
+    return check(lib().samhip_validate_quantized_payload(qtype, ne0, rows, payload.ctypes.data, payload.nbytes))
+
+
+class Buffer:
+    def __init__(self, ctx, nbytes):
+        self.ctx, self.nbytes = ctx, int(nbytes)
+        p = ctypes.c_void_p()
+        check(lib().samhip_buffer_alloc(ctx.handle, self.nbytes, ctypes.byref(p)))
+        self.ptr = p.value
+
+    def free(self):
+        if self.ptr:
+            check(lib().samhip_buffer_free(self.ctx.handle, self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and self.ctx.handle:
+                lib().samhip_buffer_free(self.ctx.handle, self.ptr)
+        except Exception:
+            pass
+
+
+class Context:
+    def __init__(self, device=0, compute=COMPUTE_Q8_NATIVE, q8_rounding=ROUND_X86):
+        o = Options(ABI_VERSION, device, compute, q8_rounding)
+        h = ctypes.c_void_p()
+        check(lib().samhip_context_create(ctypes.byref(o), ctypes.byref(h)))
+        self.handle = h.value
+
+    def close(self):
+        if self.handle:
+            lib().samhip_context_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def set_stream(self, stream_handle):
+        check(lib().samhip_context_set_stream(self.handle, stream_handle))
+
+    def synchronize(self):
+        check(lib().samhip_synchronize(self.handle))
+
+    def alloc(self, nbytes):
+        return Buffer(self, nbytes)
+
+    def upload(self, array):
+        a = np.ascontiguousarray(array)
+        b = Buffer(self, max(a.nbytes, 1))
+        check(lib().samhip_tensor_set(self.handle, b.ptr, a.ctypes.data, a.nbytes))
+        return b
+
+    def write(self, buf, array, offset=0):
+        a = np.ascontiguousarray(array)
+        check(lib().samhip_tensor_set(self.handle, buf.ptr + offset, a.ctypes.data, a.nbytes))
+
+    def download(self, buf, shape, dtype, offset=0):
+        out = np.empty(shape, dtype)
+        check(lib().samhip_tensor_get(self.handle, out.ctypes.data, buf.ptr + offset, out.nbytes))
+        return out
+
+    def mul_mat(self, w, x, y):
+        check(lib().samhip_mul_mat(self.handle, ctypes.byref(w), ctypes.byref(x), ctypes.byref(y)))
+
+    def get_rows(self, src, ids, dst):
+        check(lib().samhip_get_rows(self.handle, ctypes.byref(src), ctypes.byref(ids), ctypes.byref(dst)))
+
+    def quantize_rows(self, qtype, src_ptr, src_stride, dst_ptr, rows, k, q8_rounding=ROUND_X86):
+        check(lib().samhip_quantize_rows(self.handle, qtype, src_ptr, src_stride, dst_ptr, rows, k, q8_rounding))
+
+    def dequantize_rows(self, qtype, src_ptr, src_stride, dst_ptr, rows, k):
+        check(lib().samhip_dequantize_rows(self.handle, qtype, src_ptr, src_stride, dst_ptr, rows, k))
+
+    def query(self):
+        info = ExecInfo()
+        check(lib().samhip_query(self.handle, ctypes.byref(info)))
+        return info
+
+    def trace_begin(self):
+        check(lib().samhip_trace_begin(self.handle))
+
+    def trace_end(self, capacity=1 << 16):
+        """Returns [(kernel, weight_type, m, n, k, ms)] of the launches since trace_begin."""
+        recs = (KernelRecord * capacity)()
+        count = ctypes.c_size_t(0)
+        check(lib().samhip_trace_end(self.handle, recs, capacity, ctypes.byref(count)))
+        return [(r.kernel.decode(), r.weight_type, r.m, r.n, r.k, r.ms) for r in recs[:min(count.value, capacity)]]
+
+    # -- numpy conveniences used by the tests ------------------------------
+    def quantize(self, qtype, x, q8_rounding=ROUND_X86):
+        x = np.ascontiguousarray(x, np.float32)
+        rows, k = x.shape
+        src = self.upload(x)
+        dst = self.alloc(rows * row_bytes(qtype, k))
+        self.quantize_rows(qtype, src.ptr, 4 * k, dst.ptr, rows, k, q8_rounding)
+        return self.download(dst, (rows, row_bytes(qtype, k)), np.uint8)
+
+    def dequantize(self, qtype, packed, k):
+        packed = np.ascontiguousarray(packed, np.uint8)
+        rows = packed.size // row_bytes(qtype, k)
+        src = self.upload(packed)
+        dst = self.alloc(rows * k * 4)
+        self.dequantize_rows(qtype, src.ptr, row_bytes(qtype, k), dst.ptr, rows, k)
+        return self.download(dst, (rows, k), np.float32)
+
+    def matmul(self, qtype, w_packed, x, w_row_offset=0, w_rows=None, x_row_stride=None):
+        """Y = X W^T through samhip_mul_mat on device copies of numpy inputs.
+
+        w_packed: [rows, row_bytes] uint8 (the whole packed tensor); the
+        product uses rows [w_row_offset, w_row_offset + w_rows) as a view.
+        x: [M, K] F32; with x_row_stride (floats) > K the rows are strided.
+        """
+        w_packed = np.ascontiguousarray(w_packed, np.uint8)
+        x = np.ascontiguousarray(x, np.float32)
+        m, k = x.shape
+        rb = row_bytes(qtype, k)
+        n = w_packed.shape[0] - w_row_offset if w_rows is None else w_rows
+        wb = self.upload(w_packed)
+        xs = k if x_row_stride is None else x_row_stride
+        if xs != k:
+            xp = np.full((m, xs), 91.0, np.float32)
+            xp[:, :k] = x
+        else:
+            xp = x
+        xb = self.upload(xp)
+        yb = self.alloc(m * n * 4)
+        wt = tensor(qtype, k, n, wb.ptr + w_row_offset * rb, nb1=rb)
+        xt = tensor(F32, k, m, xb.ptr, nb1=4 * xs)
+        yt = tensor(F32, n, m, yb.ptr)
+        self.mul_mat(wt, xt, yt)
+        return self.download(yb, (m, n), np.float32)

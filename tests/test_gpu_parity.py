@@ -1,0 +1,275 @@
+"""HIP path parity against the CPU oracle, through the C ABI.
+
+Bars (stated per test):
+  * packing (quantize_rows, dequantize_rows, get_rows): bit-exact;
+  * mul_mat: max per-row relative L2 <= 1e-3 against the oracle's matching
+    CPU path (native Q8 packing for COMPUTE_Q8_NATIVE, F32 decode for
+    COMPUTE_F16), plus the reference tests' element tolerances against a
+    double-precision dot over decoded operands.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+
+from tests.reference_fixtures import (DECODED_TOL, matrix_values, max_row_rel_l2, probe_rhs,
+                                      probe_weights, within)
+
+pytestmark = pytest.mark.gpu
+
+ROW_REL_L2 = 1e-3
+TYPES = [8, 14, 13, 12]   # Q8_0, Q6_K, Q5_K, Q4_K
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def assert_same_bytes(got, ref, block_bytes, x=None, block_elems=None):
+    """Bit-exact comparison that names the first differing blocks."""
+    if np.array_equal(got, ref):
+        return
+    bad = np.argwhere(got != ref)
+    lines = [f"{len(bad)} differing bytes of {got.size}"]
+    for r, c in bad[:6]:
+        b = c // block_bytes
+        msg = f"row {r} byte {c} (block {b}, offset {c % block_bytes}): gpu {got[r, c]} cpu {ref[r, c]}"
+        if x is not None:
+            seg = x[r, b * block_elems:(b + 1) * block_elems]
+            msg += f" | block amax {np.abs(seg).max():.9g}"
+            if c % block_bytes >= 2 and block_elems == 32:
+                msg += f" value {seg[c % block_bytes - 2]:.9g}"
+        lines.append(msg)
+    raise AssertionError("\n".join(lines))
+
+
+@pytest.fixture(scope="module")
+def f16_ctx(samhip):
+    ctx = samhip.Context(0, samhip.COMPUTE_F16)
+    yield ctx
+    ctx.close()
+
+
+# ---- packing ---------------------------------------------------------------
+
+@pytest.mark.parametrize("rounding", ["x86", "ref"])
+def test_quantize_q8_0_bit_exact(gpu_ctx, oracle, samhip, rounding):
+    say("case quantize q8_0 rounding", rounding)
+    gpu_mode = samhip.ROUND_X86 if rounding == "x86" else samhip.ROUND_REF
+    cpu_mode = oracle.ROUND_X86 if rounding == "x86" else oracle.ROUND_REF
+    rng = np.random.default_rng(21)
+    x = (rng.standard_normal((67, 4736)) * np.exp(rng.uniform(-8, 8, (67, 1)))).astype(np.float32)
+    x[0, :8] = [127, 0.5, 1.5, -0.5, -1.5, np.nextafter(np.float32(0.5), np.float32(0)), -127, 0]
+    x[1, :32] = 0.0
+    x[2, :32] = np.arange(32) - 15.5           # many exact ties
+    got = gpu_ctx.quantize(8, x, gpu_mode)
+    ref = oracle.quantize(oracle.Q8_0, x, cpu_mode)
+    assert_same_bytes(got, ref, 34, x, 32)
+    kat = [127, 1, 2, -1, -2, 0, -127, 0] if rounding == "ref" else [127, 0, 2, 0, -2, 0, -127, 0]
+    assert got[0, 2:10].view(np.int8).tolist() == kat
+
+
+def test_quantize_q8_k_bit_exact(gpu_ctx, oracle):
+    say("case quantize q8_K")
+    rng = np.random.default_rng(22)
+    x = (rng.standard_normal((33, 1024)) * np.exp(rng.uniform(-8, 8, (33, 1)))).astype(np.float32)
+    x[3, :256] = 0.0
+    x[4, :2] = [5.0, -5.0]
+    x[4, 2:256] = 0.1
+    x[5, 10] = -1e6
+    got = gpu_ctx.quantize(15, x)
+    assert_same_bytes(got, oracle.quantize(oracle.Q8_K, x), 292, x, 256)
+
+
+@pytest.mark.parametrize("qtype", [12, 13, 14])
+def test_weight_quantizer_bit_exact(gpu_ctx, oracle, qtype):
+    say("case weight quantize", qtype)
+    rng = np.random.default_rng(23)
+    w = (rng.standard_normal((40, 1024)) * 0.02).astype(np.float32)
+    w[3] = 0.0
+    w[4, :300] = 0.0
+    w[5] = matrix_values(1024, 6, 3)[5]
+    w[6, 7] = 3.0
+    got = gpu_ctx.quantize(qtype, w)
+    ref = oracle.quantize(qtype, w)
+    assert_same_bytes(got, ref, oracle.BLOCK_BYTES[qtype], w, 256)
+
+
+@pytest.mark.parametrize("qtype", [8, 12, 13, 14, 15])
+def test_dequantize_bit_exact(gpu_ctx, oracle, qtype):
+    say("case dequantize", qtype)
+    rng = np.random.default_rng(24)
+    x = (rng.standard_normal((19, 512)) * 0.3).astype(np.float32)
+    packed = oracle.quantize(qtype, x, oracle.ROUND_REF)
+    got = gpu_ctx.dequantize(qtype, packed, 512)
+    ref = oracle.dequantize(qtype, packed, 512)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", [0, 8, 12, 14])
+def test_get_rows(gpu_ctx, oracle, samhip, qtype):
+    say("case get_rows", qtype)
+    rng = np.random.default_rng(25)
+    k, rows = 1024, 49
+    src_f = (rng.standard_normal((rows, k)) * 0.1).astype(np.float32)
+    payload = src_f if qtype == 0 else oracle.quantize(qtype, src_f, oracle.ROUND_REF)
+    expect_rows = src_f if qtype == 0 else oracle.dequantize(qtype, payload, k)
+    ids = np.array([5, 0, 48, 5, 17, 31, 2], np.int32)
+    sb, ib = gpu_ctx.upload(payload), gpu_ctx.upload(ids)
+    db = gpu_ctx.alloc(len(ids) * k * 4)
+    src = samhip.tensor(qtype, k, rows, sb.ptr)
+    idt = samhip.tensor(samhip.I32, len(ids), 1, ib.ptr)
+    dst = samhip.tensor(samhip.F32, k, len(ids), db.ptr)
+    gpu_ctx.get_rows(src, idt, dst)
+    got = gpu_ctx.download(db, (len(ids), k), np.float32)
+    assert np.array_equal(got, expect_rows[ids])
+    bad = gpu_ctx.upload(np.array([1, rows], np.int32))
+    with pytest.raises(samhip.InvalidArgument, match="out of range"):
+        gpu_ctx.get_rows(src, samhip.tensor(samhip.I32, 2, 1, bad.ptr),
+                         samhip.tensor(samhip.F32, k, 2, db.ptr))
+
+
+# ---- mul_mat: the reference's own cases -------------------------------------
+
+def fp16_operand_bound(wd, xd):
+    """Rigorous bound, shape [N, M], for sum_k fl16(w_k) fl16(x_k) accumulated
+    in F32 against the exact sum: (2u + u^2 + gamma_K) * sum_k |w_k x_k| with
+    u = 2^-11 (binary16 unit roundoff, both operands rounded once) and
+    gamma_K = K 2^-24 (F32 accumulation; binary16 products are exact in F32),
+    plus the absolute error of binary16 subnormals: 2^-25 per weight, and
+    2^-25 * 2^e per activation of a row staged with scale 2^e (row max in
+    [2^14, 2^15) after scaling)."""
+    k = wd.shape[1]
+    u = 2.0 ** -11
+    gamma = k * 2.0 ** -24 * 1.01
+    aw, ax = np.abs(wd).astype(np.float64), np.abs(xd).astype(np.float64)
+    rel = (2 * u + u * u + gamma) * aw @ ax.T
+    row_scale = ax.max(axis=1) * 2.0 ** -13
+    sub = 2.0 ** -25 * (aw.sum(axis=1)[:, None] * row_scale[None, :] + ax.sum(axis=1)[None, :]) * (1 + 2 * u)
+    return rel + sub
+
+
+def _check_product(oracle, qtype, packed, x, y_native, y_f16, ref_tol=None):
+    k = x.shape[1]
+    wd = oracle.dequantize(qtype, packed, k)
+    xtype = oracle.Q8_0 if qtype == oracle.Q8_0 else oracle.Q8_K
+    xd = oracle.dequantize(xtype, oracle.quantize(xtype, x, oracle.ROUND_X86), k)
+    for y, xs, label in ((y_native, xd, "native"), (y_f16, x, "f16")):
+        exact = oracle.gemm_f64(wd, xs)
+        err = np.abs(y.astype(np.float64) - exact)
+        bound = fp16_operand_bound(wd, xs).T + 1e-30
+        assert np.all(np.isfinite(y)) and np.all(err <= bound), f"{label}: worst err/bound {(err / bound).max()}"
+        if ref_tol is not None:
+            ok, e = within(y, exact, ref_tol)
+            assert ok, f"{label} vs reference tolerance: {e}"
+    r1 = max_row_rel_l2(y_native, oracle.mul_mat_native(qtype, packed, x, oracle.ROUND_X86))
+    r2 = max_row_rel_l2(y_f16, oracle.mul_mat_decode(qtype, packed, x))
+    assert r1 <= ROW_REL_L2 and r2 <= ROW_REL_L2, (r1, r2)
+    return r1, r2
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("width", [256, 1024])
+@pytest.mark.parametrize("columns", [3, 33])
+def test_mul_mat_qkv_views_and_tail(gpu_ctx, f16_ctx, oracle, qtype, width, columns):
+    """check_backend_quantized_math (tests/runtime/ggml/test_quantization.cpp:496-559)."""
+    say("case mul_mat views/tail", qtype, width, columns)
+    x = matrix_values(width, columns, 3)
+    qkv = oracle.quantize(qtype, matrix_values(width, 3 * width, TYPES.index(qtype) + 1))
+    for s in range(3):
+        yn = gpu_ctx.matmul(qtype, qkv, x, w_row_offset=s * width, w_rows=width)
+        yf = f16_ctx.matmul(qtype, qkv, x, w_row_offset=s * width, w_rows=width)
+        _check_product(oracle, qtype, qkv[s * width:(s + 1) * width], x, yn, yf, DECODED_TOL)
+    tail = oracle.quantize(qtype, matrix_values(width, 257, TYPES.index(qtype) + 7))
+    _check_product(oracle, qtype, tail, x, gpu_ctx.matmul(qtype, tail, x), f16_ctx.matmul(qtype, tail, x), DECODED_TOL)
+
+
+@pytest.mark.parametrize("columns", [3, 33])
+def test_mul_mat_q8_0_4736(gpu_ctx, f16_ctx, oracle, columns):
+    """check_backend_q8_k_fallback: Q8_0 at the 4736-wide fc2 row."""
+    say("case mul_mat q8_0 4736", columns)
+    x = matrix_values(4736, columns, 13)
+    w = oracle.quantize(oracle.Q8_0, matrix_values(4736, 17, 17))
+    _check_product(oracle, 8, w, x, gpu_ctx.matmul(8, w, x), f16_ctx.matmul(8, w, x), DECODED_TOL)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("case", [(256, 65, 1, "ordinary"), (256, 65, 8, "ordinary"), (256, 65, 17, "strided"),
+                                  (1024, 33, 3, "outlier"), (256, 33, 3, "zero")])
+def test_mul_mat_probe_cases(gpu_ctx, f16_ctx, oracle, qtype, case):
+    """test_cpu_quantized_matmul.cpp:79-88 cases, native tolerance 5e-4 + 5e-5|ref|."""
+    width, rows, columns, scenario = case
+    say("case mul_mat probe", qtype, case)
+    w = oracle.quantize(qtype, probe_weights(width, rows))
+    x = probe_rhs(width, columns, "ordinary" if scenario == "strided" else scenario)
+    stride = 2 * width if scenario == "strided" else None
+    yn = gpu_ctx.matmul(qtype, w, x, x_row_stride=stride)
+    yf = f16_ctx.matmul(qtype, w, x, x_row_stride=stride)
+    _check_product(oracle, qtype, w, x, yn, yf)
+    if scenario == "zero":
+        assert not yn.any() and not yf.any()
+
+
+def test_mul_mat_q8_0_k32(gpu_ctx, f16_ctx, oracle):
+    say("case mul_mat q8_0 k32")
+    w = oracle.quantize(oracle.Q8_0, probe_weights(32, 3))
+    x = probe_rhs(32, 3)
+    _check_product(oracle, 8, w, x, gpu_ctx.matmul(8, w, x), f16_ctx.matmul(8, w, x))
+
+
+def test_mul_mat_extreme_row_magnitudes(gpu_ctx, f16_ctx, oracle):
+    """F16 mode keeps rows far outside binary16's range accurate (per-row
+    power-of-two scale).  Native Q8_0 packing is ggml's: a block scale above
+    65504 overflows and a tiny one flushes to zero, on the CPU as here, so
+    native rows must reproduce the oracle's non-finite and zero rows exactly."""
+    say("case mul_mat extreme rows")
+    rng = np.random.default_rng(26)
+    w = oracle.quantize(oracle.Q8_0, (rng.standard_normal((96, 512)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((6, 512)).astype(np.float32)
+    x *= np.array([1e-30, 1e-12, 1.0, 1e4, 1e7, 1e12], np.float32)[:, None]
+    yf = f16_ctx.matmul(8, w, x)
+    assert max_row_rel_l2(yf, oracle.mul_mat_decode(8, w, x)) <= ROW_REL_L2
+    yn, ref = gpu_ctx.matmul(8, w, x), oracle.mul_mat_native(8, w, x)
+    assert np.array_equal(np.isnan(yn), np.isnan(ref)) and np.array_equal(yn == 0, ref == 0)
+    finite = np.isfinite(ref).all(axis=1) & (np.abs(ref).sum(axis=1) > 0)
+    assert finite.sum() >= 2
+    assert max_row_rel_l2(yn[finite], ref[finite]) <= ROW_REL_L2
+
+
+# ---- mul_mat at the SAM 3 ViT shapes (M = 5184 tokens) ----------------------
+
+VIT = {"qkv": (1024, 3072), "proj": (1024, 1024), "fc1": (1024, 4736), "fc2": (4736, 1024)}
+
+
+@pytest.mark.parametrize("name", list(VIT))
+@pytest.mark.parametrize("qtype", TYPES)
+def test_mul_mat_vit_shapes_sampled_rows(gpu_ctx, f16_ctx, oracle, samhip, name, qtype):
+    k, n = VIT[name]
+    if k % samhip.BLOCK_ELEMS[qtype]:
+        pytest.skip("4736-wide rows are stored as Q8_0 (src/models/sam3/weights.hpp:159-160)")
+    say("case vit", name, qtype)
+    m = 5184
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = gpu_ctx.quantize(qtype, (np.random.default_rng(0).standard_normal((n, k)) * 0.02).astype(np.float32),
+                         samhip.ROUND_REF)
+    rows = np.unique(np.concatenate([np.arange(0, m, 97), [m - 1]]))
+    yn = gpu_ctx.matmul(qtype, w, x)
+    r1 = max_row_rel_l2(yn[rows], oracle.mul_mat_native(qtype, w, x[rows]))
+    del yn
+    yf = f16_ctx.matmul(qtype, w, x)
+    r2 = max_row_rel_l2(yf[rows], oracle.mul_mat_decode(qtype, w, x[rows]))
+    say("  row rel L2 native", r1, "f16", r2)
+    assert r1 <= ROW_REL_L2 and r2 <= ROW_REL_L2
+    # size-independent property: linearity in X
+    y2 = f16_ctx.matmul(qtype, w, (2.0 * x[:64]).astype(np.float32))
+    assert np.array_equal(y2, 2.0 * yf[:64])
+
+
+def test_exec_info_counts(gpu_ctx, samhip):
+    info = gpu_ctx.query()
+    assert info.version == 1 and info.mul_mat_calls > 0 and info.gemm_launches > 0
+    assert b"gfx950" in info.device_name
+    assert info.arithmetic_profile == b"samhip-q8-native-f16mfma-v1"
