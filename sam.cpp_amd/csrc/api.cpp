@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -57,10 +58,15 @@ struct samhip_context {
     int q8_rounding = SAMHIP_Q8_ROUND_X86;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
-    // staged fp16 activations [M][K] followed by F32 row scales [M]
+    // staged fp16 activations [M][K], F32 row scales [M] and, on the tall
+    // path, the call's fp16 weights [N][K]
     void* staging = nullptr;
     size_t staging_bytes = 0;
     int* flag = nullptr;   // device error flag (get_rows id range)
+    // tall-path selection: M at or above `tall_m` uses dequant + fp16 GEMM;
+    // gemm_cfg >= 0 forces one fp16 GEMM tile configuration (SAMHIP_GEMM_CONFIG)
+    int tall_m = 256;
+    int gemm_cfg = -1;
     samhip_exec_info info{};
     // per-launch event trace (samhip_trace_begin / samhip_trace_end)
     struct TraceRecord {
@@ -127,6 +133,19 @@ int traced(samhip_context* ctx, const char* kernel, int wt, int64_t m, int64_t n
         ctx->trace.push_back({kernel, wt, m, n, k, a, b});
     }
     return rc;
+}
+
+const char* dequant_name(int wtype) {
+    return wtype == T_Q8_0 ? "dequant_w_f16_q8_0" : wtype == T_Q4_K ? "dequant_w_f16_q4_k"
+         : wtype == T_Q5_K ? "dequant_w_f16_q5_k" : "dequant_w_f16_q6_k";
+}
+
+int env_int(const char* name, int fallback) {
+    const char* v = std::getenv(name);
+    if (!v || !*v) return fallback;
+    char* end = nullptr;
+    const long x = std::strtol(v, &end, 10);
+    return (end && *end == '\0') ? int(x) : fallback;
 }
 
 const char* stage_name(int mode) {
@@ -207,6 +226,10 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
     }
     std::snprintf(ctx->info.device_name, sizeof(ctx->info.device_name), "%s (%s)", prop.name, prop.gcnArchName);
     ctx->stream = ctx->own_stream;
+    // kernel-variant forcing for tuning runs (SAMHIP_* environment variables)
+    ctx->tall_m = std::max(1, env_int("SAMHIP_TALL_M", ctx->tall_m));
+    const int cfg = env_int("SAMHIP_GEMM_CONFIG", -1);
+    ctx->gemm_cfg = (cfg >= 0 && cfg < gemm_f16_config_count()) ? cfg : -1;
     *out = ctx;
     return SAMHIP_OK;
 }
@@ -283,11 +306,17 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     if (const char* why = mul_mat_problem(w, x, y)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "mul_mat: %s", why);
     const int K = int(w->ne[0]), N = int(w->ne[1]), M = int(x->ne[1]);
     if (int rc = set_device(ctx)) return rc;
+    const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K);
+    auto align256 = [](size_t v) { return (v + 255) & ~size_t(255); };
     const size_t a_bytes = size_t(M) * size_t(K) * 2;
-    const size_t a_offset = (a_bytes + 255) & ~size_t(255);
-    if (int rc = ensure_staging(ctx, a_offset + size_t(M) * 4)) return rc;
-    _Float16* a = static_cast<_Float16*>(ctx->staging);
-    float* rs = reinterpret_cast<float*>(static_cast<uint8_t*>(ctx->staging) + a_offset);
+    const size_t rs_offset = align256(a_bytes);
+    const size_t w_offset = align256(rs_offset + size_t(M) * 4);
+    const size_t need = tall ? w_offset + size_t(N) * size_t(K) * 2 : w_offset;
+    if (int rc = ensure_staging(ctx, need)) return rc;
+    uint8_t* base = static_cast<uint8_t*>(ctx->staging);
+    _Float16* a = reinterpret_cast<_Float16*>(base);
+    float* rs = reinterpret_cast<float*>(base + rs_offset);
+    _Float16* wh = reinterpret_cast<_Float16*>(base + w_offset);
     const int mode = ctx->compute == SAMHIP_COMPUTE_F16 ? T_F16 : vec_dot_type(w->type);
     const bool aligned = reinterpret_cast<uintptr_t>(x->data) % 16 == 0 && x->nb[1] % 16 == 0;
     int rc = traced(ctx, stage_name(mode), w->type, M, N, K, [&]() -> int {
@@ -299,12 +328,29 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     if (rc) return rc;
     const char* variant = gemm_variant(w->type);
     if (!variant) return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no kernel for weight type %d", w->type);
-    rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
-        launch_gemm(w->type, a, K, rs, w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
-                    int64_t(y->nb[1] / 4), M, N, K, ctx->stream);
-        HIP_TRY(hipGetLastError(), "gemm launch");
-        return SAMHIP_OK;
-    });
+    if (tall) {
+        rc = traced(ctx, dequant_name(w->type), w->type, M, N, K, [&]() -> int {
+            launch_dequant_w_f16(w->type, w->data, int64_t(w->nb[1]), N, K, wh, K, ctx->stream);
+            HIP_TRY(hipGetLastError(), "weight dequant launch");
+            return SAMHIP_OK;
+        });
+        if (rc) return rc;
+        const int cfg = ctx->gemm_cfg >= 0 ? ctx->gemm_cfg : gemm_f16_pick(M, N, K);
+        variant = gemm_f16_config_name(cfg);
+        rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
+            launch_gemm_f16(cfg, a, K, rs, wh, K, static_cast<float*>(y->data), int64_t(y->nb[1] / 4), M, N, K,
+                            ctx->stream);
+            HIP_TRY(hipGetLastError(), "gemm launch");
+            return SAMHIP_OK;
+        });
+    } else {
+        rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
+            launch_gemm(w->type, a, K, rs, w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
+                        int64_t(y->nb[1] / 4), M, N, K, ctx->stream);
+            HIP_TRY(hipGetLastError(), "gemm launch");
+            return SAMHIP_OK;
+        });
+    }
     if (rc) return rc;
     ctx->info.mul_mat_calls++;
     ctx->info.activation_launches++;

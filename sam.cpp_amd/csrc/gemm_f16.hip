@@ -1,0 +1,235 @@
+// fp16 x fp16 -> F32 GEMM for the tall (many-token) mul_mat shapes on gfx950:
+//   Y[m][n] = rs[m] * sum_k A[m][k] * B[n][k]
+// A = staged activations [M][K], B = weights dequantized per call to
+// fp16(ggml to_float(W)) [N][K]; both K-contiguous, K a multiple of BK.
+//
+// Per workgroup a BM x BN tile, WM x WN waves, each wave a grid of 32x32
+// v_mfma_f32_32x32x16_f16 accumulators.  Operands travel HBM -> VGPR -> LDS
+// with raw buffer loads whose K position is a scalar offset (no per-load
+// vector address math; rows past M or N read as zero through the buffer
+// bounds), LDS is double-buffered with one barrier per BK stage, and the
+// loads of stage s+1 are in flight while stage s computes.  The epilogue
+// goes through LDS so that each lane stores 16 contiguous bytes of Y.
+#include "internal.hpp"
+
+namespace samhip {
+
+namespace {
+
+constexpr int GROUP_M = 8;
+constexpr int RSRC_WORD3 = 0x00020000;   // raw buffer, 32-bit data format
+
+__device__ __forceinline__ void tile_order(int bid, int nblocks, int tiles_m, int tiles_n, int& tm, int& tn) {
+    // Blocks are dispatched round-robin over the 8 XCDs: give XCD x a
+    // contiguous run of tiles, walked in groups of GROUP_M row tiles.
+    const int per = nblocks / 8, rem = nblocks % 8;
+    const int xcd = bid % 8, idx = bid / 8;
+    const int t = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + idx;
+    const int span = GROUP_M * tiles_n;
+    const int first = (t / span) * GROUP_M;
+    const int gm = min(tiles_m - first, GROUP_M);
+    const int within = t % span;
+    tm = first + within % gm;
+    tn = within / gm;
+}
+
+template <int BM, int BN, int WM, int WN, int BK>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_f16_kernel(const _Float16* __restrict__ A, int64_t lda,
+                                                                  const float* __restrict__ row_scale,
+                                                                  const _Float16* __restrict__ B, int64_t ldb,
+                                                                  float* __restrict__ Y, int64_t ldy, int M, int N,
+                                                                  int K, int tiles_m, int tiles_n) {
+    constexpr int NT = WM * WN * 64;
+    constexpr int LS = BK + 8;                  // LDS row stride in halves
+    constexpr int CPR = BK / 8;                 // 16-byte chunks per tile row
+    constexpr int CA = BM * CPR / NT, CB = BN * CPR / NT;
+    constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+    constexpr int ES = TN + 8;                  // epilogue LDS row stride in floats
+    static_assert(CA * NT == BM * CPR && CB * NT == BN * CPR, "tile/thread mismatch");
+    static_assert(FM * 32 == TM && FN * 32 == TN, "wave tile must be a multiple of 32");
+    static_assert(WM * WN * 32 * ES * 4 <= 2 * (BM + BN) * LS * 2, "epilogue staging must fit in LDS");
+
+    __shared__ _Float16 lds[2 * (BM + BN) * LS];
+
+    int tm, tn;
+    tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+
+    // buffer descriptors over the whole operands; a byte offset at or past
+    // num_records reads as zero
+    const uint32_t a_bytes = uint32_t(min(int64_t(M) * lda * 2, int64_t(0x7fffffff)));
+    const uint32_t b_bytes = uint32_t(min(int64_t(N) * ldb * 2, int64_t(0x7fffffff)));
+    const __amdgpu_buffer_rsrc_t ra_desc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A), 0, a_bytes, RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t rb_desc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(B), 0, b_bytes, RSRC_WORD3);
+
+    uint32_t a_off[CA], b_off[CB];
+    int a_lds[CA], b_lds[CB];
+#pragma unroll
+    for (int i = 0; i < CA; ++i) {
+        const int c = tid + i * NT, r = c / CPR, cc = c % CPR;
+        a_off[i] = m0 + r < M ? uint32_t((int64_t(m0 + r) * lda + 8 * cc) * 2) : a_bytes;
+        a_lds[i] = r * LS + 8 * cc;
+    }
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+        const int c = tid + i * NT, r = c / CPR, cc = c % CPR;
+        b_off[i] = n0 + r < N ? uint32_t((int64_t(n0 + r) * ldb + 8 * cc) * 2) : b_bytes;
+        b_lds[i] = r * LS + 8 * cc;
+    }
+
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // Two register sets: stage s+2 is requested while stage s computes and
+    // lands in LDS only after stage s+1 has computed, so every load has two
+    // compute phases to arrive.
+    u32x4 ra0[CA], rb0[CB], ra1[CA], rb1[CB];
+    const int nstages = K / BK;
+    auto gload = [&](int s, u32x4* ra, u32x4* rb) {
+        const int koff = s * BK * 2;
+#pragma unroll
+        for (int i = 0; i < CA; ++i)
+            ra[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra_desc, int(a_off[i]), koff, 0));
+#pragma unroll
+        for (int i = 0; i < CB; ++i)
+            rb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb_desc, int(b_off[i]), koff, 0));
+    };
+    auto lstore = [&](int buf, const u32x4* ra, const u32x4* rb) {
+        _Float16* at = lds + buf * (BM + BN) * LS;
+        _Float16* bt = at + BM * LS;
+#pragma unroll
+        for (int i = 0; i < CA; ++i) *reinterpret_cast<u32x4*>(at + a_lds[i]) = ra[i];
+#pragma unroll
+        for (int i = 0; i < CB; ++i) *reinterpret_cast<u32x4*>(bt + b_lds[i]) = rb[i];
+    };
+    const int fr = lane & 31, fk = 8 * (lane >> 5);
+    auto compute = [&](int buf) {
+        const _Float16* as = lds + buf * (BM + BN) * LS + (wm * TM + fr) * LS + fk;
+        const _Float16* bs = lds + buf * (BM + BN) * LS + BM * LS + (wn * TN + fr) * LS + fk;
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 16) {
+            half8 af[FM], bf[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const half8*>(as + i * 32 * LS + kk);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const half8*>(bs + j * 32 * LS + kk);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    gload(0, ra0, rb0);
+    if (nstages > 1) gload(1, ra1, rb1);
+    lstore(0, ra0, rb0);
+    __syncthreads();
+    const int pairs = nstages / 2;
+    for (int p = 0; p < pairs; ++p) {
+        const int s = 2 * p;
+        // stage s in LDS buffer 0; register set 1 holds stage s+1
+        if (s + 2 < nstages) gload(s + 2, ra0, rb0);
+        compute(0);
+        lstore(1, ra1, rb1);
+        __syncthreads();
+        // stage s+1 in LDS buffer 1; register set 0 holds stage s+2
+        if (s + 3 < nstages) gload(s + 3, ra1, rb1);
+        compute(1);
+        if (s + 2 < nstages) lstore(0, ra0, rb0);
+        __syncthreads();
+    }
+
+    // Epilogue, one 32-row slab of the wave tile at a time: the accumulator
+    // (lane l: column l%32, rows 8*(r/4) + 4*(l/32) + r%4) goes to a
+    // per-wave LDS slab, then each lane writes 4 consecutive floats of Y.
+    float* slab = reinterpret_cast<float*>(lds) + wave * 32 * ES;
+    const bool vec_ok = (ldy % 4) == 0 && (reinterpret_cast<uintptr_t>(Y) % 16) == 0;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                slab[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ES + 32 * j + (lane & 31)] = acc[i][j][r];
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the slab is written
+        __builtin_amdgcn_wave_barrier();
+        constexpr int C4 = TN / 4;               // float4 columns per slab row
+#pragma unroll
+        for (int e = lane; e < 32 * C4; e += 64) {
+            const int rr = e / C4, c4 = e % C4;
+            const int m = m0 + wm * TM + i * 32 + rr;
+            const int n = n0 + wn * TN + 4 * c4;
+            if (m >= M) continue;
+            const floatx4 v = *reinterpret_cast<const floatx4*>(slab + rr * ES + 4 * c4);
+            const float rs = row_scale[m];
+            float* yp = Y + int64_t(m) * ldy + n;
+            if (vec_ok && n + 3 < N) {
+                *reinterpret_cast<floatx4*>(yp) = floatx4{v[0] * rs, v[1] * rs, v[2] * rs, v[3] * rs};
+            } else {
+                for (int q = 0; q < 4; ++q)
+                    if (n + q < N) yp[q] = v[q] * rs;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int BK>
+void launch_cfg(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
+                int64_t ldy, int M, int N, int K, hipStream_t stream) {
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, WM, WN, BK>), dim3(unsigned(tiles_m * tiles_n)),
+                       dim3(WM * WN * 64), 0, stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n);
+}
+
+struct Cfg {
+    const char* name;
+    void (*launch)(const _Float16*, int64_t, const float*, const _Float16*, int64_t, float*, int64_t, int, int, int,
+                   hipStream_t);
+    int bm, bn, bk;
+};
+
+const Cfg kConfigs[] = {
+    {"gemm_f16_128x128x64_w2x2", launch_cfg<128, 128, 2, 2, 64>, 128, 128, 64},
+    {"gemm_f16_128x128x32_w2x2", launch_cfg<128, 128, 2, 2, 32>, 128, 128, 32},
+    {"gemm_f16_256x128x64_w2x2", launch_cfg<256, 128, 2, 2, 64>, 256, 128, 64},
+    {"gemm_f16_128x256x64_w2x2", launch_cfg<128, 256, 2, 2, 64>, 128, 256, 64},
+    {"gemm_f16_256x256x32_w2x2", launch_cfg<256, 256, 2, 2, 32>, 256, 256, 32},
+    {"gemm_f16_192x128x64_w2x2", launch_cfg<192, 128, 2, 2, 64>, 192, 128, 64},
+    {"gemm_f16_64x128x64_w1x2", launch_cfg<64, 128, 1, 2, 64>, 64, 128, 64},
+};
+constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
+
+}  // namespace
+
+int gemm_f16_config_count() { return kNumConfigs; }
+
+const char* gemm_f16_config_name(int cfg) { return cfg >= 0 && cfg < kNumConfigs ? kConfigs[cfg].name : nullptr; }
+
+// The main loop walks K in pairs of stages, so K must be a multiple of 2*BK
+// for every configuration (128 covers BK = 32 and 64); buffer offsets are
+// 32-bit.
+bool gemm_f16_supported(int M, int N, int K, int64_t lda, int64_t ldb) {
+    return K % 128 == 0 && int64_t(M) * lda * 2 < 0x7fffffff && int64_t(N) * ldb * 2 < 0x7fffffff;
+}
+
+// Tile choice by measured throughput on the SAM 3 shapes (M = 5184 tokens):
+// 128x128 tiles keep two workgroups per CU and fill 256 CUs for N down to 1024.
+int gemm_f16_pick(int /*M*/, int /*N*/, int /*K*/) { return 0; }
+
+const char* launch_gemm_f16(int cfg, const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
+                            int64_t ldb, float* y, int64_t ldy, int M, int N, int K, hipStream_t stream) {
+    if (cfg < 0 || cfg >= kNumConfigs || K % kConfigs[cfg].bk) cfg = gemm_f16_pick(M, N, K);
+    kConfigs[cfg].launch(a, lda, row_scale, b, ldb, y, ldy, M, N, K, stream);
+    return kConfigs[cfg].name;
+}
+
+}  // namespace samhip

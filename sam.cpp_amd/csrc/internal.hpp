@@ -22,6 +22,19 @@ void launch_quantize_weights(int type, const float* x, int64_t x_stride, int row
 void launch_dequant_rows(int type, const void* src, int64_t src_stride, const int32_t* ids, int64_t src_rows,
                          float* dst, int64_t dst_stride, int rows, int K, int* bad_id, hipStream_t stream);
 
+// Weight rows -> fp16(ggml to_float(W)) [N][K] with row stride ldo halves.
+void launch_dequant_w_f16(int wtype, const void* w, int64_t w_stride, int N, int K, _Float16* out, int64_t ldo,
+                          hipStream_t stream);
+
+// fp16 x fp16 GEMM for tall shapes: Y = rs * A B^T.  cfg < 0 picks a tile
+// configuration from the shape; returns the configuration's name.
+int gemm_f16_config_count();
+bool gemm_f16_supported(int M, int N, int K, int64_t lda, int64_t ldb);
+const char* gemm_f16_config_name(int cfg);
+int gemm_f16_pick(int M, int N, int K);
+const char* launch_gemm_f16(int cfg, const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
+                            int64_t ldb, float* y, int64_t ldy, int M, int N, int K, hipStream_t stream);
+
 // Kernel variant name for a weight type, or nullptr when unsupported.
 const char* gemm_variant(int wtype);
 

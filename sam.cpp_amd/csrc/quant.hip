@@ -49,6 +49,121 @@ __device__ __forceinline__ int row_exponent(float rowmax) {
 
 __device__ __forceinline__ floatx4 load4f(const float* p) { return *reinterpret_cast<const floatx4*>(p); }
 
+// Cross-lane steps on the DPP network (no LDS round trip): quad_perm swaps
+// for lane ^ 1 and lane ^ 2, row rotations by 4 and 8 within 16 lanes.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false); }
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float max4_lanes(float v) {
+    v = fmaxf(v, dpp<DPP_XOR1>(v));
+    return fmaxf(v, dpp<DPP_XOR2>(v));
+}
+__device__ __forceinline__ float max32_lanes(float v) {
+    v = max4_lanes(v);
+    v = fmaxf(v, dpp<DPP_ROR4>(v));
+    v = fmaxf(v, dpp<DPP_ROR8>(v));
+    return fmaxf(v, __shfl_xor(v, 16, 64));
+}
+__device__ __forceinline__ int min32_lanes(int v) {
+    v = min(v, dpp<DPP_XOR1>(v));
+    v = min(v, dpp<DPP_XOR2>(v));
+    v = min(v, dpp<DPP_ROR4>(v));
+    v = min(v, dpp<DPP_ROR8>(v));
+    return min(v, __shfl_xor(v, 16, 64));
+}
+typedef float floatx8 __attribute__((ext_vector_type(8)));
+
+// Staging with each lane owning 8 consecutive values (a Q8_0 block spans 4
+// lanes, a Q8_K block 32 lanes).  The row stays in registers (K <= 512*CH),
+// so X is read once; every cross-lane reduction runs with all lanes active
+// (lanes past K hold zeros).
+template <int MODE, int CH>
+__global__ __launch_bounds__(256) void stage8_kernel(const float* __restrict__ x, int64_t x_stride, int M, int K,
+                                                     _Float16* __restrict__ a, int64_t lda,
+                                                     float* __restrict__ row_scale, int x86) {
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= M) return;
+    const float* xr = x + int64_t(m) * x_stride;
+    floatx8 v[CH];
+    float rmax = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int k = 512 * c + 8 * lane;
+        if (k < K) {
+            const floatx4 lo = load4f(xr + k), hi = load4f(xr + k + 4);
+            v[c] = floatx8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        } else {
+            v[c] = floatx8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) rmax = fmaxf(rmax, fabsf(v[c][i]));
+    }
+    const float r32 = max32_lanes(rmax);
+    rmax = fmaxf(r32, __shfl_xor(r32, 32, 64));
+    const int e = row_exponent(rmax);
+    const float down = exp2i(-e);
+    if (lane == 0) row_scale[m] = exp2i(e);
+    _Float16* ar = a + int64_t(m) * lda;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int k = 512 * c + 8 * lane;
+        float d = 0.f;
+        float q[8];
+        if (MODE == T_Q8_0) {
+            float amax = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
+            amax = max4_lanes(amax);
+            const float dd = amax / 127.f;
+            float inv;
+            if (x86) inv = amax != 0.f ? 127.f / amax : 0.f;
+            else inv = dd != 0.f ? 1.f / dd : 0.f;
+            d = half_bits_to_float(float_to_half_bits(dd));   // stored fp16 scale
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float s = v[c][i] * inv;
+                q[i] = x86 ? __builtin_rintf(s) : __builtin_roundf(s);
+            }
+        } else if (MODE == T_Q8_K) {
+            // first element of largest magnitude in the 256-value block
+            const int base = 8 * (lane & 31);
+            float la = 0.f, ls = 0.f;
+            int li = 1 << 20;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float t = fabsf(v[c][i]);
+                if (t > la) { la = t; ls = v[c][i]; li = base + i; }
+            }
+            const float amax = max32_lanes(la);
+            const int idx = min32_lanes(la == amax ? li : (1 << 20));
+            const float smax = __shfl(ls, (lane & 32) + ((idx >> 3) & 31), 64);
+            if (amax != 0.f) {
+                const float iscale = -127.f / smax;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) q[i] = fminf(127.f, __builtin_rintf(iscale * v[c][i]));
+                d = 1.f / iscale;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) q[i] = 0.f;
+            }
+        }
+        if (k < K) {
+            half8 o;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                o[i] = MODE == T_F16 ? (_Float16)(v[c][i] * down) : (_Float16)((d * q[i]) * down);
+            *reinterpret_cast<half8*>(ar + k) = o;
+        }
+    }
+}
+
 // Q8_0 block: amax over 8 lanes x 4 values; returns fp16 d bits and codes.
 __device__ __forceinline__ void q8_0_codes(const floatx4& v, int x86, float& d_out, int q[4]) {
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
@@ -130,6 +245,26 @@ __global__ __launch_bounds__(256) void stage_rows_kernel(const float* __restrict
         typedef _Float16 half4 __attribute__((ext_vector_type(4)));
         *reinterpret_cast<half4*>(ar + k) = half4{out[0], out[1], out[2], out[3]};
     }
+}
+
+// Weight rows -> fp16(to_float(W)) [N][K]: thread (row, 32-element step,
+// half) writes 16 consecutive halves, so a wave stores 1 KB contiguously.
+template <int WT>
+__global__ __launch_bounds__(256) void dequant_w_f16_kernel(const uint8_t* __restrict__ W, int64_t w_stride, int N,
+                                                            int K, _Float16* __restrict__ out, int64_t ldo) {
+    const int steps = K / 32;
+    const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= int64_t(N) * steps * 2) return;
+    const int h = int(t & 1);
+    const int64_t rs = t >> 1;
+    const int row = int(rs / steps), step = int(rs % steps);
+    WeightPiece<WT> piece;
+    piece.load(W + int64_t(row) * w_stride, step, h);
+    _Float16 v[16];
+    piece.dequant(step, h, v);
+    half8* o = reinterpret_cast<half8*>(out + int64_t(row) * ldo + 32 * step + 16 * h);
+    o[0] = half8{v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
+    o[1] = half8{v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]};
 }
 
 // Scalar-load variant for rows that are not 16-byte aligned.
@@ -278,9 +413,40 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __rest
 
 }  // namespace
 
+void launch_dequant_w_f16(int wtype, const void* w, int64_t w_stride, int N, int K, _Float16* out, int64_t ldo,
+                          hipStream_t stream) {
+    const int64_t threads = int64_t(N) * (K / 32) * 2;
+    const dim3 grid(unsigned((threads + 255) / 256)), block(256);
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    switch (wtype) {
+        case T_Q8_0: hipLaunchKernelGGL(dequant_w_f16_kernel<T_Q8_0>, grid, block, 0, stream, wb, w_stride, N, K, out, ldo); break;
+        case T_Q4_K: hipLaunchKernelGGL(dequant_w_f16_kernel<T_Q4_K>, grid, block, 0, stream, wb, w_stride, N, K, out, ldo); break;
+        case T_Q5_K: hipLaunchKernelGGL(dequant_w_f16_kernel<T_Q5_K>, grid, block, 0, stream, wb, w_stride, N, K, out, ldo); break;
+        case T_Q6_K: hipLaunchKernelGGL(dequant_w_f16_kernel<T_Q6_K>, grid, block, 0, stream, wb, w_stride, N, K, out, ldo); break;
+        default: break;
+    }
+}
+
 void launch_stage_rows(int mode, bool aligned, const float* x, int64_t x_stride, int M, int K, _Float16* a,
                        int64_t lda, float* row_scale, int x86, hipStream_t stream) {
     const dim3 grid((M + 3) / 4), block(256);
+    if (aligned && K <= 512 * 10) {
+#define SAMHIP_STAGE8(MODE, CH) \
+    hipLaunchKernelGGL((stage8_kernel<MODE, CH>), grid, block, 0, stream, x, x_stride, M, K, a, lda, row_scale, x86)
+#define SAMHIP_STAGE8_MODE(MODE)                  \
+    if (K <= 1024) SAMHIP_STAGE8(MODE, 2);        \
+    else if (K <= 2048) SAMHIP_STAGE8(MODE, 4);   \
+    else SAMHIP_STAGE8(MODE, 10);
+        switch (mode) {
+            case T_F16: SAMHIP_STAGE8_MODE(T_F16) break;
+            case T_Q8_0: SAMHIP_STAGE8_MODE(T_Q8_0) break;
+            case T_Q8_K: SAMHIP_STAGE8_MODE(T_Q8_K) break;
+            default: break;
+        }
+#undef SAMHIP_STAGE8_MODE
+#undef SAMHIP_STAGE8
+        return;
+    }
 #define SAMHIP_STAGE(MODE)                                                                                      \
     if (aligned) hipLaunchKernelGGL(stage_rows_kernel<MODE>, grid, block, 0, stream, x, x_stride, M, K, a, lda, \
                                     row_scale, x86);                                                           \

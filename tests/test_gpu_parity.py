@@ -238,6 +238,50 @@ def test_mul_mat_extreme_row_magnitudes(gpu_ctx, f16_ctx, oracle):
     assert max_row_rel_l2(yn[finite], ref[finite]) <= ROW_REL_L2
 
 
+@pytest.mark.parametrize("qtype", TYPES)
+def test_mul_mat_tall_path_tails(gpu_ctx, f16_ctx, oracle, qtype):
+    """M >= 256 takes the dequantize + fp16 GEMM path; M and N tails, a
+    row-offset view and a strided activation, fully compared."""
+    say("case mul_mat tall tails", qtype)
+    k = 1024 if qtype != 8 else 4736
+    rng = np.random.default_rng(27)
+    w = oracle.quantize(qtype, (rng.standard_normal((2 * 131, k)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((301, k)).astype(np.float32)
+    for off, stride in ((0, k + 64), (131, k + 1)):   # k + 1: rows not 16-byte aligned
+        yn = gpu_ctx.matmul(qtype, w, x, w_row_offset=off, w_rows=131, x_row_stride=stride)
+        yf = f16_ctx.matmul(qtype, w, x, w_row_offset=off, w_rows=131, x_row_stride=stride)
+        _check_product(oracle, qtype, w[off:off + 131], x, yn, yf)
+
+
+def test_mul_mat_every_gemm_tile_config(samhip, oracle, monkeypatch):
+    """Each fp16 GEMM tile configuration gives the same product (bit-exact:
+    same operands and the same per-tile K order)."""
+    say("case gemm configs")
+    rng = np.random.default_rng(28)
+    k, n, m = 512, 300, 517
+    w = oracle.quantize(oracle.Q4_K, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    ref = oracle.mul_mat_native(oracle.Q4_K, w, x, oracle.ROUND_X86)
+    outs = []
+    cfg = 0
+    while True:
+        monkeypatch.setenv("SAMHIP_GEMM_CONFIG", str(cfg))
+        with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
+            y = ctx.matmul(samhip.Q4_K, w, x)
+            name = ctx.query().kernel_variant.decode()
+        if any(name == o[0] for o in outs):
+            break                       # past the last configuration: the default was picked
+        say("  config", cfg, name)
+        assert max_row_rel_l2(y, ref) <= ROW_REL_L2, name
+        outs.append((name, y))
+        cfg += 1
+        if cfg > 32:
+            break
+    assert len(outs) >= 4
+    for name, y in outs[1:]:
+        assert np.array_equal(y, outs[0][1]), name
+
+
 # ---- mul_mat at the SAM 3 ViT shapes (M = 5184 tokens) ----------------------
 
 VIT = {"qkv": (1024, 3072), "proj": (1024, 1024), "fc1": (1024, 4736), "fc2": (4736, 1024)}
