@@ -29,6 +29,21 @@ PEAK_INT8_TOPS = 5000.0       # MI355X dense int8 MFMA
 PEAK_HBM_GBPS = 8000.0
 
 
+# rocprofv3 commands whose CSV output summarize_profiles() reads
+PROFILE_COMMANDS = {
+    "trace": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/trace -o bench -- "
+             "python3 bench.py --steps 20 --warmup 5 --no-cpu-baseline",
+    "fetch": "rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/fetch -o bench -- "
+             "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline",
+    "write": "rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/write -o bench -- "
+             "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline",
+    "copy_fetch": "rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/copy_FETCH_SIZE -o copy -- "
+                  "python3 bench.py --copy-calibration",
+    "copy_write": "rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/copy_WRITE_SIZE -o copy -- "
+                  "python3 bench.py --copy-calibration",
+}
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -53,6 +68,137 @@ def products(sh):
 
 def bytes_per_weight(sh, qt):
     return sh.BLOCK_BYTES[qt] / sh.BLOCK_ELEMS[qt]
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_vit_sweep_m5184.json")
+COPY_ELEMS = 1 << 26          # F32 elements of the calibration copy (256 MiB read + 256 MiB written)
+
+
+def kernel_symbol(variant):
+    """Template symbol of a GEMM variant name, as rocprofv3 reports it demangled:
+    gemm_f16_{BM}x{BN}x{BK}_w{WM}x{WN} -> gemm_f16_kernel<BM, BN, WM, WN, BK>,
+    gemm_f16dma_{BM}x{BN}x{BK}_s{S}    -> gemm_f16_dma_kernel<BM, BN, BK, S>.
+    Returns (symbol, threads per workgroup, BM, BN) or None."""
+    import re
+    m = re.fullmatch(r"gemm_f16_(\d+)x(\d+)x(\d+)_w(\d+)x(\d+)", variant)
+    if m:
+        bm, bn, bk, wm, wn = map(int, m.groups())
+        return f"gemm_f16_kernel<{bm}, {bn}, {wm}, {wn}, {bk}>", 64 * wm * wn, bm, bn
+    m = re.fullmatch(r"gemm_f16dma_(\d+)x(\d+)x(\d+)_s(\d+)", variant)
+    if m:
+        bm, bn, bk, st = map(int, m.groups())
+        return f"gemm_f16_dma_kernel<{bm}, {bn}, {bk}, {st}>", 256, bm, bn
+    return None
+
+
+def hbm_traffic(variant, shape):
+    """HBM bytes per launch of `variant` at `shape` = (M, N, K) from the
+    committed FETCH_SIZE / WRITE_SIZE summary (each counter scaled by what it
+    reads for a plain copy of known size), or None when not profiled."""
+    sym = kernel_symbol(variant)
+    if sym is None or not os.path.exists(TRAFFIC_FILE):
+        return None
+    symbol, threads, bm, bn = sym
+    m, n, _ = shape
+    grid = -(-m // bm) * -(-n // bn) * threads
+    with open(TRAFFIC_FILE) as f:
+        table = json.load(f)
+    for e in table["kernels"]:
+        if e["symbol"] == symbol and e["grid"] == grid:
+            return int(e["fetch_bytes"] + e["write_bytes"])
+    return None
+
+
+def copy_calibration():
+    """A plain streaming copy of known size (COPY_ELEMS F32 read, the same
+    written) for scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+    x = torch.ones(COPY_ELEMS, device="cuda")
+    torch.cuda.synchronize()
+    y = x + 0.0
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": 4 * COPY_ELEMS, "copy_bytes_written": 4 * COPY_ELEMS,
+                      "check": float(y[-1].item())}), flush=True)
+
+
+def summarize_profiles(d, commands):
+    """Writes the committed text summaries from a rocprofv3 output folder
+    `d` holding trace/, fetch/, write/, copy_FETCH_SIZE/ and copy_WRITE_SIZE/
+    (CSV output of the commands listed in `commands`)."""
+    import csv
+
+    def rows(path):
+        with open(path) as f:
+            return list(csv.DictReader(f))
+
+    def short(name):
+        """`kernel<args>` from a demangled or Itanium-mangled kernel symbol
+        (mangled names here carry only integer template arguments)."""
+        import re
+        m = re.match(r"_ZN6samhip12_GLOBAL__N_1(\d+)", name)
+        if m:
+            n = int(m.group(1))
+            base = name[m.end():m.end() + n]
+            rest = name[m.end() + n:]
+            args = re.match(r"I((?:Li-?\d+E)+)E", rest)
+            if args:
+                base += "<" + ", ".join(re.findall(r"Li(-?\d+)E", args.group(1))) + ">"
+            return base
+        name = name.replace("void ", "", 1).replace("samhip::(anonymous namespace)::", "")
+        return name.split("(")[0]
+
+    copy_kib = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        rs = [r for r in rows(os.path.join(d, f"copy_{c}", "copy_counter_collection.csv")) if "add" in r["Kernel_Name"]]
+        copy_kib[c] = float(rs[0]["Counter_Value"])
+    fetch_factor = 4 * COPY_ELEMS / 1024 / copy_kib["FETCH_SIZE"]
+    write_factor = 4 * COPY_ELEMS / 1024 / copy_kib["WRITE_SIZE"]
+
+    agg = {}
+    for c, sub in (("FETCH_SIZE", "fetch"), ("WRITE_SIZE", "write")):
+        rs = rows(os.path.join(d, sub, "bench_counter_collection.csv"))
+        for r in rs:
+            key = (short(r["Kernel_Name"]), int(r["Grid_Size"]))
+            agg.setdefault(key, {}).setdefault(c, []).append(float(r["Counter_Value"]))
+    kernels = []
+    for (sym, grid), v in sorted(agg.items()):
+        if "FETCH_SIZE" not in v or "WRITE_SIZE" not in v:
+            continue
+        fk = float(np.mean(v["FETCH_SIZE"]))
+        wk = float(np.mean(v["WRITE_SIZE"]))
+        kernels.append({"symbol": sym, "grid": grid, "dispatches": len(v["FETCH_SIZE"]),
+                        "fetch_kib": round(fk, 1), "write_kib": round(wk, 1),
+                        "fetch_bytes": int(fk * 1024 * fetch_factor), "write_bytes": int(wk * 1024 * write_factor)})
+    table = {"fetch_factor": fetch_factor, "write_factor": write_factor, "copy_kib": copy_kib,
+             "commands": commands, "kernels": kernels}
+    os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(table, f, indent=1)
+
+    stats = rows(os.path.join(d, "trace", "bench_kernel_stats.csv"))
+    lines = ["# Kernel time, SAM 3 ViT linear sweep at M=5184 (12 mul_mat per step)", "",
+             "Command (from the repository root, `cd /tmp && export TMPDIR=/tmp` first):", "",
+             "```", commands["trace"], "```", "",
+             "| kernel | calls | avg us | min us | max us | share % |", "|---|---|---|---|---|---|"]
+    for r in stats:
+        lines.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                     f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
+    with open(os.path.join(ROOT, "profiles", "kernel_stats_vit_sweep_m5184.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+    lines = ["# HBM traffic per dispatch, SAM 3 ViT linear sweep at M=5184", "",
+             "Commands (from the repository root, `cd /tmp && export TMPDIR=/tmp` first):", "", "```",
+             commands["fetch"], commands["write"], commands["copy_fetch"], commands["copy_write"], "```", "",
+             f"Calibration: a plain copy of {4 * COPY_ELEMS} bytes (read, and the same written) reads "
+             f"FETCH_SIZE {copy_kib['FETCH_SIZE']:.1f} KiB and WRITE_SIZE {copy_kib['WRITE_SIZE']:.1f} KiB, so "
+             f"HBM bytes = FETCH_SIZE x 1024 x {fetch_factor:.3f} + WRITE_SIZE x 1024 x {write_factor:.3f}.", "",
+             "| kernel | grid (threads) | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM MB read | HBM MB written |",
+             "|---|---|---|---|---|---|---|"]
+    for e in kernels:
+        lines.append(f"| `{e['symbol']}` | {e['grid']} | {e['dispatches']} | {e['fetch_kib']} | {e['write_kib']} | "
+                     f"{e['fetch_bytes'] / 1e6:.2f} | {e['write_bytes'] / 1e6:.2f} |")
+    with open(os.path.join(ROOT, "profiles", "hbm_traffic_vit_sweep_m5184.md"), "w") as f:
+        f.write("\n".join(lines) + "\n")
 
 
 def cpu_baseline(plan, seconds, rows):
@@ -91,7 +237,19 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-rows", type=int, default=96)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--trace", choices=["dominant", "all", "none"], default="dominant",
+                    help="launches bracketed by HIP events inside the timed region")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only the plain copy used to scale HBM traffic counters")
+    ap.add_argument("--summarize-profiles", metavar="DIR",
+                    help="write profiles/ summaries from rocprofv3 CSV output in DIR and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
+    if args.summarize_profiles:
+        summarize_profiles(args.summarize_profiles, PROFILE_COMMANDS)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}, "
@@ -128,14 +286,49 @@ def main():
     for _ in range(args.warmup):
         step()
     ctx.synchronize()
-    log(f"warmup done ({args.warmup} steps); timing {args.steps} steps")
+    log(f"warmup done ({args.warmup} steps)")
 
-    ctx.synchronize()
+    # untimed profiling pass: every launch bracketed by events, for the
+    # per-product breakdown and to name the dominant kernel
+    prof_steps = max(1, min(args.steps, 5))
     ctx.trace_begin()
+    for _ in range(prof_steps):
+        step()
+    prof = ctx.trace_end(capacity=4 * len(ops) * prof_steps + 16)
+    by_kernel = {}
+    for name, wt, m, n, k, ms in prof:
+        by_kernel.setdefault(name, []).append((wt, m, n, k, ms))
+    total = {name: sum(r[4] for r in rs) for name, rs in by_kernel.items()}
+    dominant = max(total, key=total.get)
+
+    def mean_ms(recs, qt, n, k, prefix):
+        sel = [r[5] for r in recs if r[1] == qt and r[3] == n and r[4] == k and r[0].startswith(prefix)]
+        return float(np.mean(sel)) if sel else 0.0
+
+    per_product = []
+    for label, qt, k, n, *_ in ops:
+        g = mean_ms(prof, qt, n, k, "gemm")
+        s = mean_ms(prof, qt, n, k, "stage")
+        d = mean_ms(prof, qt, n, k, "dequant")
+        per_product.append({"product": label, "M": M_TOKENS, "N": n, "K": k, "gemm_ms": round(g, 5),
+                            "stage_ms": round(s, 5), "dequant_ms": round(d, 5),
+                            "gemm_tflops": round(2.0 * M_TOKENS * n * k / g / 1e9, 2) if g else None,
+                            "linear_tops": round(2.0 * M_TOKENS * n * k / (g + s + d) / 1e9, 2) if g else None})
+    kernel_share = {name: round(v / sum(total.values()), 4) for name, v in sorted(total.items(), key=lambda t: -t[1])}
+
+    # timed region: events only around the dominant kernel (or none / all)
+    log(f"timing {args.steps} steps (trace: {args.trace}, dominant kernel {dominant})")
+    ctx.synchronize()
+    if args.trace != "none":
+        ctx.trace_begin(dominant if args.trace == "dominant" else None)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
-    records = ctx.trace_end(capacity=4 * len(ops) * args.steps + 16)   # waits for the stream
+    if args.trace != "none":
+        records = ctx.trace_end(capacity=4 * len(ops) * args.steps + 16)   # waits for the stream
+    else:
+        ctx.synchronize()
+        records = []
     elapsed = time.perf_counter() - t0
     log(f"timed {args.steps} steps in {elapsed * 1e3:.1f} ms")
 
@@ -143,36 +336,23 @@ def main():
     ms_step = elapsed * 1e3 / args.steps
     tops = flops_step * args.steps / elapsed / 1e12
 
-    # per-kernel statistics from the HIP events on the launch stream
-    by_kernel = {}
-    for name, wt, m, n, k, ms in records:
-        by_kernel.setdefault(name, []).append((m, n, k, ms))
-    per_product = []
-    for label, qt, k, n, *_ in ops:
-        gname = [r for r in records if r[1] == qt and r[3] == n and r[4] == k and r[0].startswith("gemm")]
-        sname = [r for r in records if r[1] == qt and r[3] == n and r[4] == k and r[0].startswith("stage")]
-        g = float(np.mean([r[5] for r in gname])) if gname else float("nan")
-        s = float(np.mean([r[5] for r in sname])) if sname else float("nan")
-        per_product.append({"product": label, "M": M_TOKENS, "N": n, "K": k, "gemm_ms": round(g, 5),
-                            "stage_ms": round(s, 5),
-                            "gemm_tflops": round(2.0 * M_TOKENS * n * k / g / 1e9, 2),
-                            "linear_tops": round(2.0 * M_TOKENS * n * k / (g + s) / 1e9, 2)})
-    total = {name: sum(r[3] for r in rs) for name, rs in by_kernel.items()}
-    dominant = max(total, key=total.get)
-    launches = by_kernel[dominant]
-    shapes = {(m, n, k) for m, n, k, _ in launches}
-    m_, n_, k_ = max(shapes, key=lambda s: sum(r[3] for r in launches if r[:3] == s))
-    same = [r[3] for r in launches if r[:3] == (m_, n_, k_)]
+    # roofline of the dominant kernel from the HIP events on its launch stream
+    # (timed region when traced there, else the profiling pass)
+    launches = [r for r in (records or prof) if r[0] == dominant]
+    shapes = {(r[2], r[3], r[4]) for r in launches}
+    m_, n_, k_ = max(shapes, key=lambda sh_: sum(r[5] for r in launches if (r[2], r[3], r[4]) == sh_))
+    same = [r[5] for r in launches if (r[2], r[3], r[4]) == (m_, n_, k_)]
     avg_ms = float(np.mean(same))
-    qt_dom = next(r[1] for r in records if r[0] == dominant)
+    qt_dom = launches[0][1]
     flops = 2.0 * m_ * n_ * k_
     achieved = flops / (avg_ms * 1e-3) / 1e12
-    alg_bytes = n_ * k_ * bytes_per_weight(sh, qt_dom) + m_ * k_ * 2 + m_ * n_ * 4
+    alg_bytes = n_ * k_ * 2 + m_ * k_ * 2 + m_ * n_ * 4
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": None,
-                "kernel": dominant, "shape": {"M": m_, "N": n_, "K": k_}, "launch_ms": round(avg_ms, 5),
-                "launches": len(same), "flops_per_launch": flops,
-                "algorithmic_bytes_per_launch": int(alg_bytes),
+                "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": hbm_traffic(dominant, (m_, n_, k_)),
+                "kernel": dominant, "weight_type": sh.TYPE_NAMES.get(qt_dom, str(qt_dom)),
+                "shape": {"M": m_, "N": n_, "K": k_}, "launch_ms": round(avg_ms, 5),
+                "launches": len(same), "events_in": "timed region" if records else "profiling pass",
+                "flops_per_launch": flops, "algorithmic_bytes_per_launch": int(alg_bytes),
                 "hbm_gbps_algorithmic": round(alg_bytes / (avg_ms * 1e-3) / 1e9, 1),
                 "pct_int8_peak": round(100 * achieved / PEAK_INT8_TOPS, 2)}
 
@@ -187,6 +367,7 @@ def main():
         "pct_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 2),
         "roofline": roofline,
         "products": per_product,
+        "kernel_time_share": kernel_share,
         "device": ctx.query().device_name.decode(),
     }
     ctx.close()

@@ -179,14 +179,16 @@ int samhip_query(samhip_context* ctx, samhip_exec_info* info);
  * 47-80): between trace_begin and trace_end every kernel launch of the context
  * is bracketed by HIP events on the context's stream.  trace_end waits for the
  * stream and copies up to `capacity` records; *count receives the number
- * recorded (which may exceed capacity). */
+ * recorded (which may exceed capacity).  A non-NULL `kernel_filter` limits
+ * the bracketing to kernels whose name contains that text, so that a timed
+ * run carries events around one kernel only. */
 typedef struct samhip_kernel_record {
     char kernel[64];
     int32_t weight_type;
     int64_t m, n, k;
     float ms;
 } samhip_kernel_record;
-int samhip_trace_begin(samhip_context* ctx);
+int samhip_trace_begin(samhip_context* ctx, const char* kernel_filter);
 int samhip_trace_end(samhip_context* ctx, samhip_kernel_record* records, size_t capacity, size_t* count);
 /* Copies the calling thread's last error message; returns its full length. */
 size_t samhip_last_error(char* buffer, size_t size);

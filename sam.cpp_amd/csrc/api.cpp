@@ -76,6 +76,7 @@ struct samhip_context {
         hipEvent_t start, stop;
     };
     bool tracing = false;
+    std::string trace_filter;
     std::vector<TraceRecord> trace;
     std::vector<hipEvent_t> event_pool;
 };
@@ -120,7 +121,8 @@ hipEvent_t pooled_event(samhip_context* ctx) {
 template <class Body>
 int traced(samhip_context* ctx, const char* kernel, int wt, int64_t m, int64_t n, int64_t k, Body body) {
     hipEvent_t a = nullptr, b = nullptr;
-    const bool record = ctx->tracing && ctx->trace.size() < kMaxTraceRecords;
+    const bool record = ctx->tracing && ctx->trace.size() < kMaxTraceRecords &&
+                        (ctx->trace_filter.empty() || std::strstr(kernel, ctx->trace_filter.c_str()) != nullptr);
     if (record) {
         a = pooled_event(ctx);
         b = pooled_event(ctx);
@@ -450,8 +452,9 @@ int samhip_validate_quantized_payload(int32_t type, int64_t ne0, int64_t rows, c
     return SAMHIP_OK;
 }
 
-int samhip_trace_begin(samhip_context* ctx) {
+int samhip_trace_begin(samhip_context* ctx, const char* kernel_filter) {
     if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    ctx->trace_filter = kernel_filter ? kernel_filter : "";
     for (auto& r : ctx->trace) {
         ctx->event_pool.push_back(r.start);
         ctx->event_pool.push_back(r.stop);

@@ -4,12 +4,15 @@
 // fp16(ggml to_float(W)) [N][K]; both K-contiguous, K a multiple of BK.
 //
 // Per workgroup a BM x BN tile, WM x WN waves, each wave a grid of 32x32
-// v_mfma_f32_32x32x16_f16 accumulators.  Operands travel HBM -> VGPR -> LDS
-// with raw buffer loads whose K position is a scalar offset (no per-load
-// vector address math; rows past M or N read as zero through the buffer
-// bounds), LDS is double-buffered with one barrier per BK stage, and the
-// loads of stage s+1 are in flight while stage s computes.  The epilogue
-// goes through LDS so that each lane stores 16 contiguous bytes of Y.
+// v_mfma_f32_32x32x16_f16 accumulators.  Two operand pipelines:
+//  * register-staged (gemm_f16_kernel): raw buffer loads whose K position is
+//    a scalar offset (rows past M or N read as zero through the buffer
+//    bounds) land in VGPRs two stages ahead and are written to a
+//    double-buffered, padded LDS tile;
+//  * direct-to-LDS (gemm_f16_dma_kernel): buffer_load_dwordx4 ... lds fills
+//    a ring of 3-4 XOR-swizzled LDS stages without a VGPR round trip.
+// Both keep one barrier per BK stage.  The epilogue goes through LDS so that
+// each lane stores 16 contiguous bytes of Y.
 #include "internal.hpp"
 
 namespace samhip {
@@ -182,6 +185,186 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f16_kernel(const _Float16* 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Direct-to-LDS variant: operands go HBM -> LDS with buffer_load_dwordx4 ...
+// lds (no VGPR round trip, no ds_write), through a ring of STAGES buffers, so
+// the loads of stage s+STAGES-1 are requested while stage s computes.  One
+// wave-wide load fills 1 KB of LDS contiguously (lane l -> bytes 16l..16l+15);
+// each lane picks the global chunk that belongs at its slot, which lays every
+// tile row out with its 16-byte K chunks XOR-swizzled by the row index:
+//   chunk kc of row r lives at slot kc ^ swz(r)
+// so that the 32 rows an MFMA fragment read touches fall in distinct banks.
+// ---------------------------------------------------------------------------
+
+template <int CPR>
+__device__ __forceinline__ int swz(int r) {
+    return CPR == 8 ? ((r >> 1) & 7) : ((r >> 2) & 3);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    // s_waitcnt vmcnt(N), expcnt/lgkmcnt left at their maximum (gfx9 encoding)
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+template <int BM, int BN, int BK, int STAGES>
+__global__ __launch_bounds__(256) void gemm_f16_dma_kernel(const _Float16* __restrict__ A, int64_t lda,
+                                                           const float* __restrict__ row_scale,
+                                                           const _Float16* __restrict__ B, int64_t ldb,
+                                                           float* __restrict__ Y, int64_t ldy, int M, int N, int K,
+                                                           int tiles_m, int tiles_n) {
+#if defined(__HIP_DEVICE_COMPILE__)   // LDS-DMA builtins exist only in the device pass
+    constexpr int WM = 2, WN = 2;
+    constexpr int CPR = BK / 8, RB = BK * 2;            // chunks / bytes per tile row
+    constexpr int RPB = 64 / CPR;                       // tile rows per 1 KB wave load
+    constexpr int A_BLOCKS = BM / RPB, B_BLOCKS = BN / RPB;
+    constexpr int A_PER_WAVE = A_BLOCKS / 4, B_PER_WAVE = B_BLOCKS / 4;
+    constexpr int LOADS = A_PER_WAVE + B_PER_WAVE;      // wave loads per stage
+    constexpr int STAGE_BYTES = (BM + BN) * RB;
+    constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+    constexpr int ES = TN + 8;
+    static_assert(A_PER_WAVE * 4 == A_BLOCKS && B_PER_WAVE * 4 == B_BLOCKS, "tile rows must split over 4 waves");
+    static_assert(STAGES >= 2 && STAGES <= 4, "ring depth");
+    static_assert(4 * 32 * ES * 4 <= STAGES * STAGE_BYTES, "epilogue staging must fit in LDS");
+
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * STAGE_BYTES];
+
+    int tm, tn;
+    tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: LDS targets stay scalar
+    const int wm = wave / WN, wn = wave % WN;
+
+    const uint32_t a_bytes = uint32_t(min(int64_t(M) * lda * 2, int64_t(0x7fffffff)));
+    const uint32_t b_bytes = uint32_t(min(int64_t(N) * ldb * 2, int64_t(0x7fffffff)));
+    const __amdgpu_buffer_rsrc_t ra_desc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A), 0, a_bytes, RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t rb_desc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(B), 0, b_bytes, RSRC_WORD3);
+
+    // global byte offset (at k = 0) of the chunk this lane fetches for each of
+    // its wave loads; past-the-end rows read as zero
+    uint32_t a_off[A_PER_WAVE], b_off[B_PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < A_PER_WAVE; ++i) {
+        const int blk = wave * A_PER_WAVE + i, r = blk * RPB + lane / CPR, slot = lane % CPR;
+        const int kc = slot ^ swz<CPR>(r);
+        a_off[i] = m0 + r < M ? uint32_t((int64_t(m0 + r) * lda + 8 * kc) * 2) : a_bytes;
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER_WAVE; ++i) {
+        const int blk = wave * B_PER_WAVE + i, r = blk * RPB + lane / CPR, slot = lane % CPR;
+        const int kc = slot ^ swz<CPR>(r);
+        b_off[i] = n0 + r < N ? uint32_t((int64_t(n0 + r) * ldb + 8 * kc) * 2) : b_bytes;
+    }
+    auto issue = [&](int s) {
+        uint8_t* st = lds + (s % STAGES) * STAGE_BYTES;
+        const int koff = s * RB;
+#pragma unroll
+        for (int i = 0; i < A_PER_WAVE; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra_desc, (__attribute__((address_space(3))) void*)(st + (wave * A_PER_WAVE + i) * 1024), 16,
+                a_off[i], koff, 0, 0);
+#pragma unroll
+        for (int i = 0; i < B_PER_WAVE; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb_desc, (__attribute__((address_space(3))) void*)(st + BM * RB + (wave * B_PER_WAVE + i) * 1024),
+                16, b_off[i], koff, 0, 0);
+    };
+
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int nst = K / BK;
+    // per-lane fragment coordinates: row wm*TM + i*32 + (lane&31), chunk 2*kk + (lane>>5)
+    const int frow = lane & 31, fhalf = lane >> 5;
+    auto compute = [&](int s) {
+        const uint8_t* st = lds + (s % STAGES) * STAGE_BYTES;
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; ++kk) {
+            half8 af[FM], bf[FN];
+            const int kc = 2 * kk + fhalf;
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const int r = wm * TM + i * 32 + frow;
+                af[i] = *reinterpret_cast<const half8*>(st + r * RB + 16 * (kc ^ swz<CPR>(r)));
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int r = wn * TN + j * 32 + frow;
+                bf[j] = *reinterpret_cast<const half8*>(st + BM * RB + r * RB + 16 * (kc ^ swz<CPR>(r)));
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < nst) issue(s);
+    for (int s = 0; s < nst; ++s) {
+        // this wave's loads of stage s are the oldest in flight: allow the
+        // later stages' loads (up to STAGES-2 of them) to remain outstanding
+        const int later = min(STAGES - 2, nst - 1 - s);
+        if (later >= 2) wait_vmcnt<2 * LOADS>();
+        else if (later == 1) wait_vmcnt<LOADS>();
+        else wait_vmcnt<0>();
+        // every wave's stage-s data landed; stage s-1 reads are done.  A bare
+        // s_barrier (no fence) keeps the later stages' loads in flight.
+        asm volatile("s_barrier" ::: "memory");
+        if (s + STAGES - 1 < nst) issue(s + STAGES - 1);
+        compute(s);
+    }
+    __syncthreads();
+
+    float* slab = reinterpret_cast<float*>(lds) + wave * 32 * ES;
+    const bool vec_ok = (ldy % 4) == 0 && (reinterpret_cast<uintptr_t>(Y) % 16) == 0;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                slab[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ES + 32 * j + (lane & 31)] = acc[i][j][r];
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+        constexpr int C4 = TN / 4;
+#pragma unroll
+        for (int e = lane; e < 32 * C4; e += 64) {
+            const int rr = e / C4, c4 = e % C4;
+            const int m = m0 + wm * TM + i * 32 + rr;
+            const int n = n0 + wn * TN + 4 * c4;
+            if (m >= M) continue;
+            const floatx4 v = *reinterpret_cast<const floatx4*>(slab + rr * ES + 4 * c4);
+            const float rs = row_scale[m];
+            float* yp = Y + int64_t(m) * ldy + n;
+            if (vec_ok && n + 3 < N) {
+                *reinterpret_cast<floatx4*>(yp) = floatx4{v[0] * rs, v[1] * rs, v[2] * rs, v[3] * rs};
+            } else {
+                for (int q = 0; q < 4; ++q)
+                    if (n + q < N) yp[q] = v[q] * rs;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+#endif
+}
+
+template <int BM, int BN, int BK, int STAGES>
+void launch_dma(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
+                int64_t ldy, int M, int N, int K, hipStream_t stream) {
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, STAGES>), dim3(unsigned(tiles_m * tiles_n)), dim3(256), 0,
+                       stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n);
+}
+
 template <int BM, int BN, int WM, int WN, int BK>
 void launch_cfg(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
                 int64_t ldy, int M, int N, int K, hipStream_t stream) {
@@ -205,6 +388,12 @@ const Cfg kConfigs[] = {
     {"gemm_f16_256x256x32_w2x2", launch_cfg<256, 256, 2, 2, 32>, 256, 256, 32},
     {"gemm_f16_192x128x64_w2x2", launch_cfg<192, 128, 2, 2, 64>, 192, 128, 64},
     {"gemm_f16_64x128x64_w1x2", launch_cfg<64, 128, 1, 2, 64>, 64, 128, 64},
+    {"gemm_f16dma_256x128x64_s3", launch_dma<256, 128, 64, 3>, 256, 128, 64},
+    {"gemm_f16dma_256x128x32_s3", launch_dma<256, 128, 32, 3>, 256, 128, 32},
+    {"gemm_f16dma_128x128x64_s3", launch_dma<128, 128, 64, 3>, 128, 128, 64},
+    {"gemm_f16dma_128x128x32_s4", launch_dma<128, 128, 32, 4>, 128, 128, 32},
+    {"gemm_f16dma_128x256x32_s3", launch_dma<128, 256, 32, 3>, 128, 256, 32},
+    {"gemm_f16dma_256x256x32_s3", launch_dma<256, 256, 32, 3>, 256, 256, 32},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -221,9 +410,18 @@ bool gemm_f16_supported(int M, int N, int K, int64_t lda, int64_t ldb) {
     return K % 128 == 0 && int64_t(M) * lda * 2 < 0x7fffffff && int64_t(N) * ldb * 2 < 0x7fffffff;
 }
 
-// Tile choice by measured throughput on the SAM 3 shapes (M = 5184 tokens):
-// 128x128 tiles keep two workgroups per CU and fill 256 CUs for N down to 1024.
-int gemm_f16_pick(int /*M*/, int /*N*/, int /*K*/) { return 0; }
+// Tile choice from a measured sweep of every configuration on the SAM 3
+// linear shapes at M = 5184 tokens on MI355X (kernel time, HIP events):
+//   N % 256 == 0, N >= 2048 (qkv 3072)   -> 128x256 LDS-DMA ring  (652 TFLOP/s)
+//   N <= 1024, K >= 2048 (fc2 4736->1024) -> 192x128 register-staged (597)
+//   N <= 1024 (proj, fusion/decoder 256..1024) -> 128x128x32 LDS-DMA, 4 stages (387)
+//   otherwise (fc1 1024->4736)            -> 128x128x64 register-staged (626)
+int gemm_f16_pick(int /*M*/, int N, int K) {
+    if (N % 256 == 0 && N >= 2048) return 11;
+    if (N <= 1024 && K >= 2048) return 5;
+    if (N <= 1024) return 10;
+    return 0;
+}
 
 const char* launch_gemm_f16(int cfg, const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
                             int64_t ldb, float* y, int64_t ldy, int M, int N, int K, hipStream_t stream) {

@@ -70,7 +70,7 @@ SIGNATURES = {
     "samhip_validate_quantized_payload": ([_I32, _I64, _I64, _P, _SZ], _I),
     "samhip_query": ([_P, ctypes.POINTER(ExecInfo)], _I),
     "samhip_last_error": ([ctypes.c_char_p, _SZ], _SZ),
-    "samhip_trace_begin": ([_P], _I),
+    "samhip_trace_begin": ([_P, ctypes.c_char_p], _I),
     "samhip_trace_end": ([_P, ctypes.POINTER(KernelRecord), _SZ, ctypes.POINTER(_SZ)], _I),
 }
 
@@ -226,8 +226,9 @@ class Context:
         check(lib().samhip_query(self.handle, ctypes.byref(info)))
         return info
 
-    def trace_begin(self):
-        check(lib().samhip_trace_begin(self.handle))
+    def trace_begin(self, kernel_filter=None):
+        """Bracket launches (all, or those whose name contains kernel_filter) with HIP events."""
+        check(lib().samhip_trace_begin(self.handle, kernel_filter.encode() if kernel_filter else None))
 
     def trace_end(self, capacity=1 << 16):
         """Returns [(kernel, weight_type, m, n, k, ms)] of the launches since trace_begin."""
