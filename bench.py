@@ -228,6 +228,95 @@ def cpu_baseline(plan, seconds, rows):
                       f"integer dots), OpenMP"}
 
 
+TEXT_LAYERS = 24
+TEXT_M = 32
+TEXT_SHAPES = [("in_proj", 1024, 3072), ("out_proj", 1024, 1024), ("fc1", 1024, 4096), ("fc2", 4096, 1024)]
+
+
+def text_stream(args, sh, ctx, fmt):
+    """The text encoder's linear stream at M = 32 tokens: 24 layers of
+    in_proj 1024->3072, out_proj 1024->1024, fc1 1024->4096, fc2 4096->1024
+    and the resizer 1024->256 (src/models/sam3/text_encoder.hpp:83-174), 97
+    mul_mat per step, every layer with its own weight buffers so that the
+    stream's weights (321 MB in Q8_0) pass through HBM as they do in the
+    model.  The timed steps replay the stream captured as one HIP graph (the
+    eager per-call time is reported beside it).  One JSON line: algorithmic
+    bytes (packed W + F32 X + F32 Y) per second over the whole stream, and
+    the skinny kernel's roofline."""
+    qt = {"q8_0": sh.Q8_0, "q4_k": sh.Q4_K, "q5_k": sh.Q5_K, "q6_k": sh.Q6_K}[fmt]
+    log("preparing text stream weights")
+    rng = np.random.default_rng(1)
+    xbuf = {k: ctx.upload(rng.standard_normal((TEXT_M, k)).astype(np.float32)) for k in (1024, 4096)}
+    shapes = [(f"L{l}.{name}", k, n) for l in range(TEXT_LAYERS) for name, k, n in TEXT_SHAPES]
+    shapes.append(("resizer", 1024, 256))
+    packed = {}
+    for name, k, n in set((nm.split(".")[-1], k, n) for nm, k, n in shapes):
+        wf = ctx.upload((np.random.default_rng(0).standard_normal((n, k)) * 0.02).astype(np.float32))
+        packed[(k, n)] = wf
+    ops, alg_bytes = [], 0
+    for label, k, n in shapes:
+        wq = ctx.alloc(n * sh.row_bytes(qt, k))
+        ctx.quantize_rows(qt, packed[(k, n)].ptr, 4 * k, wq.ptr, n, k, sh.ROUND_REF)
+        yb = ctx.alloc(TEXT_M * n * 4)
+        ops.append((label, k, n, sh.tensor(qt, k, n, wq.ptr), sh.tensor(sh.F32, k, TEXT_M, xbuf[k].ptr),
+                    sh.tensor(sh.F32, n, TEXT_M, yb.ptr), wq, yb))
+        alg_bytes += n * sh.row_bytes(qt, k) + TEXT_M * k * 4 + TEXT_M * n * 4
+    ctx.synchronize()
+    for wf in packed.values():
+        wf.free()
+
+    def step():
+        for _, _, _, w, x, y, _, _ in ops:
+            ctx.mul_mat(w, x, y)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.trace_begin()
+    step()
+    prof = ctx.trace_end(capacity=4 * len(ops) + 16)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    ctx.synchronize()
+    eager = time.perf_counter() - t0
+    # the same stream captured once and replayed: one host call per step
+    ctx.capture_begin()
+    step()
+    graph = ctx.capture_end()
+    graph.launch()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.launch()
+    ctx.synchronize()
+    elapsed = time.perf_counter() - t0
+    graph.destroy()
+    kern = [r for r in prof if r[0].startswith("skinny")]
+    stage = [r for r in prof if r[0].startswith("stage")]
+    fc1 = [r[5] for r in kern if r[3] == 4096 and r[4] == 1024]
+    fc1_ms = float(np.mean(fc1))
+    fc1_bytes = 4096 * sh.row_bytes(qt, 1024) + TEXT_M * 1024 * 4 + TEXT_M * 4096 * 4
+    ach = fc1_bytes / (fc1_ms * 1e-3) / 1e9
+    return {
+        "metric": "text linear stream algorithmic GB/s (M=32, 24 layers)", "value": round(alg_bytes * args.steps / elapsed / 1e9, 1),
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": f"SAM 3 text encoder linear stream, {fmt.upper()} weights, M=32 tokens, 97 mul_mat per step",
+                   "weights_mb": round(sum(o[6].nbytes for o in ops) / 1e6, 1), "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(ach / PEAK_HBM_GBPS, 4), "traffic": None, "kernel": kern[0][0] if kern else None,
+                     "shape": {"M": TEXT_M, "N": 4096, "K": 1024}, "launch_ms": round(fc1_ms, 5),
+                     "algorithmic_bytes_per_launch": int(fc1_bytes)},
+        "eager_ms_per_step": round(eager * 1e3 / args.steps, 4),
+        "replay": "one HIP graph launch per step (samhip_capture_begin/end)",
+        "kernel_ms_per_step": round(sum(r[5] for r in kern), 4),
+        "stage_ms_per_step": round(sum(r[5] for r in stage), 4),
+        "device": ctx.query().device_name.decode(),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -239,6 +328,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--trace", choices=["dominant", "all", "none"], default="dominant",
                     help="launches bracketed by HIP events inside the timed region")
+    ap.add_argument("--workload", choices=["vit", "text"], default="vit",
+                    help="vit: the ViT linear sweep (headline); text: the M=32 text-encoder linear stream")
+    ap.add_argument("--format", choices=["q8_0", "q4_k", "q5_k", "q6_k"], default="q8_0",
+                    help="weight format of the text stream")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the plain copy used to scale HBM traffic counters")
     ap.add_argument("--summarize-profiles", metavar="DIR",
@@ -259,6 +352,11 @@ def main():
     sh = load_samhip()
     compute = sh.COMPUTE_Q8_NATIVE if args.compute == "native" else sh.COMPUTE_F16
     ctx = sh.Context(0, compute, sh.ROUND_X86)
+    if args.workload == "text":
+        result = text_stream(args, sh, ctx, args.format)
+        ctx.close()
+        print(json.dumps(result), flush=True)
+        return
     plan = products(sh)
 
     log("preparing inputs")

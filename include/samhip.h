@@ -190,6 +190,24 @@ typedef struct samhip_kernel_record {
 } samhip_kernel_record;
 int samhip_trace_begin(samhip_context* ctx, const char* kernel_filter);
 int samhip_trace_end(samhip_context* ctx, samhip_kernel_record* records, size_t capacity, size_t* count);
+/* --- stream capture (no reference counterpart) ----------------------------
+ * For launch-bound streams of small products (the text encoder's 97 linears
+ * at M = 32): the calls between capture_begin and capture_end are recorded
+ * into a HIP graph instead of running, and graph_launch replays them on the
+ * context's stream with one host call.  Only samhip_mul_mat,
+ * samhip_quantize_rows and samhip_dequantize_rows may be captured; every
+ * other entry point fails with INVALID_ARGUMENT while a capture is open.  A
+ * captured call must fit the context's current staging (run the same
+ * product once before capturing); staging that has to grow later is
+ * reallocated without freeing the buffer that live graphs use.  Replays
+ * read and write the device buffers named at capture time.  Destroy graphs
+ * before their context. */
+typedef struct samhip_graph samhip_graph;
+int samhip_capture_begin(samhip_context* ctx);
+int samhip_capture_end(samhip_context* ctx, samhip_graph** graph);
+int samhip_graph_launch(samhip_context* ctx, const samhip_graph* graph);
+void samhip_graph_destroy(samhip_graph* graph);
+
 /* Copies the calling thread's last error message; returns its full length. */
 size_t samhip_last_error(char* buffer, size_t size);
 

@@ -52,6 +52,11 @@ size_t row_bytes(int t, int64_t k) { return size_t(k / block_elems(t)) * size_t(
 
 }  // namespace
 
+struct samhip_graph {
+    samhip_context* ctx;
+    hipGraphExec_t exec;
+};
+
 struct samhip_context {
     int device = 0;
     int compute = SAMHIP_COMPUTE_Q8_NATIVE;
@@ -67,6 +72,8 @@ struct samhip_context {
     // gemm_cfg >= 0 forces one fp16 GEMM tile configuration (SAMHIP_GEMM_CONFIG)
     int tall_m = 256;
     int gemm_cfg = -1;
+    bool fused_skinny = true;   // SAMHIP_FUSED_SKINNY=0 routes M <= 128 through staging + the skinny kernel
+    int fused_max_splits = 16;  // SAMHIP_FUSED_MAX_SPLITS: cap on the fused kernel's K splits
     samhip_exec_info info{};
     // per-launch event trace (samhip_trace_begin / samhip_trace_end)
     struct TraceRecord {
@@ -76,12 +83,22 @@ struct samhip_context {
         hipEvent_t start, stop;
     };
     bool tracing = false;
+    // stream capture: staging buffers that captured graphs still use
+    bool capturing = false;
+    int live_graphs = 0;
+    std::vector<void*> retired_staging;
     std::string trace_filter;
     std::vector<TraceRecord> trace;
     std::vector<hipEvent_t> event_pool;
 };
 
 namespace {
+
+// Entry points that synchronize or allocate cannot be recorded into a graph.
+#define SAMHIP_NOT_WHILE_CAPTURING(ctx, what)                                                  \
+    do {                                                                                      \
+        if ((ctx)->capturing) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "%s cannot be called while a capture is open", what); \
+    } while (0)
 
 int set_device(samhip_context* ctx) {
     HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
@@ -90,9 +107,17 @@ int set_device(samhip_context* ctx) {
 
 int ensure_staging(samhip_context* ctx, size_t bytes) {
     if (bytes <= ctx->staging_bytes) return SAMHIP_OK;
+    if (ctx->capturing)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT,
+                    "capture: this product needs %zu bytes of staging but %zu are reserved; run it once before "
+                    "capturing", bytes, ctx->staging_bytes);
     if (ctx->staging) {
         HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
-        HIP_TRY(hipFree(ctx->staging), "hipFree");
+        if (ctx->live_graphs > 0) {
+            ctx->retired_staging.push_back(ctx->staging);   // still named by captured graphs
+        } else {
+            HIP_TRY(hipFree(ctx->staging), "hipFree");
+        }
         ctx->staging = nullptr;
         ctx->staging_bytes = 0;
     }
@@ -230,6 +255,8 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
     ctx->stream = ctx->own_stream;
     // kernel-variant forcing for tuning runs (SAMHIP_* environment variables)
     ctx->tall_m = std::max(1, env_int("SAMHIP_TALL_M", ctx->tall_m));
+    ctx->fused_skinny = env_int("SAMHIP_FUSED_SKINNY", 1) != 0;
+    ctx->fused_max_splits = std::max(1, env_int("SAMHIP_FUSED_MAX_SPLITS", 16));
     const int cfg = env_int("SAMHIP_GEMM_CONFIG", -1);
     ctx->gemm_cfg = (cfg >= 0 && cfg < gemm_f16_config_count()) ? cfg : -1;
     *out = ctx;
@@ -239,9 +266,15 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
 void samhip_context_destroy(samhip_context* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
+    if (ctx->capturing) {
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(ctx->stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+    }
     if (ctx->own_stream) (void)hipStreamSynchronize(ctx->own_stream);
     if (ctx->stream && ctx->stream != ctx->own_stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->staging) (void)hipFree(ctx->staging);
+    for (void* p : ctx->retired_staging) (void)hipFree(p);
     if (ctx->flag) (void)hipFree(ctx->flag);
     for (auto& r : ctx->trace) {
         (void)hipEventDestroy(r.start);
@@ -254,12 +287,14 @@ void samhip_context_destroy(samhip_context* ctx) {
 
 int samhip_context_set_stream(samhip_context* ctx, void* hip_stream) {
     if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "context_set_stream");
     ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
     return SAMHIP_OK;
 }
 
 int samhip_synchronize(samhip_context* ctx) {
     if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "synchronize");
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     return SAMHIP_OK;
@@ -267,6 +302,7 @@ int samhip_synchronize(samhip_context* ctx) {
 
 int samhip_buffer_alloc(samhip_context* ctx, size_t bytes, void** device_ptr) {
     if (!ctx || !device_ptr || bytes == 0) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "invalid buffer request");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "buffer_alloc");
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipMalloc(device_ptr, bytes), "hipMalloc");
     return SAMHIP_OK;
@@ -274,6 +310,7 @@ int samhip_buffer_alloc(samhip_context* ctx, size_t bytes, void** device_ptr) {
 
 int samhip_buffer_free(samhip_context* ctx, void* device_ptr) {
     if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "buffer_free");
     if (!device_ptr) return SAMHIP_OK;
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
@@ -283,6 +320,7 @@ int samhip_buffer_free(samhip_context* ctx, void* device_ptr) {
 
 int samhip_tensor_set(samhip_context* ctx, void* device_dst, const void* host_src, size_t bytes) {
     if (!ctx || (bytes && (!device_dst || !host_src))) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "invalid tensor_set");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "tensor_set");
     if (!bytes) return SAMHIP_OK;
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipMemcpyAsync(device_dst, host_src, bytes, hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync H2D");
@@ -292,6 +330,7 @@ int samhip_tensor_set(samhip_context* ctx, void* device_dst, const void* host_sr
 
 int samhip_tensor_get(samhip_context* ctx, void* host_dst, const void* device_src, size_t bytes) {
     if (!ctx || (bytes && (!device_src || !host_dst))) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "invalid tensor_get");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "tensor_get");
     if (!bytes) return SAMHIP_OK;
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipMemcpyAsync(host_dst, device_src, bytes, hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync D2H");
@@ -309,6 +348,26 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     const int K = int(w->ne[0]), N = int(w->ne[1]), M = int(x->ne[1]);
     if (int rc = set_device(ctx)) return rc;
     const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K);
+    if (!tall && M <= kFusedMaxM && ctx->fused_skinny) {
+        // one launch: activation packing, weight decode and product
+        const FusedPlan plan = fused_skinny_plan(M, N, K, ctx->fused_max_splits);
+        if (int rc = ensure_staging(ctx, std::max<size_t>(plan.part_bytes, 256))) return rc;
+        const char* variant = fused_skinny_variant(w->type);
+        if (!variant) return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no kernel for weight type %d", w->type);
+        int rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
+            launch_fused_skinny(w->type, ctx->compute == SAMHIP_COMPUTE_F16, static_cast<const float*>(x->data),
+                                int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
+                                int64_t(y->nb[1] / 4), static_cast<float*>(ctx->staging), M, N, K,
+                                ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->fused_max_splits, ctx->stream);
+            HIP_TRY(hipGetLastError(), "fused skinny launch");
+            return SAMHIP_OK;
+        });
+        if (rc) return rc;
+        ctx->info.mul_mat_calls++;
+        ctx->info.skinny_launches++;
+        std::snprintf(ctx->info.kernel_variant, sizeof(ctx->info.kernel_variant), "%s", variant);
+        return SAMHIP_OK;
+    }
     auto align256 = [](size_t v) { return (v + 255) & ~size_t(255); };
     const size_t a_bytes = size_t(M) * size_t(K) * 2;
     const size_t rs_offset = align256(a_bytes);
@@ -345,6 +404,15 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
             HIP_TRY(hipGetLastError(), "gemm launch");
             return SAMHIP_OK;
         });
+    } else if (M <= kSkinnyMaxM) {
+        variant = skinny_variant(w->type, M, N);
+        rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
+            launch_skinny(w->type, a, K, rs, w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
+                          int64_t(y->nb[1] / 4), M, N, K, ctx->stream);
+            HIP_TRY(hipGetLastError(), "skinny launch");
+            return SAMHIP_OK;
+        });
+        if (!rc) ctx->info.skinny_launches++;
     } else {
         rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
             launch_gemm(w->type, a, K, rs, w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
@@ -356,7 +424,7 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     if (rc) return rc;
     ctx->info.mul_mat_calls++;
     ctx->info.activation_launches++;
-    ctx->info.gemm_launches++;
+    if (tall || M > kSkinnyMaxM) ctx->info.gemm_launches++;
     ctx->info.activation_payload_peak_bytes = std::max<uint64_t>(ctx->info.activation_payload_peak_bytes, a_bytes);
     std::snprintf(ctx->info.kernel_variant, sizeof(ctx->info.kernel_variant), "%s", variant);
     return SAMHIP_OK;
@@ -364,6 +432,7 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
 
 int samhip_get_rows(samhip_context* ctx, const samhip_tensor* src, const samhip_tensor* ids, const samhip_tensor* dst) {
     if (!ctx || !src || !ids || !dst) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "get_rows: null argument");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "get_rows");
     const int t = src->type;
     if (t != T_F32 && t != T_F16 && !is_weight_type(t)) return fail(SAMHIP_ERR_UNSUPPORTED, "get_rows: unsupported source type %d", t);
     if (ids->type != T_I32 || dst->type != T_F32) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "get_rows: ids must be I32 and dst F32");
@@ -454,6 +523,7 @@ int samhip_validate_quantized_payload(int32_t type, int64_t ne0, int64_t rows, c
 
 int samhip_trace_begin(samhip_context* ctx, const char* kernel_filter) {
     if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "trace_begin");
     ctx->trace_filter = kernel_filter ? kernel_filter : "";
     for (auto& r : ctx->trace) {
         ctx->event_pool.push_back(r.start);
@@ -466,6 +536,7 @@ int samhip_trace_begin(samhip_context* ctx, const char* kernel_filter) {
 
 int samhip_trace_end(samhip_context* ctx, samhip_kernel_record* records, size_t capacity, size_t* count) {
     if (!ctx || (capacity && !records)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "invalid trace_end argument");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "trace_end");
     ctx->tracing = false;
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
@@ -492,6 +563,61 @@ int samhip_query(samhip_context* ctx, samhip_exec_info* info) {
     if (!ctx || !info) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null query argument");
     *info = ctx->info;
     return SAMHIP_OK;
+}
+
+int samhip_capture_begin(samhip_context* ctx) {
+    if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "capture_begin");
+    if (ctx->tracing) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "capture_begin: a trace is open");
+    if (!ctx->stream) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "capture_begin: the null stream cannot be captured");
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    ctx->capturing = true;
+    return SAMHIP_OK;
+}
+
+int samhip_capture_end(samhip_context* ctx, samhip_graph** graph) {
+    if (!ctx || !graph) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "capture_end: null argument");
+    *graph = nullptr;
+    if (!ctx->capturing) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "capture_end: no capture is open");
+    ctx->capturing = false;
+    if (int rc = set_device(ctx)) return rc;
+    hipGraph_t g = nullptr;
+    HIP_TRY(hipStreamEndCapture(ctx->stream, &g), "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    samhip_graph* out = new (std::nothrow) samhip_graph{ctx, exec};
+    if (!out) {
+        (void)hipGraphExecDestroy(exec);
+        return fail(SAMHIP_ERR_OUT_OF_MEMORY, "graph allocation failed");
+    }
+    ctx->live_graphs++;
+    *graph = out;
+    return SAMHIP_OK;
+}
+
+int samhip_graph_launch(samhip_context* ctx, const samhip_graph* graph) {
+    if (!ctx || !graph) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "graph_launch: null argument");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "graph_launch");
+    if (graph->ctx != ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "graph_launch: graph belongs to another context");
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipGraphLaunch(graph->exec, ctx->stream), "hipGraphLaunch");
+    return SAMHIP_OK;
+}
+
+void samhip_graph_destroy(samhip_graph* graph) {
+    if (!graph) return;
+    samhip_context* ctx = graph->ctx;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipGraphExecDestroy(graph->exec);
+    if (--ctx->live_graphs == 0) {
+        for (void* p : ctx->retired_staging) (void)hipFree(p);
+        ctx->retired_staging.clear();
+    }
+    delete graph;
 }
 
 size_t samhip_last_error(char* buffer, size_t size) {

@@ -119,8 +119,49 @@ __device__ __forceinline__ void mul_i8x4_to_half(uint32_t w, _Float16 d, _Float1
 }
 
 // ---------------------------------------------------------------------------
+// Byte readers over one packed weight row (offsets in bytes from the row
+// start; 2-byte reads at even offsets, 4- and 16-byte reads at even offsets).
+// ---------------------------------------------------------------------------
+
+// A row in device memory at a 2-byte aligned address.
+struct GlobalRow {
+    const uint8_t* p;
+    __device__ __forceinline__ uint32_t u8(int o) const { return load1(p + o); }
+    __device__ __forceinline__ uint32_t u16(int o) const { return load2_a2(p + o); }
+    __device__ __forceinline__ uint32_t u32(int o) const { return load4_a2(p + o); }
+    __device__ __forceinline__ u32x4 u128(int o) const { return load16_a2(p + o); }
+};
+
+// A row copied into LDS as whole dwords: the row's first byte is byte `sh`
+// (0 or 2) of dw[0].
+struct LdsRow {
+    const uint32_t* dw;
+    int sh;
+    __device__ __forceinline__ uint32_t word(int i) const { return dw[i]; }
+    __device__ __forceinline__ uint32_t u8(int o) const {
+        const int b = o + sh;
+        return (dw[b >> 2] >> (8 * (b & 3))) & 0xffu;
+    }
+    __device__ __forceinline__ uint32_t u16(int o) const {
+        const int b = o + sh;
+        return (dw[b >> 2] >> (8 * (b & 2))) & 0xffffu;
+    }
+    __device__ __forceinline__ uint32_t u32(int o) const {
+        const int b = o + sh, i = b >> 2;
+        return funnel_bytes(dw[i + 1], dw[i], uint32_t(b & 3));
+    }
+    // five dword reads and four byte funnels, no branch on the alignment
+    __device__ __forceinline__ u32x4 u128(int o) const {
+        const int b = o + sh, i = b >> 2;
+        const uint32_t s = uint32_t(b & 3);
+        const uint32_t w0 = dw[i], w1 = dw[i + 1], w2 = dw[i + 2], w3 = dw[i + 3], w4 = dw[i + 4];
+        return u32x4{funnel_bytes(w1, w0, s), funnel_bytes(w2, w1, s), funnel_bytes(w3, w2, s), funnel_bytes(w4, w3, s)};
+    }
+};
+
+// ---------------------------------------------------------------------------
 // Weight operand loaders: one thread owns 16 consecutive K elements (half h of
-// a 32-element K step) of one weight row.  load() issues the global reads,
+// a 32-element K step) of one weight row.  load() issues the reads,
 // dequant() turns them into 16 fp16 values equal to fp16(ggml to_float(W)).
 // ---------------------------------------------------------------------------
 
@@ -129,11 +170,13 @@ template <int WT> struct WeightPiece;
 template <> struct WeightPiece<T_Q8_0> {
     u32x4 q;
     uint32_t d;
-    __device__ __forceinline__ void load(const uint8_t* row, int step, int h) {
-        const uint8_t* blk = row + 34 * step;
-        d = load2_a2(blk);
-        q = load16_a2(blk + 2 + 16 * h);
+    template <class R>
+    __device__ __forceinline__ void load(const R& r, int step, int h) {
+        const int blk = 34 * step;
+        d = r.u16(blk);
+        q = r.u128(blk + 2 + 16 * h);
     }
+    __device__ __forceinline__ void load(const uint8_t* row, int step, int h) { load(GlobalRow{row}, step, h); }
     __device__ __forceinline__ void dequant(int /*step*/, int /*h*/, _Float16* out) const {
         const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)d);
         mul_i8x4_to_half(q[0], dh, out + 0);
@@ -146,15 +189,17 @@ template <> struct WeightPiece<T_Q8_0> {
 template <> struct WeightPiece<T_Q4_K> {
     uint32_t hdr, sc[3];
     u32x4 qs;
-    __device__ __forceinline__ void load(const uint8_t* row, int step, int h) {
-        const uint8_t* blk = row + 144 * (step >> 3);
+    template <class R>
+    __device__ __forceinline__ void load(const R& r, int step, int h) {
+        const int blk = 144 * (step >> 3);
         const int j = step & 7;
-        hdr = load4_a2(blk);
-        sc[0] = load4_a2(blk + 4);
-        sc[1] = load4_a2(blk + 8);
-        sc[2] = load4_a2(blk + 12);
-        qs = load16_a2(blk + 16 + 32 * (j >> 1) + 16 * h);
+        hdr = r.u32(blk);
+        sc[0] = r.u32(blk + 4);
+        sc[1] = r.u32(blk + 8);
+        sc[2] = r.u32(blk + 12);
+        qs = r.u128(blk + 16 + 32 * (j >> 1) + 16 * h);
     }
+    __device__ __forceinline__ void load(const uint8_t* row, int step, int h) { load(GlobalRow{row}, step, h); }
     __device__ __forceinline__ void dequant(int step, int /*h*/, _Float16* out) const {
         const int j = step & 7;
         int s, m;
@@ -169,16 +214,18 @@ template <> struct WeightPiece<T_Q4_K> {
 template <> struct WeightPiece<T_Q5_K> {
     uint32_t hdr, sc[3];
     u32x4 qs, qh;
-    __device__ __forceinline__ void load(const uint8_t* row, int step, int h) {
-        const uint8_t* blk = row + 176 * (step >> 3);
+    template <class R>
+    __device__ __forceinline__ void load(const R& r, int step, int h) {
+        const int blk = 176 * (step >> 3);
         const int j = step & 7;
-        hdr = load4_a2(blk);
-        sc[0] = load4_a2(blk + 4);
-        sc[1] = load4_a2(blk + 8);
-        sc[2] = load4_a2(blk + 12);
-        qh = load16_a2(blk + 16 + 16 * h);
-        qs = load16_a2(blk + 48 + 32 * (j >> 1) + 16 * h);
+        hdr = r.u32(blk);
+        sc[0] = r.u32(blk + 4);
+        sc[1] = r.u32(blk + 8);
+        sc[2] = r.u32(blk + 12);
+        qh = r.u128(blk + 16 + 16 * h);
+        qs = r.u128(blk + 48 + 32 * (j >> 1) + 16 * h);
     }
+    __device__ __forceinline__ void load(const uint8_t* row, int step, int h) { load(GlobalRow{row}, step, h); }
     __device__ __forceinline__ void dequant(int step, int /*h*/, _Float16* out) const {
         const int j = step & 7;
         int s, m;
@@ -196,14 +243,16 @@ template <> struct WeightPiece<T_Q5_K> {
 template <> struct WeightPiece<T_Q6_K> {
     u32x4 ql, qh;
     uint32_t sc, d;
-    __device__ __forceinline__ void load(const uint8_t* row, int step, int h) {
-        const uint8_t* blk = row + 210 * (step >> 3);
+    template <class R>
+    __device__ __forceinline__ void load(const R& r, int step, int h) {
+        const int blk = 210 * (step >> 3);
         const int j = step & 7, half = j >> 2, g = j & 3;
-        ql = load16_a2(blk + 64 * half + 32 * (g & 1) + 16 * h);
-        qh = load16_a2(blk + 128 + 32 * half + 16 * h);
-        sc = load1(blk + 192 + 8 * half + 2 * g + h);
-        d = load2_a2(blk + 208);
+        ql = r.u128(blk + 64 * half + 32 * (g & 1) + 16 * h);
+        qh = r.u128(blk + 128 + 32 * half + 16 * h);
+        sc = r.u8(blk + 192 + 8 * half + 2 * g + h);
+        d = r.u16(blk + 208);
     }
+    __device__ __forceinline__ void load(const uint8_t* row, int step, int h) { load(GlobalRow{row}, step, h); }
     __device__ __forceinline__ void dequant(int step, int /*h*/, _Float16* out) const {
         const int g = (step & 7) & 3;
         const float t = half_bits_to_float(d) * (float)(int8_t)sc;   // exact in f32

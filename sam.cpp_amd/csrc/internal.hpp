@@ -42,4 +42,26 @@ const char* gemm_variant(int wtype);
 const char* launch_gemm(int wtype, const _Float16* a, int64_t lda, const float* row_scale, const void* w,
                         int64_t w_stride, float* y, int64_t ldy, int M, int N, int K, hipStream_t stream);
 
+// Skinny / medium products (M <= kSkinnyMaxM): weights decoded in registers,
+// one pass over the packed bytes.  Returns the variant name, or nullptr.
+constexpr int kSkinnyMaxM = 256;
+const char* skinny_variant(int wtype, int M, int N);
+const char* launch_skinny(int wtype, const _Float16* a, int64_t lda, const float* row_scale, const void* w,
+                          int64_t w_stride, float* y, int64_t ldy, int M, int N, int K, hipStream_t stream);
+
+// Fused skinny products (M <= kFusedMaxM): activation packing, weight decode
+// and product in one launch; when the K range is split over workgroups their
+// partial sums go through `part` (FusedPlan::part_bytes) and a second, small
+// launch adds them.
+constexpr int kFusedMaxM = 128;
+struct FusedPlan {
+    int rg, splits, cps;
+    size_t part_bytes;
+};
+FusedPlan fused_skinny_plan(int M, int N, int K, int max_splits);
+const char* fused_skinny_variant(int wtype);
+const char* launch_fused_skinny(int wtype, bool f16, const float* x, int64_t ldx, const void* w, int64_t w_stride,
+                                float* y, int64_t ldy, float* part, int M, int N, int K, int x86, int max_splits,
+                                hipStream_t stream);
+
 }  // namespace samhip

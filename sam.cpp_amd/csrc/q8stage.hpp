@@ -1,0 +1,134 @@
+// Activation packing shared by the staging kernels and the fused skinny
+// kernel: lane-level reductions on the DPP network, the power-of-two operand
+// scale, and the conversion of 8 consecutive F32 activations per lane into
+// the fp16 MFMA operand
+//   Q8_0 mode : fp16(to_float(q8_0 block) * 2^-e)   (Q8_0 weights)
+//   Q8_K mode : fp16(to_float(q8_K block) * 2^-e)   (K-quant weights)
+//   F16 mode  : fp16(x * 2^-e)
+// with Q8 blocks bit-exact with ggml's CPU from_float for the weight's
+// vec_dot_type (src/runtime/ggml/backends/cpu.hpp:13-23).
+#pragma once
+
+#include "blocks.hpp"
+
+namespace samhip {
+
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// max over aligned groups of `width` lanes
+template <int width>
+__device__ __forceinline__ float group_max(float v) {
+    for (int off = width / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+template <int width>
+__device__ __forceinline__ int group_sum(int v) {
+    for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// 2^e as a float for |e| <= 126.
+__device__ __forceinline__ float exp2i(int e) { return __builtin_bit_cast(float, uint32_t(127 + e) << 23); }
+
+// Row exponent e with rowmax * 2^-e in [2^14, 2^15), clamped to [-110, 110]
+// so that both 2^e and 2^-e are normal floats.
+__device__ __forceinline__ int row_exponent(float rowmax) {
+    if (!(rowmax > 0.f) || !__builtin_isfinite(rowmax)) return 0;
+    const int biased = int((__builtin_bit_cast(uint32_t, rowmax) >> 23) & 0xffu);
+    int e = (biased == 0 ? -126 : biased - 127) - 14;
+    return e < -110 ? -110 : (e > 110 ? 110 : e);
+}
+
+__device__ __forceinline__ floatx4 load4f(const float* p) { return *reinterpret_cast<const floatx4*>(p); }
+
+// Cross-lane steps on the DPP network (no LDS round trip): quad_perm swaps
+// for lane ^ 1 and lane ^ 2, row rotations by 4 and 8 within 16 lanes.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false); }
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float max4_lanes(float v) {
+    v = fmaxf(v, dpp<DPP_XOR1>(v));
+    return fmaxf(v, dpp<DPP_XOR2>(v));
+}
+__device__ __forceinline__ float max32_lanes(float v) {
+    v = max4_lanes(v);
+    v = fmaxf(v, dpp<DPP_ROR4>(v));
+    v = fmaxf(v, dpp<DPP_ROR8>(v));
+    return fmaxf(v, __shfl_xor(v, 16, 64));
+}
+__device__ __forceinline__ int min32_lanes(int v) {
+    v = min(v, dpp<DPP_XOR1>(v));
+    v = min(v, dpp<DPP_XOR2>(v));
+    v = min(v, dpp<DPP_ROR4>(v));
+    v = min(v, dpp<DPP_ROR8>(v));
+    return min(v, __shfl_xor(v, 16, 64));
+}
+typedef float floatx8 __attribute__((ext_vector_type(8)));
+
+// The fp16 operand of 8 consecutive activations held by each lane; lanes
+// 4g..4g+3 hold one Q8_0 block, lanes 32h..32h+31 one Q8_K block.  Every
+// lane of the wave must call it (cross-lane reductions); lanes past the
+// row's end hold zeros.  `down` = 2^-e.  X86 selects the Q8_0 rounding of
+// ggml's x86-64 from_float (scale 127/amax, ties to even) over the
+// reference quantize_row_q8_0_ref (scale 1/d, ties away from zero).
+template <int MODE, bool X86>
+__device__ __forceinline__ half8 quant8(const floatx8& v, int lane, float down) {
+#pragma clang fp contract(off)
+    float d = 0.f;
+    float q[8];
+    if (MODE == T_Q8_0) {
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        amax = max4_lanes(amax);
+        const float dd = amax / 127.f;
+        float inv;
+        if (X86) inv = amax != 0.f ? 127.f / amax : 0.f;
+        else inv = dd != 0.f ? 1.f / dd : 0.f;
+        d = half_bits_to_float(float_to_half_bits(dd));   // stored fp16 scale
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float s = v[i] * inv;
+            q[i] = X86 ? __builtin_rintf(s) : __builtin_roundf(s);
+        }
+    } else if (MODE == T_Q8_K) {
+        // first element of largest magnitude in the 256-value block
+        const int base = 8 * (lane & 31);
+        float la = 0.f, ls = 0.f;
+        int li = 1 << 20;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float t = fabsf(v[i]);
+            if (t > la) { la = t; ls = v[i]; li = base + i; }
+        }
+        const float amax = max32_lanes(la);
+        const int idx = min32_lanes(la == amax ? li : (1 << 20));
+        const float smax = __shfl(ls, (lane & 32) + ((idx >> 3) & 31), 64);
+        if (amax != 0.f) {
+            const float iscale = -127.f / smax;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) q[i] = fminf(127.f, __builtin_rintf(iscale * v[i]));
+            d = 1.f / iscale;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) q[i] = 0.f;
+        }
+    }
+    half8 o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = MODE == T_F16 ? (_Float16)(v[i] * down) : (_Float16)((d * q[i]) * down);
+    return o;
+}
+
+}  // namespace samhip

@@ -10,6 +10,7 @@
 // a per-row power of two that keeps the row maximum inside fp16's range; the
 // GEMM epilogue multiplies it back exactly.
 #include "internal.hpp"
+#include "q8stage.hpp"
 
 #pragma clang fp contract(off)
 
@@ -17,76 +18,14 @@ namespace samhip {
 
 namespace {
 
-__device__ __forceinline__ float wave_max(float v) {
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-// max over aligned groups of `width` lanes
-template <int width>
-__device__ __forceinline__ float group_max(float v) {
-    for (int off = width / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-template <int width>
-__device__ __forceinline__ int group_sum(int v) {
-    for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-// 2^e as a float for |e| <= 126.
-__device__ __forceinline__ float exp2i(int e) { return __builtin_bit_cast(float, uint32_t(127 + e) << 23); }
-
-// Row exponent e with rowmax * 2^-e in [2^14, 2^15), clamped to [-110, 110]
-// so that both 2^e and 2^-e are normal floats.
-__device__ __forceinline__ int row_exponent(float rowmax) {
-    if (!(rowmax > 0.f) || !__builtin_isfinite(rowmax)) return 0;
-    const int biased = int((__builtin_bit_cast(uint32_t, rowmax) >> 23) & 0xffu);
-    int e = (biased == 0 ? -126 : biased - 127) - 14;
-    return e < -110 ? -110 : (e > 110 ? 110 : e);
-}
-
-__device__ __forceinline__ floatx4 load4f(const float* p) { return *reinterpret_cast<const floatx4*>(p); }
-
-// Cross-lane steps on the DPP network (no LDS round trip): quad_perm swaps
-// for lane ^ 1 and lane ^ 2, row rotations by 4 and 8 within 16 lanes.
-constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_ROR4 = 0x124, DPP_ROR8 = 0x128;
-
-template <int CTRL>
-__device__ __forceinline__ int dpp(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false); }
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-
-__device__ __forceinline__ float max4_lanes(float v) {
-    v = fmaxf(v, dpp<DPP_XOR1>(v));
-    return fmaxf(v, dpp<DPP_XOR2>(v));
-}
-__device__ __forceinline__ float max32_lanes(float v) {
-    v = max4_lanes(v);
-    v = fmaxf(v, dpp<DPP_ROR4>(v));
-    v = fmaxf(v, dpp<DPP_ROR8>(v));
-    return fmaxf(v, __shfl_xor(v, 16, 64));
-}
-__device__ __forceinline__ int min32_lanes(int v) {
-    v = min(v, dpp<DPP_XOR1>(v));
-    v = min(v, dpp<DPP_XOR2>(v));
-    v = min(v, dpp<DPP_ROR4>(v));
-    v = min(v, dpp<DPP_ROR8>(v));
-    return min(v, __shfl_xor(v, 16, 64));
-}
-typedef float floatx8 __attribute__((ext_vector_type(8)));
-
 // Staging with each lane owning 8 consecutive values (a Q8_0 block spans 4
 // lanes, a Q8_K block 32 lanes).  The row stays in registers (K <= 512*CH),
 // so X is read once; every cross-lane reduction runs with all lanes active
 // (lanes past K hold zeros).
-template <int MODE, int CH>
+template <int MODE, int CH, bool X86>
 __global__ __launch_bounds__(256) void stage8_kernel(const float* __restrict__ x, int64_t x_stride, int M, int K,
                                                      _Float16* __restrict__ a, int64_t lda,
-                                                     float* __restrict__ row_scale, int x86) {
+                                                     float* __restrict__ row_scale) {
     const int lane = threadIdx.x & 63;
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (m >= M) return;
@@ -114,53 +53,8 @@ __global__ __launch_bounds__(256) void stage8_kernel(const float* __restrict__ x
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int k = 512 * c + 8 * lane;
-        float d = 0.f;
-        float q[8];
-        if (MODE == T_Q8_0) {
-            float amax = 0.f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
-            amax = max4_lanes(amax);
-            const float dd = amax / 127.f;
-            float inv;
-            if (x86) inv = amax != 0.f ? 127.f / amax : 0.f;
-            else inv = dd != 0.f ? 1.f / dd : 0.f;
-            d = half_bits_to_float(float_to_half_bits(dd));   // stored fp16 scale
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float s = v[c][i] * inv;
-                q[i] = x86 ? __builtin_rintf(s) : __builtin_roundf(s);
-            }
-        } else if (MODE == T_Q8_K) {
-            // first element of largest magnitude in the 256-value block
-            const int base = 8 * (lane & 31);
-            float la = 0.f, ls = 0.f;
-            int li = 1 << 20;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float t = fabsf(v[c][i]);
-                if (t > la) { la = t; ls = v[c][i]; li = base + i; }
-            }
-            const float amax = max32_lanes(la);
-            const int idx = min32_lanes(la == amax ? li : (1 << 20));
-            const float smax = __shfl(ls, (lane & 32) + ((idx >> 3) & 31), 64);
-            if (amax != 0.f) {
-                const float iscale = -127.f / smax;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) q[i] = fminf(127.f, __builtin_rintf(iscale * v[c][i]));
-                d = 1.f / iscale;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) q[i] = 0.f;
-            }
-        }
-        if (k < K) {
-            half8 o;
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                o[i] = MODE == T_F16 ? (_Float16)(v[c][i] * down) : (_Float16)((d * q[i]) * down);
-            *reinterpret_cast<half8*>(ar + k) = o;
-        }
+        const half8 o = quant8<MODE, X86>(v[c], lane, down);
+        if (k < K) *reinterpret_cast<half8*>(ar + k) = o;
     }
 }
 
@@ -431,8 +325,15 @@ void launch_stage_rows(int mode, bool aligned, const float* x, int64_t x_stride,
                        int64_t lda, float* row_scale, int x86, hipStream_t stream) {
     const dim3 grid((M + 3) / 4), block(256);
     if (aligned && K <= 512 * 10) {
-#define SAMHIP_STAGE8(MODE, CH) \
-    hipLaunchKernelGGL((stage8_kernel<MODE, CH>), grid, block, 0, stream, x, x_stride, M, K, a, lda, row_scale, x86)
+#define SAMHIP_STAGE8(MODE, CH)                                                                                 \
+    do {                                                                                                        \
+        if (MODE == T_Q8_0 && x86)                                                                              \
+            hipLaunchKernelGGL((stage8_kernel<MODE, CH, true>), grid, block, 0, stream, x, x_stride, M, K, a,   \
+                               lda, row_scale);                                                                 \
+        else                                                                                                    \
+            hipLaunchKernelGGL((stage8_kernel<MODE, CH, false>), grid, block, 0, stream, x, x_stride, M, K, a,  \
+                               lda, row_scale);                                                                 \
+    } while (0)
 #define SAMHIP_STAGE8_MODE(MODE)                  \
     if (K <= 1024) SAMHIP_STAGE8(MODE, 2);        \
     else if (K <= 2048) SAMHIP_STAGE8(MODE, 4);   \

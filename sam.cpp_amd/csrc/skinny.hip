@@ -1,0 +1,471 @@
+// Skinny and medium quantized-weight products (M < 256 activation rows):
+//   Y[m][n] = rs[m] * sum_k A[m][k] * fp16(to_float(Wq[n][k]))
+// the shapes of SAM 3's text encoder (M = 32), the K/V projections of text
+// tokens (M = 33) and the decoder queries (M = 201), where every packed
+// weight byte is read once and the product is HBM-bound (ggml's MMVQ / MMQ
+// dispatch for these widths: tests/runtime/ggml/test_quantization.cpp:604-614;
+// call sites src/models/sam3/text_encoder.hpp:83-174,
+// src/models/sam3/detector.hpp:343-479).
+//
+// One workgroup owns 32 consecutive weight rows and the whole K range; its
+// KSPLIT waves (4 to 16) take contiguous shares of the K steps.  Each
+// lane decodes 16 weights of one row per 32-wide K step straight from the
+// packed bytes into registers (the same fp16 operand as the tall path), and
+// the wave multiplies them against up to eight 32-row activation tiles with
+// v_mfma_f32_32x32x16_f16.  Lanes 0-31 take K elements 0-15 of the step and
+// lanes 32-63 elements 16-31 (the A fragments follow the same permutation),
+// so a lane's operands come from 16 contiguous bytes of codes.  The KSPLIT
+// partial sums meet in LDS and leave as coalesced 128-byte row segments.
+#include <algorithm>
+
+#include "internal.hpp"
+#include "q8stage.hpp"
+
+namespace samhip {
+
+namespace {
+
+constexpr int ROWS = 32;            // weight rows per workgroup
+constexpr int PART_STRIDE = 33;     // floats; padded LDS rows for the partial sums
+
+template <int WT, int MT, int KSPLIT, int U>
+__global__ __launch_bounds__(64 * KSPLIT) void skinny_kernel(const _Float16* __restrict__ A, int64_t lda,
+                                                             const float* __restrict__ row_scale,
+                                                             const uint8_t* __restrict__ W, int64_t w_stride,
+                                                             float* __restrict__ Y, int64_t ldy, int M, int N,
+                                                             int K) {
+    __shared__ float part[KSPLIT][ROWS * PART_STRIDE];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * ROWS;
+    const int col = lane & 31, h = lane >> 5;
+    const uint8_t* w_row = W + int64_t(min(n0 + col, N - 1)) * w_stride;
+    const int nsteps = K / 32;
+    const int per = (nsteps + KSPLIT - 1) / KSPLIT;
+    const int s0 = min(nsteps, wave * per), s1 = min(nsteps, s0 + per);
+
+    const _Float16* a_row[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) a_row[t] = A + int64_t(min(t * 32 + col, M - 1)) * lda + 16 * h;
+
+    floatx16 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+
+    // U steps per batch: every load of the batch is issued before the first
+    // product, so each wave keeps U steps of weights and activations in flight
+    for (int s = s0; s < s1; s += U) {
+        WeightPiece<WT> wp[U];
+        half8 a_lo[U][MT], a_hi[U][MT];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int st = min(s + u, s1 - 1);   // past the range: a repeat of the last step, never multiplied
+            wp[u].load(w_row, st, h);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const half8* p = reinterpret_cast<const half8*>(a_row[t] + 32 * st);
+                a_lo[u][t] = p[0];
+                a_hi[u][t] = p[1];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (s + u >= s1) break;
+            _Float16 wv[16];
+            wp[u].dequant(s + u, h, wv);
+            const half8 b_lo{wv[0], wv[1], wv[2], wv[3], wv[4], wv[5], wv[6], wv[7]};
+            const half8 b_hi{wv[8], wv[9], wv[10], wv[11], wv[12], wv[13], wv[14], wv[15]};
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_lo[u][t], b_lo, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_hi[u][t], b_hi, acc[t], 0, 0, 0);
+            }
+        }
+    }
+
+    // 32x32 accumulator layout: lane l holds column (weight row) l%32 and
+    // activation rows 8*(r/4) + 4*(l/32) + r%4.
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        if (t * 32 >= M) break;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int ml = 8 * (r >> 2) + 4 * h + (r & 3);
+            part[wave][ml * PART_STRIDE + col] = acc[t][r];
+        }
+        __syncthreads();
+        for (int o = threadIdx.x; o < ROWS * 32; o += 64 * KSPLIT) {
+            const int ml = o >> 5, nl = o & 31;
+            const int m = t * 32 + ml, n = n0 + nl;
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < KSPLIT; ++w) v += part[w][ml * PART_STRIDE + nl];
+            if (m < M && n < N) Y[int64_t(m) * ldy + n] = v * row_scale[m];
+        }
+        __syncthreads();
+    }
+}
+
+// Waves per workgroup and steps per batch: a grid with fewer workgroups than
+// CUs gets more waves per workgroup (all on one CU) and deeper batches, sized
+// so that the wave's registers still allow KSPLIT / 4 waves per SIMD.
+template <int WT, int MT>
+void launch_mt(const _Float16* a, int64_t lda, const float* rs, const uint8_t* w, int64_t w_stride, float* y,
+               int64_t ldy, int M, int N, int K, bool wide, hipStream_t stream) {
+    const dim3 grid(unsigned((N + ROWS - 1) / ROWS));
+    constexpr int KS = MT == 1 ? 16 : MT == 2 ? 8 : 4;
+    constexpr int UW = MT == 1 ? (WT == T_Q8_0 ? 4 : 2) : MT == 2 ? 4 : MT <= 4 ? 2 : 1;
+    if (wide)
+        hipLaunchKernelGGL((skinny_kernel<WT, MT, KS, UW>), grid, dim3(64 * KS), 0, stream, a, lda, rs, w, w_stride, y,
+                           ldy, M, N, K);
+    else
+        hipLaunchKernelGGL((skinny_kernel<WT, MT, 4, MT <= 2 ? 2 : 1>), grid, dim3(256), 0, stream, a, lda, rs, w,
+                           w_stride, y, ldy, M, N, K);
+}
+
+template <int WT>
+void launch_wt(const _Float16* a, int64_t lda, const float* rs, const uint8_t* w, int64_t w_stride, float* y,
+               int64_t ldy, int M, int N, int K, bool wide, hipStream_t stream) {
+    switch ((M + 31) / 32) {
+        case 1: launch_mt<WT, 1>(a, lda, rs, w, w_stride, y, ldy, M, N, K, wide, stream); break;
+        case 2: launch_mt<WT, 2>(a, lda, rs, w, w_stride, y, ldy, M, N, K, wide, stream); break;
+        case 3: launch_mt<WT, 3>(a, lda, rs, w, w_stride, y, ldy, M, N, K, wide, stream); break;
+        case 4: launch_mt<WT, 4>(a, lda, rs, w, w_stride, y, ldy, M, N, K, wide, stream); break;
+        case 5: launch_mt<WT, 5>(a, lda, rs, w, w_stride, y, ldy, M, N, K, wide, stream); break;
+        case 6: launch_mt<WT, 6>(a, lda, rs, w, w_stride, y, ldy, M, N, K, wide, stream); break;
+        case 7: launch_mt<WT, 7>(a, lda, rs, w, w_stride, y, ldy, M, N, K, wide, stream); break;
+        default: launch_mt<WT, 8>(a, lda, rs, w, w_stride, y, ldy, M, N, K, wide, stream); break;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Fused path for M <= 128: one launch per product (two when K is split).  A
+// workgroup of 8 waves owns 128 weight rows (a 32-row tile per wave pair)
+// and a range of 256-wide K chunks.  Per chunk:
+//  * the waves copy the packed bytes of their tiles with coalesced dword
+//    loads into LDS (rows padded to an odd dword count, so the per-lane piece
+//    reads of one column are bank-conflict free);
+//  * the workgroup packs the activation chunk (M rows x 256, F32) into the
+//    fp16 operand in LDS with quant8 (Q8_0 / Q8_K blocks bit-exact with
+//    ggml's from_float) under a power-of-two scale 2^-e per row and chunk;
+//  * each wave decodes its pieces from LDS and runs 4 of the chunk's 8 K
+//    steps of v_mfma_f32_32x32x16_f16, then adds the products times 2^e;
+//    the wave pair's two sums meet in LDS at the end.
+// When the K range is split over S workgroups, each writes its partial sums
+// to scratch and splitk_reduce_kernel adds the S partials in split order
+// (results do not depend on scheduling).  A reduction inside the kernel
+// would need agent-scope release/acquire fences, which on gfx950 write back
+// and invalidate the XCD's whole L2; the second launch is cheaper.
+// ---------------------------------------------------------------------------
+
+constexpr int FROWS = 128;          // weight rows per workgroup
+constexpr int CHUNK = 256;          // K elements per chunk
+constexpr int ALD = CHUNK + 8;      // halves per LDS activation row
+
+template <int WT>
+constexpr int chunk_bytes() { return WT == T_Q8_0 ? 8 * 34 : block_bytes(WT); }
+// dwords per LDS weight row: the row's bytes start at byte 0 or 2 of the
+// first dword; an odd count keeps column reads conflict free
+template <int WT>
+constexpr int wrow_dw() { return ((chunk_bytes<WT>() + 2 + 3) / 4) | 1; }
+
+template <int WT, int MODE, bool X86, int MT, bool XVEC>
+__global__ __launch_bounds__(512) void fused_skinny_kernel(const float* __restrict__ X, int64_t ldx,
+                                                           const uint8_t* __restrict__ W, int64_t w_stride,
+                                                           float* __restrict__ Y, int64_t ldy,
+                                                           float* __restrict__ part, int M, int N, int K, int RG,
+                                                           int cps) {
+    constexpr int WDW = wrow_dw<WT>();
+    constexpr int CB = chunk_bytes<WT>();
+    // the activation tile; after the last chunk it holds the K-half partial sums
+    __shared__ __attribute__((aligned(16))) _Float16 As[MT * 32 * ALD];
+    __shared__ __attribute__((aligned(16))) float escale[MT * 32];
+    __shared__ __attribute__((aligned(16))) uint32_t Ws[4][32 * WDW];
+    static_assert(MT * 32 * ALD * 2 >= 4 * MT * 1024 * 4, "partial-sum exchange must fit the activation tile");
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tile = wave & 3, kh = wave >> 2;   // 32-row tile, half of the chunk's K steps
+    const int rg = blockIdx.x % RG, sp = blockIdx.x / RG;
+    const int n0 = rg * FROWS + 32 * tile;
+    const int col = lane & 31, h = lane >> 5;
+    const int nchunks = (K + CHUNK - 1) / CHUNK;
+    const int c0 = sp * cps, c1 = min(nchunks, c0 + cps);
+
+    // this lane's weight row (for its pieces) and its byte shift in LDS
+    const uint8_t* my_row = W + int64_t(min(n0 + col, N - 1)) * w_stride;
+
+    floatx16 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+
+    for (int c = c0; c < c1; ++c) {
+        const int kc = c * CHUNK;
+        const int steps = min(8, (K - kc) / 32);
+        const int cb = WT == T_Q8_0 ? 34 * steps : CB;
+        const int64_t off = int64_t(c) * CB;
+
+        // 1. packed weight bytes: each wave copies 16 rows of its tile with
+        //    coalesced dword loads (two rows per pass), and the first
+        //    activation rows are issued before any wait
+        constexpr int DPR = (CB + 2 + 3) / 4;   // dwords a row can span
+        constexpr int RI = (DPR + 31) / 32;
+        uint32_t wreg[8][RI];
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const int r = 16 * kh + 2 * p + h;
+            const uintptr_t g = reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + r, N - 1)) * w_stride + off);
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(g & ~uintptr_t(3));
+            const int ndw = int(((g & 3) + cb + 3) >> 2);
+#pragma unroll
+            for (int q = 0; q < RI; ++q) {
+                const int d = col + 32 * q;
+                wreg[p][q] = d < ndw ? src[d] : 0u;
+            }
+        }
+        auto load_x = [&](int pass) -> floatx8 {
+            const int r = pass * 16 + wave * 2 + h;
+            const int k = kc + 8 * col;
+            floatx8 v{0, 0, 0, 0, 0, 0, 0, 0};
+            if (r < M && k < K) {
+                const float* xr = X + int64_t(r) * ldx + k;
+                if (XVEC) {
+                    const floatx4 lo = load4f(xr), hi = load4f(xr + 4);
+                    v = floatx8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[i] = xr[i];
+                }
+            }
+            return v;
+        };
+        floatx8 xv[2 * MT];
+#pragma unroll
+        for (int p = 0; p < 2 * MT; ++p) xv[p] = load_x(p);
+#pragma unroll
+        for (int p = 0; p < 8; ++p)
+#pragma unroll
+            for (int q = 0; q < RI; ++q) {
+                const int d = col + 32 * q;
+                if (d < WDW) Ws[tile][(16 * kh + 2 * p + h) * WDW + d] = wreg[p][q];
+            }
+
+        // 2. activation chunk -> fp16 operand (two rows per wave per pass)
+#pragma unroll
+        for (int p = 0; p < 2 * MT; ++p) {
+            const int r = p * 16 + wave * 2 + h;
+            float rmax = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) rmax = fmaxf(rmax, fabsf(xv[p][i]));
+            rmax = max32_lanes(rmax);
+            const int e = row_exponent(rmax);
+            const half8 o = quant8<MODE, X86>(xv[p], lane, exp2i(-e));
+            *reinterpret_cast<half8*>(&As[r * ALD + 8 * col]) = o;
+            if (col == 0) escale[r] = exp2i(e);
+        }
+        __syncthreads();
+
+        // 3. products of this wave's K steps of the chunk
+        floatx16 cacc[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) cacc[t][r] = 0.f;
+        const LdsRow wrow{&Ws[tile][col * WDW], int((reinterpret_cast<uintptr_t>(my_row) + uintptr_t(off)) & 3)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int s = 4 * kh + i;
+            if (s >= steps) break;
+            WeightPiece<WT> wp;
+            wp.load(wrow, s, h);
+            _Float16 wv[16];
+            wp.dequant(s, h, wv);
+            const half8 b_lo{wv[0], wv[1], wv[2], wv[3], wv[4], wv[5], wv[6], wv[7]};
+            const half8 b_hi{wv[8], wv[9], wv[10], wv[11], wv[12], wv[13], wv[14], wv[15]};
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const half8* ap = reinterpret_cast<const half8*>(&As[(t * 32 + col) * ALD + 32 * s + 16 * h]);
+                cacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ap[0], b_lo, cacc[t], 0, 0, 0);
+                cacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ap[1], b_hi, cacc[t], 0, 0, 0);
+            }
+        }
+        // accumulator element r of tile t is activation row t*32 + 8*(r/4) + 4*h + r%4
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const floatx4 sc = *reinterpret_cast<const floatx4*>(&escale[t * 32 + 8 * q + 4 * h]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][4 * q + i] += cacc[t][4 * q + i] * sc[i];
+            }
+        __syncthreads();
+    }
+
+    // the second K half hands its sums to the first through LDS
+    float* xch = reinterpret_cast<float*>(As);
+    if (kh == 1) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) xch[((tile * MT + t) * 16 + r) * 64 + lane] = acc[t][r];
+    }
+    __syncthreads();
+    if (kh == 1) return;
+
+    // S == 1: the product; otherwise this split's partial sums
+    const int n = n0 + col;
+    float* out = part ? part + int64_t(sp) * M * N : Y;
+    const int64_t ld = part ? int64_t(N) : ldy;
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = t * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            const float v = acc[t][r] + xch[((tile * MT + t) * 16 + r) * 64 + lane];
+            if (m < M && n < N) out[int64_t(m) * ld + n] = v;
+        }
+}
+
+// Y[m][n] = sum over q = 0 .. S-1 of part[q][m][n], in that order.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, float* __restrict__ Y,
+                                                            int64_t ldy, int M, int N, int S) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= int64_t(M) * N) return;
+    const int m = int(i / N), n = int(i % N);
+    const int64_t plane = int64_t(M) * N;
+    float v = 0.f;
+    int q = 0;
+    for (; q + 8 <= S; q += 8) {   // eight independent loads in flight, added in split order
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = part[(q + j) * plane + i];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v += t[j];
+    }
+    for (; q < S; ++q) v += part[q * plane + i];
+    Y[int64_t(m) * ldy + n] = v;
+}
+
+template <int WT, int MODE, bool X86, int MT>
+void launch_fused_mt(const float* x, int64_t ldx, bool xvec, const uint8_t* w, int64_t w_stride, float* y,
+                     int64_t ldy, float* part, int M, int N, int K, int RG, int S, int cps, int x86,
+                     hipStream_t stream) {
+    const dim3 grid(unsigned(RG * S)), block(512);
+    if (xvec)
+        hipLaunchKernelGGL((fused_skinny_kernel<WT, MODE, X86, MT, true>), grid, block, 0, stream, x, ldx, w, w_stride,
+                           y, ldy, part, M, N, K, RG, cps);
+    else
+        hipLaunchKernelGGL((fused_skinny_kernel<WT, MODE, X86, MT, false>), grid, block, 0, stream, x, ldx, w, w_stride,
+                           y, ldy, part, M, N, K, RG, cps);
+}
+
+template <int WT, int MODE, bool X86>
+void launch_fused_mode(const float* x, int64_t ldx, bool xvec, const uint8_t* w, int64_t w_stride, float* y,
+                       int64_t ldy, float* part, int M, int N, int K, int RG, int S, int cps, int x86,
+                       hipStream_t stream) {
+    switch ((M + 31) / 32) {
+        case 1: launch_fused_mt<WT, MODE, X86, 1>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, x86, stream); break;
+        case 2: launch_fused_mt<WT, MODE, X86, 2>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, x86, stream); break;
+        case 3: launch_fused_mt<WT, MODE, X86, 3>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, x86, stream); break;
+        default: launch_fused_mt<WT, MODE, X86, 4>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, x86, stream); break;
+    }
+}
+
+template <int WT>
+void launch_fused_wt(bool f16, const float* x, int64_t ldx, bool xvec, const uint8_t* w, int64_t w_stride, float* y,
+                     int64_t ldy, float* part, int M, int N, int K, int RG, int S, int cps, int x86,
+                     hipStream_t stream) {
+    constexpr int Q = WT == T_Q8_0 ? T_Q8_0 : T_Q8_K;
+    if (f16)
+        launch_fused_mode<WT, T_F16, false>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, x86, stream);
+    else if (Q == T_Q8_0 && x86)
+        launch_fused_mode<WT, Q, true>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, x86, stream);
+    else
+        launch_fused_mode<WT, Q, false>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, x86, stream);
+}
+
+}  // namespace
+
+const char* skinny_variant(int wtype, int M, int N) {
+    const bool wide = (N + ROWS - 1) / ROWS < 256;
+    static const char* names[4][2] = {
+        {"skinny_f16mfma_q8_0", "skinny_f16mfma_q8_0_wide"},
+        {"skinny_f16mfma_q4_k", "skinny_f16mfma_q4_k_wide"},
+        {"skinny_f16mfma_q5_k", "skinny_f16mfma_q5_k_wide"},
+        {"skinny_f16mfma_q6_k", "skinny_f16mfma_q6_k_wide"},
+    };
+    (void)M;
+    switch (wtype) {
+        case T_Q8_0: return names[0][wide];
+        case T_Q4_K: return names[1][wide];
+        case T_Q5_K: return names[2][wide];
+        case T_Q6_K: return names[3][wide];
+        default: return nullptr;
+    }
+}
+
+const char* launch_skinny(int wtype, const _Float16* a, int64_t lda, const float* row_scale, const void* w,
+                          int64_t w_stride, float* y, int64_t ldy, int M, int N, int K, hipStream_t stream) {
+    if (M < 1 || M > kSkinnyMaxM || N < 1 || K < 32 || K % 32) return nullptr;
+    const bool wide = (N + ROWS - 1) / ROWS < 256;
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    switch (wtype) {
+        case T_Q8_0: launch_wt<T_Q8_0>(a, lda, row_scale, wb, w_stride, y, ldy, M, N, K, wide, stream); break;
+        case T_Q4_K: launch_wt<T_Q4_K>(a, lda, row_scale, wb, w_stride, y, ldy, M, N, K, wide, stream); break;
+        case T_Q5_K: launch_wt<T_Q5_K>(a, lda, row_scale, wb, w_stride, y, ldy, M, N, K, wide, stream); break;
+        case T_Q6_K: launch_wt<T_Q6_K>(a, lda, row_scale, wb, w_stride, y, ldy, M, N, K, wide, stream); break;
+        default: return nullptr;
+    }
+    return skinny_variant(wtype, M, N);
+}
+
+}  // namespace samhip
+
+namespace samhip {
+
+FusedPlan fused_skinny_plan(int M, int N, int K, int max_splits) {
+    FusedPlan p{};
+    p.rg = (N + FROWS - 1) / FROWS;
+    const int nchunks = (K + CHUNK - 1) / CHUNK;
+    const int S = std::min(std::min(nchunks, std::max(1, max_splits)), std::max(1, (256 + p.rg - 1) / p.rg));
+    p.cps = (nchunks + S - 1) / S;
+    p.splits = (nchunks + p.cps - 1) / p.cps;
+    p.part_bytes = p.splits > 1 ? size_t(p.splits) * size_t(M) * size_t(N) * 4 : 0;
+    return p;
+}
+
+const char* fused_skinny_variant(int wtype) {
+    switch (wtype) {
+        case T_Q8_0: return "skinny_fused_q8_0";
+        case T_Q4_K: return "skinny_fused_q4_k";
+        case T_Q5_K: return "skinny_fused_q5_k";
+        case T_Q6_K: return "skinny_fused_q6_k";
+        default: return nullptr;
+    }
+}
+
+const char* launch_fused_skinny(int wtype, bool f16, const float* x, int64_t ldx, const void* w, int64_t w_stride,
+                                float* y, int64_t ldy, float* part, int M, int N, int K, int x86, int max_splits,
+                                hipStream_t stream) {
+    if (M < 1 || M > kFusedMaxM || N < 1 || K < 32 || K % 32) return nullptr;
+    const FusedPlan p = fused_skinny_plan(M, N, K, max_splits);
+    const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    switch (wtype) {
+        case T_Q8_0: launch_fused_wt<T_Q8_0>(f16, x, ldx, xvec, wb, w_stride, y, ldy, p.splits > 1 ? part : nullptr, M, N, K, p.rg, p.splits, p.cps, x86, stream); break;
+        case T_Q4_K: launch_fused_wt<T_Q4_K>(f16, x, ldx, xvec, wb, w_stride, y, ldy, p.splits > 1 ? part : nullptr, M, N, K, p.rg, p.splits, p.cps, x86, stream); break;
+        case T_Q5_K: launch_fused_wt<T_Q5_K>(f16, x, ldx, xvec, wb, w_stride, y, ldy, p.splits > 1 ? part : nullptr, M, N, K, p.rg, p.splits, p.cps, x86, stream); break;
+        case T_Q6_K: launch_fused_wt<T_Q6_K>(f16, x, ldx, xvec, wb, w_stride, y, ldy, p.splits > 1 ? part : nullptr, M, N, K, p.rg, p.splits, p.cps, x86, stream); break;
+        default: return nullptr;
+    }
+    if (p.splits > 1) {
+        const int64_t outs = int64_t(M) * N;
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(unsigned((outs + 255) / 256)), dim3(256), 0, stream, part, y, ldy,
+                           M, N, p.splits);
+    }
+    return fused_skinny_variant(wtype);
+}
+
+}  // namespace samhip

@@ -72,6 +72,10 @@ SIGNATURES = {
     "samhip_last_error": ([ctypes.c_char_p, _SZ], _SZ),
     "samhip_trace_begin": ([_P, ctypes.c_char_p], _I),
     "samhip_trace_end": ([_P, ctypes.POINTER(KernelRecord), _SZ, ctypes.POINTER(_SZ)], _I),
+    "samhip_capture_begin": ([_P], _I),
+    "samhip_capture_end": ([_P, ctypes.POINTER(_P)], _I),
+    "samhip_graph_launch": ([_P, _P], _I),
+    "samhip_graph_destroy": ([_P], None),
 }
 
 _lib = None
@@ -167,6 +171,21 @@ class Buffer:
             pass
 
 
+class Graph:
+    """A captured sequence of calls (samhip_capture_begin / _end)."""
+
+    def __init__(self, ctx, handle):
+        self.ctx, self.handle = ctx, handle
+
+    def launch(self):
+        check(lib().samhip_graph_launch(self.ctx.handle, self.handle))
+
+    def destroy(self):
+        if self.handle:
+            lib().samhip_graph_destroy(self.handle)
+            self.handle = None
+
+
 class Context:
     def __init__(self, device=0, compute=COMPUTE_Q8_NATIVE, q8_rounding=ROUND_X86):
         o = Options(ABI_VERSION, device, compute, q8_rounding)
@@ -236,6 +255,15 @@ class Context:
         count = ctypes.c_size_t(0)
         check(lib().samhip_trace_end(self.handle, recs, capacity, ctypes.byref(count)))
         return [(r.kernel.decode(), r.weight_type, r.m, r.n, r.k, r.ms) for r in recs[:min(count.value, capacity)]]
+
+    def capture_begin(self):
+        check(lib().samhip_capture_begin(self.handle))
+
+    def capture_end(self):
+        """Ends the open capture; returns a Graph replayable on this context."""
+        g = ctypes.c_void_p()
+        check(lib().samhip_capture_end(self.handle, ctypes.byref(g)))
+        return Graph(self, g.value)
 
     # -- numpy conveniences used by the tests ------------------------------
     def quantize(self, qtype, x, q8_rounding=ROUND_X86):

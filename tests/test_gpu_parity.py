@@ -253,6 +253,71 @@ def test_mul_mat_tall_path_tails(gpu_ctx, f16_ctx, oracle, qtype):
         _check_product(oracle, qtype, w[off:off + 131], x, yn, yf)
 
 
+SKINNY_CASES = [(1, 96, 256), (32, 257, 1024), (33, 300, 512), (64, 64, 256), (65, 33, 256), (201, 256, 512),
+                (255, 70, 256), (32, 4096, 1024), (201, 2048, 256)]
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+@pytest.mark.parametrize("shape", SKINNY_CASES, ids=lambda s: "m%d_n%d_k%d" % s)
+def test_mul_mat_skinny_shapes(gpu_ctx, f16_ctx, oracle, samhip, qtype, shape):
+    """M < 256 takes the register-decode skinny kernel: the text encoder's
+    M = 32, text K/V M = 33, decoder queries M = 201 and the M / N tails
+    around them, with a strided activation on every other case."""
+    m, n, k = shape
+    if qtype != 8 and k % 256:
+        pytest.skip("K-quant rows need K % 256 == 0")
+    say("case mul_mat skinny", qtype, shape)
+    rng = np.random.default_rng(31 + m + n)
+    w = oracle.quantize(qtype, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    stride = k + 32 if (m + n) % 2 else None
+    before = gpu_ctx.query().skinny_launches
+    yn = gpu_ctx.matmul(qtype, w, x, x_row_stride=stride)
+    info = gpu_ctx.query()
+    assert info.skinny_launches == before + 1 and info.kernel_variant.startswith(b"skinny")
+    yf = f16_ctx.matmul(qtype, w, x, x_row_stride=stride)
+    _check_product(oracle, qtype, w, x, yn, yf)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_mul_mat_fused_split_k_deterministic(gpu_ctx, f16_ctx, oracle, samhip, qtype):
+    """Few weight rows and a long K: the fused kernel splits K over 16
+    workgroups whose partials meet through the arrival counters; repeated
+    calls (counters reset by the last workgroup) give identical bits, and a
+    row-offset view with a strided activation is covered."""
+    say("case fused split-K", qtype)
+    rng = np.random.default_rng(43)
+    k, n, m = 4096, 96, 40
+    w = oracle.quantize(qtype, (rng.standard_normal((2 * n, k)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    first = gpu_ctx.matmul(qtype, w, x, w_row_offset=n, w_rows=n, x_row_stride=k + 4)
+    assert gpu_ctx.query().kernel_variant.startswith(b"skinny_fused")
+    for _ in range(2):
+        again = gpu_ctx.matmul(qtype, w, x, w_row_offset=n, w_rows=n, x_row_stride=k + 4)
+        assert np.array_equal(first, again)
+    yf = f16_ctx.matmul(qtype, w, x, w_row_offset=n, w_rows=n)
+    _check_product(oracle, qtype, w[n:], x, first, yf)
+
+
+@pytest.mark.parametrize("qtype", [8, 12])
+def test_mul_mat_skinny_unfused_path(samhip, oracle, monkeypatch, qtype):
+    """SAMHIP_FUSED_SKINNY=0 routes M <= 128 through activation staging and
+    the register-decode skinny kernel; both paths agree with the oracle."""
+    say("case skinny unfused", qtype)
+    monkeypatch.setenv("SAMHIP_FUSED_SKINNY", "0")
+    ctx = samhip.Context(0)
+    try:
+        rng = np.random.default_rng(44)
+        for m, n, k in ((32, 257, 1024), (7, 64, 512)):
+            w = oracle.quantize(qtype, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            y = ctx.matmul(qtype, w, x)
+            assert ctx.query().kernel_variant.startswith(b"skinny_f16mfma")
+            assert max_row_rel_l2(y, oracle.mul_mat_native(qtype, w, x)) <= ROW_REL_L2
+    finally:
+        ctx.close()
+
+
 def test_mul_mat_every_gemm_tile_config(samhip, oracle, monkeypatch):
     """Each fp16 GEMM tile configuration gives the same product (bit-exact:
     same operands and the same per-tile K order)."""
@@ -307,9 +372,11 @@ def test_mul_mat_vit_shapes_sampled_rows(gpu_ctx, f16_ctx, oracle, samhip, name,
     r2 = max_row_rel_l2(yf[rows], oracle.mul_mat_decode(qtype, w, x[rows]))
     say("  row rel L2 native", r1, "f16", r2)
     assert r1 <= ROW_REL_L2 and r2 <= ROW_REL_L2
-    # size-independent property: linearity in X
-    y2 = f16_ctx.matmul(qtype, w, (2.0 * x[:64]).astype(np.float32))
-    assert np.array_equal(y2, 2.0 * yf[:64])
+    # size-independent property: linearity in X (exact for a power of two;
+    # 300 rows stay on the same tall kernel, whose per-element K order does
+    # not depend on M)
+    y2 = f16_ctx.matmul(qtype, w, (2.0 * x[:300]).astype(np.float32))
+    assert np.array_equal(y2, 2.0 * yf[:300])
 
 
 def test_exec_info_counts(gpu_ctx, samhip):
@@ -317,3 +384,61 @@ def test_exec_info_counts(gpu_ctx, samhip):
     assert info.version == 1 and info.mul_mat_calls > 0 and info.gemm_launches > 0
     assert b"gfx950" in info.device_name
     assert info.arithmetic_profile == b"samhip-q8-native-f16mfma-v1"
+
+
+def test_capture_replays_match_eager(samhip, oracle):
+    """A captured skinny + tall pair replays bit-identically to the eager
+    calls, three times, with eager work and synchronizations in between."""
+    say("case capture replay")
+    ctx = samhip.Context(0)
+    try:
+        rng = np.random.default_rng(41)
+        k, n = 1024, 300
+        w = ctx.upload(oracle.quantize(12, (rng.standard_normal((n, k)) * 0.02).astype(np.float32)))
+        xs = [rng.standard_normal((m, k)).astype(np.float32) for m in (32, 300)]
+        xb = [ctx.upload(x) for x in xs]
+        yb = [ctx.alloc(x.shape[0] * n * 4) for x in xs]
+        wt = samhip.tensor(12, k, n, w.ptr)
+        xt = [samhip.tensor(samhip.F32, k, x.shape[0], b.ptr) for x, b in zip(xs, xb)]
+        yt = [samhip.tensor(samhip.F32, n, x.shape[0], b.ptr) for x, b in zip(xs, yb)]
+        for i in range(2):
+            ctx.mul_mat(wt, xt[i], yt[i])
+        eager = [ctx.download(yb[i], (xs[i].shape[0], n), np.float32) for i in range(2)]
+        ctx.capture_begin()
+        with pytest.raises(samhip.InvalidArgument, match="capture"):
+            ctx.download(yb[0], (32, n), np.float32)
+        for i in range(2):
+            ctx.mul_mat(wt, xt[i], yt[i])
+        g = ctx.capture_end()
+        try:
+            other = ctx.alloc(32 * n * 4)
+            for rep in range(3):
+                for i in range(2):
+                    ctx.write(yb[i], np.zeros((xs[i].shape[0], n), np.float32))
+                ctx.mul_mat(wt, xt[0], samhip.tensor(samhip.F32, n, 32, other.ptr))
+                ctx.synchronize()
+                g.launch()
+                ctx.synchronize()
+                for i in range(2):
+                    got = ctx.download(yb[i], (xs[i].shape[0], n), np.float32)
+                    assert np.array_equal(got, eager[i]), (rep, i)
+        finally:
+            g.destroy()
+    finally:
+        ctx.close()
+
+
+def test_capture_needs_reserved_staging(samhip, oracle):
+    say("case capture staging")
+    ctx = samhip.Context(0)
+    try:
+        k, n, m = 256, 64, 40
+        w = ctx.upload(oracle.quantize(8, np.ones((n, k), np.float32)))
+        x, y = ctx.upload(np.ones((m, k), np.float32)), ctx.alloc(m * n * 4)
+        ctx.capture_begin()
+        with pytest.raises(samhip.InvalidArgument, match="run it once before capturing"):
+            ctx.mul_mat(samhip.tensor(8, k, n, w.ptr), samhip.tensor(samhip.F32, k, m, x.ptr),
+                        samhip.tensor(samhip.F32, n, m, y.ptr))
+        ctx.capture_end().destroy()
+    finally:
+        ctx.close()
