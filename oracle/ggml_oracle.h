@@ -9,7 +9,7 @@
  *
  * Pinning status of each function (what checks it besides its own formula):
  *   fp16 <-> fp32        : numpy float16 conversion over all 65536 halves and
- *                          random/edge floats (tests/test_oracle_formats.py).
+ *                          random/edge floats (tests/test_oracle.py).
  *   q8_0 quantize (ref)  : known-answer vector of
  *                          tests/tools/test_cache_quantization.py:26-43.
  *   q8_0 quantize (x86)  : known-answer vector of
