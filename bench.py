@@ -33,6 +33,8 @@ PEAK_HBM_GBPS = 8000.0
 PROFILE_COMMANDS = {
     "trace": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/trace -o bench -- "
              "python3 bench.py --steps 20 --warmup 5 --no-cpu-baseline",
+    "text": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/text -o bench -- "
+            "python3 bench.py --workload text --steps 10 --warmup 2",
     "fetch": "rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/fetch -o bench -- "
              "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline",
     "write": "rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/write -o bench -- "
@@ -140,9 +142,11 @@ def summarize_profiles(d, commands):
             n = int(m.group(1))
             base = name[m.end():m.end() + n]
             rest = name[m.end() + n:]
-            args = re.match(r"I((?:Li-?\d+E)+)E", rest)
+            args = re.match(r"I((?:L[ib]-?\d+E)+)E", rest)
             if args:
-                base += "<" + ", ".join(re.findall(r"Li(-?\d+)E", args.group(1))) + ">"
+                vals = [("true" if v == "1" else "false") if t == "b" else v
+                        for t, v in re.findall(r"L([ib])(-?\d+)E", args.group(1))]
+                base += "<" + ", ".join(vals) + ">"
             return base
         name = name.replace("void ", "", 1).replace("samhip::(anonymous namespace)::", "")
         return name.split("(")[0]
@@ -175,16 +179,23 @@ def summarize_profiles(d, commands):
     with open(TRAFFIC_FILE, "w") as f:
         json.dump(table, f, indent=1)
 
-    stats = rows(os.path.join(d, "trace", "bench_kernel_stats.csv"))
-    lines = ["# Kernel time, SAM 3 ViT linear sweep at M=5184 (12 mul_mat per step)", "",
-             "Command (from the repository root, `cd /tmp && export TMPDIR=/tmp` first):", "",
-             "```", commands["trace"], "```", "",
-             "| kernel | calls | avg us | min us | max us | share % |", "|---|---|---|---|---|---|"]
-    for r in stats:
-        lines.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
-                     f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
-    with open(os.path.join(ROOT, "profiles", "kernel_stats_vit_sweep_m5184.md"), "w") as f:
-        f.write("\n".join(lines) + "\n")
+    def stats_table(sub, title, command, out_name):
+        path = os.path.join(d, sub, "bench_kernel_stats.csv")
+        if not os.path.exists(path):
+            return
+        lines = [f"# {title}", "", "Command (from the repository root, `cd /tmp && export TMPDIR=/tmp` first):", "",
+                 "```", command, "```", "",
+                 "| kernel | calls | avg us | min us | max us | share % |", "|---|---|---|---|---|---|"]
+        for r in rows(path):
+            lines.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                         f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
+        with open(os.path.join(ROOT, "profiles", out_name), "w") as f:
+            f.write("\n".join(lines) + "\n")
+
+    stats_table("trace", "Kernel time, SAM 3 ViT linear sweep at M=5184 (12 mul_mat per step)", commands["trace"],
+                "kernel_stats_vit_sweep_m5184.md")
+    stats_table("text", "Kernel time, SAM 3 text-encoder linear stream at M=32 (97 mul_mat per step, Q8_0)",
+                commands["text"], "kernel_stats_text_stream_m32_q8_0.md")
 
     lines = ["# HBM traffic per dispatch, SAM 3 ViT linear sweep at M=5184", "",
              "Commands (from the repository root, `cd /tmp && export TMPDIR=/tmp` first):", "", "```",
