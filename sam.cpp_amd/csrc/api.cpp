@@ -70,6 +70,7 @@ struct samhip_context {
     int* flag = nullptr;   // device error flag (get_rows id range)
     // tall-path selection: M at or above `tall_m` uses dequant + fp16 GEMM;
     // gemm_cfg >= 0 forces one fp16 GEMM tile configuration (SAMHIP_GEMM_CONFIG)
+    int cus = 256;             // compute units of the device
     int tall_m = 256;
     int gemm_cfg = -1;
     bool fused_skinny = true;   // SAMHIP_FUSED_SKINNY=0 routes M <= 128 through staging + the skinny kernel
@@ -175,6 +176,10 @@ int env_int(const char* name, int fallback) {
     return (end && *end == '\0') ? int(x) : fallback;
 }
 
+const char* prep_name(int mode) {
+    return mode == T_F16 ? "stage_dequant_f16" : mode == T_Q8_0 ? "stage_dequant_q8_0" : "stage_dequant_q8_k";
+}
+
 const char* stage_name(int mode) {
     return mode == T_F16 ? "stage_rows_f16" : mode == T_Q8_0 ? "stage_rows_q8_0" : "stage_rows_q8_k";
 }
@@ -252,6 +257,7 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
         return fail(SAMHIP_ERR_DEVICE, "HIP context initialization failed");
     }
     std::snprintf(ctx->info.device_name, sizeof(ctx->info.device_name), "%s (%s)", prop.name, prop.gcnArchName);
+    ctx->cus = std::max(1, prop.multiProcessorCount);
     ctx->stream = ctx->own_stream;
     // kernel-variant forcing for tuning runs (SAMHIP_* environment variables)
     ctx->tall_m = std::max(1, env_int("SAMHIP_TALL_M", ctx->tall_m));
@@ -380,27 +386,44 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     _Float16* wh = reinterpret_cast<_Float16*>(base + w_offset);
     const int mode = ctx->compute == SAMHIP_COMPUTE_F16 ? T_F16 : vec_dot_type(w->type);
     const bool aligned = reinterpret_cast<uintptr_t>(x->data) % 16 == 0 && x->nb[1] % 16 == 0;
-    int rc = traced(ctx, stage_name(mode), w->type, M, N, K, [&]() -> int {
-        launch_stage_rows(mode, aligned, static_cast<const float*>(x->data), int64_t(x->nb[1] / 4), M, K, a, K, rs,
-                          ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->stream);
-        HIP_TRY(hipGetLastError(), "activation staging launch");
-        return SAMHIP_OK;
-    });
-    if (rc) return rc;
+    const int x86 = ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0;
     const char* variant = gemm_variant(w->type);
     if (!variant) return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no kernel for weight type %d", w->type);
-    if (tall) {
-        rc = traced(ctx, dequant_name(w->type), w->type, M, N, K, [&]() -> int {
-            launch_dequant_w_f16(w->type, w->data, int64_t(w->nb[1]), N, K, wh, K, ctx->stream);
-            HIP_TRY(hipGetLastError(), "weight dequant launch");
+    int rc = SAMHIP_OK;
+    // activation staging and weight decode in one launch (aligned rows, K <= 5120)
+    bool prepared = false;
+    if (tall && aligned && K <= 5120) {
+        rc = traced(ctx, prep_name(mode), w->type, M, N, K, [&]() -> int {
+            prepared = launch_prep(mode, w->type, static_cast<const float*>(x->data), int64_t(x->nb[1] / 4), M, K, a,
+                                   K, rs, x86, w->data, int64_t(w->nb[1]), N, wh, K, ctx->stream);
+            HIP_TRY(hipGetLastError(), "staging and weight decode launch");
+            return prepared ? SAMHIP_OK : fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no staging kernel for this shape");
+        });
+        if (rc) return rc;
+    }
+    if (!prepared) {
+        rc = traced(ctx, stage_name(mode), w->type, M, N, K, [&]() -> int {
+            launch_stage_rows(mode, aligned, static_cast<const float*>(x->data), int64_t(x->nb[1] / 4), M, K, a, K,
+                              rs, x86, ctx->stream);
+            HIP_TRY(hipGetLastError(), "activation staging launch");
             return SAMHIP_OK;
         });
         if (rc) return rc;
+    }
+    if (tall) {
+        if (!prepared) {
+            rc = traced(ctx, dequant_name(w->type), w->type, M, N, K, [&]() -> int {
+                launch_dequant_w_f16(w->type, w->data, int64_t(w->nb[1]), N, K, wh, K, ctx->stream);
+                HIP_TRY(hipGetLastError(), "weight dequant launch");
+                return SAMHIP_OK;
+            });
+            if (rc) return rc;
+        }
         const int cfg = ctx->gemm_cfg >= 0 ? ctx->gemm_cfg : gemm_f16_pick(M, N, K);
         variant = gemm_f16_config_name(cfg);
         rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
             launch_gemm_f16(cfg, a, K, rs, wh, K, static_cast<float*>(y->data), int64_t(y->nb[1] / 4), M, N, K,
-                            ctx->stream);
+                            ctx->cus, ctx->stream);
             HIP_TRY(hipGetLastError(), "gemm launch");
             return SAMHIP_OK;
         });

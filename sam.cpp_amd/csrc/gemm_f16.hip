@@ -36,6 +36,46 @@ __device__ __forceinline__ void tile_order(int bid, int nblocks, int tiles_m, in
     tn = within / gm;
 }
 
+// Epilogue of a wave's (32*FM) x (32*FN) tile at (row0, col0): each 32-row
+// block goes through the wave's LDS slab (stride ES floats; accumulator
+// element r of lane l sits on row 8*(r/4) + 4*(l/32) + r%4) and leaves as
+// 16-byte row segments scaled by their row's 2^e.  (Staging the row scales
+// in LDS at kernel start measured up to 35 % slower on the long-K shapes.)
+template <int FM, int FN, int ES>
+__device__ __forceinline__ void store_tile(floatx16 (&acc)[FM][FN], const float* row_scale, float* slab, int lane,
+                                           int row0, int col0, int M, int N, float* Y, int64_t ldy) {
+    constexpr int TN = 32 * FN, C4 = TN / 4;
+    const bool vec_ok = (ldy % 4) == 0 && (reinterpret_cast<uintptr_t>(Y) % 16) == 0;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                slab[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ES + 32 * j + (lane & 31)] = acc[i][j][r];
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the slab is written
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int e = lane; e < 32 * C4; e += 64) {
+            const int rr = e / C4, c4 = e % C4;
+            const int m = row0 + i * 32 + rr;
+            const int n = col0 + 4 * c4;
+            if (m >= M) continue;
+            const float sc = row_scale[m];
+            const floatx4 raw = *reinterpret_cast<const floatx4*>(slab + rr * ES + 4 * c4);
+            const floatx4 v{raw[0] * sc, raw[1] * sc, raw[2] * sc, raw[3] * sc};
+            float* yp = Y + int64_t(m) * ldy + n;
+            if (vec_ok && n + 3 < N) {
+                *reinterpret_cast<floatx4*>(yp) = v;
+            } else {
+                for (int q = 0; q < 4; ++q)
+                    if (n + q < N) yp[q] = v[q];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
 template <int BM, int BN, int WM, int WN, int BK>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_f16_kernel(const _Float16* __restrict__ A, int64_t lda,
                                                                   const float* __restrict__ row_scale,
@@ -153,36 +193,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_f16_kernel(const _Float16* 
     // Epilogue, one 32-row slab of the wave tile at a time: the accumulator
     // (lane l: column l%32, rows 8*(r/4) + 4*(l/32) + r%4) goes to a
     // per-wave LDS slab, then each lane writes 4 consecutive floats of Y.
-    float* slab = reinterpret_cast<float*>(lds) + wave * 32 * ES;
-    const bool vec_ok = (ldy % 4) == 0 && (reinterpret_cast<uintptr_t>(Y) % 16) == 0;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                slab[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ES + 32 * j + (lane & 31)] = acc[i][j][r];
-        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the slab is written
-        __builtin_amdgcn_wave_barrier();
-        constexpr int C4 = TN / 4;               // float4 columns per slab row
-#pragma unroll
-        for (int e = lane; e < 32 * C4; e += 64) {
-            const int rr = e / C4, c4 = e % C4;
-            const int m = m0 + wm * TM + i * 32 + rr;
-            const int n = n0 + wn * TN + 4 * c4;
-            if (m >= M) continue;
-            const floatx4 v = *reinterpret_cast<const floatx4*>(slab + rr * ES + 4 * c4);
-            const float rs = row_scale[m];
-            float* yp = Y + int64_t(m) * ldy + n;
-            if (vec_ok && n + 3 < N) {
-                *reinterpret_cast<floatx4*>(yp) = floatx4{v[0] * rs, v[1] * rs, v[2] * rs, v[3] * rs};
-            } else {
-                for (int q = 0; q < 4; ++q)
-                    if (n + q < N) yp[q] = v[q] * rs;
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
-    }
+    store_tile<FM, FN, ES>(acc, row_scale, reinterpret_cast<float*>(lds) + wave * 32 * ES, lane, m0 + wm * TM, n0 + wn * TN, M, N,
+                           Y, ldy);
 }
 
 // ---------------------------------------------------------------------------
@@ -324,59 +336,222 @@ __global__ __launch_bounds__(256) void gemm_f16_dma_kernel(const _Float16* __res
     }
     __syncthreads();
 
-    float* slab = reinterpret_cast<float*>(lds) + wave * 32 * ES;
-    const bool vec_ok = (ldy % 4) == 0 && (reinterpret_cast<uintptr_t>(Y) % 16) == 0;
+    store_tile<FM, FN, ES>(acc, row_scale, reinterpret_cast<float*>(lds) + wave * 32 * ES, lane, m0 + wm * TM, n0 + wn * TN, M, N,
+                           Y, ldy);
+#endif
+}
+
+// ---------------------------------------------------------------------------
+// Pipelined variant of the LDS-DMA kernel: every wave holds two sets of MFMA
+// fragments, and the ds_reads of K substep kk+1 are interleaved with the
+// MFMAs of substep kk (pinned with sched_group_barrier), so the matrix cores
+// never wait on LDS latency inside a stage.  The stage hand-over (wait for
+// this wave's loads of the next stage, a bare s_barrier, the next ring slot's
+// loads and the first fragments of the next stage) sits between the two
+// halves of the last substep's MFMAs.  4 waves, each a (BM/2) x (BN/2) tile:
+// 256x128 gives 8 independent 32x32 accumulators per wave.
+// ---------------------------------------------------------------------------
+
+template <int BM, int BN, int BK, int STAGES>
+__global__ __launch_bounds__(256) void gemm_f16_pipe_kernel(const _Float16* __restrict__ A, int64_t lda,
+                                                            const float* __restrict__ row_scale,
+                                                            const _Float16* __restrict__ B, int64_t ldb,
+                                                            float* __restrict__ Y, int64_t ldy, int M, int N, int K,
+                                                            int tiles_m, int tiles_n) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    constexpr int WM = 2, WN = 2;
+    constexpr int CPR = BK / 8, RB = BK * 2;
+    constexpr int RPB = 64 / CPR;
+    constexpr int A_BLOCKS = BM / RPB, B_BLOCKS = BN / RPB;
+    constexpr int A_PER_WAVE = A_BLOCKS / 4, B_PER_WAVE = B_BLOCKS / 4;
+    constexpr int LOADS = A_PER_WAVE + B_PER_WAVE;
+    constexpr int STAGE_BYTES = (BM + BN) * RB;
+    constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+    constexpr int KK = BK / 16;
+    constexpr int NF = FM * FN;
+    constexpr int ES = TN + 8;
+    static_assert(A_PER_WAVE * 4 == A_BLOCKS && B_PER_WAVE * 4 == B_BLOCKS, "tile rows must split over 4 waves");
+    static_assert(STAGES >= 2 && STAGES <= 4, "ring depth");
+    static_assert(KK % 2 == 0, "fragment double buffer alternates per substep");
+    static_assert(4 * 32 * ES * 4 <= STAGES * STAGE_BYTES, "epilogue staging must fit in LDS");
+
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * STAGE_BYTES];
+
+    int tm, tn;
+    tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+
+    const uint32_t a_bytes = uint32_t(min(int64_t(M) * lda * 2, int64_t(0x7fffffff)));
+    const uint32_t b_bytes = uint32_t(min(int64_t(N) * ldb * 2, int64_t(0x7fffffff)));
+    const __amdgpu_buffer_rsrc_t ra_desc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A), 0, a_bytes, RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t rb_desc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(B), 0, b_bytes, RSRC_WORD3);
+
+    uint32_t a_off[A_PER_WAVE], b_off[B_PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < A_PER_WAVE; ++i) {
+        const int blk = wave * A_PER_WAVE + i, r = blk * RPB + lane / CPR, slot = lane % CPR;
+        const int kc = slot ^ swz<CPR>(r);
+        a_off[i] = m0 + r < M ? uint32_t((int64_t(m0 + r) * lda + 8 * kc) * 2) : a_bytes;
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER_WAVE; ++i) {
+        const int blk = wave * B_PER_WAVE + i, r = blk * RPB + lane / CPR, slot = lane % CPR;
+        const int kc = slot ^ swz<CPR>(r);
+        b_off[i] = n0 + r < N ? uint32_t((int64_t(n0 + r) * ldb + 8 * kc) * 2) : b_bytes;
+    }
+    auto issue = [&](int s) {
+        uint8_t* st = lds + (s % STAGES) * STAGE_BYTES;
+        const int koff = s * RB;
+#pragma unroll
+        for (int i = 0; i < A_PER_WAVE; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra_desc, (__attribute__((address_space(3))) void*)(st + (wave * A_PER_WAVE + i) * 1024), 16,
+                a_off[i], koff, 0, 0);
+#pragma unroll
+        for (int i = 0; i < B_PER_WAVE; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb_desc, (__attribute__((address_space(3))) void*)(st + BM * RB + (wave * B_PER_WAVE + i) * 1024),
+                16, b_off[i], koff, 0, 0);
+    };
+
+    // LDS byte offsets of this lane's fragment rows (stage 0, chunk 0); the
+    // swizzle only depends on the row, so a substep adds 32 bytes XOR-ed
+    const int frow = lane & 31, fhalf = lane >> 5;
+    int a_row[FM], b_row[FN], a_sw[FM], b_sw[FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
+        const int r = wm * TM + i * 32 + frow;
+        a_row[i] = r * RB;
+        a_sw[i] = swz<CPR>(r);
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int r = wn * TN + j * 32 + frow;
+        b_row[j] = BM * RB + r * RB;
+        b_sw[j] = swz<CPR>(r);
+    }
+    auto load_frags = [&](int s, int kk, half8* fa, half8* fb) {
+        const uint8_t* st = lds + (s % STAGES) * STAGE_BYTES;
+        const int kc = 2 * kk + fhalf;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) fa[i] = *reinterpret_cast<const half8*>(st + a_row[i] + 16 * (kc ^ a_sw[i]));
+#pragma unroll
+        for (int j = 0; j < FN; ++j) fb[j] = *reinterpret_cast<const half8*>(st + b_row[j] + 16 * (kc ^ b_sw[j]));
+    };
+
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                slab[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ES + 32 * j + (lane & 31)] = acc[i][j][r];
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        __builtin_amdgcn_wave_barrier();
-        constexpr int C4 = TN / 4;
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int nst = K / BK;
+    // hand-over into stage t: this wave's reads of stage t-1 are complete and
+    // its loads of stage t landed; after the barrier every wave's have, and
+    // the ring slot of stage t-1 is refilled with stage t+STAGES-1
+    auto enter = [&](int t) {
+        const int later = min(STAGES - 2, nst - 1 - t);
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+        if (later >= 2) wait_vmcnt<2 * LOADS>();
+        else if (later == 1) wait_vmcnt<LOADS>();
+        else wait_vmcnt<0>();
+        asm volatile("s_barrier" ::: "memory");
+        if (t + STAGES - 1 < nst) issue(t + STAGES - 1);
+    };
+
+    half8 fa[2][FM], fb[2][FN];
 #pragma unroll
-        for (int e = lane; e < 32 * C4; e += 64) {
-            const int rr = e / C4, c4 = e % C4;
-            const int m = m0 + wm * TM + i * 32 + rr;
-            const int n = n0 + wn * TN + 4 * c4;
-            if (m >= M) continue;
-            const floatx4 v = *reinterpret_cast<const floatx4*>(slab + rr * ES + 4 * c4);
-            const float rs = row_scale[m];
-            float* yp = Y + int64_t(m) * ldy + n;
-            if (vec_ok && n + 3 < N) {
-                *reinterpret_cast<floatx4*>(yp) = floatx4{v[0] * rs, v[1] * rs, v[2] * rs, v[3] * rs};
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < nst) issue(s);
+    enter(0);
+    load_frags(0, 0, fa[0], fb[0]);
+
+    for (int s = 0; s < nst; ++s) {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            const int cur = kk & 1;
+            if (kk + 1 < KK) {
+                load_frags(s, kk + 1, fa[cur ^ 1], fb[cur ^ 1]);
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
+                // one fragment read between consecutive MFMAs, then the rest
+#pragma unroll
+                for (int q = 0; q < FM + FN; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, NF - (FM + FN), 0);
             } else {
-                for (int q = 0; q < 4; ++q)
-                    if (n + q < N) yp[q] = v[q] * rs;
+                // first half of the last substep's products, the hand-over,
+                // then the second half while the next stage's fragments load
+#pragma unroll
+                for (int q = 0; q < NF / 2; ++q) {
+                    const int i = q / FN, j = q % FN;
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
+                }
+                if (s + 1 < nst) {
+                    enter(s + 1);
+                    load_frags(s + 1, 0, fa[0], fb[0]);
+                }
+#pragma unroll
+                for (int q = NF / 2; q < NF; ++q) {
+                    const int i = q / FN, j = q % FN;
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
+                }
             }
         }
-        __builtin_amdgcn_wave_barrier();
     }
+    __syncthreads();
+
+    store_tile<FM, FN, ES>(acc, row_scale, reinterpret_cast<float*>(lds) + wave * 32 * ES, lane, m0 + wm * TM, n0 + wn * TN, M, N,
+                           Y, ldy);
 #endif
+}
+
+// Dynamic LDS that keeps a second workgroup off a CU: when a grid has no
+// more tiles than CUs, two resident workgroups per CU would leave other CUs
+// idle (the dispatcher fills a CU before moving on).
+constexpr size_t spread_pad(size_t static_lds) { return static_lds > 82944 ? 0 : 82944 - static_lds; }
+
+template <int BM, int BN, int BK, int STAGES>
+void launch_pipe(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
+                 int64_t ldy, int M, int N, int K, bool spread, hipStream_t stream) {
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const size_t pad = spread ? spread_pad(size_t(STAGES) * (BM + BN) * BK * 2) : 0;
+    hipLaunchKernelGGL((gemm_f16_pipe_kernel<BM, BN, BK, STAGES>), dim3(unsigned(tiles_m * tiles_n)), dim3(256), pad,
+                       stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n);
 }
 
 template <int BM, int BN, int BK, int STAGES>
 void launch_dma(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
-                int64_t ldy, int M, int N, int K, hipStream_t stream) {
+                int64_t ldy, int M, int N, int K, bool spread, hipStream_t stream) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, STAGES>), dim3(unsigned(tiles_m * tiles_n)), dim3(256), 0,
+    const size_t pad = spread ? spread_pad(size_t(STAGES) * (BM + BN) * BK * 2) : 0;
+    hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, STAGES>), dim3(unsigned(tiles_m * tiles_n)), dim3(256), pad,
                        stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n);
 }
 
 template <int BM, int BN, int WM, int WN, int BK>
 void launch_cfg(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
-                int64_t ldy, int M, int N, int K, hipStream_t stream) {
+                int64_t ldy, int M, int N, int K, bool spread, hipStream_t stream) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const size_t pad = spread ? spread_pad(size_t(2) * (BM + BN) * (BK + 8) * 2) : 0;
     hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, WM, WN, BK>), dim3(unsigned(tiles_m * tiles_n)),
-                       dim3(WM * WN * 64), 0, stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n);
+                       dim3(WM * WN * 64), pad, stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n);
 }
 
 struct Cfg {
     const char* name;
     void (*launch)(const _Float16*, int64_t, const float*, const _Float16*, int64_t, float*, int64_t, int, int, int,
-                   hipStream_t);
+                   bool, hipStream_t);
     int bm, bn, bk;
 };
 
@@ -394,6 +569,12 @@ const Cfg kConfigs[] = {
     {"gemm_f16dma_128x128x32_s4", launch_dma<128, 128, 32, 4>, 128, 128, 32},
     {"gemm_f16dma_128x256x32_s3", launch_dma<128, 256, 32, 3>, 128, 256, 32},
     {"gemm_f16dma_256x256x32_s3", launch_dma<256, 256, 32, 3>, 256, 256, 32},
+    {"gemm_f16pipe_256x128x32_s3", launch_pipe<256, 128, 32, 3>, 256, 128, 32},
+    {"gemm_f16pipe_256x128x64_s2", launch_pipe<256, 128, 64, 2>, 256, 128, 64},
+    {"gemm_f16pipe_128x256x32_s3", launch_pipe<128, 256, 32, 3>, 128, 256, 32},
+    {"gemm_f16pipe_256x256x32_s3", launch_pipe<256, 256, 32, 3>, 256, 256, 32},
+    {"gemm_f16pipe_128x128x32_s4", launch_pipe<128, 128, 32, 4>, 128, 128, 32},
+    {"gemm_f16pipe_256x128x32_s4", launch_pipe<256, 128, 32, 4>, 256, 128, 32},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -410,23 +591,25 @@ bool gemm_f16_supported(int M, int N, int K, int64_t lda, int64_t ldb) {
     return K % 128 == 0 && int64_t(M) * lda * 2 < 0x7fffffff && int64_t(N) * ldb * 2 < 0x7fffffff;
 }
 
-// Tile choice from a measured sweep of every configuration on the SAM 3
-// linear shapes at M = 5184 tokens on MI355X (kernel time, HIP events):
-//   N % 256 == 0, N >= 2048 (qkv 3072)   -> 128x256 LDS-DMA ring  (652 TFLOP/s)
-//   N <= 1024, K >= 2048 (fc2 4736->1024) -> 192x128 register-staged (597)
-//   N <= 1024 (proj, fusion/decoder 256..1024) -> 128x128x32 LDS-DMA, 4 stages (387)
-//   otherwise (fc1 1024->4736)            -> 128x128x64 register-staged (626)
+// Tile choice from a measured sweep of the configurations on the SAM 3 linear
+// shapes at M = 5184 tokens on MI355X (kernel time, HIP events, random
+// operands; differences below ~3 % are within run-to-run noise):
+//   N % 256 == 0, N >= 2048 (qkv 3072)    -> pipelined 256x128x32, 3 stages (652 TFLOP/s)
+//   N <= 1024, K >= 2048 (fc2 4736->1024)  -> pipelined 256x128x64, 2 stages (615)
+//   otherwise (proj 1024, fc1 4736, fusion/decoder widths)
+//                                          -> pipelined 128x128x32, 4 stages (406 proj, 658 fc1)
 int gemm_f16_pick(int /*M*/, int N, int K) {
-    if (N % 256 == 0 && N >= 2048) return 11;
-    if (N <= 1024 && K >= 2048) return 5;
-    if (N <= 1024) return 10;
-    return 0;
+    if (N % 256 == 0 && N >= 2048) return 13;
+    if (N <= 1024 && K >= 2048) return 14;
+    return 17;
 }
 
 const char* launch_gemm_f16(int cfg, const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
-                            int64_t ldb, float* y, int64_t ldy, int M, int N, int K, hipStream_t stream) {
+                            int64_t ldb, float* y, int64_t ldy, int M, int N, int K, int cus, hipStream_t stream) {
     if (cfg < 0 || cfg >= kNumConfigs || K % kConfigs[cfg].bk) cfg = gemm_f16_pick(M, N, K);
-    kConfigs[cfg].launch(a, lda, row_scale, b, ldb, y, ldy, M, N, K, stream);
+    const Cfg& c = kConfigs[cfg];
+    const int64_t tiles = int64_t((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+    c.launch(a, lda, row_scale, b, ldb, y, ldy, M, N, K, tiles <= cus, stream);
     return kConfigs[cfg].name;
 }
 

@@ -32,8 +32,16 @@ int gemm_f16_config_count();
 bool gemm_f16_supported(int M, int N, int K, int64_t lda, int64_t ldb);
 const char* gemm_f16_config_name(int cfg);
 int gemm_f16_pick(int M, int N, int K);
+// `cus`: compute units of the device; grids with at most that many tiles run
+// one workgroup per CU.
 const char* launch_gemm_f16(int cfg, const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
-                            int64_t ldb, float* y, int64_t ldy, int M, int N, int K, hipStream_t stream);
+                            int64_t ldb, float* y, int64_t ldy, int M, int N, int K, int cus, hipStream_t stream);
+
+// Activation staging and weight decode of a tall product in one launch
+// (16-byte aligned activation rows, K <= 5120); false when not applicable.
+bool launch_prep(int mode, int wtype, const float* x, int64_t x_stride, int M, int K, _Float16* a, int64_t lda,
+                 float* row_scale, int x86, const void* w, int64_t w_stride, int N, _Float16* wout, int64_t ldo,
+                 hipStream_t stream);
 
 // Kernel variant name for a weight type, or nullptr when unsupported.
 const char* gemm_variant(int wtype);

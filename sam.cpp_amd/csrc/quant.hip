@@ -23,12 +23,9 @@ namespace {
 // so X is read once; every cross-lane reduction runs with all lanes active
 // (lanes past K hold zeros).
 template <int MODE, int CH, bool X86>
-__global__ __launch_bounds__(256) void stage8_kernel(const float* __restrict__ x, int64_t x_stride, int M, int K,
-                                                     _Float16* __restrict__ a, int64_t lda,
-                                                     float* __restrict__ row_scale) {
-    const int lane = threadIdx.x & 63;
-    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (m >= M) return;
+__device__ __forceinline__ void stage8_row(const float* __restrict__ x, int64_t x_stride, int m, int K,
+                                           _Float16* __restrict__ a, int64_t lda, float* __restrict__ row_scale,
+                                           int lane) {
     const float* xr = x + int64_t(m) * x_stride;
     floatx8 v[CH];
     float rmax = 0.f;
@@ -56,6 +53,49 @@ __global__ __launch_bounds__(256) void stage8_kernel(const float* __restrict__ x
         const half8 o = quant8<MODE, X86>(v[c], lane, down);
         if (k < K) *reinterpret_cast<half8*>(ar + k) = o;
     }
+}
+
+template <int MODE, int CH, bool X86>
+__global__ __launch_bounds__(256) void stage8_kernel(const float* __restrict__ x, int64_t x_stride, int M, int K,
+                                                     _Float16* __restrict__ a, int64_t lda,
+                                                     float* __restrict__ row_scale) {
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= M) return;
+    stage8_row<MODE, CH, X86>(x, x_stride, m, K, a, lda, row_scale, threadIdx.x & 63);
+}
+
+// thread t: half (t & 1) of 32-value step of one weight row -> 16 fp16 values
+template <int WT>
+__device__ __forceinline__ void dequant_piece(const uint8_t* __restrict__ W, int64_t w_stride, int K, int64_t t,
+                                              _Float16* __restrict__ out, int64_t ldo) {
+    const int steps = K / 32;
+    const int h = int(t & 1);
+    const int64_t rs = t >> 1;
+    const int row = int(rs / steps), step = int(rs % steps);
+    WeightPiece<WT> piece;
+    piece.load(W + int64_t(row) * w_stride, step, h);
+    _Float16 v[16];
+    piece.dequant(step, h, v);
+    half8* o = reinterpret_cast<half8*>(out + int64_t(row) * ldo + 32 * step + 16 * h);
+    o[0] = half8{v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
+    o[1] = half8{v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]};
+}
+
+// Both per-call preparations of a tall product in one launch: workgroups
+// [0, stage_blocks) pack four activation rows each, the rest decode 256
+// weight pieces each (the two roles touch disjoint memory).
+template <int MODE, int CH, bool X86, int WT>
+__global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ x, int64_t x_stride, int M, int K,
+                                                   _Float16* __restrict__ a, int64_t lda, float* __restrict__ row_scale,
+                                                   int stage_blocks, const uint8_t* __restrict__ W, int64_t w_stride,
+                                                   int N, _Float16* __restrict__ wout, int64_t ldo) {
+    if (int(blockIdx.x) < stage_blocks) {
+        const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+        if (m < M) stage8_row<MODE, CH, X86>(x, x_stride, m, K, a, lda, row_scale, threadIdx.x & 63);
+        return;
+    }
+    const int64_t t = int64_t(blockIdx.x - stage_blocks) * 256 + threadIdx.x;
+    if (t < int64_t(N) * (K / 32) * 2) dequant_piece<WT>(W, w_stride, K, t, wout, ldo);
 }
 
 // Q8_0 block: amax over 8 lanes x 4 values; returns fp16 d bits and codes.
@@ -146,19 +186,9 @@ __global__ __launch_bounds__(256) void stage_rows_kernel(const float* __restrict
 template <int WT>
 __global__ __launch_bounds__(256) void dequant_w_f16_kernel(const uint8_t* __restrict__ W, int64_t w_stride, int N,
                                                             int K, _Float16* __restrict__ out, int64_t ldo) {
-    const int steps = K / 32;
     const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (t >= int64_t(N) * steps * 2) return;
-    const int h = int(t & 1);
-    const int64_t rs = t >> 1;
-    const int row = int(rs / steps), step = int(rs % steps);
-    WeightPiece<WT> piece;
-    piece.load(W + int64_t(row) * w_stride, step, h);
-    _Float16 v[16];
-    piece.dequant(step, h, v);
-    half8* o = reinterpret_cast<half8*>(out + int64_t(row) * ldo + 32 * step + 16 * h);
-    o[0] = half8{v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]};
-    o[1] = half8{v[8], v[9], v[10], v[11], v[12], v[13], v[14], v[15]};
+    if (t >= int64_t(N) * (K / 32) * 2) return;
+    dequant_piece<WT>(W, w_stride, K, t, out, ldo);
 }
 
 // Scalar-load variant for rows that are not 16-byte aligned.
@@ -319,6 +349,48 @@ void launch_dequant_w_f16(int wtype, const void* w, int64_t w_stride, int N, int
         case T_Q6_K: hipLaunchKernelGGL(dequant_w_f16_kernel<T_Q6_K>, grid, block, 0, stream, wb, w_stride, N, K, out, ldo); break;
         default: break;
     }
+}
+
+bool launch_prep(int mode, int wtype, const float* x, int64_t x_stride, int M, int K, _Float16* a, int64_t lda,
+                 float* row_scale, int x86, const void* w, int64_t w_stride, int N, _Float16* wout, int64_t ldo,
+                 hipStream_t stream) {
+    if (K > 512 * 10 || reinterpret_cast<uintptr_t>(x) % 16 || x_stride % 4) return false;
+    const int sb = (M + 3) / 4;
+    const int64_t db = (int64_t(N) * (K / 32) * 2 + 255) / 256;
+    const dim3 grid(unsigned(sb + db)), block(256);
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+#define SAMHIP_PREP(MODE, CH, X86, WT)                                                                        \
+    hipLaunchKernelGGL((prep_kernel<MODE, CH, X86, WT>), grid, block, 0, stream, x, x_stride, M, K, a, lda, \
+                       row_scale, sb, wb, w_stride, N, wout, ldo)
+#define SAMHIP_PREP_CH(MODE, X86, WT)                    \
+    do {                                                 \
+        if (K <= 1024) SAMHIP_PREP(MODE, 2, X86, WT);    \
+        else if (K <= 2048) SAMHIP_PREP(MODE, 4, X86, WT); \
+        else SAMHIP_PREP(MODE, 10, X86, WT);             \
+    } while (0)
+    switch (wtype) {
+        case T_Q8_0:
+            if (mode == T_F16) SAMHIP_PREP_CH(T_F16, false, T_Q8_0);
+            else if (x86) SAMHIP_PREP_CH(T_Q8_0, true, T_Q8_0);
+            else SAMHIP_PREP_CH(T_Q8_0, false, T_Q8_0);
+            break;
+        case T_Q4_K:
+            if (mode == T_F16) SAMHIP_PREP_CH(T_F16, false, T_Q4_K);
+            else SAMHIP_PREP_CH(T_Q8_K, false, T_Q4_K);
+            break;
+        case T_Q5_K:
+            if (mode == T_F16) SAMHIP_PREP_CH(T_F16, false, T_Q5_K);
+            else SAMHIP_PREP_CH(T_Q8_K, false, T_Q5_K);
+            break;
+        case T_Q6_K:
+            if (mode == T_F16) SAMHIP_PREP_CH(T_F16, false, T_Q6_K);
+            else SAMHIP_PREP_CH(T_Q8_K, false, T_Q6_K);
+            break;
+        default: return false;
+    }
+#undef SAMHIP_PREP_CH
+#undef SAMHIP_PREP
+    return true;
 }
 
 void launch_stage_rows(int mode, bool aligned, const float* x, int64_t x_stride, int M, int K, _Float16* a,
