@@ -80,18 +80,23 @@ def kernel_symbol(variant):
     """Template symbol of a GEMM variant name, as rocprofv3 reports it demangled:
     gemm_f16_{BM}x{BN}x{BK}_w{WM}x{WN} -> gemm_f16_kernel<BM, BN, WM, WN, BK>,
     gemm_f16dma_{BM}x{BN}x{BK}_s{S}    -> gemm_f16_dma_kernel<BM, BN, BK, S>,
-    gemm_f16pipe_{BM}x{BN}x{BK}_s{S}   -> gemm_f16_pipe_kernel<BM, BN, BK, S>.
+    gemm_f16pipe_{BM}x{BN}x{BK}_s{S}[_w{WM}x{WN}]
+                                       -> gemm_f16_pipe_kernel<BM, BN, BK, S, WM, WN> (2x2 waves by default).
     Returns (symbol, threads per workgroup, BM, BN) or None."""
     import re
     m = re.fullmatch(r"gemm_f16_(\d+)x(\d+)x(\d+)_w(\d+)x(\d+)", variant)
     if m:
         bm, bn, bk, wm, wn = map(int, m.groups())
         return f"gemm_f16_kernel<{bm}, {bn}, {wm}, {wn}, {bk}>", 64 * wm * wn, bm, bn
-    m = re.fullmatch(r"gemm_f16(dma|pipe)_(\d+)x(\d+)x(\d+)_s(\d+)", variant)
+    m = re.fullmatch(r"gemm_f16dma_(\d+)x(\d+)x(\d+)_s(\d+)", variant)
     if m:
-        kind = m.group(1)
-        bm, bn, bk, st = map(int, m.groups()[1:])
-        return f"gemm_f16_{kind}_kernel<{bm}, {bn}, {bk}, {st}>", 256, bm, bn
+        bm, bn, bk, st = map(int, m.groups())
+        return f"gemm_f16_dma_kernel<{bm}, {bn}, {bk}, {st}>", 256, bm, bn
+    m = re.fullmatch(r"gemm_f16pipe_(\d+)x(\d+)x(\d+)_s(\d+)(?:_w(\d+)x(\d+))?", variant)
+    if m:
+        bm, bn, bk, st = map(int, m.groups()[:4])
+        wm, wn = (int(m.group(5)), int(m.group(6))) if m.group(5) else (2, 2)
+        return f"gemm_f16_pipe_kernel<{bm}, {bn}, {bk}, {st}, {wm}, {wn}>", 64 * wm * wn, bm, bn
     return None
 
 

@@ -348,32 +348,33 @@ __global__ __launch_bounds__(256) void gemm_f16_dma_kernel(const _Float16* __res
 // never wait on LDS latency inside a stage.  The stage hand-over (wait for
 // this wave's loads of the next stage, a bare s_barrier, the next ring slot's
 // loads and the first fragments of the next stage) sits between the two
-// halves of the last substep's MFMAs.  4 waves, each a (BM/2) x (BN/2) tile:
-// 256x128 gives 8 independent 32x32 accumulators per wave.
+// halves of the last substep's MFMAs.  WM x WN waves, each a (BM/WM) x
+// (BN/WN) tile: 256x128 on 2x2 waves or 256x256 on 2x4 / 4x2 waves gives 8
+// independent 32x32 accumulators per wave (8 waves: two per SIMD).
 // ---------------------------------------------------------------------------
 
-template <int BM, int BN, int BK, int STAGES>
-__global__ __launch_bounds__(256) void gemm_f16_pipe_kernel(const _Float16* __restrict__ A, int64_t lda,
+template <int BM, int BN, int BK, int STAGES, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_f16_pipe_kernel(const _Float16* __restrict__ A, int64_t lda,
                                                             const float* __restrict__ row_scale,
                                                             const _Float16* __restrict__ B, int64_t ldb,
                                                             float* __restrict__ Y, int64_t ldy, int M, int N, int K,
                                                             int tiles_m, int tiles_n) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    constexpr int WM = 2, WN = 2;
+    constexpr int NW = WM * WN;
     constexpr int CPR = BK / 8, RB = BK * 2;
     constexpr int RPB = 64 / CPR;
     constexpr int A_BLOCKS = BM / RPB, B_BLOCKS = BN / RPB;
-    constexpr int A_PER_WAVE = A_BLOCKS / 4, B_PER_WAVE = B_BLOCKS / 4;
+    constexpr int A_PER_WAVE = A_BLOCKS / NW, B_PER_WAVE = B_BLOCKS / NW;
     constexpr int LOADS = A_PER_WAVE + B_PER_WAVE;
     constexpr int STAGE_BYTES = (BM + BN) * RB;
     constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
     constexpr int KK = BK / 16;
     constexpr int NF = FM * FN;
     constexpr int ES = TN + 8;
-    static_assert(A_PER_WAVE * 4 == A_BLOCKS && B_PER_WAVE * 4 == B_BLOCKS, "tile rows must split over 4 waves");
+    static_assert(A_PER_WAVE * NW == A_BLOCKS && B_PER_WAVE * NW == B_BLOCKS, "tile rows must split over the waves");
     static_assert(STAGES >= 2 && STAGES <= 4, "ring depth");
     static_assert(KK % 2 == 0, "fragment double buffer alternates per substep");
-    static_assert(4 * 32 * ES * 4 <= STAGES * STAGE_BYTES, "epilogue staging must fit in LDS");
+    static_assert(NW * 32 * ES * 4 <= STAGES * STAGE_BYTES, "epilogue staging must fit in LDS");
 
     __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * STAGE_BYTES];
 
@@ -521,13 +522,13 @@ __global__ __launch_bounds__(256) void gemm_f16_pipe_kernel(const _Float16* __re
 // idle (the dispatcher fills a CU before moving on).
 constexpr size_t spread_pad(size_t static_lds) { return static_lds > 82944 ? 0 : 82944 - static_lds; }
 
-template <int BM, int BN, int BK, int STAGES>
+template <int BM, int BN, int BK, int STAGES, int WM = 2, int WN = 2>
 void launch_pipe(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
                  int64_t ldy, int M, int N, int K, bool spread, hipStream_t stream) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const size_t pad = spread ? spread_pad(size_t(STAGES) * (BM + BN) * BK * 2) : 0;
-    hipLaunchKernelGGL((gemm_f16_pipe_kernel<BM, BN, BK, STAGES>), dim3(unsigned(tiles_m * tiles_n)), dim3(256), pad,
-                       stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n);
+    hipLaunchKernelGGL((gemm_f16_pipe_kernel<BM, BN, BK, STAGES, WM, WN>), dim3(unsigned(tiles_m * tiles_n)),
+                       dim3(64 * WM * WN), pad, stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n);
 }
 
 template <int BM, int BN, int BK, int STAGES>
@@ -575,6 +576,17 @@ const Cfg kConfigs[] = {
     {"gemm_f16pipe_256x256x32_s3", launch_pipe<256, 256, 32, 3>, 256, 256, 32},
     {"gemm_f16pipe_128x128x32_s4", launch_pipe<128, 128, 32, 4>, 128, 128, 32},
     {"gemm_f16pipe_256x128x32_s4", launch_pipe<256, 128, 32, 4>, 256, 128, 32},
+    {"gemm_f16pipe_256x256x32_s3_w2x4", launch_pipe<256, 256, 32, 3, 2, 4>, 256, 256, 32},
+    {"gemm_f16pipe_256x256x64_s2_w2x4", launch_pipe<256, 256, 64, 2, 2, 4>, 256, 256, 64},
+    {"gemm_f16pipe_256x128x32_s4_w4x2", launch_pipe<256, 128, 32, 4, 4, 2>, 256, 128, 32},
+    {"gemm_f16pipe_256x128x64_s2_w4x2", launch_pipe<256, 128, 64, 2, 4, 2>, 256, 128, 64},
+    {"gemm_f16pipe_128x256x32_s4_w2x4", launch_pipe<128, 256, 32, 4, 2, 4>, 128, 256, 32},
+    {"gemm_f16pipe_256x256x32_s4_w2x4", launch_pipe<256, 256, 32, 4, 2, 4>, 256, 256, 32},
+    {"gemm_f16pipe_128x128x32_s4_w2x4", launch_pipe<128, 128, 32, 4, 2, 4>, 128, 128, 32},
+    {"gemm_f16pipe_256x128x64_s3_w4x2", launch_pipe<256, 128, 64, 3, 4, 2>, 256, 128, 64},
+    {"gemm_f16pipe_128x128x64_s3_w2x4", launch_pipe<128, 128, 64, 3, 2, 4>, 128, 128, 64},
+    {"gemm_f16pipe_128x256x64_s2_w2x4", launch_pipe<128, 256, 64, 2, 2, 4>, 128, 256, 64},
+    {"gemm_f16pipe_128x128x128_s2_w2x4", launch_pipe<128, 128, 128, 2, 2, 4>, 128, 128, 128},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -593,15 +605,13 @@ bool gemm_f16_supported(int M, int N, int K, int64_t lda, int64_t ldb) {
 
 // Tile choice from a measured sweep of the configurations on the SAM 3 linear
 // shapes at M = 5184 tokens on MI355X (kernel time, HIP events, random
-// operands; differences below ~3 % are within run-to-run noise):
-//   N % 256 == 0, N >= 2048 (qkv 3072)    -> pipelined 256x128x32, 3 stages (652 TFLOP/s)
-//   N <= 1024, K >= 2048 (fc2 4736->1024)  -> pipelined 256x128x64, 2 stages (615)
-//   otherwise (proj 1024, fc1 4736, fusion/decoder widths)
-//                                          -> pipelined 128x128x32, 4 stages (406 proj, 658 fc1)
-int gemm_f16_pick(int /*M*/, int N, int K) {
-    if (N % 256 == 0 && N >= 2048) return 13;
-    if (N <= 1024 && K >= 2048) return 14;
-    return 17;
+// operands; differences below ~3 % are within run-to-run noise).  Eight-wave
+// workgroups (two waves per SIMD of one workgroup) win on every shape:
+//   N >= 2048 (qkv 3072, fc1 4736)        -> 256x256x64, 2 stages, 2x4 waves (733-773 / 668-685 TFLOP/s)
+//   N <= 1024 (proj 1024, fc2 4736->1024, fusion/decoder widths)
+//                                          -> 256x128x64, 2 stages, 4x2 waves (452 proj, 706-713 fc2)
+int gemm_f16_pick(int /*M*/, int N, int /*K*/) {
+    return N >= 2048 ? 20 : 22;
 }
 
 const char* launch_gemm_f16(int cfg, const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
