@@ -170,6 +170,61 @@ int samhip_dequantize_rows(samhip_context* ctx, int32_t type, const void* src, s
  * non-finite decoded value is rejected. */
 int samhip_validate_quantized_payload(int32_t type, int64_t ne0, int64_t rows, const void* host_bytes, size_t bytes);
 
+/* --- SAM 3 vision encoder ----------------------------------------------------
+ * The ViT of sam3_build_vit_graph (src/models/sam3/vision.hpp:248-283) as two
+ * fused subgraph operators on device buffers, for a backend that takes the
+ * whole vision encoder instead of its ggml nodes.  Activations are
+ * token-major F32 rows of `embed` floats, token (x, y) of the grid at row
+ * y*grid_w + x (ggml ne = {embed, grid_w, grid_h}).  Linears run as
+ * samhip_mul_mat does (same activation packing and arithmetic), with bias,
+ * erf-GELU, window unpartition and residual folded into the product's store;
+ * layer norms, RoPE and softmax are F32, attention products fp16 (MFMA) with
+ * F32 accumulation.  Supported: head_dim 64, embed a multiple of 256 (at
+ * most 2048), embed and mlp multiples of 128 (mlp at most 5120), grid sides
+ * multiples of the window. */
+typedef struct samhip_vit_block_desc {
+    int32_t version;                                  /* SAMHIP_ABI_VERSION */
+    int32_t embed, heads, mlp;                        /* SAM 3: 1024, 16, 4736 */
+    int32_t grid_w, grid_h, window;                   /* 72, 72, 24; window 0 = global attention */
+    const float *norm1_w, *norm1_b, *norm2_w, *norm2_b;   /* device F32 [embed] */
+    samhip_tensor qkv_w, proj_w, fc1_w, fc2_w;        /* packed weights [embed->3*embed], [embed->embed],
+                                                         [embed->mlp], [mlp->embed] (ggml ne = {K, N}) */
+    const float *qkv_b, *proj_b, *fc1_b, *fc2_b;      /* device F32 [N] */
+    const float* freqs_cis;                           /* device F32 [tokens per window (or grid)][head_dim/2][2]
+                                                         (cos, sin); NULL = no RoPE */
+} samhip_vit_block_desc;
+
+/* sam3_vit_block_forward (src/models/sam3/vision.hpp:157-243): x (device F32
+ * [grid_h*grid_w][embed]) is replaced by the block's output. */
+int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* block, float* x);
+
+typedef struct samhip_vit_prefix_desc {
+    int32_t version;                                  /* SAMHIP_ABI_VERSION */
+    int32_t image_size, patch, embed, pos_grid;       /* SAM 3: 1008, 14, 1024, 24 */
+    const float* patch_w;                             /* device F32, ggml {patch, patch, 3, embed} */
+    const float* pos_embed;                           /* device F32, ggml {embed, pos_grid, pos_grid} */
+    const float *ln_pre_w, *ln_pre_b;                 /* device F32 [embed] */
+} samhip_vit_prefix_desc;
+
+/* sam3_build_vit_prefix_graph (src/models/sam3/vision.hpp:248-272): image
+ * (device F32, ggml {image_size, image_size, 3}) -> x (device F32
+ * [(image_size/patch)^2][embed]): patch convolution (F32-accurate: split
+ * fp16 operands), tiled position embedding, ln_pre. */
+int samhip_vit_prefix(samhip_context* ctx, const samhip_vit_prefix_desc* prefix, const float* image, float* x);
+
+/* Pieces of the same graph as single operators.
+ * GGML_OP_NORM followed by the gain/bias of sam3_layer_norm
+ * (src/models/sam3/ops.hpp:56-66): y = ggml_norm(x, eps) * w + b over rows of
+ * n floats (n a multiple of 256, at most 2048; w, b may be NULL). */
+int samhip_layer_norm(samhip_context* ctx, const float* x, float* y, int64_t rows, int64_t n, const float* w,
+                      const float* b, float eps);
+/* GGML_OP_FLASH_ATTN_EXT without mask (src/models/sam3/vision.hpp:214-218):
+ * per batch and head, out = softmax(scale * Q K^T) V over n tokens.  q, k, v
+ * (device F32) rows b*n + t with stride ld floats, head h at columns
+ * h*head_dim; out rows of heads*head_dim floats.  head_dim must be 64. */
+int samhip_flash_attn(samhip_context* ctx, const float* q, const float* k, const float* v, int64_t ld, float* out,
+                      int64_t batches, int64_t n, int32_t heads, int32_t head_dim, float scale);
+
 /* --- diagnostics ------------------------------------------------------------ */
 int samhip_query(samhip_context* ctx, samhip_exec_info* info);
 

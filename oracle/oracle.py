@@ -1,7 +1,7 @@
 """ctypes bridge to the CPU oracle (libggml_oracle.so) — TEST INFRASTRUCTURE ONLY.
 
 The oracle restates ggml 0.26.0's CPU quantization and mul_mat arithmetic in C
-(ggml_oracle.c).  Only tests/, __graft_entry__.smoke() and bench.py's
+(ggml_oracle.c) and the SAM 3 vision encoder graph built on it (vit_oracle.c).  Only tests/, __graft_entry__.smoke() and bench.py's
 cpu_baseline leg may import this module; the product path never does.
 """
 
@@ -21,6 +21,14 @@ BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292}
 NAMES = {Q8_0: "q8_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K"}
 
 _lib = None
+
+
+class VitBlockWeights(ctypes.Structure):
+    """or_vit_block_weights (vit_oracle.h)."""
+    _fields_ = [(n, ctypes.c_void_p) for n in ("norm1_w", "norm1_b", "norm2_w", "norm2_b")] + \
+               [(n, ctypes.c_int) for n in ("qkv_type", "proj_type", "fc1_type", "fc2_type")] + \
+               [(n, ctypes.c_void_p) for n in ("qkv_w", "proj_w", "fc1_w", "fc2_w", "qkv_b", "proj_b", "fc1_b",
+                                               "fc2_b", "freqs")]
 
 
 def build():
@@ -48,6 +56,14 @@ def lib():
         L.or_mul_mat_decode.argtypes = [I, P, ctypes.c_size_t, P, ctypes.c_size_t, P, I64, I64, I64, I]
         L.or_gemm_f64.argtypes = [P, P, P, I64, I64, I64, I]
         L.or_max_threads.restype = I
+        L.or_layer_norm.argtypes = [P, P, I64, I64, P, P, ctypes.c_float, I]
+        L.or_gelu_erf.argtypes = [P, P, I64]
+        L.or_win_part.argtypes = [P, P, I, I, I, I]
+        L.or_win_unpart.argtypes = [P, P, I, I, I, I]
+        L.or_rope.argtypes = [P, I64, I64, I, I, P]
+        L.or_attention.argtypes = [P, P, P, I64, I64, I, I, ctypes.c_float, P, I]
+        L.or_vit_block.argtypes = [ctypes.POINTER(VitBlockWeights), P, P, I, I, I, I, I, I, I, I, I]
+        L.or_vit_prefix.argtypes = [P, I, I, P, P, I, P, P, I, P, I]
         _lib = L
     return _lib
 
@@ -140,3 +156,96 @@ def gemm_f64(w, x, threads=0):
 
 def max_threads():
     return lib().or_max_threads()
+
+
+# ---- SAM 3 vision encoder pieces (vit_oracle.c) ----------------------------
+
+def _f32(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def layer_norm(x, w=None, b=None, eps=1e-5, threads=0):
+    x = _f32(x)
+    y = np.empty_like(x)
+    n = x.shape[-1]
+    lib().or_layer_norm(_ptr(x), _ptr(y), x.size // n, n, None if w is None else _ptr(_f32(w)),
+                        None if b is None else _ptr(_f32(b)), eps, threads)
+    return y
+
+
+def gelu_erf(x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().or_gelu_erf(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def win_part(x, W, H, ws):
+    x = _f32(x)
+    C = x.shape[-1]
+    n = ((W + ws - 1) // ws) * ((H + ws - 1) // ws) * ws * ws
+    y = np.empty((n, C), np.float32)
+    lib().or_win_part(_ptr(x), _ptr(y), W, H, C, ws)
+    return y
+
+
+def win_unpart(y, W, H, ws):
+    y = _f32(y)
+    C = y.shape[-1]
+    x = np.empty((W * H, C), np.float32)
+    lib().or_win_unpart(_ptr(y), _ptr(x), W, H, C, ws)
+    return x
+
+
+def rope(x, heads, hd, freqs):
+    """x: [tokens][ld] (first heads*hd columns roped, returned as a copy)."""
+    x = _f32(x).copy()
+    lib().or_rope(_ptr(x), x.shape[1], x.shape[0], heads, hd, _ptr(_f32(freqs)))
+    return x
+
+
+def attention(q, k, v, heads, hd, scale, threads=0):
+    """q, k, v: [n][heads*hd] each."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    n, ld = q.shape
+    assert k.shape == q.shape and v.shape == q.shape and ld == heads * hd
+    out = np.empty((n, heads * hd), np.float32)
+    lib().or_attention(_ptr(q), _ptr(k), _ptr(v), ld, n, heads, hd, scale, _ptr(out), threads)
+    return out
+
+
+def vit_block(weights, x, W, H, E, heads, mlp, ws, rounding=ROUND_X86, threads=0, decode=False):
+    """weights: dict with norm1_w/b, norm2_w/b, {qkv,proj,fc1,fc2}_{type,w,b}, freqs (numpy arrays)."""
+    keep = {}
+
+    def p(name, dtype):
+        a = weights.get(name)
+        if a is None:
+            return None
+        a = np.ascontiguousarray(a, dtype)
+        keep[name] = a
+        return _ptr(a)
+
+    s = VitBlockWeights()
+    for n in ("norm1_w", "norm1_b", "norm2_w", "norm2_b", "qkv_b", "proj_b", "fc1_b", "fc2_b", "freqs"):
+        setattr(s, n, p(n, np.float32))
+    for n in ("qkv", "proj", "fc1", "fc2"):
+        setattr(s, n + "_type", weights[n + "_type"])
+        setattr(s, n + "_w", p(n + "_w", np.uint8))
+    x = _f32(x)
+    y = np.empty_like(x)
+    if lib().or_vit_block(ctypes.byref(s), _ptr(x), _ptr(y), W, H, E, heads, mlp, ws, rounding, int(decode), threads):
+        raise ValueError("oracle vit block rejected its arguments")
+    return y
+
+
+def vit_prefix(image, patch, kernel, pos, pos_grid, ln_w, ln_b, E, threads=0):
+    """image: [3][img][img] (ggml {img, img, 3}); kernel: [E][3][p][p]; pos: [pg][pg][E]."""
+    image = _f32(image)
+    img = image.shape[-1]
+    grid = img // patch
+    out = np.empty((grid * grid, E), np.float32)
+    if lib().or_vit_prefix(_ptr(image), img, patch, _ptr(_f32(kernel)), _ptr(_f32(pos)), pos_grid, _ptr(_f32(ln_w)),
+                           _ptr(_f32(ln_b)), E, _ptr(out), threads):
+        raise ValueError("oracle vit prefix rejected its arguments")
+    return out

@@ -91,6 +91,10 @@ struct samhip_context {
     std::string trace_filter;
     std::vector<TraceRecord> trace;
     std::vector<hipEvent_t> event_pool;
+    // vision-encoder intermediates (samhip_vit_block / samhip_vit_prefix /
+    // samhip_flash_attn); grown on demand, never while capturing
+    void* work = nullptr;
+    size_t work_bytes = 0;
 };
 
 namespace {
@@ -280,6 +284,7 @@ void samhip_context_destroy(samhip_context* ctx) {
     if (ctx->own_stream) (void)hipStreamSynchronize(ctx->own_stream);
     if (ctx->stream && ctx->stream != ctx->own_stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->staging) (void)hipFree(ctx->staging);
+    if (ctx->work) (void)hipFree(ctx->work);
     for (void* p : ctx->retired_staging) (void)hipFree(p);
     if (ctx->flag) (void)hipFree(ctx->flag);
     for (auto& r : ctx->trace) {
@@ -542,6 +547,286 @@ int samhip_validate_quantized_payload(int32_t type, int64_t ne0, int64_t rows, c
         // |d| * 128 * 32 (Q6_K), all finite in F32.
     }
     return SAMHIP_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// SAM 3 vision encoder
+// ---------------------------------------------------------------------------
+
+namespace {
+
+int ensure_work(samhip_context* ctx, size_t bytes) {
+    if (bytes <= ctx->work_bytes) return SAMHIP_OK;
+    if (ctx->work) {
+        HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        HIP_TRY(hipFree(ctx->work), "hipFree");
+        ctx->work = nullptr;
+        ctx->work_bytes = 0;
+    }
+    const size_t rounded = (bytes + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
+    HIP_TRY(hipMalloc(&ctx->work, rounded), "hipMalloc vision workspace");
+    ctx->work_bytes = rounded;
+    return SAMHIP_OK;
+}
+
+// Carves aligned sub-buffers out of one allocation.
+struct Carve {
+    size_t used = 0;
+    size_t take(size_t bytes) {
+        const size_t at = used;
+        used = (used + bytes + 255) & ~size_t(255);
+        return at;
+    }
+};
+
+bool layer_norm_supported(int64_t n) {
+    return n >= 256 && n <= 2048 && n % 256 == 0 && n != 1792;
+}
+
+// Tall product through staging + weight decode + the fp16 GEMM with an
+// epilogue; x rows are K contiguous floats (16-byte aligned), y rows ldy.
+int linear(samhip_context* ctx, const samhip_tensor& w, const float* x, int M, float* y, int64_t ldy,
+           const Epilogue& ep, const char* what) {
+    const int K = int(w.ne[0]), N = int(w.ne[1]);
+    auto align256 = [](size_t v) { return (v + 255) & ~size_t(255); };
+    const size_t rs_offset = align256(size_t(M) * size_t(K) * 2);
+    const size_t w_offset = align256(rs_offset + size_t(M) * 4);
+    if (int rc = ensure_staging(ctx, w_offset + size_t(N) * size_t(K) * 2)) return rc;
+    uint8_t* base = static_cast<uint8_t*>(ctx->staging);
+    _Float16* a = reinterpret_cast<_Float16*>(base);
+    float* rs = reinterpret_cast<float*>(base + rs_offset);
+    _Float16* wh = reinterpret_cast<_Float16*>(base + w_offset);
+    const int mode = ctx->compute == SAMHIP_COMPUTE_F16 ? T_F16 : vec_dot_type(w.type);
+    const int x86 = ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0;
+    int rc = traced(ctx, prep_name(mode), w.type, M, N, K, [&]() -> int {
+        if (!launch_prep(mode, w.type, x, K, M, K, a, K, rs, x86, w.data, int64_t(w.nb[1]), N, wh, K, ctx->stream))
+            return fail(SAMHIP_ERR_UNSUPPORTED, "%s: no staging kernel for K = %d", what, K);
+        HIP_TRY(hipGetLastError(), "staging and weight decode launch");
+        return SAMHIP_OK;
+    });
+    if (rc) return rc;
+    rc = traced(ctx, what, w.type, M, N, K, [&]() -> int {
+        if (!launch_gemm_f16_epi(a, K, rs, wh, K, y, ldy, M, N, K, ctx->cus, ep, ctx->stream))
+            return fail(SAMHIP_ERR_UNSUPPORTED, "%s: no GEMM epilogue variant", what);
+        HIP_TRY(hipGetLastError(), "gemm launch");
+        return SAMHIP_OK;
+    });
+    if (rc) return rc;
+    ctx->info.mul_mat_calls++;
+    ctx->info.activation_launches++;
+    ctx->info.gemm_launches++;
+    return SAMHIP_OK;
+}
+
+// 0 when the packed weight fits the block, else a status with the message set.
+int weight_check(const samhip_tensor& t, int64_t K, int64_t N, int64_t M, const char* name) {
+    const char* why = nullptr;
+    if (!is_weight_type(t.type)) why = "type must be Q8_0, Q4_K, Q5_K or Q6_K";
+    else if (t.ne[0] != K || t.ne[1] != N || t.ne[2] != 1 || t.ne[3] != 1) why = "shape differs from the block's";
+    else if (K % block_elems(t.type)) why = "width is not a multiple of its block";
+    else if (t.nb[0] != size_t(block_bytes(t.type)) || t.nb[1] < row_bytes(t.type, K)) why = "bad strides";
+    else if (!t.data || reinterpret_cast<uintptr_t>(t.data) % 2 || t.nb[1] % 2) why = "bad data pointer";
+    if (why) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_block: %s weight: %s", name, why);
+    if (K > 5120 || !gemm_f16_supported(int(M), int(N), int(K), K, K))
+        return fail(SAMHIP_ERR_UNSUPPORTED, "vit_block: %s weight: width %lld unsupported (multiple of 128, at most 5120)",
+                    name, (long long)K);
+    return SAMHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int samhip_layer_norm(samhip_context* ctx, const float* x, float* y, int64_t rows, int64_t n, const float* w,
+                      const float* b, float eps) {
+    if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "layer_norm");
+    if (!x || !y || rows <= 0 || rows > (int64_t(1) << 30)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "layer_norm: bad operands");
+    if (!layer_norm_supported(n)) return fail(SAMHIP_ERR_UNSUPPORTED, "layer_norm: row width %lld unsupported", (long long)n);
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(y) % 16)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "layer_norm: rows must be 16-byte aligned");
+    if (!(eps >= 0.f)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "layer_norm: eps must be nonnegative");
+    if (int rc = set_device(ctx)) return rc;
+    return traced(ctx, "layer_norm", T_F32, rows, n, 0, [&]() -> int {
+        launch_layer_norm(x, nullptr, 1, 1, int(rows), 0, w, b, eps, y, int(rows), int(n), ctx->stream);
+        HIP_TRY(hipGetLastError(), "layer_norm launch");
+        return SAMHIP_OK;
+    });
+}
+
+int samhip_flash_attn(samhip_context* ctx, const float* q, const float* k, const float* v, int64_t ld, float* out,
+                      int64_t batches, int64_t n, int32_t heads, int32_t head_dim, float scale) {
+    if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "flash_attn");
+    if (!q || !k || !v || !out || batches <= 0 || n <= 0 || heads <= 0)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "flash_attn: bad operands");
+    if (head_dim != 64) return fail(SAMHIP_ERR_UNSUPPORTED, "flash_attn: head_dim %d unsupported (64)", head_dim);
+    if (ld < int64_t(heads) * 64 || ld % 4 || batches * n > (int64_t(1) << 26) || heads > 4096 || batches > 65535)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "flash_attn: bad row stride or sizes");
+    for (const float* p : {q, k, v, static_cast<const float*>(out)})
+        if (reinterpret_cast<uintptr_t>(p) % 16) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "flash_attn: 16-byte alignment");
+    if (!std::isfinite(scale)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "flash_attn: scale");
+    if (int rc = set_device(ctx)) return rc;
+    const int64_t np = (n + 63) / 64 * 64;
+    const size_t packed = size_t(batches) * heads * np * 64 * 2;
+    Carve c;
+    const size_t oq = c.take(packed), ok = c.take(packed), ov = c.take(packed);
+    if (int rc = ensure_work(ctx, c.used)) return rc;
+    uint8_t* wb = static_cast<uint8_t*>(ctx->work);
+    _Float16 *qh = reinterpret_cast<_Float16*>(wb + oq), *kh = reinterpret_cast<_Float16*>(wb + ok),
+             *vt = reinterpret_cast<_Float16*>(wb + ov);
+    int rc = traced(ctx, "vit_pack_qkv", T_F32, batches * n, heads * 64, 0, [&]() -> int {
+        launch_pack_qkv(q, k, v, ld, nullptr, scale, qh, kh, vt, int(batches), heads, int(n), ctx->stream);
+        HIP_TRY(hipGetLastError(), "pack launch");
+        return SAMHIP_OK;
+    });
+    if (rc) return rc;
+    return traced(ctx, "vit_attention", T_F32, batches * n, heads * 64, n, [&]() -> int {
+        launch_attention(qh, kh, vt, out, int64_t(heads) * 64, int(batches), heads, int(n), ctx->stream);
+        HIP_TRY(hipGetLastError(), "attention launch");
+        return SAMHIP_OK;
+    });
+}
+
+int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float* x) {
+    if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "vit_block");
+    if (!d || !x) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_block: null argument");
+    if (d->version != SAMHIP_ABI_VERSION) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_block: descriptor version");
+    const int64_t E = d->embed, H = d->heads, MLP = d->mlp, GW = d->grid_w, GH = d->grid_h, WS = d->window;
+    if (E <= 0 || H <= 0 || MLP <= 0 || GW <= 0 || GH <= 0 || WS < 0 || GW * GH > (int64_t(1) << 22))
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_block: nonpositive or oversized dimension");
+    if (E != H * 64) return fail(SAMHIP_ERR_UNSUPPORTED, "vit_block: head_dim must be 64 (embed = 64 * heads)");
+    if (!layer_norm_supported(E)) return fail(SAMHIP_ERR_UNSUPPORTED, "vit_block: embed must be a multiple of 256 up to 2048");
+    if (WS > 0 && (GW % WS || GH % WS))
+        return fail(SAMHIP_ERR_UNSUPPORTED, "vit_block: grid sides must be multiples of the window");
+    if (!d->norm1_w || !d->norm1_b || !d->norm2_w || !d->norm2_b || !d->qkv_b || !d->proj_b || !d->fc1_b || !d->fc2_b)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_block: null norm or bias pointer");
+    const struct { const samhip_tensor* t; int64_t k, n; const char* name; } weights[] = {
+        {&d->qkv_w, E, 3 * E, "qkv"}, {&d->proj_w, E, E, "proj"}, {&d->fc1_w, E, MLP, "fc1"}, {&d->fc2_w, MLP, E, "fc2"}};
+    for (const auto& w : weights)
+        if (int rc = weight_check(*w.t, w.k, w.n, GW * GH, w.name)) return rc;
+    if (reinterpret_cast<uintptr_t>(x) % 16) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_block: x must be 16-byte aligned");
+    if (int rc = set_device(ctx)) return rc;
+
+    const int64_t T = GW * GH, per = WS > 0 ? WS * WS : T, B = T / per, np = (per + 63) / 64 * 64;
+    Carve c;
+    const size_t o_ln = c.take(size_t(T * E) * 4), o_qkv = c.take(size_t(T * 3 * E) * 4),
+                 o_x1 = c.take(size_t(T * E) * 4), o_h1 = c.take(size_t(T * MLP) * 4);
+    const size_t packed = size_t(B * H * np * 64) * 2;
+    const size_t o_qh = c.take(packed), o_kh = c.take(packed), o_vt = c.take(packed);
+    if (int rc = ensure_work(ctx, c.used)) return rc;
+    uint8_t* wb = static_cast<uint8_t*>(ctx->work);
+    float* ln = reinterpret_cast<float*>(wb + o_ln);
+    float* qkv = reinterpret_cast<float*>(wb + o_qkv);
+    float* x1 = reinterpret_cast<float*>(wb + o_x1);
+    float* h1 = reinterpret_cast<float*>(wb + o_h1);
+    _Float16 *qh = reinterpret_cast<_Float16*>(wb + o_qh), *kh = reinterpret_cast<_Float16*>(wb + o_kh),
+             *vt = reinterpret_cast<_Float16*>(wb + o_vt);
+    const int iT = int(T), iE = int(E);
+
+    // attention half: LN1 (rows leave in window order), qkv + bias, RoPE and
+    // packing, attention, proj + bias + unpartition + residual -> x1
+    int rc = traced(ctx, "vit_layer_norm", T_F32, T, E, 0, [&]() -> int {
+        launch_layer_norm(x, nullptr, 1, int(GW), int(GH), int(WS), d->norm1_w, d->norm1_b, 1e-5f, ln, iT, iE,
+                          ctx->stream);
+        HIP_TRY(hipGetLastError(), "layer_norm launch");
+        return SAMHIP_OK;
+    });
+    if (rc) return rc;
+    Epilogue e_qkv;
+    e_qkv.bias = d->qkv_b;
+    if ((rc = linear(ctx, d->qkv_w, ln, iT, qkv, 3 * E, e_qkv, "vit_qkv"))) return rc;
+    rc = traced(ctx, "vit_pack_qkv", T_F32, T, 3 * E, 0, [&]() -> int {
+        launch_pack_qkv(qkv, qkv + E, qkv + 2 * E, 3 * E, d->freqs_cis, 0.125f, qh, kh, vt, int(B), int(H), int(per),
+                        ctx->stream);
+        HIP_TRY(hipGetLastError(), "pack launch");
+        return SAMHIP_OK;
+    });
+    if (rc) return rc;
+    rc = traced(ctx, "vit_attention", T_F32, T, E, per, [&]() -> int {
+        launch_attention(qh, kh, vt, ln, E, int(B), int(H), int(per), ctx->stream);
+        HIP_TRY(hipGetLastError(), "attention launch");
+        return SAMHIP_OK;
+    });
+    if (rc) return rc;
+    Epilogue e_proj;
+    e_proj.bias = d->proj_b;
+    e_proj.res = x;
+    if (WS > 0) {
+        e_proj.ws = int(WS);
+        e_proj.gw = int(GW);
+        e_proj.gh = int(GH);
+    }
+    if ((rc = linear(ctx, d->proj_w, ln, iT, x1, E, e_proj, "vit_proj"))) return rc;
+
+    // MLP half: LN2, fc1 + bias + GELU, fc2 + bias + residual -> x
+    rc = traced(ctx, "vit_layer_norm", T_F32, T, E, 0, [&]() -> int {
+        launch_layer_norm(x1, nullptr, 1, int(GW), int(GH), 0, d->norm2_w, d->norm2_b, 1e-5f, ln, iT, iE, ctx->stream);
+        HIP_TRY(hipGetLastError(), "layer_norm launch");
+        return SAMHIP_OK;
+    });
+    if (rc) return rc;
+    Epilogue e_fc1;
+    e_fc1.bias = d->fc1_b;
+    e_fc1.gelu = true;
+    if ((rc = linear(ctx, d->fc1_w, ln, iT, h1, MLP, e_fc1, "vit_fc1"))) return rc;
+    Epilogue e_fc2;
+    e_fc2.bias = d->fc2_b;
+    e_fc2.res = x1;
+    return linear(ctx, d->fc2_w, h1, iT, x, E, e_fc2, "vit_fc2");
+}
+
+int samhip_vit_prefix(samhip_context* ctx, const samhip_vit_prefix_desc* d, const float* image, float* x) {
+    if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "vit_prefix");
+    if (!d || !image || !x) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_prefix: null argument");
+    if (d->version != SAMHIP_ABI_VERSION) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_prefix: descriptor version");
+    if (!d->patch_w || !d->pos_embed || !d->ln_pre_w || !d->ln_pre_b)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_prefix: null weight pointer");
+    const int64_t img = d->image_size, p = d->patch, E = d->embed, pg = d->pos_grid;
+    if (img <= 0 || p <= 0 || E <= 0 || pg <= 0 || img % p || img > 16384 || p > 64)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_prefix: image size must be a positive multiple of the patch");
+    const int64_t grid = img / p;
+    if (grid % pg) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_prefix: grid must be a multiple of pos_grid");
+    if (!layer_norm_supported(E)) return fail(SAMHIP_ERR_UNSUPPORTED, "vit_prefix: embed must be a multiple of 256 up to 2048");
+    const int64_t kp = (3 * p * p + 127) / 128 * 128, T = grid * grid;
+    if (3 * kp > 5120 * 4) return fail(SAMHIP_ERR_UNSUPPORTED, "vit_prefix: patch too large");
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(d->pos_embed) % 16)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_prefix: 16-byte alignment");
+    if (int rc = set_device(ctx)) return rc;
+    Carve c;
+    const size_t o_a = c.take(size_t(T * 3 * kp) * 2), o_rs = c.take(size_t(T) * 4),
+                 o_w = c.take(size_t(E * 3 * kp) * 2), o_conv = c.take(size_t(T * E) * 4);
+    if (int rc = ensure_work(ctx, c.used)) return rc;
+    uint8_t* wb = static_cast<uint8_t*>(ctx->work);
+    _Float16* a = reinterpret_cast<_Float16*>(wb + o_a);
+    float* rs = reinterpret_cast<float*>(wb + o_rs);
+    _Float16* w = reinterpret_cast<_Float16*>(wb + o_w);
+    float* conv = reinterpret_cast<float*>(wb + o_conv);
+    int rc = traced(ctx, "vit_patch_operands", T_F32, T, E, 3 * kp, [&]() -> int {
+        launch_patch_columns(image, int(img), int(p), a, rs, int(kp), ctx->stream);
+        launch_patch_kernel(d->patch_w, int(E), int(p), w, int(kp), ctx->stream);
+        HIP_TRY(hipGetLastError(), "patch operand launch");
+        return SAMHIP_OK;
+    });
+    if (rc) return rc;
+    rc = traced(ctx, "vit_patch_gemm", T_F32, T, E, 3 * kp, [&]() -> int {
+        if (!launch_gemm_f16_epi(a, 3 * kp, rs, w, 3 * kp, conv, E, int(T), int(E), int(3 * kp), ctx->cus, Epilogue{},
+                                 ctx->stream))
+            return fail(SAMHIP_ERR_UNSUPPORTED, "vit_prefix: no GEMM variant");
+        HIP_TRY(hipGetLastError(), "patch gemm launch");
+        return SAMHIP_OK;
+    });
+    if (rc) return rc;
+    return traced(ctx, "vit_layer_norm", T_F32, T, E, 0, [&]() -> int {
+        launch_layer_norm(conv, d->pos_embed, int(pg), int(grid), int(grid), 0, d->ln_pre_w, d->ln_pre_b, 1e-5f, x,
+                          int(T), int(E), ctx->stream);
+        HIP_TRY(hipGetLastError(), "layer_norm launch");
+        return SAMHIP_OK;
+    });
 }
 
 int samhip_trace_begin(samhip_context* ctx, const char* kernel_filter) {

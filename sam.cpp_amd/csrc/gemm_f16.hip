@@ -41,9 +41,26 @@ __device__ __forceinline__ void tile_order(int bid, int nblocks, int tiles_m, in
 // element r of lane l sits on row 8*(r/4) + 4*(l/32) + r%4) and leaves as
 // 16-byte row segments scaled by their row's 2^e.  (Staging the row scales
 // in LDS at kernel start measured up to 35 % slower on the long-K shapes.)
-template <int FM, int FN, int ES>
+// Epilogue flags (EPI template bits) for Epilogue fields.
+constexpr int EPI_BIAS = 1, EPI_GELU = 2, EPI_RES = 4, EPI_REMAP = 8;
+
+__device__ __forceinline__ float gelu_erf(float v) {
+#pragma clang fp contract(off)
+    return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+}
+
+// Output row of window-order row m (ggml_win_unpart on a gw-wide grid).
+__device__ __forceinline__ int64_t unpart_row(int m, int ws, int gw) {
+    const int per = ws * ws, win = m / per, r = m - win * per;
+    const int npx = gw / ws, py = win / npx, px = win - py * npx;
+    return int64_t(py * ws + r / ws) * gw + px * ws + r % ws;
+}
+
+template <int FM, int FN, int ES, int EPI = 0>
 __device__ __forceinline__ void store_tile(floatx16 (&acc)[FM][FN], const float* row_scale, float* slab, int lane,
-                                           int row0, int col0, int M, int N, float* Y, int64_t ldy) {
+                                           int row0, int col0, int M, int N, float* Y, int64_t ldy,
+                                           const Epilogue& ep = Epilogue{}) {
+#pragma clang fp contract(off)
     constexpr int TN = 32 * FN, C4 = TN / 4;
     const bool vec_ok = (ldy % 4) == 0 && (reinterpret_cast<uintptr_t>(Y) % 16) == 0;
 #pragma unroll
@@ -63,9 +80,24 @@ __device__ __forceinline__ void store_tile(floatx16 (&acc)[FM][FN], const float*
             if (m >= M) continue;
             const float sc = row_scale[m];
             const floatx4 raw = *reinterpret_cast<const floatx4*>(slab + rr * ES + 4 * c4);
-            const floatx4 v{raw[0] * sc, raw[1] * sc, raw[2] * sc, raw[3] * sc};
-            float* yp = Y + int64_t(m) * ldy + n;
-            if (vec_ok && n + 3 < N) {
+            floatx4 v{raw[0] * sc, raw[1] * sc, raw[2] * sc, raw[3] * sc};
+            const bool full = n + 3 < N;
+            if (EPI & EPI_BIAS) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] = v[q] + (full || n + q < N ? ep.bias[n + q] : 0.f);
+            }
+            if (EPI & EPI_GELU) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] = gelu_erf(v[q]);
+            }
+            const int64_t d = (EPI & EPI_REMAP) ? unpart_row(m, ep.ws, ep.gw) : int64_t(m);
+            if (EPI & EPI_RES) {
+                const float* rp = ep.res + d * ldy + n;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] = (full || n + q < N ? rp[q] : 0.f) + v[q];
+            }
+            float* yp = Y + d * ldy + n;
+            if (vec_ok && full) {
                 *reinterpret_cast<floatx4*>(yp) = v;
             } else {
                 for (int q = 0; q < 4; ++q)
@@ -353,12 +385,12 @@ __global__ __launch_bounds__(256) void gemm_f16_dma_kernel(const _Float16* __res
 // independent 32x32 accumulators per wave (8 waves: two per SIMD).
 // ---------------------------------------------------------------------------
 
-template <int BM, int BN, int BK, int STAGES, int WM, int WN>
+template <int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI = 0>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_pipe_kernel(const _Float16* __restrict__ A, int64_t lda,
                                                             const float* __restrict__ row_scale,
                                                             const _Float16* __restrict__ B, int64_t ldb,
-                                                            float* __restrict__ Y, int64_t ldy, int M, int N, int K,
-                                                            int tiles_m, int tiles_n) {
+                                                            float* Y, int64_t ldy, int M, int N, int K,
+                                                            int tiles_m, int tiles_n, Epilogue ep) {
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int NW = WM * WN;
     constexpr int CPR = BK / 8, RB = BK * 2;
@@ -512,8 +544,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_pipe_kernel(const _Floa
     }
     __syncthreads();
 
-    store_tile<FM, FN, ES>(acc, row_scale, reinterpret_cast<float*>(lds) + wave * 32 * ES, lane, m0 + wm * TM, n0 + wn * TN, M, N,
-                           Y, ldy);
+    store_tile<FM, FN, ES, EPI>(acc, row_scale, reinterpret_cast<float*>(lds) + wave * 32 * ES, lane, m0 + wm * TM,
+                                n0 + wn * TN, M, N, Y, ldy, ep);
 #endif
 }
 
@@ -522,13 +554,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_pipe_kernel(const _Floa
 // idle (the dispatcher fills a CU before moving on).
 constexpr size_t spread_pad(size_t static_lds) { return static_lds > 82944 ? 0 : 82944 - static_lds; }
 
-template <int BM, int BN, int BK, int STAGES, int WM = 2, int WN = 2>
+template <int BM, int BN, int BK, int STAGES, int WM = 2, int WN = 2, int EPI = 0>
 void launch_pipe(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
-                 int64_t ldy, int M, int N, int K, bool spread, hipStream_t stream) {
+                 int64_t ldy, int M, int N, int K, bool spread, hipStream_t stream, const Epilogue& ep = Epilogue{}) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const size_t pad = spread ? spread_pad(size_t(STAGES) * (BM + BN) * BK * 2) : 0;
-    hipLaunchKernelGGL((gemm_f16_pipe_kernel<BM, BN, BK, STAGES, WM, WN>), dim3(unsigned(tiles_m * tiles_n)),
-                       dim3(64 * WM * WN), pad, stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n);
+    hipLaunchKernelGGL((gemm_f16_pipe_kernel<BM, BN, BK, STAGES, WM, WN, EPI>), dim3(unsigned(tiles_m * tiles_n)),
+                       dim3(64 * WM * WN), pad, stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n, ep);
 }
 
 template <int BM, int BN, int BK, int STAGES>
@@ -547,6 +579,13 @@ void launch_cfg(const _Float16* a, int64_t lda, const float* rs, const _Float16*
     const size_t pad = spread ? spread_pad(size_t(2) * (BM + BN) * (BK + 8) * 2) : 0;
     hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, WM, WN, BK>), dim3(unsigned(tiles_m * tiles_n)),
                        dim3(WM * WN * 64), pad, stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n);
+}
+
+// Configuration-table entry point (plain epilogue).
+template <int BM, int BN, int BK, int STAGES, int WM = 2, int WN = 2>
+void launch_pipe_plain(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
+                       int64_t ldy, int M, int N, int K, bool spread, hipStream_t stream) {
+    launch_pipe<BM, BN, BK, STAGES, WM, WN, 0>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream);
 }
 
 struct Cfg {
@@ -570,23 +609,23 @@ const Cfg kConfigs[] = {
     {"gemm_f16dma_128x128x32_s4", launch_dma<128, 128, 32, 4>, 128, 128, 32},
     {"gemm_f16dma_128x256x32_s3", launch_dma<128, 256, 32, 3>, 128, 256, 32},
     {"gemm_f16dma_256x256x32_s3", launch_dma<256, 256, 32, 3>, 256, 256, 32},
-    {"gemm_f16pipe_256x128x32_s3", launch_pipe<256, 128, 32, 3>, 256, 128, 32},
-    {"gemm_f16pipe_256x128x64_s2", launch_pipe<256, 128, 64, 2>, 256, 128, 64},
-    {"gemm_f16pipe_128x256x32_s3", launch_pipe<128, 256, 32, 3>, 128, 256, 32},
-    {"gemm_f16pipe_256x256x32_s3", launch_pipe<256, 256, 32, 3>, 256, 256, 32},
-    {"gemm_f16pipe_128x128x32_s4", launch_pipe<128, 128, 32, 4>, 128, 128, 32},
-    {"gemm_f16pipe_256x128x32_s4", launch_pipe<256, 128, 32, 4>, 256, 128, 32},
-    {"gemm_f16pipe_256x256x32_s3_w2x4", launch_pipe<256, 256, 32, 3, 2, 4>, 256, 256, 32},
-    {"gemm_f16pipe_256x256x64_s2_w2x4", launch_pipe<256, 256, 64, 2, 2, 4>, 256, 256, 64},
-    {"gemm_f16pipe_256x128x32_s4_w4x2", launch_pipe<256, 128, 32, 4, 4, 2>, 256, 128, 32},
-    {"gemm_f16pipe_256x128x64_s2_w4x2", launch_pipe<256, 128, 64, 2, 4, 2>, 256, 128, 64},
-    {"gemm_f16pipe_128x256x32_s4_w2x4", launch_pipe<128, 256, 32, 4, 2, 4>, 128, 256, 32},
-    {"gemm_f16pipe_256x256x32_s4_w2x4", launch_pipe<256, 256, 32, 4, 2, 4>, 256, 256, 32},
-    {"gemm_f16pipe_128x128x32_s4_w2x4", launch_pipe<128, 128, 32, 4, 2, 4>, 128, 128, 32},
-    {"gemm_f16pipe_256x128x64_s3_w4x2", launch_pipe<256, 128, 64, 3, 4, 2>, 256, 128, 64},
-    {"gemm_f16pipe_128x128x64_s3_w2x4", launch_pipe<128, 128, 64, 3, 2, 4>, 128, 128, 64},
-    {"gemm_f16pipe_128x256x64_s2_w2x4", launch_pipe<128, 256, 64, 2, 2, 4>, 128, 256, 64},
-    {"gemm_f16pipe_128x128x128_s2_w2x4", launch_pipe<128, 128, 128, 2, 2, 4>, 128, 128, 128},
+    {"gemm_f16pipe_256x128x32_s3", launch_pipe_plain<256, 128, 32, 3>, 256, 128, 32},
+    {"gemm_f16pipe_256x128x64_s2", launch_pipe_plain<256, 128, 64, 2>, 256, 128, 64},
+    {"gemm_f16pipe_128x256x32_s3", launch_pipe_plain<128, 256, 32, 3>, 128, 256, 32},
+    {"gemm_f16pipe_256x256x32_s3", launch_pipe_plain<256, 256, 32, 3>, 256, 256, 32},
+    {"gemm_f16pipe_128x128x32_s4", launch_pipe_plain<128, 128, 32, 4>, 128, 128, 32},
+    {"gemm_f16pipe_256x128x32_s4", launch_pipe_plain<256, 128, 32, 4>, 256, 128, 32},
+    {"gemm_f16pipe_256x256x32_s3_w2x4", launch_pipe_plain<256, 256, 32, 3, 2, 4>, 256, 256, 32},
+    {"gemm_f16pipe_256x256x64_s2_w2x4", launch_pipe_plain<256, 256, 64, 2, 2, 4>, 256, 256, 64},
+    {"gemm_f16pipe_256x128x32_s4_w4x2", launch_pipe_plain<256, 128, 32, 4, 4, 2>, 256, 128, 32},
+    {"gemm_f16pipe_256x128x64_s2_w4x2", launch_pipe_plain<256, 128, 64, 2, 4, 2>, 256, 128, 64},
+    {"gemm_f16pipe_128x256x32_s4_w2x4", launch_pipe_plain<128, 256, 32, 4, 2, 4>, 128, 256, 32},
+    {"gemm_f16pipe_256x256x32_s4_w2x4", launch_pipe_plain<256, 256, 32, 4, 2, 4>, 256, 256, 32},
+    {"gemm_f16pipe_128x128x32_s4_w2x4", launch_pipe_plain<128, 128, 32, 4, 2, 4>, 128, 128, 32},
+    {"gemm_f16pipe_256x128x64_s3_w4x2", launch_pipe_plain<256, 128, 64, 3, 4, 2>, 256, 128, 64},
+    {"gemm_f16pipe_128x128x64_s3_w2x4", launch_pipe_plain<128, 128, 64, 3, 2, 4>, 128, 128, 64},
+    {"gemm_f16pipe_128x256x64_s2_w2x4", launch_pipe_plain<128, 256, 64, 2, 2, 4>, 128, 256, 64},
+    {"gemm_f16pipe_128x128x128_s2_w2x4", launch_pipe_plain<128, 128, 128, 2, 2, 4>, 128, 128, 128},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -612,6 +651,46 @@ bool gemm_f16_supported(int M, int N, int K, int64_t lda, int64_t ldb) {
 //                                          -> 256x128x64, 2 stages, 4x2 waves (452 proj, 706-713 fc2)
 int gemm_f16_pick(int /*M*/, int N, int /*K*/) {
     return N >= 2048 ? 20 : 22;
+}
+
+// The picked configurations (20: 256x256x64 on 2x4 waves, 22: 256x128x64 on
+// 4x2 waves) with each epilogue the vision encoder uses.
+template <int BM, int BN, int WM, int WN>
+bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
+                int64_t ldy, int M, int N, int K, bool spread, const Epilogue& ep, hipStream_t stream) {
+    const int flags = (ep.bias ? EPI_BIAS : 0) | (ep.gelu ? EPI_GELU : 0) | (ep.res ? EPI_RES : 0) |
+                      (ep.ws > 0 ? EPI_REMAP : 0);
+    switch (flags) {
+        case 0: launch_pipe<BM, BN, 64, 2, WM, WN, 0>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream, ep); break;
+        case EPI_BIAS:
+            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream, ep);
+            break;
+        case EPI_BIAS | EPI_GELU:
+            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_GELU>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread,
+                                                                   stream, ep);
+            break;
+        case EPI_BIAS | EPI_RES:
+            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_RES>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream,
+                                                                  ep);
+            break;
+        case EPI_BIAS | EPI_RES | EPI_REMAP:
+            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_RES | EPI_REMAP>(a, lda, rs, b, ldb, y, ldy, M, N, K,
+                                                                              spread, stream, ep);
+            break;
+        default: return false;   // combinations the encoder does not use
+    }
+    return true;
+}
+
+const char* launch_gemm_f16_epi(const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
+                                int64_t ldb, float* y, int64_t ldy, int M, int N, int K, int cus, const Epilogue& ep,
+                                hipStream_t stream) {
+    const int cfg = gemm_f16_pick(M, N, K);
+    const Cfg& c = kConfigs[cfg];
+    const bool spread = int64_t((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) <= cus;
+    const bool ok = cfg == 20 ? launch_epi<256, 256, 2, 4>(a, lda, row_scale, b, ldb, y, ldy, M, N, K, spread, ep, stream)
+                              : launch_epi<256, 128, 4, 2>(a, lda, row_scale, b, ldb, y, ldy, M, N, K, spread, ep, stream);
+    return ok ? c.name : nullptr;
 }
 
 const char* launch_gemm_f16(int cfg, const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,

@@ -37,6 +37,50 @@ int gemm_f16_pick(int M, int N, int K);
 const char* launch_gemm_f16(int cfg, const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
                             int64_t ldb, float* y, int64_t ldy, int M, int N, int K, int cus, hipStream_t stream);
 
+// Epilogue applied to the tall GEMM's tile before the store, in the order of
+// the reference graph (src/models/sam3/vision.hpp:186-241):
+//   v = rs[m] * acc;  v += bias[n];  v = gelu_erf(v);  y[d] = res[d] + v
+// where d is the output row: m itself, or with `ws` > 0 the grid row that
+// window-order row m returns to (ggml_win_unpart of a gw x gh grid with
+// ws x ws windows, gw and gh multiples of ws).  res may alias y.
+struct Epilogue {
+    const float* bias = nullptr;
+    const float* res = nullptr;   // row stride = ldy
+    bool gelu = false;
+    int ws = 0, gw = 0, gh = 0;
+};
+// Same product as launch_gemm_f16 with the shape's picked configuration and
+// the epilogue; returns the configuration's name, or nullptr for an
+// epilogue combination without a kernel (bias; bias + gelu; bias + res;
+// bias + res + remap; or none are built).
+const char* launch_gemm_f16_epi(const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
+                                int64_t ldb, float* y, int64_t ldy, int M, int N, int K, int cus, const Epilogue& ep,
+                                hipStream_t stream);
+
+// SAM 3 vision-encoder kernels (vit.hip).
+// Layer norm over rows of E floats (E a multiple of 256): y[dst(r)] =
+// ggml_norm(x[r] + add[tile(r)], eps) * w + b, with `add` (nullable) tiled
+// with period `add_grid` over the gw x gh grid, and dst(r) the window-order
+// row of grid row r when ws > 0 (else r).
+void launch_layer_norm(const float* x, const float* add, int add_grid, int gw, int gh, int ws, const float* w,
+                       const float* b, float eps, float* y, int rows, int E, hipStream_t stream);
+// q/k/v rows (row b*N + n, stride ld floats, head h at columns h*64) ->
+// Qh [B][H][Np][64] (RoPE, times q_scale), Kh [B][H][Np][64] (RoPE),
+// Vt [B][H][64][Np], fp16, Np = N rounded up to 64 with zero padding;
+// freqs (nullable): [N][32][2] (cos, sin).
+void launch_pack_qkv(const float* q, const float* k, const float* v, int64_t ld, const float* freqs, float q_scale,
+                     _Float16* qh, _Float16* kh, _Float16* vt, int B, int H, int N, hipStream_t stream);
+// softmax(Q K^T) V per (batch, head) on the packed operands (head dim 64);
+// out row b*N + n, columns h*64.. (row stride ldo floats).
+void launch_attention(const _Float16* qh, const _Float16* kh, const _Float16* vt, float* out, int64_t ldo, int B,
+                      int H, int N, hipStream_t stream);
+// Patch convolution operands as split fp16: A [T][3*Kp] = [hi | hi | lo] of
+// the image patches, W [E][3*Kp] = [hi | lo | hi] of the kernel rows, so
+// A W^T = hi*hi + hi*lo + lo*hi (F32-accurate); Kp = 3*p*p rounded up to 128.
+void launch_patch_columns(const float* image, int img, int patch, _Float16* a, float* row_scale, int kp,
+                          hipStream_t stream);
+void launch_patch_kernel(const float* kernel, int E, int patch, _Float16* w, int kp, hipStream_t stream);
+
 // Activation staging and weight decode of a tall product in one launch
 // (16-byte aligned activation rows, K <= 5120); false when not applicable.
 bool launch_prep(int mode, int wtype, const float* x, int64_t x_stride, int M, int K, _Float16* a, int64_t lda,

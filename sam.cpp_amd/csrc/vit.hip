@@ -1,0 +1,410 @@
+// SAM 3 vision-encoder kernels for gfx950: the non-linear parts of the ViT
+// prefix and block (src/models/sam3/vision.hpp:157-272) around the quantized
+// linears.
+//   layer_norm_kernel : ggml_norm * w + b over one 1024-float row per wave,
+//                       optionally adding the tiled position embedding first
+//                       and writing rows in window order (ggml_win_part)
+//   pack_qkv_kernel   : q/k/v columns of the qkv product -> per-head fp16
+//                       operands, complex RoPE on q and k, v transposed
+//   attention_kernel  : softmax(Q K^T) V per window and head on
+//                       v_mfma_f32_32x32x16_f16 with an online softmax in F32
+//   patch_*_kernel    : the 14x14 patch convolution as a split-fp16 GEMM
+// Arithmetic follows the reference graph's order (products rounded before
+// adds, no contraction).
+#include "internal.hpp"
+
+#pragma clang fp contract(off)
+
+namespace samhip {
+
+namespace {
+
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ floatx4 ld4(const float* p) { return *reinterpret_cast<const floatx4*>(p); }
+
+// ---------------------------------------------------------------------------
+// Layer norm: one wave per row of E = 256 * CH floats.
+// ---------------------------------------------------------------------------
+template <int CH>
+__global__ __launch_bounds__(256) void layer_norm_kernel(const float* __restrict__ x, const float* __restrict__ add,
+                                                         int add_grid, int gw, int ws, const float* __restrict__ w,
+                                                         const float* __restrict__ b, float eps, float* __restrict__ y,
+                                                         int rows) {
+    constexpr int E = 256 * CH;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const int lane = threadIdx.x & 63;
+    const int gy = r / gw, gx = r - gy * gw;
+    const float* xr = x + int64_t(r) * E;
+    const float* ar = add ? add + int64_t((gy % add_grid) * add_grid + gx % add_grid) * E : nullptr;
+    floatx4 v[CH];
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        v[c] = ld4(xr + 256 * c + 4 * lane);
+        if (ar) {
+            const floatx4 a = ld4(ar + 256 * c + 4 * lane);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[c][i] = v[c][i] + a[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s += v[c][i];
+    }
+    const float mean = wave_sum(s) / float(E);
+    float s2 = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float d = v[c][i] - mean;
+            v[c][i] = d;
+            s2 += d * d;
+        }
+    const float variance = wave_sum(s2) / float(E);
+    const float scale = 1.0f / sqrtf(variance + eps);
+    int64_t dst = r;
+    if (ws > 0) {
+        const int win = (gy / ws) * (gw / ws) + gx / ws;
+        dst = int64_t(win) * ws * ws + (gy % ws) * ws + gx % ws;
+    }
+    float* yr = y + dst * E;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int k = 256 * c + 4 * lane;
+        floatx4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float t = v[c][i] * scale;
+            if (w) t = t * w[k + i];
+            if (b) t = t + b[k + i];
+            o[i] = t;
+        }
+        *reinterpret_cast<floatx4*>(yr + k) = o;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// q/k/v packing with RoPE.  Block: 64 tokens of one (batch, head); thread t
+// owns token t/4 and the 16 head dims 16*(t%4)..; v goes through LDS to be
+// written transposed.
+// ---------------------------------------------------------------------------
+constexpr int VT_STRIDE = 72;   // halves per LDS row of the v transpose
+
+__global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                       const float* __restrict__ v, int64_t ld,
+                                                       const float* __restrict__ freqs, float q_scale,
+                                                       _Float16* __restrict__ qh, _Float16* __restrict__ kh,
+                                                       _Float16* __restrict__ vt, int H, int N, int Np) {
+    __shared__ __attribute__((aligned(16))) _Float16 vl[64 * VT_STRIDE];
+    const int n0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z;
+    const int t = threadIdx.x, tok = t >> 2, d0 = 16 * (t & 3);
+    const int n = n0 + tok;
+    const bool valid = n < N;
+    const int64_t src = (int64_t(b) * N + n) * ld + h * 64 + d0;
+    const int64_t bh = int64_t(b) * H + h;
+    const int64_t dst = (bh * Np + n) * 64 + d0;
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+        float xs[16];
+        if (valid) {
+            const float* p = (which ? k : q) + src;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const floatx4 f = ld4(p + 4 * j);
+                xs[4 * j] = f[0], xs[4 * j + 1] = f[1], xs[4 * j + 2] = f[2], xs[4 * j + 3] = f[3];
+            }
+            if (freqs) {
+                // pair i of the head: (x[2i], x[2i+1]) * (cos_i + j sin_i)
+                const float* f = freqs + (int64_t(n) * 32 + d0 / 2) * 2;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float re = xs[2 * i], im = xs[2 * i + 1], c = f[2 * i], s = f[2 * i + 1];
+                    const float a = re * c, bb = im * s, cc = re * s, dd = im * c;
+                    xs[2 * i] = a - bb;
+                    xs[2 * i + 1] = cc + dd;
+                }
+            }
+            if (!which)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) xs[j] = xs[j] * q_scale;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) xs[j] = 0.f;
+        }
+        half8 lo, hi;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            lo[j] = (_Float16)xs[j];
+            hi[j] = (_Float16)xs[8 + j];
+        }
+        half8* o = reinterpret_cast<half8*>((which ? kh : qh) + dst);
+        o[0] = lo;
+        o[1] = hi;
+    }
+    {
+        float xs[16];
+        if (valid) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const floatx4 f = ld4(v + src + 4 * j);
+                xs[4 * j] = f[0], xs[4 * j + 1] = f[1], xs[4 * j + 2] = f[2], xs[4 * j + 3] = f[3];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) xs[j] = 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) vl[(d0 + j) * VT_STRIDE + tok] = (_Float16)xs[j];
+    }
+    __syncthreads();
+    const int d = t >> 2, c0 = 16 * (t & 3);
+    const half8* s = reinterpret_cast<const half8*>(vl + d * VT_STRIDE + c0);
+    half8* o = reinterpret_cast<half8*>(vt + (bh * 64 + d) * Np + n0 + c0);
+    o[0] = s[0];
+    o[1] = s[1];
+}
+
+// ---------------------------------------------------------------------------
+// Attention.  Workgroup: 128 queries (4 waves x 32) of one (batch, head);
+// 64-key tiles of K [key][d] and V^T [d][key] double-buffered in LDS.
+// Each wave computes S^T = K Q^T (lane: query l%32, 16 keys per 32-key
+// tile), so the softmax statistics of a query sit in one lane pair (l,
+// l^32), and O^T = V^T P^T with P^T used as the B operand straight from the
+// S^T accumulator registers (the K index of both operands is the same
+// permutation of the tile's keys).
+// ---------------------------------------------------------------------------
+constexpr int K_STRIDE = 72;   // halves per LDS key row (144 B: conflict-free 16-byte reads)
+constexpr int V_STRIDE = 68;   // halves per LDS d row (136 B: conflict-free 8-byte reads)
+constexpr float LOG2E = 1.44269504088896340736f;
+
+__global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restrict__ qh, const _Float16* __restrict__ kh,
+                                                        const _Float16* __restrict__ vt, float* __restrict__ out,
+                                                        int64_t ldo, int H, int N, int Np) {
+    __shared__ __attribute__((aligned(16))) _Float16 ks[2][64 * K_STRIDE];
+    __shared__ __attribute__((aligned(16))) _Float16 vs[2][64 * V_STRIDE];
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 31, hh = lane >> 5;
+    const int64_t bh = int64_t(b) * H + h;
+    const _Float16* Q = qh + bh * Np * 64;
+    const _Float16* Kg = kh + bh * Np * 64;
+    const _Float16* Vg = vt + bh * 64 * Np;
+    const int q0 = blockIdx.x * 128 + wave * 32;
+    const int qrow = min(q0 + li, Np - 1);
+
+    half8 qf[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const half8*>(Q + int64_t(qrow) * 64 + 16 * s + 8 * hh);
+
+    // tile loads: thread t moves 16-byte chunks t and t + 256 of each tile
+    half8 kreg[2], vreg[2];
+    auto gload = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = tid + 256 * i, r = idx >> 3, c = idx & 7;
+            kreg[i] = *reinterpret_cast<const half8*>(Kg + int64_t(kb * 64 + r) * 64 + 8 * c);
+            vreg[i] = *reinterpret_cast<const half8*>(Vg + int64_t(r) * Np + kb * 64 + 8 * c);
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = tid + 256 * i, r = idx >> 3, c = idx & 7;
+            *reinterpret_cast<half8*>(&ks[buf][r * K_STRIDE + 8 * c]) = kreg[i];
+            half4* vp = reinterpret_cast<half4*>(&vs[buf][r * V_STRIDE + 8 * c]);
+            vp[0] = half4{vreg[i][0], vreg[i][1], vreg[i][2], vreg[i][3]};
+            vp[1] = half4{vreg[i][4], vreg[i][5], vreg[i][6], vreg[i][7]};
+        }
+    };
+
+    floatx16 o0, o1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o0[r] = o1[r] = 0.f;
+    float mrun = -__builtin_inff(), lsum = 0.f;
+    const int nkb = Np / 64;
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int buf = kb & 1;
+        if (kb + 1 < nkb) gload(kb + 1);
+        const _Float16* kt = ks[buf];
+        floatx16 s0, s1;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s0[r] = s1[r] = 0.f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const half8 a0 = *reinterpret_cast<const half8*>(kt + li * K_STRIDE + 16 * s + 8 * hh);
+            const half8 a1 = *reinterpret_cast<const half8*>(kt + (32 + li) * K_STRIDE + 16 * s + 8 * hh);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qf[s], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qf[s], s1, 0, 0, 0);
+        }
+        // keys past N (only in the last tile)
+        const int kbase = kb * 64;
+        if (kbase + 64 > N) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kbase + 8 * (r >> 2) + 4 * hh + (r & 3);
+                if (key >= N) s0[r] = -__builtin_inff();
+                if (key + 32 >= N) s1[r] = -__builtin_inff();
+            }
+        }
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(mrun, mx);
+        const float alpha = exp2f((mrun - mnew) * LOG2E);
+        mrun = mnew;
+        const float mb = mnew * LOG2E;
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            s0[r] = exp2f(__builtin_fmaf(s0[r], LOG2E, -mb));
+            s1[r] = exp2f(__builtin_fmaf(s1[r], LOG2E, -mb));
+            ps += s0[r] + s1[r];
+        }
+        lsum = lsum * alpha + ps;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            o0[r] = o0[r] * alpha;
+            o1[r] = o1[r] * alpha;
+        }
+        half8 pf[4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            pf[0][j] = (_Float16)s0[j];
+            pf[1][j] = (_Float16)s0[8 + j];
+            pf[2][j] = (_Float16)s1[j];
+            pf[3][j] = (_Float16)s1[8 + j];
+        }
+        const _Float16* vtile = vs[buf];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int kofs = 32 * (u >> 1) + 16 * (u & 1) + 4 * hh;
+            const half4 a_lo0 = *reinterpret_cast<const half4*>(vtile + li * V_STRIDE + kofs);
+            const half4 a_hi0 = *reinterpret_cast<const half4*>(vtile + li * V_STRIDE + kofs + 8);
+            const half4 a_lo1 = *reinterpret_cast<const half4*>(vtile + (32 + li) * V_STRIDE + kofs);
+            const half4 a_hi1 = *reinterpret_cast<const half4*>(vtile + (32 + li) * V_STRIDE + kofs + 8);
+            const half8 a0 = __builtin_shufflevector(a_lo0, a_hi0, 0, 1, 2, 3, 4, 5, 6, 7);
+            const half8 a1 = __builtin_shufflevector(a_lo1, a_hi1, 0, 1, 2, 3, 4, 5, 6, 7);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, pf[u], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, pf[u], o1, 0, 0, 0);
+        }
+        if (kb + 1 < nkb) {
+            sstore(buf ^ 1);
+            __syncthreads();
+        }
+    }
+    const float inv = 1.0f / (lsum + __shfl_xor(lsum, 32, 64));
+    const int qo = q0 + li;
+    if (qo < N) {
+        float* orow = out + (int64_t(b) * N + qo) * ldo + h * 64;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int d0 = 8 * g + 4 * hh;
+            *reinterpret_cast<floatx4*>(orow + d0) =
+                floatx4{o0[4 * g] * inv, o0[4 * g + 1] * inv, o0[4 * g + 2] * inv, o0[4 * g + 3] * inv};
+            *reinterpret_cast<floatx4*>(orow + 32 + d0) =
+                floatx4{o1[4 * g] * inv, o1[4 * g + 1] * inv, o1[4 * g + 2] * inv, o1[4 * g + 3] * inv};
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Patch convolution operands (split fp16): v = hi + lo with hi = fp16(v),
+// lo = fp16(v - hi).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void patch_columns_kernel(const float* __restrict__ image, int img, int patch,
+                                                            _Float16* __restrict__ a, float* __restrict__ row_scale,
+                                                            int kp) {
+    const int grid = img / patch, pp = patch * patch, kk = 3 * pp;
+    const int64_t tokens = int64_t(grid) * grid;
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= tokens * kp) return;
+    const int64_t t = i / kp;
+    const int c = int(i - t * kp);
+    float v = 0.f;
+    if (c < kk) {
+        const int ci = c / pp, rem = c - ci * pp, ky = rem / patch, kx = rem - ky * patch;
+        const int oy = int(t / grid), ox = int(t - int64_t(oy) * grid);
+        v = image[(int64_t(ci) * img + oy * patch + ky) * img + ox * patch + kx];
+    }
+    const _Float16 hi = (_Float16)v;
+    const _Float16 lo = (_Float16)(v - (float)hi);
+    _Float16* row = a + t * 3 * kp;
+    row[c] = hi;
+    row[kp + c] = hi;
+    row[2 * kp + c] = lo;
+    if (c == 0) row_scale[t] = 1.0f;
+}
+
+__global__ __launch_bounds__(256) void patch_kernel_kernel(const float* __restrict__ kernel, int E, int patch,
+                                                           _Float16* __restrict__ w, int kp) {
+    const int kk = 3 * patch * patch;
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= int64_t(E) * kp) return;
+    const int64_t e = i / kp;
+    const int c = int(i - e * kp);
+    const float v = c < kk ? kernel[e * kk + c] : 0.f;
+    const _Float16 hi = (_Float16)v;
+    const _Float16 lo = (_Float16)(v - (float)hi);
+    _Float16* row = w + e * 3 * kp;
+    row[c] = hi;
+    row[kp + c] = lo;
+    row[2 * kp + c] = hi;
+}
+
+}  // namespace
+
+void launch_layer_norm(const float* x, const float* add, int add_grid, int gw, int gh, int ws, const float* w,
+                       const float* b, float eps, float* y, int rows, int E, hipStream_t stream) {
+    (void)gh;
+    const dim3 grid((rows + 3) / 4), block(256);
+    switch (E / 256) {
+        case 1: hipLaunchKernelGGL(layer_norm_kernel<1>, grid, block, 0, stream, x, add, add_grid, gw, ws, w, b, eps, y, rows); break;
+        case 2: hipLaunchKernelGGL(layer_norm_kernel<2>, grid, block, 0, stream, x, add, add_grid, gw, ws, w, b, eps, y, rows); break;
+        case 3: hipLaunchKernelGGL(layer_norm_kernel<3>, grid, block, 0, stream, x, add, add_grid, gw, ws, w, b, eps, y, rows); break;
+        case 4: hipLaunchKernelGGL(layer_norm_kernel<4>, grid, block, 0, stream, x, add, add_grid, gw, ws, w, b, eps, y, rows); break;
+        case 5: hipLaunchKernelGGL(layer_norm_kernel<5>, grid, block, 0, stream, x, add, add_grid, gw, ws, w, b, eps, y, rows); break;
+        case 6: hipLaunchKernelGGL(layer_norm_kernel<6>, grid, block, 0, stream, x, add, add_grid, gw, ws, w, b, eps, y, rows); break;
+        case 8: hipLaunchKernelGGL(layer_norm_kernel<8>, grid, block, 0, stream, x, add, add_grid, gw, ws, w, b, eps, y, rows); break;
+        default: break;   // callers check layer_norm_supported
+    }
+}
+
+void launch_pack_qkv(const float* q, const float* k, const float* v, int64_t ld, const float* freqs, float q_scale,
+                     _Float16* qh, _Float16* kh, _Float16* vt, int B, int H, int N, hipStream_t stream) {
+    const int np = (N + 63) / 64 * 64;
+    hipLaunchKernelGGL(pack_qkv_kernel, dim3(unsigned(np / 64), unsigned(H), unsigned(B)), dim3(256), 0, stream, q, k,
+                       v, ld, freqs, q_scale, qh, kh, vt, H, N, np);
+}
+
+void launch_attention(const _Float16* qh, const _Float16* kh, const _Float16* vt, float* out, int64_t ldo, int B,
+                      int H, int N, hipStream_t stream) {
+    const int np = (N + 63) / 64 * 64;
+    hipLaunchKernelGGL(attention_kernel, dim3(unsigned((np + 127) / 128), unsigned(H), unsigned(B)), dim3(256), 0,
+                       stream, qh, kh, vt, out, ldo, H, N, np);
+}
+
+void launch_patch_columns(const float* image, int img, int patch, _Float16* a, float* row_scale, int kp,
+                          hipStream_t stream) {
+    const int64_t grid = img / patch, n = grid * grid * kp;
+    hipLaunchKernelGGL(patch_columns_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, image, img, patch,
+                       a, row_scale, kp);
+}
+
+void launch_patch_kernel(const float* kernel, int E, int patch, _Float16* w, int kp, hipStream_t stream) {
+    const int64_t n = int64_t(E) * kp;
+    hipLaunchKernelGGL(patch_kernel_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, kernel, E, patch, w,
+                       kp);
+}
+
+}  // namespace samhip

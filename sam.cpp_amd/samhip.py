@@ -51,6 +51,23 @@ class KernelRecord(ctypes.Structure):
                 ("n", ctypes.c_int64), ("k", ctypes.c_int64), ("ms", ctypes.c_float)]
 
 
+class VitBlockDesc(ctypes.Structure):
+    """samhip_vit_block_desc."""
+    _fields_ = [("version", ctypes.c_int32), ("embed", ctypes.c_int32), ("heads", ctypes.c_int32),
+                ("mlp", ctypes.c_int32), ("grid_w", ctypes.c_int32), ("grid_h", ctypes.c_int32),
+                ("window", ctypes.c_int32)] + \
+               [(n, ctypes.c_void_p) for n in ("norm1_w", "norm1_b", "norm2_w", "norm2_b")] + \
+               [(n, Tensor) for n in ("qkv_w", "proj_w", "fc1_w", "fc2_w")] + \
+               [(n, ctypes.c_void_p) for n in ("qkv_b", "proj_b", "fc1_b", "fc2_b", "freqs_cis")]
+
+
+class VitPrefixDesc(ctypes.Structure):
+    """samhip_vit_prefix_desc."""
+    _fields_ = [("version", ctypes.c_int32), ("image_size", ctypes.c_int32), ("patch", ctypes.c_int32),
+                ("embed", ctypes.c_int32), ("pos_grid", ctypes.c_int32)] + \
+               [(n, ctypes.c_void_p) for n in ("patch_w", "pos_embed", "ln_pre_w", "ln_pre_b")]
+
+
 SIGNATURES = {
     "samhip_abi_version": ([], _I),
     "samhip_device_count": ([_P], _I),
@@ -76,6 +93,10 @@ SIGNATURES = {
     "samhip_capture_end": ([_P, ctypes.POINTER(_P)], _I),
     "samhip_graph_launch": ([_P, _P], _I),
     "samhip_graph_destroy": ([_P], None),
+    "samhip_vit_block": ([_P, ctypes.POINTER(VitBlockDesc), _P], _I),
+    "samhip_vit_prefix": ([_P, ctypes.POINTER(VitPrefixDesc), _P, _P], _I),
+    "samhip_layer_norm": ([_P, _P, _P, _I64, _I64, _P, _P, ctypes.c_float], _I),
+    "samhip_flash_attn": ([_P, _P, _P, _P, _I64, _P, _I64, _I64, _I32, _I32, ctypes.c_float], _I),
 }
 
 _lib = None
@@ -282,6 +303,26 @@ class Context:
         self.dequantize_rows(qtype, src.ptr, row_bytes(qtype, k), dst.ptr, rows, k)
         return self.download(dst, (rows, k), np.float32)
 
+    def layer_norm(self, x, w=None, b=None, eps=1e-5):
+        """samhip_layer_norm on a device copy of numpy rows x [rows][n]."""
+        x = np.ascontiguousarray(x, np.float32)
+        rows, n = x.shape
+        xb, yb = self.upload(x), self.alloc(x.nbytes)
+        wb = self.upload(np.ascontiguousarray(w, np.float32)) if w is not None else None
+        bb = self.upload(np.ascontiguousarray(b, np.float32)) if b is not None else None
+        check(lib().samhip_layer_norm(self.handle, xb.ptr, yb.ptr, rows, n, wb.ptr if wb else None,
+                                      bb.ptr if bb else None, eps))
+        return self.download(yb, (rows, n), np.float32)
+
+    def flash_attn(self, q, k, v, batches, heads, scale, head_dim=64):
+        """samhip_flash_attn on device copies of q, k, v [batches*n][heads*head_dim]."""
+        q, k, v = (np.ascontiguousarray(a, np.float32) for a in (q, k, v))
+        rows, ld = q.shape
+        qb, kb, vb, ob = self.upload(q), self.upload(k), self.upload(v), self.alloc(rows * heads * head_dim * 4)
+        check(lib().samhip_flash_attn(self.handle, qb.ptr, kb.ptr, vb.ptr, ld, ob.ptr, batches, rows // batches,
+                                      heads, head_dim, scale))
+        return self.download(ob, (rows, heads * head_dim), np.float32)
+
     def matmul(self, qtype, w_packed, x, w_row_offset=0, w_rows=None, x_row_stride=None):
         """Y = X W^T through samhip_mul_mat on device copies of numpy inputs.
 
@@ -308,3 +349,62 @@ class Context:
         yt = tensor(F32, n, m, yb.ptr)
         self.mul_mat(wt, xt, yt)
         return self.download(yb, (m, n), np.float32)
+
+
+class VitBlock:
+    """One SAM 3 ViT block's weights on the device (numpy arrays in, as
+    produced for the oracle: norm*_w/b, {qkv,proj,fc1,fc2}_{type,w,b},
+    freqs) and its samhip_vit_block descriptor."""
+
+    def __init__(self, ctx, weights, embed, heads, mlp, grid_w, grid_h, window):
+        self.ctx = ctx
+        self.buffers = {}
+        d = VitBlockDesc()
+        d.version = ABI_VERSION
+        d.embed, d.heads, d.mlp, d.grid_w, d.grid_h, d.window = embed, heads, mlp, grid_w, grid_h, window
+        for n in ("norm1_w", "norm1_b", "norm2_w", "norm2_b", "qkv_b", "proj_b", "fc1_b", "fc2_b"):
+            self.buffers[n] = ctx.upload(np.ascontiguousarray(weights[n], np.float32))
+            setattr(d, n, self.buffers[n].ptr)
+        if weights.get("freqs") is not None:
+            self.buffers["freqs"] = ctx.upload(np.ascontiguousarray(weights["freqs"], np.float32))
+            d.freqs_cis = self.buffers["freqs"].ptr
+        shapes = {"qkv": (embed, 3 * embed), "proj": (embed, embed), "fc1": (embed, mlp), "fc2": (mlp, embed)}
+        for n, (k, rows) in shapes.items():
+            qt = weights[n + "_type"]
+            self.buffers[n] = ctx.upload(np.ascontiguousarray(weights[n + "_w"], np.uint8))
+            setattr(d, n + "_w", tensor(qt, k, rows, self.buffers[n].ptr))
+        self.desc = d
+
+    def forward(self, x_buf):
+        """Runs the block in place on device buffer x_buf."""
+        check(lib().samhip_vit_block(self.ctx.handle, ctypes.byref(self.desc), x_buf.ptr))
+
+    def free(self):
+        for b in self.buffers.values():
+            b.free()
+        self.buffers = {}
+
+
+class VitPrefix:
+    """The ViT prefix weights on the device: patch kernel [E][3][p][p]
+    (ggml {p, p, 3, E}), pos_embed [pg][pg][E], ln_pre w/b."""
+
+    def __init__(self, ctx, patch_w, pos_embed, ln_w, ln_b, image_size, patch, embed, pos_grid):
+        self.ctx = ctx
+        self.buffers = {n: ctx.upload(np.ascontiguousarray(a, np.float32))
+                        for n, a in (("patch_w", patch_w), ("pos_embed", pos_embed), ("ln_pre_w", ln_w),
+                                     ("ln_pre_b", ln_b))}
+        d = VitPrefixDesc()
+        d.version = ABI_VERSION
+        d.image_size, d.patch, d.embed, d.pos_grid = image_size, patch, embed, pos_grid
+        for n, b in self.buffers.items():
+            setattr(d, n, b.ptr)
+        self.desc = d
+
+    def forward(self, image_buf, x_buf):
+        check(lib().samhip_vit_prefix(self.ctx.handle, ctypes.byref(self.desc), image_buf.ptr, x_buf.ptr))
+
+    def free(self):
+        for b in self.buffers.values():
+            b.free()
+        self.buffers = {}
