@@ -335,6 +335,202 @@ def text_stream(args, sh, ctx, fmt):
     }
 
 
+ENC = {"E": 1024, "HEADS": 16, "MLP": 4736, "GRID": 72, "WINDOW": 24, "IMG": 1008, "PATCH": 14, "POS_GRID": 24,
+       "DEPTH": 32, "GLOBAL": (7, 15, 23, 31)}
+
+
+def axial_rope_table(width, height, hd, theta=10000.0):
+    """Axial 2-D RoPE table (cos, sin) [width*height][hd/2][2]: hd/4
+    frequencies per axis, token t = y*width + x.  A converted checkpoint
+    carries its own table (vit.blocks.N.attn.freqs_cis); any unit-modulus
+    table costs the same."""
+    freqs = 1.0 / theta ** (np.arange(0, hd, 4)[: hd // 4].astype(np.float64) / hd)
+    t = np.arange(width * height)
+    ang = np.concatenate([np.outer(t % width, freqs), np.outer(t // width, freqs)], axis=1)
+    return np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
+
+
+class Encoder:
+    """A random-init SAM 3 vision encoder on the device (1008 px, 72x72
+    tokens, width 1024, 32 pre-LN blocks, 16 heads, MLP 4736, window 24 with
+    global attention in blocks 7/15/23/31): qkv/proj/fc1 in the K-quant
+    `qt`, fc2 in Q8_0 (4736-wide rows), norms/biases/embeddings F32.  Linear
+    weights N(0, 0.02^2) packed on the device by samhip_quantize_rows."""
+
+    def __init__(self, sh, ctx, qt, seed=0):
+        import ctypes
+        self.sh, self.ctx, self.ctypes = sh, ctx, ctypes
+        e = ENC
+        E, H, MLP, G, WS = e["E"], e["HEADS"], e["MLP"], e["GRID"], e["WINDOW"]
+        rng = np.random.default_rng(seed)
+        self.keep, self.blocks = [], []
+        tables = {False: ctx.upload(axial_rope_table(WS, WS, E // H)), True: ctx.upload(axial_rope_table(G, G, E // H))}
+        self.keep += list(tables.values())
+
+        def f32(a):
+            b = ctx.upload(np.ascontiguousarray(a, np.float32))
+            self.keep.append(b)
+            return b.ptr
+
+        def packed(t, n, k):
+            wf = ctx.upload((rng.standard_normal((n, k), dtype=np.float32) * 0.02))
+            wq = ctx.alloc(n * sh.row_bytes(t, k))
+            ctx.quantize_rows(t, wf.ptr, 4 * k, wq.ptr, n, k, sh.ROUND_REF)
+            ctx.synchronize()
+            wf.free()
+            self.keep.append(wq)
+            return sh.tensor(t, k, n, wq.ptr)
+
+        for i in range(e["DEPTH"]):
+            glob = i in e["GLOBAL"]
+            d = sh.VitBlockDesc()
+            d.version = sh.ABI_VERSION
+            d.embed, d.heads, d.mlp, d.grid_w, d.grid_h, d.window = E, H, MLP, G, G, 0 if glob else WS
+            d.norm1_w, d.norm2_w = f32(1 + 0.1 * rng.standard_normal(E)), f32(1 + 0.1 * rng.standard_normal(E))
+            d.norm1_b, d.norm2_b = f32(0.05 * rng.standard_normal(E)), f32(0.05 * rng.standard_normal(E))
+            d.qkv_b, d.proj_b = f32(0.02 * rng.standard_normal(3 * E)), f32(0.02 * rng.standard_normal(E))
+            d.fc1_b, d.fc2_b = f32(0.02 * rng.standard_normal(MLP)), f32(0.02 * rng.standard_normal(E))
+            d.freqs_cis = tables[glob].ptr
+            d.qkv_w, d.proj_w = packed(qt, 3 * E, E), packed(qt, E, E)
+            d.fc1_w, d.fc2_w = packed(qt, MLP, E), packed(sh.Q8_0, E, MLP)
+            self.blocks.append(d)
+        self.prefix = sh.VitPrefix(ctx, rng.standard_normal((E, 3, e["PATCH"], e["PATCH"]), dtype=np.float32) * 0.02,
+                                   rng.standard_normal((e["POS_GRID"], e["POS_GRID"], E), dtype=np.float32) * 0.1,
+                                   1 + 0.1 * rng.standard_normal(E), 0.05 * rng.standard_normal(E), e["IMG"],
+                                   e["PATCH"], E, e["POS_GRID"])
+        self.image = ctx.upload(np.random.default_rng(seed + 1).standard_normal((3, e["IMG"], e["IMG"]), dtype=np.float32))
+        self.x = ctx.alloc(G * G * E * 4)
+        self.flops = self._flops()
+
+    def _flops(self):
+        e = ENC
+        T, E, MLP, hd = e["GRID"] ** 2, e["E"], e["MLP"], e["E"] // e["HEADS"]
+        lin = 2.0 * T * E * (3 * E + E + 2 * MLP)
+        att_w = 4.0 * T * (e["WINDOW"] ** 2) * E          # QK^T and PV over each token's window
+        att_g = 4.0 * T * T * E
+        kp = -(-3 * e["PATCH"] ** 2 // 128) * 128
+        return 2.0 * T * E * 3 * kp + sum(lin + (att_g if i in e["GLOBAL"] else att_w) for i in range(e["DEPTH"]))
+
+    def forward(self):
+        self.prefix.forward(self.image, self.x)
+        for d in self.blocks:
+            self.sh.check(self.sh.lib().samhip_vit_block(self.ctx.handle, self.ctypes.byref(d), self.x.ptr))
+
+    def host_block(self, i):
+        """Block i's weights as numpy arrays (device bytes downloaded) for the oracle."""
+        d, sh, ctx = self.blocks[i], self.sh, self.ctx
+        e = ENC
+        E, MLP = e["E"], e["MLP"]
+        out = {}
+
+        class At:
+            def __init__(self, ptr):
+                self.ptr = ptr
+
+        def get(ptr, n):
+            return ctx.download(At(ptr), (n,), np.float32)
+        for n, sz in (("norm1_w", E), ("norm1_b", E), ("norm2_w", E), ("norm2_b", E), ("qkv_b", 3 * E),
+                      ("proj_b", E), ("fc1_b", MLP), ("fc2_b", E)):
+            out[n] = get(getattr(d, n), sz)
+        for n in ("qkv", "proj", "fc1", "fc2"):
+            t = getattr(d, n + "_w")
+            rows, rb = t.ne[1], sh.row_bytes(t.type, t.ne[0])
+            out[n + "_type"] = t.type
+            out[n + "_w"] = ctx.download(At(t.data), (rows, rb), np.uint8)
+        glob = i in e["GLOBAL"]
+        n_tok = e["GRID"] ** 2 if glob else e["WINDOW"] ** 2
+        out["freqs"] = ctx.download(At(d.freqs_cis), (n_tok, E // e["HEADS"] // 2, 2), np.float32)
+        return out
+
+
+def encoder_cpu_baseline(enc, seconds_cap=60.0):
+    """The oracle's restatement of the same encoder (native quantized
+    linears, exact softmax attention) on the host cores, on a bounded
+    sample: the prefix, one windowed and one global block, extrapolated to
+    the 28 windowed + 4 global blocks of one image."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as O
+    O.lib()
+    threads = O.max_threads()
+    e = ENC
+    G, E = e["GRID"], e["E"]
+    x = np.random.default_rng(5).standard_normal((G * G, E)).astype(np.float32)
+    times = {}
+    for label, i in (("windowed", 0), ("global", e["GLOBAL"][0])):
+        w = enc.host_block(i)
+        t0 = time.perf_counter()
+        O.vit_block(w, x, G, G, E, e["HEADS"], e["MLP"], 0 if i in e["GLOBAL"] else e["WINDOW"], O.ROUND_X86, threads)
+        times[label] = time.perf_counter() - t0
+        if sum(times.values()) > seconds_cap:
+            break
+    rng = np.random.default_rng(6)
+    img = rng.standard_normal((3, e["IMG"], e["IMG"])).astype(np.float32)
+    t0 = time.perf_counter()
+    O.vit_prefix(img, e["PATCH"], rng.standard_normal((E, 3, e["PATCH"], e["PATCH"])).astype(np.float32) * 0.02,
+                 rng.standard_normal((e["POS_GRID"], e["POS_GRID"], E)).astype(np.float32) * 0.1, e["POS_GRID"],
+                 np.ones(E, np.float32), np.zeros(E, np.float32), E, threads)
+    times["prefix"] = time.perf_counter() - t0
+    n_glob = len(e["GLOBAL"])
+    per_image = times["prefix"] + (e["DEPTH"] - n_glob) * times["windowed"] + n_glob * times.get("global", times["windowed"])
+    return {"value": round(per_image * 1e3, 1), "unit": "ms/image", "cores": threads, "kind": "port",
+            "sample": f"prefix {times['prefix']:.2f} s + one windowed block {times['windowed']:.2f} s + one global "
+                      f"block {times.get('global', float('nan')):.2f} s, extrapolated to 28 windowed + 4 global "
+                      f"blocks; oracle/vit_oracle.c (native Q8 linears, exact-softmax attention), OpenMP"}
+
+
+def encoder_measure(sh, ctx, enc, warmup, iters):
+    """ms/image of the forward (prefix + 32 blocks) and its kernel breakdown."""
+    for _ in range(warmup):
+        enc.forward()
+    ctx.synchronize()
+    ctx.trace_begin()
+    enc.forward()
+    prof = ctx.trace_end(capacity=1 << 12)
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        enc.forward()
+    ctx.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / iters
+    by = {}
+    for name, wt, m, n, k, kms in prof:
+        by.setdefault(name, []).append((m, n, k, kms))
+    breakdown = {name: round(sum(r[3] for r in rs), 4) for name, rs in sorted(by.items(), key=lambda t: -sum(r[3] for r in t[1]))}
+    return ms, prof, breakdown
+
+
+def encoder_workload(args, sh, ctx):
+    """--workload encoder: the full vision encoder forward, ms/image."""
+    qt = {"q4_k": sh.Q4_K, "q5_k": sh.Q5_K, "q6_k": sh.Q6_K, "q8_0": sh.Q8_0}[args.format]
+    log("building the vision encoder")
+    enc = Encoder(sh, ctx, qt)
+    ms, prof, breakdown = encoder_measure(sh, ctx, enc, args.warmup, args.steps)
+    # dominant kernel's roofline (MFMA): the fc1 product of a block
+    fc1 = [r for r in prof if r[0] == "vit_fc1"]
+    m_, n_, k_ = fc1[0][2], fc1[0][3], fc1[0][4]
+    fc1_ms = float(np.mean([r[5] for r in fc1]))
+    ach = 2.0 * m_ * n_ * k_ / (fc1_ms * 1e-3) / 1e12
+    result = {
+        "metric": "SAM3 vision encode ms/image @1008px", "value": round(ms, 3), "unit": "ms/image", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": f"SAM 3 vision encoder forward, 1008x1008x3 image, 72x72 tokens, width 1024, 32 blocks "
+                               f"(window 24, global 7/15/23/31), 16 heads, MLP 4736; {sh.TYPE_NAMES[qt]} qkv/proj/fc1, "
+                               f"q8_0 fc2; random-init weights", "batch": 1, "parallelism": "single-gpu"},
+        "tflops_effective": round(enc.flops / (ms * 1e-3) / 1e12, 2),
+        "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(ach / PEAK_FP16_TFLOPS, 4), "traffic": None, "kernel": "vit_fc1 (fp16 GEMM + bias + GELU)",
+                     "shape": {"M": m_, "N": n_, "K": k_}, "launch_ms": round(fc1_ms, 5)},
+        "kernel_ms_per_image": breakdown,
+        "device": ctx.query().device_name.decode(),
+    }
+    if not args.no_cpu_baseline:
+        log("timing the encoder CPU baseline")
+        result["cpu_baseline"] = encoder_cpu_baseline(enc)
+    else:
+        result["cpu_baseline"] = None
+    return result
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -346,10 +542,13 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--trace", choices=["dominant", "all", "none"], default="dominant",
                     help="launches bracketed by HIP events inside the timed region")
-    ap.add_argument("--workload", choices=["vit", "text"], default="vit",
-                    help="vit: the ViT linear sweep (headline); text: the M=32 text-encoder linear stream")
-    ap.add_argument("--format", choices=["q8_0", "q4_k", "q5_k", "q6_k"], default="q8_0",
-                    help="weight format of the text stream")
+    ap.add_argument("--workload", choices=["vit", "text", "encoder"], default="vit",
+                    help="vit: the ViT linear sweep (headline, with the encoder's ms/image beside it); text: the "
+                         "M=32 text-encoder linear stream; encoder: the vision encoder forward alone")
+    ap.add_argument("--format", choices=["q8_0", "q4_k", "q5_k", "q6_k"], default=None,
+                    help="weight format of the text stream (default q8_0) or of the encoder's K-quant linears "
+                         "(default q4_k)")
+    ap.add_argument("--no-encoder", action="store_true", help="skip the vision-encoder measurement of the headline run")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the plain copy used to scale HBM traffic counters")
     ap.add_argument("--summarize-profiles", metavar="DIR",
@@ -371,7 +570,13 @@ def main():
     compute = sh.COMPUTE_Q8_NATIVE if args.compute == "native" else sh.COMPUTE_F16
     ctx = sh.Context(0, compute, sh.ROUND_X86)
     if args.workload == "text":
-        result = text_stream(args, sh, ctx, args.format)
+        result = text_stream(args, sh, ctx, args.format or "q8_0")
+        ctx.close()
+        print(json.dumps(result), flush=True)
+        return
+    if args.workload == "encoder":
+        args.format = args.format or "q4_k"
+        result = encoder_workload(args, sh, ctx)
         ctx.close()
         print(json.dumps(result), flush=True)
         return
@@ -486,12 +691,31 @@ def main():
         "kernel_time_share": kernel_share,
         "device": ctx.query().device_name.decode(),
     }
-    ctx.close()
+    enc = None
+    if not args.no_encoder:
+        # the metric's second figure: the Q4_K vision encoder forward, measured
+        # after the sweep's timed region (its own warmup and timing)
+        for b in [o[7] for o in ops] + [o[8] for o in ops] + list(xbuf.values()):
+            b.free()
+        log("building the Q4_K vision encoder")
+        enc = Encoder(sh, ctx, sh.Q4_K)
+        enc_ms, _, breakdown = encoder_measure(sh, ctx, enc, 3, 10)
+        result["vision_encoder"] = {
+            "ms_per_image": round(enc_ms, 3), "images_per_s": round(1e3 / enc_ms, 2),
+            "tflops_effective": round(enc.flops / (enc_ms * 1e-3) / 1e12, 2),
+            "config": "1008x1008x3 image, 72x72 tokens, width 1024, 32 blocks (window 24, global 7/15/23/31), "
+                      "16 heads, MLP 4736; Q4_K qkv/proj/fc1, Q8_0 fc2; random-init weights; batch 1; 3 warmup + "
+                      "10 timed forwards",
+            "kernel_ms_per_image": breakdown}
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline([(p[0], p[1], p[2], p[3]) for p in ops], args.cpu_seconds, args.cpu_rows)
+        if enc is not None:
+            log("timing the encoder CPU baseline")
+            result["vision_encoder"]["cpu_baseline"] = encoder_cpu_baseline(enc)
     else:
         result["cpu_baseline"] = None
+    ctx.close()
     print(json.dumps(result), flush=True)
 
 
