@@ -95,6 +95,9 @@ struct samhip_context {
     // samhip_flash_attn); grown on demand, never while capturing
     void* work = nullptr;
     size_t work_bytes = 0;
+    // window-unpartition row table of the last (grid_w, grid_h, window)
+    int* row_map = nullptr;
+    int row_map_key[3] = {0, 0, 0};
 };
 
 namespace {
@@ -285,6 +288,7 @@ void samhip_context_destroy(samhip_context* ctx) {
     if (ctx->stream && ctx->stream != ctx->own_stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->staging) (void)hipFree(ctx->staging);
     if (ctx->work) (void)hipFree(ctx->work);
+    if (ctx->row_map) (void)hipFree(ctx->row_map);
     for (void* p : ctx->retired_staging) (void)hipFree(p);
     if (ctx->flag) (void)hipFree(ctx->flag);
     for (auto& r : ctx->trace) {
@@ -585,10 +589,34 @@ bool layer_norm_supported(int64_t n) {
     return n >= 256 && n <= 2048 && n % 256 == 0 && n != 1792;
 }
 
-// Tall product through staging + weight decode + the fp16 GEMM with an
-// epilogue; x rows are K contiguous floats (16-byte aligned), y rows ldy.
+// Row r of a window-order product (ggml_win_part of a gw x gh grid) returns
+// to grid row row_map[r] (ggml_win_unpart); built on the host once per shape.
+int ensure_row_map(samhip_context* ctx, int gw, int gh, int ws) {
+    if (ctx->row_map && ctx->row_map_key[0] == gw && ctx->row_map_key[1] == gh && ctx->row_map_key[2] == ws)
+        return SAMHIP_OK;
+    std::vector<int> map(size_t(gw) * gh);
+    const int npx = gw / ws;
+    for (int gy = 0; gy < gh; ++gy)
+        for (int gx = 0; gx < gw; ++gx) {
+            const int win = (gy / ws) * npx + gx / ws;
+            map[size_t(win) * ws * ws + (gy % ws) * ws + gx % ws] = gy * gw + gx;
+        }
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (ctx->row_map) HIP_TRY(hipFree(ctx->row_map), "hipFree");
+    ctx->row_map = nullptr;
+    HIP_TRY(hipMalloc(&ctx->row_map, map.size() * sizeof(int)), "hipMalloc row map");
+    HIP_TRY(hipMemcpy(ctx->row_map, map.data(), map.size() * sizeof(int), hipMemcpyHostToDevice), "hipMemcpy row map");
+    ctx->row_map_key[0] = gw;
+    ctx->row_map_key[1] = gh;
+    ctx->row_map_key[2] = ws;
+    return SAMHIP_OK;
+}
+
+// Tall product through staging (with the producing node folded in, `pre`)
+// + weight decode + the fp16 GEMM with an epilogue; x rows are K contiguous
+// floats (16-byte aligned), y rows ldy.
 int linear(samhip_context* ctx, const samhip_tensor& w, const float* x, int M, float* y, int64_t ldy,
-           const Epilogue& ep, const char* what) {
+           const Epilogue& ep, const char* what, const RowPre& pre = RowPre{}) {
     const int K = int(w.ne[0]), N = int(w.ne[1]);
     auto align256 = [](size_t v) { return (v + 255) & ~size_t(255); };
     const size_t rs_offset = align256(size_t(M) * size_t(K) * 2);
@@ -601,7 +629,8 @@ int linear(samhip_context* ctx, const samhip_tensor& w, const float* x, int M, f
     const int mode = ctx->compute == SAMHIP_COMPUTE_F16 ? T_F16 : vec_dot_type(w.type);
     const int x86 = ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0;
     int rc = traced(ctx, prep_name(mode), w.type, M, N, K, [&]() -> int {
-        if (!launch_prep(mode, w.type, x, K, M, K, a, K, rs, x86, w.data, int64_t(w.nb[1]), N, wh, K, ctx->stream))
+        if (!launch_prep(mode, w.type, x, K, M, K, a, K, rs, x86, w.data, int64_t(w.nb[1]), N, wh, K, ctx->stream,
+                         pre))
             return fail(SAMHIP_ERR_UNSUPPORTED, "%s: no staging kernel for K = %d", what, K);
         HIP_TRY(hipGetLastError(), "staging and weight decode launch");
         return SAMHIP_OK;
@@ -725,20 +754,24 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
     float* h1 = reinterpret_cast<float*>(wb + o_h1);
     _Float16 *qh = reinterpret_cast<_Float16*>(wb + o_qh), *kh = reinterpret_cast<_Float16*>(wb + o_kh),
              *vt = reinterpret_cast<_Float16*>(wb + o_vt);
-    const int iT = int(T), iE = int(E);
+    const int iT = int(T);
 
-    // attention half: LN1 (rows leave in window order), qkv + bias, RoPE and
-    // packing, attention, proj + bias + unpartition + residual -> x1
-    int rc = traced(ctx, "vit_layer_norm", T_F32, T, E, 0, [&]() -> int {
-        launch_layer_norm(x, nullptr, 1, int(GW), int(GH), int(WS), d->norm1_w, d->norm1_b, 1e-5f, ln, iT, iE,
-                          ctx->stream);
-        HIP_TRY(hipGetLastError(), "layer_norm launch");
-        return SAMHIP_OK;
-    });
-    if (rc) return rc;
+    // attention half: LN1 folded into the qkv staging (rows leave in window
+    // order), qkv + bias, RoPE and packing, attention, proj + bias +
+    // unpartition + residual -> x1
+    if (WS > 0)
+        if (int rc = ensure_row_map(ctx, int(GW), int(GH), int(WS))) return rc;
+    RowPre ln1;
+    ln1.kind = PRE_LAYER_NORM;
+    ln1.w = d->norm1_w;
+    ln1.b = d->norm1_b;
+    ln1.eps = 1e-5f;
+    ln1.ws = int(WS);
+    ln1.gw = int(GW);
     Epilogue e_qkv;
     e_qkv.bias = d->qkv_b;
-    if ((rc = linear(ctx, d->qkv_w, ln, iT, qkv, 3 * E, e_qkv, "vit_qkv"))) return rc;
+    int rc = linear(ctx, d->qkv_w, x, iT, qkv, 3 * E, e_qkv, "vit_qkv", ln1);
+    if (rc) return rc;
     rc = traced(ctx, "vit_pack_qkv", T_F32, T, 3 * E, 0, [&]() -> int {
         launch_pack_qkv(qkv, qkv + E, qkv + 2 * E, 3 * E, d->freqs_cis, 0.125f, qh, kh, vt, int(B), int(H), int(per),
                         ctx->stream);
@@ -755,28 +788,24 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
     Epilogue e_proj;
     e_proj.bias = d->proj_b;
     e_proj.res = x;
-    if (WS > 0) {
-        e_proj.ws = int(WS);
-        e_proj.gw = int(GW);
-        e_proj.gh = int(GH);
-    }
+    if (WS > 0) e_proj.row_map = ctx->row_map;
     if ((rc = linear(ctx, d->proj_w, ln, iT, x1, E, e_proj, "vit_proj"))) return rc;
 
-    // MLP half: LN2, fc1 + bias + GELU, fc2 + bias + residual -> x
-    rc = traced(ctx, "vit_layer_norm", T_F32, T, E, 0, [&]() -> int {
-        launch_layer_norm(x1, nullptr, 1, int(GW), int(GH), 0, d->norm2_w, d->norm2_b, 1e-5f, ln, iT, iE, ctx->stream);
-        HIP_TRY(hipGetLastError(), "layer_norm launch");
-        return SAMHIP_OK;
-    });
-    if (rc) return rc;
+    // MLP half: LN2 folded into the fc1 staging, fc1 + bias, erf-GELU folded
+    // into the fc2 staging, fc2 + bias + residual -> x
+    RowPre ln2 = ln1;
+    ln2.w = d->norm2_w;
+    ln2.b = d->norm2_b;
+    ln2.ws = 0;
     Epilogue e_fc1;
     e_fc1.bias = d->fc1_b;
-    e_fc1.gelu = true;
-    if ((rc = linear(ctx, d->fc1_w, ln, iT, h1, MLP, e_fc1, "vit_fc1"))) return rc;
+    if ((rc = linear(ctx, d->fc1_w, x1, iT, h1, MLP, e_fc1, "vit_fc1", ln2))) return rc;
+    RowPre gelu;
+    gelu.kind = PRE_GELU;
     Epilogue e_fc2;
     e_fc2.bias = d->fc2_b;
     e_fc2.res = x1;
-    return linear(ctx, d->fc2_w, h1, iT, x, E, e_fc2, "vit_fc2");
+    return linear(ctx, d->fc2_w, h1, iT, x, E, e_fc2, "vit_fc2", gelu);
 }
 
 int samhip_vit_prefix(samhip_context* ctx, const samhip_vit_prefix_desc* d, const float* image, float* x) {

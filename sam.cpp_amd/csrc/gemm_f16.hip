@@ -42,25 +42,11 @@ __device__ __forceinline__ void tile_order(int bid, int nblocks, int tiles_m, in
 // 16-byte row segments scaled by their row's 2^e.  (Staging the row scales
 // in LDS at kernel start measured up to 35 % slower on the long-K shapes.)
 // Epilogue flags (EPI template bits) for Epilogue fields.
-constexpr int EPI_BIAS = 1, EPI_GELU = 2, EPI_RES = 4, EPI_REMAP = 8;
+constexpr int EPI_BIAS = 1, EPI_RES = 4, EPI_REMAP = 8;
 
-__device__ __forceinline__ float gelu_erf(float v) {
-#pragma clang fp contract(off)
-    return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
-}
-
-// Output row of window-order row m (ggml_win_unpart on a gw-wide grid).
-__device__ __forceinline__ int64_t unpart_row(int m, int ws, int gw) {
-    const int per = ws * ws, win = m / per, r = m - win * per;
-    const int npx = gw / ws, py = win / npx, px = win - py * npx;
-    return int64_t(py * ws + r / ws) * gw + px * ws + r % ws;
-}
-
-template <int FM, int FN, int ES, int EPI = 0>
+template <int FM, int FN, int ES>
 __device__ __forceinline__ void store_tile(floatx16 (&acc)[FM][FN], const float* row_scale, float* slab, int lane,
-                                           int row0, int col0, int M, int N, float* Y, int64_t ldy,
-                                           const Epilogue& ep = Epilogue{}) {
-#pragma clang fp contract(off)
+                                           int row0, int col0, int M, int N, float* Y, int64_t ldy) {
     constexpr int TN = 32 * FN, C4 = TN / 4;
     const bool vec_ok = (ldy % 4) == 0 && (reinterpret_cast<uintptr_t>(Y) % 16) == 0;
 #pragma unroll
@@ -80,23 +66,83 @@ __device__ __forceinline__ void store_tile(floatx16 (&acc)[FM][FN], const float*
             if (m >= M) continue;
             const float sc = row_scale[m];
             const floatx4 raw = *reinterpret_cast<const floatx4*>(slab + rr * ES + 4 * c4);
-            floatx4 v{raw[0] * sc, raw[1] * sc, raw[2] * sc, raw[3] * sc};
-            const bool full = n + 3 < N;
-            if (EPI & EPI_BIAS) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) v[q] = v[q] + (full || n + q < N ? ep.bias[n + q] : 0.f);
+            const floatx4 v{raw[0] * sc, raw[1] * sc, raw[2] * sc, raw[3] * sc};
+            float* yp = Y + int64_t(m) * ldy + n;
+            if (vec_ok && n + 3 < N) {
+                *reinterpret_cast<floatx4*>(yp) = v;
+            } else {
+                for (int q = 0; q < 4; ++q)
+                    if (n + q < N) yp[q] = v[q];
             }
-            if (EPI & EPI_GELU) {
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+// Epilogue variant: a lane always owns the same 4 columns (64 % C4 == 0),
+// so the bias is loaded once; each 32-row block's row scales, output rows
+// and residuals are requested before its accumulators go through the slab.
+template <int FM, int FN, int ES, int EPI>
+__device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const float* row_scale, float* slab, int lane,
+                                               int row0, int col0, int M, int N, float* Y, int64_t ldy,
+                                               const Epilogue& ep) {
+#pragma clang fp contract(off)
+    constexpr int TN = 32 * FN, C4 = TN / 4, RSTEP = 64 / C4, IT = 32 / RSTEP;
+    static_assert(64 % C4 == 0, "a lane keeps its columns");
+    const bool vec_ok = (ldy % 4) == 0 && (reinterpret_cast<uintptr_t>(Y) % 16) == 0;
+    const int c4 = lane % C4, r0 = lane / C4;
+    const int n = col0 + 4 * c4;
+    const bool full = n + 3 < N;
+    floatx4 bias{0.f, 0.f, 0.f, 0.f};
+    if (EPI & EPI_BIAS)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) v[q] = gelu_erf(v[q]);
-            }
-            const int64_t d = (EPI & EPI_REMAP) ? unpart_row(m, ep.ws, ep.gw) : int64_t(m);
-            if (EPI & EPI_RES) {
-                const float* rp = ep.res + d * ldy + n;
+        for (int q = 0; q < 4; ++q) bias[q] = (full || n + q < N) ? ep.bias[n + q] : 0.f;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) v[q] = (full || n + q < N ? rp[q] : 0.f) + v[q];
+    for (int i = 0; i < FM; ++i) {
+        float sc[IT];
+        int64_t dst[IT];
+        floatx4 res[IT];
+#pragma unroll
+        for (int t = 0; t < IT; ++t) {
+            const int m = row0 + i * 32 + r0 + RSTEP * t;
+            const bool live = m < M;
+            sc[t] = live ? row_scale[m] : 0.f;
+            dst[t] = (EPI & EPI_REMAP) ? (live ? int64_t(ep.row_map[m]) : 0) : int64_t(m);
+        }
+        if (EPI & EPI_RES) {
+#pragma unroll
+            for (int t = 0; t < IT; ++t) {
+                const int m = row0 + i * 32 + r0 + RSTEP * t;
+                const float* rp = ep.res + dst[t] * ldy + n;
+                if (m < M && full && vec_ok) {
+                    res[t] = *reinterpret_cast<const floatx4*>(rp);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) res[t][q] = (m < M && n + q < N) ? rp[q] : 0.f;
+                }
             }
-            float* yp = Y + d * ldy + n;
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                slab[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ES + 32 * j + (lane & 31)] = acc[i][j][r];
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the slab is written
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int t = 0; t < IT; ++t) {
+            const int rr = r0 + RSTEP * t;
+            if (row0 + i * 32 + rr >= M) continue;
+            const floatx4 raw = *reinterpret_cast<const floatx4*>(slab + rr * ES + 4 * c4);
+            floatx4 v;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float u = raw[q] * sc[t];
+                if (EPI & EPI_BIAS) u = u + bias[q];
+                if (EPI & EPI_RES) u = res[t][q] + u;
+                v[q] = u;
+            }
+            float* yp = Y + dst[t] * ldy + n;
             if (vec_ok && full) {
                 *reinterpret_cast<floatx4*>(yp) = v;
             } else {
@@ -544,8 +590,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_pipe_kernel(const _Floa
     }
     __syncthreads();
 
-    store_tile<FM, FN, ES, EPI>(acc, row_scale, reinterpret_cast<float*>(lds) + wave * 32 * ES, lane, m0 + wm * TM,
-                                n0 + wn * TN, M, N, Y, ldy, ep);
+    if (EPI == 0)
+        store_tile<FM, FN, ES>(acc, row_scale, reinterpret_cast<float*>(lds) + wave * 32 * ES, lane, m0 + wm * TM,
+                               n0 + wn * TN, M, N, Y, ldy);
+    else
+        store_tile_epi<FM, FN, ES, EPI>(acc, row_scale, reinterpret_cast<float*>(lds) + wave * 32 * ES, lane,
+                                        m0 + wm * TM, n0 + wn * TN, M, N, Y, ldy, ep);
 #endif
 }
 
@@ -658,16 +708,11 @@ int gemm_f16_pick(int /*M*/, int N, int /*K*/) {
 template <int BM, int BN, int WM, int WN>
 bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
                 int64_t ldy, int M, int N, int K, bool spread, const Epilogue& ep, hipStream_t stream) {
-    const int flags = (ep.bias ? EPI_BIAS : 0) | (ep.gelu ? EPI_GELU : 0) | (ep.res ? EPI_RES : 0) |
-                      (ep.ws > 0 ? EPI_REMAP : 0);
+    const int flags = (ep.bias ? EPI_BIAS : 0) | (ep.res ? EPI_RES : 0) | (ep.row_map ? EPI_REMAP : 0);
     switch (flags) {
         case 0: launch_pipe<BM, BN, 64, 2, WM, WN, 0>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream, ep); break;
         case EPI_BIAS:
             launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream, ep);
-            break;
-        case EPI_BIAS | EPI_GELU:
-            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_GELU>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread,
-                                                                   stream, ep);
             break;
         case EPI_BIAS | EPI_RES:
             launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_RES>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream,

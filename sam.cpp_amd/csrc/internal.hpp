@@ -39,20 +39,18 @@ const char* launch_gemm_f16(int cfg, const _Float16* a, int64_t lda, const float
 
 // Epilogue applied to the tall GEMM's tile before the store, in the order of
 // the reference graph (src/models/sam3/vision.hpp:186-241):
-//   v = rs[m] * acc;  v += bias[n];  v = gelu_erf(v);  y[d] = res[d] + v
-// where d is the output row: m itself, or with `ws` > 0 the grid row that
-// window-order row m returns to (ggml_win_unpart of a gw x gh grid with
-// ws x ws windows, gw and gh multiples of ws).  res may alias y.
+//   v = rs[m] * acc;  v += bias[n];  y[d] = res[d] + v
+// where d is the output row: m itself, or row_map[m] (the grid row that a
+// window-order row returns to, ggml_win_unpart).  res may alias y.
 struct Epilogue {
     const float* bias = nullptr;
     const float* res = nullptr;   // row stride = ldy
-    bool gelu = false;
-    int ws = 0, gw = 0, gh = 0;
+    const int* row_map = nullptr;
 };
 // Same product as launch_gemm_f16 with the shape's picked configuration and
 // the epilogue; returns the configuration's name, or nullptr for an
-// epilogue combination without a kernel (bias; bias + gelu; bias + res;
-// bias + res + remap; or none are built).
+// epilogue combination without a kernel (bias; bias + res; bias + res +
+// row_map; or none are built).
 const char* launch_gemm_f16_epi(const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
                                 int64_t ldb, float* y, int64_t ldy, int M, int N, int K, int cus, const Epilogue& ep,
                                 hipStream_t stream);
@@ -81,11 +79,25 @@ void launch_patch_columns(const float* image, int img, int patch, _Float16* a, f
                           hipStream_t stream);
 void launch_patch_kernel(const float* kernel, int E, int patch, _Float16* w, int kp, hipStream_t stream);
 
+// The producing graph node folded into a tall product's activation staging:
+// PRE_GELU stages gelu_erf(x) (ggml_gelu_erf), PRE_LAYER_NORM stages
+// ggml_norm(x, eps) * w + b, its rows leaving in window order (ggml_win_part
+// of a gw-wide grid) when ws > 0.  The packed operand is the one the
+// separate node's F32 output would have produced.
+constexpr int PRE_NONE = 0, PRE_GELU = 1, PRE_LAYER_NORM = 2;
+struct RowPre {
+    int kind = PRE_NONE;
+    const float* w = nullptr;
+    const float* b = nullptr;
+    float eps = 0.f;
+    int ws = 0, gw = 1;
+};
+
 // Activation staging and weight decode of a tall product in one launch
 // (16-byte aligned activation rows, K <= 5120); false when not applicable.
 bool launch_prep(int mode, int wtype, const float* x, int64_t x_stride, int M, int K, _Float16* a, int64_t lda,
                  float* row_scale, int x86, const void* w, int64_t w_stride, int N, _Float16* wout, int64_t ldo,
-                 hipStream_t stream);
+                 hipStream_t stream, const RowPre& pre = RowPre{});
 
 // Kernel variant name for a weight type, or nullptr when unsupported.
 const char* gemm_variant(int wtype);

@@ -14,6 +14,17 @@
 namespace samhip {
 
 
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// ggml_gelu_erf on one F32 value: 0.5 x (1 + erf(x / sqrt 2)).
+__device__ __forceinline__ float gelu_erf(float v) {
+#pragma clang fp contract(off)
+    return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
     return v;

@@ -22,13 +22,12 @@ namespace {
 // lanes, a Q8_K block 32 lanes).  The row stays in registers (K <= 512*CH),
 // so X is read once; every cross-lane reduction runs with all lanes active
 // (lanes past K hold zeros).
-template <int MODE, int CH, bool X86>
+template <int MODE, int CH, bool X86, int PRE = PRE_NONE>
 __device__ __forceinline__ void stage8_row(const float* __restrict__ x, int64_t x_stride, int m, int K,
                                            _Float16* __restrict__ a, int64_t lda, float* __restrict__ row_scale,
-                                           int lane) {
+                                           int lane, const RowPre& pre = RowPre{}) {
     const float* xr = x + int64_t(m) * x_stride;
     floatx8 v[CH];
-    float rmax = 0.f;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int k = 512 * c + 8 * lane;
@@ -38,15 +37,65 @@ __device__ __forceinline__ void stage8_row(const float* __restrict__ x, int64_t 
         } else {
             v[c] = floatx8{0, 0, 0, 0, 0, 0, 0, 0};
         }
+    }
+    int64_t dst = m;
+    if (PRE == PRE_GELU) {
+        // the F32 erf-GELU of the producing graph node, before packing
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[c][i] = gelu_erf(v[c][i]);   // gelu(0) = 0 keeps the padding
+    } else if (PRE == PRE_LAYER_NORM) {
+        // ggml_norm(x, eps) * w + b of the producing node, the row leaving in
+        // window order when pre.ws > 0
+        float s = 0.f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s += v[c][i];
+        const float mean = wave_sum(s) / float(K);
+        float s2 = 0.f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const bool live = 512 * c + 8 * lane < K;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float d = live ? v[c][i] - mean : 0.f;
+                v[c][i] = d;
+                s2 += d * d;
+            }
+        }
+        const float variance = wave_sum(s2) / float(K);
+        const float scale = 1.0f / sqrtf(variance + pre.eps);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int k = 512 * c + 8 * lane;
+            if (k < K) {
+                const floatx4 w0 = load4f(pre.w + k), w1 = load4f(pre.w + k + 4);
+                const floatx4 b0 = load4f(pre.b + k), b1 = load4f(pre.b + k + 4);
+                const floatx8 w{w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+                const floatx8 b{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[c][i] = (v[c][i] * scale) * w[i] + b[i];
+            }
+        }
+        if (pre.ws > 0) {
+            const int gy = m / pre.gw, gx = m - gy * pre.gw;
+            const int win = (gy / pre.ws) * (pre.gw / pre.ws) + gx / pre.ws;
+            dst = int64_t(win) * pre.ws * pre.ws + (gy % pre.ws) * pre.ws + gx % pre.ws;
+        }
+    }
+    float rmax = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
 #pragma unroll
         for (int i = 0; i < 8; ++i) rmax = fmaxf(rmax, fabsf(v[c][i]));
-    }
     const float r32 = max32_lanes(rmax);
     rmax = fmaxf(r32, __shfl_xor(r32, 32, 64));
     const int e = row_exponent(rmax);
     const float down = exp2i(-e);
-    if (lane == 0) row_scale[m] = exp2i(e);
-    _Float16* ar = a + int64_t(m) * lda;
+    if (lane == 0) row_scale[dst] = exp2i(e);
+    _Float16* ar = a + dst * lda;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int k = 512 * c + 8 * lane;
@@ -84,14 +133,14 @@ __device__ __forceinline__ void dequant_piece(const uint8_t* __restrict__ W, int
 // Both per-call preparations of a tall product in one launch: workgroups
 // [0, stage_blocks) pack four activation rows each, the rest decode 256
 // weight pieces each (the two roles touch disjoint memory).
-template <int MODE, int CH, bool X86, int WT>
+template <int MODE, int CH, bool X86, int WT, int PRE = PRE_NONE>
 __global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ x, int64_t x_stride, int M, int K,
                                                    _Float16* __restrict__ a, int64_t lda, float* __restrict__ row_scale,
                                                    int stage_blocks, const uint8_t* __restrict__ W, int64_t w_stride,
-                                                   int N, _Float16* __restrict__ wout, int64_t ldo) {
+                                                   int N, _Float16* __restrict__ wout, int64_t ldo, RowPre pre) {
     if (int(blockIdx.x) < stage_blocks) {
         const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-        if (m < M) stage8_row<MODE, CH, X86>(x, x_stride, m, K, a, lda, row_scale, threadIdx.x & 63);
+        if (m < M) stage8_row<MODE, CH, X86, PRE>(x, x_stride, m, K, a, lda, row_scale, threadIdx.x & 63, pre);
         return;
     }
     const int64_t t = int64_t(blockIdx.x - stage_blocks) * 256 + threadIdx.x;
@@ -353,15 +402,27 @@ void launch_dequant_w_f16(int wtype, const void* w, int64_t w_stride, int N, int
 
 bool launch_prep(int mode, int wtype, const float* x, int64_t x_stride, int M, int K, _Float16* a, int64_t lda,
                  float* row_scale, int x86, const void* w, int64_t w_stride, int N, _Float16* wout, int64_t ldo,
-                 hipStream_t stream) {
+                 hipStream_t stream, const RowPre& pre) {
     if (K > 512 * 10 || reinterpret_cast<uintptr_t>(x) % 16 || x_stride % 4) return false;
+    if (pre.kind == PRE_LAYER_NORM && (!pre.w || !pre.b || reinterpret_cast<uintptr_t>(pre.w) % 16 ||
+                                       reinterpret_cast<uintptr_t>(pre.b) % 16 || K % 8))
+        return false;
     const int sb = (M + 3) / 4;
     const int64_t db = (int64_t(N) * (K / 32) * 2 + 255) / 256;
     const dim3 grid(unsigned(sb + db)), block(256);
     const uint8_t* wb = static_cast<const uint8_t*>(w);
-#define SAMHIP_PREP(MODE, CH, X86, WT)                                                                        \
-    hipLaunchKernelGGL((prep_kernel<MODE, CH, X86, WT>), grid, block, 0, stream, x, x_stride, M, K, a, lda, \
-                       row_scale, sb, wb, w_stride, N, wout, ldo)
+#define SAMHIP_PREP(MODE, CH, X86, WT)                                                                               \
+    do {                                                                                                             \
+        if (pre.kind == PRE_GELU)                                                                                    \
+            hipLaunchKernelGGL((prep_kernel<MODE, CH, X86, WT, PRE_GELU>), grid, block, 0, stream, x, x_stride, M, K, \
+                               a, lda, row_scale, sb, wb, w_stride, N, wout, ldo, pre);                              \
+        else if (pre.kind == PRE_LAYER_NORM)                                                                         \
+            hipLaunchKernelGGL((prep_kernel<MODE, CH, X86, WT, PRE_LAYER_NORM>), grid, block, 0, stream, x, x_stride, \
+                               M, K, a, lda, row_scale, sb, wb, w_stride, N, wout, ldo, pre);                        \
+        else                                                                                                         \
+            hipLaunchKernelGGL((prep_kernel<MODE, CH, X86, WT>), grid, block, 0, stream, x, x_stride, M, K, a, lda,  \
+                               row_scale, sb, wb, w_stride, N, wout, ldo, pre);                                      \
+    } while (0)
 #define SAMHIP_PREP_CH(MODE, X86, WT)                    \
     do {                                                 \
         if (K <= 1024) SAMHIP_PREP(MODE, 2, X86, WT);    \
