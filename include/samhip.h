@@ -171,7 +171,7 @@ int samhip_dequantize_rows(samhip_context* ctx, int32_t type, const void* src, s
 int samhip_validate_quantized_payload(int32_t type, int64_t ne0, int64_t rows, const void* host_bytes, size_t bytes);
 
 /* --- SAM 3 vision encoder ----------------------------------------------------
- * The ViT of sam3_build_vit_graph (src/models/sam3/vision.hpp:248-283) as two
+ * The ViT of sam3_build_vit_graph (src/models/sam3/vision.hpp:248-293) as two
  * fused subgraph operators on device buffers, for a backend that takes the
  * whole vision encoder instead of its ggml nodes.  Activations are
  * token-major F32 rows of `embed` floats, token (x, y) of the grid at row
@@ -194,7 +194,7 @@ typedef struct samhip_vit_block_desc {
                                                          (cos, sin); NULL = no RoPE */
 } samhip_vit_block_desc;
 
-/* sam3_vit_block_forward (src/models/sam3/vision.hpp:157-243): x (device F32
+/* sam3_vit_block_forward (src/models/sam3/vision.hpp:152-243): x (device F32
  * [grid_h*grid_w][embed]) is replaced by the block's output. */
 int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* block, float* x);
 

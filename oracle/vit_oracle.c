@@ -152,7 +152,7 @@ static int linear(int type, const void* w, const float* x, float* y, int64_t n, 
                   : or_mul_mat_native(type, w, ws, x, (size_t)k, y, n, m, k, q8_rounding, threads);
 }
 
-/* sam3_vit_block_forward (src/models/sam3/vision.hpp:157-243). */
+/* sam3_vit_block_forward (src/models/sam3/vision.hpp:152-243). */
 int or_vit_block(const or_vit_block_weights* wt, const float* x_in, float* x_out, int W, int H, int E, int heads,
                  int mlp, int ws, int q8_rounding, int decode, int threads) {
     const int hd = E / heads;

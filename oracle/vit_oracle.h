@@ -2,7 +2,7 @@
  * CPU oracle for the SAM 3 vision encoder forward — TEST INFRASTRUCTURE ONLY.
  *
  * A plain-C restatement of the ggml graph SAM.cpp builds for the ViT
- * (src/models/sam3/vision.hpp:157-283, src/models/sam3/ops.hpp:56-89): the
+ * (src/models/sam3/vision.hpp:152-293, src/models/sam3/ops.hpp:56-89): the
  * prefix (14x14 patch convolution, tiled 24x24 position embedding, ln_pre)
  * and the pre-LN block (LN, window partition, qkv linear + bias, axial RoPE
  * on Q/K, softmax attention, proj linear + bias, window unpartition,

@@ -1,5 +1,5 @@
 // SAM 3 vision-encoder kernels for gfx950: the non-linear parts of the ViT
-// prefix and block (src/models/sam3/vision.hpp:157-272) around the quantized
+// prefix and block (src/models/sam3/vision.hpp:152-272) around the quantized
 // linears.
 //   layer_norm_kernel : ggml_norm * w + b over one 1024-float row per wave,
 //                       optionally adding the tiled position embedding first

@@ -1,7 +1,7 @@
 """Pins of the vision-encoder oracle (oracle/vit_oracle.c) against
 independent float64 restatements (numpy / scipy) and structural invariants,
 each following the reference graph it restates
-(src/models/sam3/vision.hpp:109-283, src/models/sam3/ops.hpp:56-89)."""
+(src/models/sam3/vision.hpp:109-293, src/models/sam3/ops.hpp:56-89)."""
 
 import numpy as np
 import pytest
@@ -114,7 +114,7 @@ def test_prefix_against_float64_convolution(oracle):
 
 
 def np_block(oracle, w, x, W, H, E, heads, mlp, ws):
-    """The reference block graph (src/models/sam3/vision.hpp:157-243) from
+    """The reference block graph (src/models/sam3/vision.hpp:152-243) from
     numpy pieces and the oracle's native mul_mat."""
     hd = E // heads
     xs = x
