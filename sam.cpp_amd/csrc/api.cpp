@@ -98,6 +98,9 @@ struct samhip_context {
     // window-unpartition row table of the last (grid_w, grid_h, window)
     int* row_map = nullptr;
     int row_map_key[3] = {0, 0, 0};
+    // packed-operand row table of the last (tokens, tokens per window, heads)
+    int* pack_rows = nullptr;
+    int pack_rows_key[3] = {0, 0, 0};
 };
 
 namespace {
@@ -289,6 +292,7 @@ void samhip_context_destroy(samhip_context* ctx) {
     if (ctx->staging) (void)hipFree(ctx->staging);
     if (ctx->work) (void)hipFree(ctx->work);
     if (ctx->row_map) (void)hipFree(ctx->row_map);
+    if (ctx->pack_rows) (void)hipFree(ctx->pack_rows);
     for (void* p : ctx->retired_staging) (void)hipFree(p);
     if (ctx->flag) (void)hipFree(ctx->flag);
     for (auto& r : ctx->trace) {
@@ -612,6 +616,30 @@ int ensure_row_map(samhip_context* ctx, int gw, int gh, int ws) {
     return SAMHIP_OK;
 }
 
+// Row m (window m / per, token m % per) of a qkv product lands at packed
+// row (window * heads * np + token) * 64 of the attention operands.
+int ensure_pack_rows(samhip_context* ctx, int T, int per, int heads) {
+    if (ctx->pack_rows && ctx->pack_rows_key[0] == T && ctx->pack_rows_key[1] == per && ctx->pack_rows_key[2] == heads)
+        return SAMHIP_OK;
+    const int np = (per + 63) / 64 * 64;
+    std::vector<int> rows(size_t(T) * 2);
+    for (int m = 0; m < T; ++m) {
+        const int w = m / per, t = m % per;
+        rows[2 * size_t(m)] = (w * heads * np + t) * 64;
+        rows[2 * size_t(m) + 1] = t;
+    }
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (ctx->pack_rows) HIP_TRY(hipFree(ctx->pack_rows), "hipFree");
+    ctx->pack_rows = nullptr;
+    HIP_TRY(hipMalloc(&ctx->pack_rows, rows.size() * sizeof(int)), "hipMalloc pack rows");
+    HIP_TRY(hipMemcpy(ctx->pack_rows, rows.data(), rows.size() * sizeof(int), hipMemcpyHostToDevice),
+            "hipMemcpy pack rows");
+    ctx->pack_rows_key[0] = T;
+    ctx->pack_rows_key[1] = per;
+    ctx->pack_rows_key[2] = heads;
+    return SAMHIP_OK;
+}
+
 // Tall product through staging (with the producing node folded in, `pre`)
 // + weight decode + the fp16 GEMM with an epilogue; x rows are K contiguous
 // floats (16-byte aligned), y rows ldy.
@@ -737,19 +765,20 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
         {&d->qkv_w, E, 3 * E, "qkv"}, {&d->proj_w, E, E, "proj"}, {&d->fc1_w, E, MLP, "fc1"}, {&d->fc2_w, MLP, E, "fc2"}};
     for (const auto& w : weights)
         if (int rc = weight_check(*w.t, w.k, w.n, GW * GH, w.name)) return rc;
-    if (reinterpret_cast<uintptr_t>(x) % 16) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_block: x must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(d->freqs_cis) % 16)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_block: x and freqs_cis must be 16-byte aligned");
     if (int rc = set_device(ctx)) return rc;
 
     const int64_t T = GW * GH, per = WS > 0 ? WS * WS : T, B = T / per, np = (per + 63) / 64 * 64;
+    if (B * H * np * 64 >= (int64_t(1) << 31)) return fail(SAMHIP_ERR_UNSUPPORTED, "vit_block: grid too large");
     Carve c;
-    const size_t o_ln = c.take(size_t(T * E) * 4), o_qkv = c.take(size_t(T * 3 * E) * 4),
-                 o_x1 = c.take(size_t(T * E) * 4), o_h1 = c.take(size_t(T * MLP) * 4);
+    const size_t o_ln = c.take(size_t(T * E) * 4), o_x1 = c.take(size_t(T * E) * 4),
+                 o_h1 = c.take(size_t(T * MLP) * 4);
     const size_t packed = size_t(B * H * np * 64) * 2;
     const size_t o_qh = c.take(packed), o_kh = c.take(packed), o_vt = c.take(packed);
     if (int rc = ensure_work(ctx, c.used)) return rc;
     uint8_t* wb = static_cast<uint8_t*>(ctx->work);
     float* ln = reinterpret_cast<float*>(wb + o_ln);
-    float* qkv = reinterpret_cast<float*>(wb + o_qkv);
     float* x1 = reinterpret_cast<float*>(wb + o_x1);
     float* h1 = reinterpret_cast<float*>(wb + o_h1);
     _Float16 *qh = reinterpret_cast<_Float16*>(wb + o_qh), *kh = reinterpret_cast<_Float16*>(wb + o_kh),
@@ -768,17 +797,29 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
     ln1.eps = 1e-5f;
     ln1.ws = int(WS);
     ln1.gw = int(GW);
+    if (int rc = ensure_pack_rows(ctx, iT, int(per), int(H))) return rc;
+    // qkv + bias, written by the product's epilogue as the per-head fp16
+    // attention operands (RoPE on q and k, q times 1/8)
     Epilogue e_qkv;
     e_qkv.bias = d->qkv_b;
-    int rc = linear(ctx, d->qkv_w, x, iT, qkv, 3 * E, e_qkv, "vit_qkv", ln1);
+    e_qkv.pack[0] = qh;
+    e_qkv.pack[1] = kh;
+    e_qkv.pack[2] = vt;
+    e_qkv.pack_rows = ctx->pack_rows;
+    e_qkv.freqs = d->freqs_cis;
+    e_qkv.embed = int(E);
+    e_qkv.np = int(np);
+    e_qkv.q_scale = 0.125f;
+    int rc = linear(ctx, d->qkv_w, x, iT, nullptr, 3 * E, e_qkv, "vit_qkv", ln1);
     if (rc) return rc;
-    rc = traced(ctx, "vit_pack_qkv", T_F32, T, 3 * E, 0, [&]() -> int {
-        launch_pack_qkv(qkv, qkv + E, qkv + 2 * E, 3 * E, d->freqs_cis, 0.125f, qh, kh, vt, int(B), int(H), int(per),
-                        ctx->stream);
-        HIP_TRY(hipGetLastError(), "pack launch");
-        return SAMHIP_OK;
-    });
-    if (rc) return rc;
+    if (np != per) {
+        rc = traced(ctx, "vit_zero_pad", T_F32, T, E, per, [&]() -> int {
+            launch_zero_pad(qh, kh, vt, int(B), int(H), int(per), ctx->stream);
+            HIP_TRY(hipGetLastError(), "zero pad launch");
+            return SAMHIP_OK;
+        });
+        if (rc) return rc;
+    }
     rc = traced(ctx, "vit_attention", T_F32, T, E, per, [&]() -> int {
         launch_attention(qh, kh, vt, ln, E, int(B), int(H), int(per), ctx->stream);
         HIP_TRY(hipGetLastError(), "attention launch");

@@ -42,7 +42,7 @@ __device__ __forceinline__ void tile_order(int bid, int nblocks, int tiles_m, in
 // 16-byte row segments scaled by their row's 2^e.  (Staging the row scales
 // in LDS at kernel start measured up to 35 % slower on the long-K shapes.)
 // Epilogue flags (EPI template bits) for Epilogue fields.
-constexpr int EPI_BIAS = 1, EPI_RES = 4, EPI_REMAP = 8;
+constexpr int EPI_BIAS = 1, EPI_RES = 4, EPI_REMAP = 8, EPI_PACK = 16;
 
 template <int FM, int FN, int ES>
 __device__ __forceinline__ void store_tile(floatx16 (&acc)[FM][FN], const float* row_scale, float* slab, int lane,
@@ -97,17 +97,29 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
     if (EPI & EPI_BIAS)
 #pragma unroll
         for (int q = 0; q < 4; ++q) bias[q] = (full || n + q < N) ? ep.bias[n + q] : 0.f;
+    // packed outputs: the wave's 64-aligned column block lies in one part and
+    // one head (embed is a multiple of 64)
+    const int part = (EPI & EPI_PACK) ? n / ep.embed : 0;
+    const int head_off = (EPI & EPI_PACK) ? ((n - part * ep.embed) >> 6) * ep.np * 64 + (n & 63) : 0;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
         float sc[IT];
         int64_t dst[IT];
         floatx4 res[IT];
+        floatx4 fq[IT];
 #pragma unroll
         for (int t = 0; t < IT; ++t) {
             const int m = row0 + i * 32 + r0 + RSTEP * t;
             const bool live = m < M;
             sc[t] = live ? row_scale[m] : 0.f;
-            dst[t] = (EPI & EPI_REMAP) ? (live ? int64_t(ep.row_map[m]) : 0) : int64_t(m);
+            if (EPI & EPI_PACK) {
+                const int base = live ? ep.pack_rows[2 * m] : 0, tok = live ? ep.pack_rows[2 * m + 1] : 0;
+                dst[t] = base;
+                if (part < 2 && ep.freqs)
+                    fq[t] = *reinterpret_cast<const floatx4*>(ep.freqs + (int64_t(tok) * 32 + ((n & 63) >> 1)) * 2);
+            } else {
+                dst[t] = (EPI & EPI_REMAP) ? (live ? int64_t(ep.row_map[m]) : 0) : int64_t(m);
+            }
         }
         if (EPI & EPI_RES) {
 #pragma unroll
@@ -141,6 +153,24 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
                 if (EPI & EPI_BIAS) u = u + bias[q];
                 if (EPI & EPI_RES) u = res[t][q] + u;
                 v[q] = u;
+            }
+            if (EPI & EPI_PACK) {
+                if (part < 2 && ep.freqs) {
+#pragma unroll
+                    for (int p2 = 0; p2 < 2; ++p2) {
+                        const float re = v[2 * p2], im = v[2 * p2 + 1], c = fq[t][2 * p2], s = fq[t][2 * p2 + 1];
+                        const float a = re * c, bb = im * s, cc = re * s, dd = im * c;
+                        v[2 * p2] = a - bb;
+                        v[2 * p2 + 1] = cc + dd;
+                    }
+                }
+                if (part == 0)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) v[q] = v[q] * ep.q_scale;
+                typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+                *reinterpret_cast<half4_t*>(ep.pack[part] + dst[t] + head_off) =
+                    half4_t{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+                continue;
             }
             float* yp = Y + dst[t] * ldy + n;
             if (vec_ok && full) {
@@ -708,7 +738,8 @@ int gemm_f16_pick(int /*M*/, int N, int /*K*/) {
 template <int BM, int BN, int WM, int WN>
 bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
                 int64_t ldy, int M, int N, int K, bool spread, const Epilogue& ep, hipStream_t stream) {
-    const int flags = (ep.bias ? EPI_BIAS : 0) | (ep.res ? EPI_RES : 0) | (ep.row_map ? EPI_REMAP : 0);
+    const int flags = (ep.bias ? EPI_BIAS : 0) | (ep.res ? EPI_RES : 0) | (ep.row_map ? EPI_REMAP : 0) |
+                      (ep.pack_rows ? EPI_PACK : 0);
     switch (flags) {
         case 0: launch_pipe<BM, BN, 64, 2, WM, WN, 0>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream, ep); break;
         case EPI_BIAS:
@@ -717,6 +748,10 @@ bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16*
         case EPI_BIAS | EPI_RES:
             launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_RES>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream,
                                                                   ep);
+            break;
+        case EPI_BIAS | EPI_PACK:
+            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_PACK>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream,
+                                                                   ep);
             break;
         case EPI_BIAS | EPI_RES | EPI_REMAP:
             launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_RES | EPI_REMAP>(a, lda, rs, b, ldb, y, ldy, M, N, K,

@@ -46,11 +46,22 @@ struct Epilogue {
     const float* bias = nullptr;
     const float* res = nullptr;   // row stride = ldy
     const int* row_map = nullptr;
+    // Packed attention operands instead of Y (an encoder block's qkv
+    // product): column n = part*embed + h*64 + d of row m goes to
+    // pack[part][pack_rows[2m] + h*np*64 + d] in fp16, q and k rotated by
+    // freqs[pack_rows[2m+1]] (complex RoPE, products rounded before the
+    // add), q multiplied by q_scale.  pack_rows[2m] = (window*heads*np +
+    // token)*64, pack_rows[2m+1] = token.
+    _Float16* pack[3] = {nullptr, nullptr, nullptr};
+    const int* pack_rows = nullptr;
+    const float* freqs = nullptr;
+    int embed = 0, np = 0;
+    float q_scale = 1.f;
 };
 // Same product as launch_gemm_f16 with the shape's picked configuration and
 // the epilogue; returns the configuration's name, or nullptr for an
 // epilogue combination without a kernel (bias; bias + res; bias + res +
-// row_map; or none are built).
+// row_map; bias + pack; or none are built).
 const char* launch_gemm_f16_epi(const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
                                 int64_t ldb, float* y, int64_t ldy, int M, int N, int K, int cus, const Epilogue& ep,
                                 hipStream_t stream);
@@ -63,11 +74,12 @@ const char* launch_gemm_f16_epi(const _Float16* a, int64_t lda, const float* row
 void launch_layer_norm(const float* x, const float* add, int add_grid, int gw, int gh, int ws, const float* w,
                        const float* b, float eps, float* y, int rows, int E, hipStream_t stream);
 // q/k/v rows (row b*N + n, stride ld floats, head h at columns h*64) ->
-// Qh [B][H][Np][64] (RoPE, times q_scale), Kh [B][H][Np][64] (RoPE),
-// Vt [B][H][64][Np], fp16, Np = N rounded up to 64 with zero padding;
-// freqs (nullable): [N][32][2] (cos, sin).
+// Qh [B][H][Np][64] (RoPE, times q_scale), Kh (RoPE), Vh, fp16, Np = N
+// rounded up to 64 with zero padding; freqs (nullable): [N][32][2] (cos, sin).
 void launch_pack_qkv(const float* q, const float* k, const float* v, int64_t ld, const float* freqs, float q_scale,
-                     _Float16* qh, _Float16* kh, _Float16* vt, int B, int H, int N, hipStream_t stream);
+                     _Float16* qh, _Float16* kh, _Float16* vh, int B, int H, int N, hipStream_t stream);
+// Zero the padding rows [N, Np) of the three packed operands.
+void launch_zero_pad(_Float16* qh, _Float16* kh, _Float16* vh, int B, int H, int N, hipStream_t stream);
 // softmax(Q K^T) V per (batch, head) on the packed operands (head dim 64);
 // out row b*N + n, columns h*64.. (row stride ldo floats).
 void launch_attention(const _Float16* qh, const _Float16* kh, const _Float16* vt, float* out, int64_t ldo, int B,

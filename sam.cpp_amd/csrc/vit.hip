@@ -4,8 +4,9 @@
 //   layer_norm_kernel : ggml_norm * w + b over one 1024-float row per wave,
 //                       optionally adding the tiled position embedding first
 //                       and writing rows in window order (ggml_win_part)
-//   pack_qkv_kernel   : q/k/v columns of the qkv product -> per-head fp16
-//                       operands, complex RoPE on q and k, v transposed
+//   pack_qkv_kernel   : q/k/v columns -> per-head fp16 operands with the
+//                       complex RoPE on q and k (the encoder block has the
+//                       qkv product's epilogue write them instead)
 //   attention_kernel  : softmax(Q K^T) V per window and head on
 //                       v_mfma_f32_32x32x16_f16 with an online softmax in F32
 //   patch_*_kernel    : the 14x14 patch convolution as a split-fp16 GEMM
@@ -91,35 +92,30 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float* __restrict
 
 // ---------------------------------------------------------------------------
 // q/k/v packing with RoPE.  Block: 64 tokens of one (batch, head); thread t
-// owns token t/4 and the 16 head dims 16*(t%4)..; v goes through LDS to be
-// written transposed.
+// owns token t/4 and the 16 head dims 16*(t%4)..
 // ---------------------------------------------------------------------------
-constexpr int VT_STRIDE = 72;   // halves per LDS row of the v transpose
-
 __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                        const float* __restrict__ v, int64_t ld,
                                                        const float* __restrict__ freqs, float q_scale,
                                                        _Float16* __restrict__ qh, _Float16* __restrict__ kh,
-                                                       _Float16* __restrict__ vt, int H, int N, int Np) {
-    __shared__ __attribute__((aligned(16))) _Float16 vl[64 * VT_STRIDE];
+                                                       _Float16* __restrict__ vh, int H, int N, int Np) {
     const int n0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z;
     const int t = threadIdx.x, tok = t >> 2, d0 = 16 * (t & 3);
     const int n = n0 + tok;
     const bool valid = n < N;
     const int64_t src = (int64_t(b) * N + n) * ld + h * 64 + d0;
-    const int64_t bh = int64_t(b) * H + h;
-    const int64_t dst = (bh * Np + n) * 64 + d0;
+    const int64_t dst = ((int64_t(b) * H + h) * Np + n) * 64 + d0;
 #pragma unroll
-    for (int which = 0; which < 2; ++which) {
+    for (int which = 0; which < 3; ++which) {
         float xs[16];
         if (valid) {
-            const float* p = (which ? k : q) + src;
+            const float* p = (which == 0 ? q : which == 1 ? k : v) + src;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const floatx4 f = ld4(p + 4 * j);
                 xs[4 * j] = f[0], xs[4 * j + 1] = f[1], xs[4 * j + 2] = f[2], xs[4 * j + 3] = f[3];
             }
-            if (freqs) {
+            if (freqs && which < 2) {
                 // pair i of the head: (x[2i], x[2i+1]) * (cos_i + j sin_i)
                 const float* f = freqs + (int64_t(n) * 32 + d0 / 2) * 2;
 #pragma unroll
@@ -130,7 +126,7 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__
                     xs[2 * i + 1] = cc + dd;
                 }
             }
-            if (!which)
+            if (which == 0)
 #pragma unroll
                 for (int j = 0; j < 16; ++j) xs[j] = xs[j] * q_scale;
         } else {
@@ -143,36 +139,30 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__
             lo[j] = (_Float16)xs[j];
             hi[j] = (_Float16)xs[8 + j];
         }
-        half8* o = reinterpret_cast<half8*>((which ? kh : qh) + dst);
+        half8* o = reinterpret_cast<half8*>((which == 0 ? qh : which == 1 ? kh : vh) + dst);
         o[0] = lo;
         o[1] = hi;
     }
-    {
-        float xs[16];
-        if (valid) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const floatx4 f = ld4(v + src + 4 * j);
-                xs[4 * j] = f[0], xs[4 * j + 1] = f[1], xs[4 * j + 2] = f[2], xs[4 * j + 3] = f[3];
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) xs[j] = 0.f;
-        }
-#pragma unroll
-        for (int j = 0; j < 16; ++j) vl[(d0 + j) * VT_STRIDE + tok] = (_Float16)xs[j];
-    }
-    __syncthreads();
-    const int d = t >> 2, c0 = 16 * (t & 3);
-    const half8* s = reinterpret_cast<const half8*>(vl + d * VT_STRIDE + c0);
-    half8* o = reinterpret_cast<half8*>(vt + (bh * 64 + d) * Np + n0 + c0);
-    o[0] = s[0];
-    o[1] = s[1];
+}
+
+// Zero rows [N, Np) of packed operands [B*H][Np][64] (the padding of the
+// last key tile when the qkv product wrote the packed rows itself).
+__global__ __launch_bounds__(256) void zero_pad_kernel(_Float16* __restrict__ qh, _Float16* __restrict__ kh,
+                                                       _Float16* __restrict__ vh, int N, int Np) {
+    const int64_t bh = blockIdx.y;
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;   // 8-half chunk of the pad rows
+    if (i >= int64_t(Np - N) * 8) return;
+    const int64_t off = (bh * Np + N) * 64 + 8 * i;
+    const half8 z{0, 0, 0, 0, 0, 0, 0, 0};
+    *reinterpret_cast<half8*>(qh + off) = z;
+    *reinterpret_cast<half8*>(kh + off) = z;
+    *reinterpret_cast<half8*>(vh + off) = z;
 }
 
 // ---------------------------------------------------------------------------
 // Attention.  Workgroup: 128 queries (4 waves x 32) of one (batch, head);
-// 64-key tiles of K [key][d] and V^T [d][key] double-buffered in LDS.
+// 64-key tiles of K [key][d] and V (stored [key][d], transposed on its way
+// into LDS as V^T [d][key]) double-buffered in LDS.
 // Each wave computes S^T = K Q^T (lane: query l%32, 16 keys per 32-key
 // tile), so the softmax statistics of a query sit in one lane pair (l,
 // l^32), and O^T = V^T P^T with P^T used as the B operand straight from the
@@ -184,7 +174,7 @@ constexpr int V_STRIDE = 68;   // halves per LDS d row (136 B: conflict-free 8-b
 constexpr float LOG2E = 1.44269504088896340736f;
 
 __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restrict__ qh, const _Float16* __restrict__ kh,
-                                                        const _Float16* __restrict__ vt, float* __restrict__ out,
+                                                        const _Float16* __restrict__ vh, float* __restrict__ out,
                                                         int64_t ldo, int H, int N, int Np) {
     __shared__ __attribute__((aligned(16))) _Float16 ks[2][64 * K_STRIDE];
     __shared__ __attribute__((aligned(16))) _Float16 vs[2][64 * V_STRIDE];
@@ -194,7 +184,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restri
     const int64_t bh = int64_t(b) * H + h;
     const _Float16* Q = qh + bh * Np * 64;
     const _Float16* Kg = kh + bh * Np * 64;
-    const _Float16* Vg = vt + bh * 64 * Np;
+    const _Float16* Vg = vh + bh * Np * 64;
     const int q0 = blockIdx.x * 128 + wave * 32;
     const int qrow = min(q0 + li, Np - 1);
 
@@ -209,7 +199,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restri
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + 256 * i, r = idx >> 3, c = idx & 7;
             kreg[i] = *reinterpret_cast<const half8*>(Kg + int64_t(kb * 64 + r) * 64 + 8 * c);
-            vreg[i] = *reinterpret_cast<const half8*>(Vg + int64_t(r) * Np + kb * 64 + 8 * c);
+            vreg[i] = *reinterpret_cast<const half8*>(Vg + int64_t(kb * 64 + r) * 64 + 8 * c);
         }
     };
     auto sstore = [&](int buf) {
@@ -217,9 +207,9 @@ __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restri
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + 256 * i, r = idx >> 3, c = idx & 7;
             *reinterpret_cast<half8*>(&ks[buf][r * K_STRIDE + 8 * c]) = kreg[i];
-            half4* vp = reinterpret_cast<half4*>(&vs[buf][r * V_STRIDE + 8 * c]);
-            vp[0] = half4{vreg[i][0], vreg[i][1], vreg[i][2], vreg[i][3]};
-            vp[1] = half4{vreg[i][4], vreg[i][5], vreg[i][6], vreg[i][7]};
+            // key r, dims 8c..8c+7 -> column r of V^T rows 8c..8c+7
+#pragma unroll
+            for (int j = 0; j < 8; ++j) vs[buf][(8 * c + j) * V_STRIDE + r] = vreg[i][j];
         }
     };
 
@@ -260,10 +250,22 @@ __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restri
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mnew = fmaxf(mrun, mx);
-        const float alpha = exp2f((mrun - mnew) * LOG2E);
-        mrun = mnew;
-        const float mb = mnew * LOG2E;
+        // Lazy rescaling: the exponent base mrun only moves when a score
+        // exceeds it by more than 8 / log2(e), so the weights stay below 2^8
+        // (fp16 keeps its full relative precision there) and most tiles skip
+        // the rescale of O and of the running sum.
+        if (__any(mx > mrun + 8.0f / LOG2E)) {
+            const float mnew = fmaxf(mrun, mx);
+            const float alpha = exp2f((mrun - mnew) * LOG2E);
+            mrun = mnew;
+            lsum = lsum * alpha;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                o0[r] = o0[r] * alpha;
+                o1[r] = o1[r] * alpha;
+            }
+        }
+        const float mb = mrun * LOG2E;
         float ps = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -271,12 +273,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restri
             s1[r] = exp2f(__builtin_fmaf(s1[r], LOG2E, -mb));
             ps += s0[r] + s1[r];
         }
-        lsum = lsum * alpha + ps;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            o0[r] = o0[r] * alpha;
-            o1[r] = o1[r] * alpha;
-        }
+        lsum = lsum + ps;
         half8 pf[4];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -381,17 +378,25 @@ void launch_layer_norm(const float* x, const float* add, int add_grid, int gw, i
 }
 
 void launch_pack_qkv(const float* q, const float* k, const float* v, int64_t ld, const float* freqs, float q_scale,
-                     _Float16* qh, _Float16* kh, _Float16* vt, int B, int H, int N, hipStream_t stream) {
+                     _Float16* qh, _Float16* kh, _Float16* vh, int B, int H, int N, hipStream_t stream) {
     const int np = (N + 63) / 64 * 64;
     hipLaunchKernelGGL(pack_qkv_kernel, dim3(unsigned(np / 64), unsigned(H), unsigned(B)), dim3(256), 0, stream, q, k,
-                       v, ld, freqs, q_scale, qh, kh, vt, H, N, np);
+                       v, ld, freqs, q_scale, qh, kh, vh, H, N, np);
 }
 
-void launch_attention(const _Float16* qh, const _Float16* kh, const _Float16* vt, float* out, int64_t ldo, int B,
+void launch_zero_pad(_Float16* qh, _Float16* kh, _Float16* vh, int B, int H, int N, hipStream_t stream) {
+    const int np = (N + 63) / 64 * 64;
+    if (np == N) return;
+    const int64_t chunks = int64_t(np - N) * 8;
+    hipLaunchKernelGGL(zero_pad_kernel, dim3(unsigned((chunks + 255) / 256), unsigned(B * H)), dim3(256), 0, stream,
+                       qh, kh, vh, N, np);
+}
+
+void launch_attention(const _Float16* qh, const _Float16* kh, const _Float16* vh, float* out, int64_t ldo, int B,
                       int H, int N, hipStream_t stream) {
     const int np = (N + 63) / 64 * 64;
     hipLaunchKernelGGL(attention_kernel, dim3(unsigned((np + 127) / 128), unsigned(H), unsigned(B)), dim3(256), 0,
-                       stream, qh, kh, vt, out, ldo, H, N, np);
+                       stream, qh, kh, vh, out, ldo, H, N, np);
 }
 
 void launch_patch_columns(const float* image, int img, int patch, _Float16* a, float* row_scale, int kp,
