@@ -11,7 +11,9 @@
 //                       v_mfma_f32_32x32x16_f16 with an online softmax in F32
 //   patch_*_kernel    : the 14x14 patch convolution as a split-fp16 GEMM
 // Arithmetic follows the reference graph's order (products rounded before
-// adds, no contraction).
+// adds, no contraction).  Built with MFMA results in VGPRs (Makefile): the
+// softmax reads every score, so accumulation registers would cost a copy
+// per value.
 #include "internal.hpp"
 
 #pragma clang fp contract(off)
@@ -256,7 +258,7 @@ __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restri
         // the rescale of O and of the running sum.
         if (__any(mx > mrun + 8.0f / LOG2E)) {
             const float mnew = fmaxf(mrun, mx);
-            const float alpha = exp2f((mrun - mnew) * LOG2E);
+            const float alpha = __builtin_amdgcn_exp2f((mrun - mnew) * LOG2E);
             mrun = mnew;
             lsum = lsum * alpha;
 #pragma unroll
@@ -269,8 +271,8 @@ __global__ __launch_bounds__(256) void attention_kernel(const _Float16* __restri
         float ps = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            s0[r] = exp2f(__builtin_fmaf(s0[r], LOG2E, -mb));
-            s1[r] = exp2f(__builtin_fmaf(s1[r], LOG2E, -mb));
+            s0[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], LOG2E, -mb));
+            s1[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[r], LOG2E, -mb));
             ps += s0[r] + s1[r];
         }
         lsum = lsum + ps;
