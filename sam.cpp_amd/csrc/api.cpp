@@ -98,9 +98,6 @@ struct samhip_context {
     // window-unpartition row table of the last (grid_w, grid_h, window)
     int* row_map = nullptr;
     int row_map_key[3] = {0, 0, 0};
-    // packed-operand row table of the last (tokens, tokens per window, heads)
-    int* pack_rows = nullptr;
-    int pack_rows_key[3] = {0, 0, 0};
 };
 
 namespace {
@@ -292,7 +289,6 @@ void samhip_context_destroy(samhip_context* ctx) {
     if (ctx->staging) (void)hipFree(ctx->staging);
     if (ctx->work) (void)hipFree(ctx->work);
     if (ctx->row_map) (void)hipFree(ctx->row_map);
-    if (ctx->pack_rows) (void)hipFree(ctx->pack_rows);
     for (void* p : ctx->retired_staging) (void)hipFree(p);
     if (ctx->flag) (void)hipFree(ctx->flag);
     for (auto& r : ctx->trace) {
@@ -616,30 +612,6 @@ int ensure_row_map(samhip_context* ctx, int gw, int gh, int ws) {
     return SAMHIP_OK;
 }
 
-// Row m (window m / per, token m % per) of a qkv product lands at packed
-// row (window * heads * np + token) * 64 of the attention operands.
-int ensure_pack_rows(samhip_context* ctx, int T, int per, int heads) {
-    if (ctx->pack_rows && ctx->pack_rows_key[0] == T && ctx->pack_rows_key[1] == per && ctx->pack_rows_key[2] == heads)
-        return SAMHIP_OK;
-    const int np = (per + 63) / 64 * 64;
-    std::vector<int> rows(size_t(T) * 2);
-    for (int m = 0; m < T; ++m) {
-        const int w = m / per, t = m % per;
-        rows[2 * size_t(m)] = (w * heads * np + t) * 64;
-        rows[2 * size_t(m) + 1] = t;
-    }
-    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
-    if (ctx->pack_rows) HIP_TRY(hipFree(ctx->pack_rows), "hipFree");
-    ctx->pack_rows = nullptr;
-    HIP_TRY(hipMalloc(&ctx->pack_rows, rows.size() * sizeof(int)), "hipMalloc pack rows");
-    HIP_TRY(hipMemcpy(ctx->pack_rows, rows.data(), rows.size() * sizeof(int), hipMemcpyHostToDevice),
-            "hipMemcpy pack rows");
-    ctx->pack_rows_key[0] = T;
-    ctx->pack_rows_key[1] = per;
-    ctx->pack_rows_key[2] = heads;
-    return SAMHIP_OK;
-}
-
 // Tall product through staging (with the producing node folded in, `pre`)
 // + weight decode + the fp16 GEMM with an epilogue; x rows are K contiguous
 // floats (16-byte aligned), y rows ldy.
@@ -797,7 +769,6 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
     ln1.eps = 1e-5f;
     ln1.ws = int(WS);
     ln1.gw = int(GW);
-    if (int rc = ensure_pack_rows(ctx, iT, int(per), int(H))) return rc;
     // qkv + bias, written by the product's epilogue as the per-head fp16
     // attention operands (RoPE on q and k, q times 1/8)
     Epilogue e_qkv;
@@ -805,10 +776,11 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
     e_qkv.pack[0] = qh;
     e_qkv.pack[1] = kh;
     e_qkv.pack[2] = vt;
-    e_qkv.pack_rows = ctx->pack_rows;
     e_qkv.freqs = d->freqs_cis;
     e_qkv.embed = int(E);
+    e_qkv.per = int(per);
     e_qkv.np = int(np);
+    e_qkv.heads = int(H);
     e_qkv.q_scale = 0.125f;
     int rc = linear(ctx, d->qkv_w, x, iT, nullptr, 3 * E, e_qkv, "vit_qkv", ln1);
     if (rc) return rc;

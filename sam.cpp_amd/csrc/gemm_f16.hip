@@ -100,6 +100,7 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
     // packed outputs: the wave's 64-aligned column block lies in one part and
     // one head (embed is a multiple of 64)
     const int part = (EPI & EPI_PACK) ? n / ep.embed : 0;
+    const float inv_per = (EPI & EPI_PACK) ? 1.0f / float(ep.per) : 0.f;
     const int head_off = (EPI & EPI_PACK) ? ((n - part * ep.embed) >> 6) * ep.np * 64 + (n & 63) : 0;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
@@ -113,8 +114,12 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
             const bool live = m < M;
             sc[t] = live ? row_scale[m] : 0.f;
             if (EPI & EPI_PACK) {
-                const int base = live ? ep.pack_rows[2 * m] : 0, tok = live ? ep.pack_rows[2 * m + 1] : 0;
-                dst[t] = base;
+                // window = m / per by a float reciprocal and one correction
+                int w = int(float(m) * inv_per);
+                w += (w + 1) * ep.per <= m;
+                w -= w * ep.per > m;
+                const int tok = live ? m - w * ep.per : 0;
+                dst[t] = (int64_t(w) * ep.heads * ep.np + tok) * 64;
                 if (part < 2 && ep.freqs)
                     fq[t] = *reinterpret_cast<const floatx4*>(ep.freqs + (int64_t(tok) * 32 + ((n & 63) >> 1)) * 2);
             } else {
@@ -739,7 +744,7 @@ template <int BM, int BN, int WM, int WN>
 bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
                 int64_t ldy, int M, int N, int K, bool spread, const Epilogue& ep, hipStream_t stream) {
     const int flags = (ep.bias ? EPI_BIAS : 0) | (ep.res ? EPI_RES : 0) | (ep.row_map ? EPI_REMAP : 0) |
-                      (ep.pack_rows ? EPI_PACK : 0);
+                      (ep.pack[0] ? EPI_PACK : 0);
     switch (flags) {
         case 0: launch_pipe<BM, BN, 64, 2, WM, WN, 0>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream, ep); break;
         case EPI_BIAS:

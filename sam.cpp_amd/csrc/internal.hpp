@@ -47,15 +47,13 @@ struct Epilogue {
     const float* res = nullptr;   // row stride = ldy
     const int* row_map = nullptr;
     // Packed attention operands instead of Y (an encoder block's qkv
-    // product): column n = part*embed + h*64 + d of row m goes to
-    // pack[part][pack_rows[2m] + h*np*64 + d] in fp16, q and k rotated by
-    // freqs[pack_rows[2m+1]] (complex RoPE, products rounded before the
-    // add), q multiplied by q_scale.  pack_rows[2m] = (window*heads*np +
-    // token)*64, pack_rows[2m+1] = token.
+    // product): column n = part*embed + h*64 + d of row m (window m / per,
+    // token t = m % per) goes to pack[part][((window*heads + h)*np + t)*64 +
+    // d] in fp16, q and k rotated by freqs[t] (complex RoPE, products
+    // rounded before the add), q multiplied by q_scale.
     _Float16* pack[3] = {nullptr, nullptr, nullptr};
-    const int* pack_rows = nullptr;
     const float* freqs = nullptr;
-    int embed = 0, np = 0;
+    int embed = 0, per = 0, np = 0, heads = 0;
     float q_scale = 1.f;
 };
 // Same product as launch_gemm_f16 with the shape's picked configuration and
