@@ -152,7 +152,10 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
 int samhip_get_rows(samhip_context* ctx, const samhip_tensor* src, const samhip_tensor* ids, const samhip_tensor* dst);
 
 /* Row quantization on the device, bit-exact with ggml:
- *   Q8_0: ggml from_float / quantize_row_q8_0_ref per `q8_rounding`
+ *   F16:  ggml_cast F32 -> F16 (round to nearest even; the F16 feature cache)
+ *   Q8_0: ggml from_float / quantize_row_q8_0_ref per `q8_rounding` (also
+ *         ggml_cast F32 -> Q8_0 of the Q8_0 feature cache,
+ *         src/models/sam3/execution.hpp:76-83)
  *   Q8_K: quantize_row_q8_K_ref (CPU activation packing for K weights)
  *   Q4_K, Q5_K, Q6_K: quantize_row_q*_K_ref (ggml_quantize_chunk without
  *         importance weights; tools/quantize/quantize_rows.cpp:210)
@@ -160,7 +163,8 @@ int samhip_get_rows(samhip_context* ctx, const samhip_tensor* src, const samhip_
 int samhip_quantize_rows(samhip_context* ctx, int32_t type, const float* src, size_t src_row_stride,
                          void* dst, int64_t rows, int64_t k, int32_t q8_rounding);
 
-/* ggml to_float on the device for Q8_0/Q4_K/Q5_K/Q6_K/Q8_K rows (bit-exact). */
+/* ggml to_float on the device for F16/Q8_0/Q4_K/Q5_K/Q6_K/Q8_K rows
+ * (bit-exact; F16 rows need k % 32 == 0). */
 int samhip_dequantize_rows(samhip_context* ctx, int32_t type, const void* src, size_t src_row_stride,
                            float* dst, int64_t rows, int64_t k);
 

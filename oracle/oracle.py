@@ -22,6 +22,15 @@ NAMES = {Q8_0: "q8_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K"}
 
 _lib = None
 
+NECK_FIELDS = ("s0_dc1_w", "s0_dc1_b", "s0_dc2_w", "s0_dc2_b", "s0_c1_w", "s0_c1_b", "s0_c3_w", "s0_c3_b",
+               "s1_dc_w", "s1_dc_b", "s1_c1_w", "s1_c1_b", "s1_c3_w", "s1_c3_b",
+               "s2_c1_w", "s2_c1_b", "s2_c3_w", "s2_c3_b", "s3_c1_w", "s3_c1_b", "s3_c3_w", "s3_c3_b")
+
+
+class NeckWeights(ctypes.Structure):
+    """or_neck_weights (vit_oracle.h)."""
+    _fields_ = [(n, ctypes.c_void_p) for n in NECK_FIELDS]
+
 
 class VitBlockWeights(ctypes.Structure):
     """or_vit_block_weights (vit_oracle.h)."""
@@ -64,6 +73,10 @@ def lib():
         L.or_attention.argtypes = [P, P, P, I64, I64, I, I, ctypes.c_float, P, I]
         L.or_vit_block.argtypes = [ctypes.POINTER(VitBlockWeights), P, P, I, I, I, I, I, I, I, I, I]
         L.or_vit_prefix.argtypes = [P, I, I, P, P, I, P, P, I, P, I]
+        L.or_deconv2x2.argtypes = [P, I, I, I, P, P, I, P, I]
+        L.or_conv2d.argtypes = [P, I, I, I, P, P, I, I, P, I]
+        L.or_maxpool2x2.argtypes = [P, I, I, I, P]
+        L.or_neck.argtypes = [ctypes.POINTER(NeckWeights), P, I, I, I, I, ctypes.POINTER(P), I]
         _lib = L
     return _lib
 
@@ -249,3 +262,42 @@ def vit_prefix(image, patch, kernel, pos, pos_grid, ln_w, ln_b, E, threads=0):
                            _ptr(_f32(ln_b)), E, _ptr(out), threads):
         raise ValueError("oracle vit prefix rejected its arguments")
     return out
+
+
+# ---- SimpleFPN neck ----------------------------------------------------------
+
+def deconv2x2(x, W, H, w, b, cout, threads=0):
+    """x: [H*W][Cin]; w: ggml {2, 2, Cout, Cin} flat."""
+    x = _f32(x)
+    out = np.empty((4 * W * H, cout), np.float32)
+    lib().or_deconv2x2(_ptr(x), W, H, x.shape[1], _ptr(_f32(w)), None if b is None else _ptr(_f32(b)), cout,
+                       _ptr(out), threads)
+    return out
+
+
+def conv2d(x, W, H, w, b, cout, k, threads=0):
+    """x: [H*W][Cin]; w: ggml {k, k, Cin, Cout} flat."""
+    x = _f32(x)
+    out = np.empty((W * H, cout), np.float32)
+    lib().or_conv2d(_ptr(x), W, H, x.shape[1], _ptr(_f32(w)), None if b is None else _ptr(_f32(b)), cout, k,
+                    _ptr(out), threads)
+    return out
+
+
+def maxpool2x2(x, W, H):
+    x = _f32(x)
+    out = np.empty((W * H // 4, x.shape[1]), np.float32)
+    lib().or_maxpool2x2(_ptr(x), W, H, x.shape[1], _ptr(out))
+    return out
+
+
+def neck(weights, x, grid, E, mid, D, threads=0):
+    """weights: dict of NECK_FIELDS numpy arrays (ggml layouts); returns the 4 maps."""
+    keep = {n: _f32(weights[n]) for n in NECK_FIELDS}
+    s = NeckWeights(*[_ptr(keep[n]) for n in NECK_FIELDS])
+    outs = [np.empty(((4 * grid) ** 2, D), np.float32), np.empty(((2 * grid) ** 2, D), np.float32),
+            np.empty((grid * grid, D), np.float32), np.empty(((grid // 2) ** 2, D), np.float32)]
+    arr = (ctypes.c_void_p * 4)(*[_ptr(o) for o in outs])
+    if lib().or_neck(ctypes.byref(s), _ptr(_f32(x)), grid, E, mid, D, arr, threads):
+        raise ValueError("oracle neck rejected its arguments")
+    return outs

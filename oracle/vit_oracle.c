@@ -260,3 +260,98 @@ int or_vit_prefix(const float* image, int img, int patch, const float* kernel, c
     or_layer_norm(out, out, tokens, E, ln_w, ln_b, 1e-5f, threads);
     return 0;
 }
+
+/* ---- SimpleFPN neck ------------------------------------------------------ */
+
+void or_deconv2x2(const float* in, int W, int H, int Cin, const float* w, const float* b, int Cout, float* out,
+                  int threads) {
+    use_threads(threads);
+#pragma omp parallel for schedule(static)
+    for (int64_t p = 0; p < (int64_t)W * H; ++p) {
+        const int x = (int)(p % W), y = (int)(p / W);
+        const float* ir = in + p * Cin;
+        for (int ky = 0; ky < 2; ++ky)
+            for (int kx = 0; kx < 2; ++kx) {
+                float* orow = out + ((int64_t)(2 * y + ky) * 2 * W + 2 * x + kx) * Cout;
+                for (int co = 0; co < Cout; ++co) {
+                    double s = 0.0;
+                    for (int ci = 0; ci < Cin; ++ci)
+                        s += (double)w[kx + 2 * (ky + 2 * (co + (int64_t)Cout * ci))] * (double)ir[ci];
+                    orow[co] = (float)s + (b ? b[co] : 0.f);
+                }
+            }
+    }
+}
+
+void or_conv2d(const float* in, int W, int H, int Cin, const float* w, const float* b, int Cout, int k, float* out,
+               int threads) {
+    const int pad = k / 2;
+    use_threads(threads);
+#pragma omp parallel for schedule(static)
+    for (int64_t p = 0; p < (int64_t)W * H; ++p) {
+        const int x = (int)(p % W), y = (int)(p / W);
+        for (int co = 0; co < Cout; ++co) {
+            double s = 0.0;
+            for (int ky = 0; ky < k; ++ky) {
+                const int iy = y + ky - pad;
+                if (iy < 0 || iy >= H) continue;
+                for (int kx = 0; kx < k; ++kx) {
+                    const int ix = x + kx - pad;
+                    if (ix < 0 || ix >= W) continue;
+                    const float* ir = in + ((int64_t)iy * W + ix) * Cin;
+                    for (int ci = 0; ci < Cin; ++ci)
+                        s += (double)w[kx + k * (ky + k * (ci + (int64_t)Cin * co))] * (double)ir[ci];
+                }
+            }
+            out[p * Cout + co] = (float)s + (b ? b[co] : 0.f);
+        }
+    }
+}
+
+void or_maxpool2x2(const float* in, int W, int H, int C, float* out) {
+    const int W2 = W / 2, H2 = H / 2;
+    for (int y = 0; y < H2; ++y)
+        for (int x = 0; x < W2; ++x)
+            for (int c = 0; c < C; ++c) {
+                float m = in[((int64_t)(2 * y) * W + 2 * x) * C + c];
+                for (int d = 1; d < 4; ++d) {
+                    const float v = in[((int64_t)(2 * y + d / 2) * W + 2 * x + d % 2) * C + c];
+                    if (v > m) m = v;
+                }
+                out[((int64_t)y * W2 + x) * C + c] = m;
+            }
+}
+
+/* sam3_build_neck_graph (src/models/sam3/vision.hpp:307-366). */
+int or_neck(const or_neck_weights* w, const float* x, int grid, int E, int mid, int D, float* out[4], int threads) {
+    const int64_t g = grid, g2 = 2 * g, g4 = 4 * g, gh = g / 2;
+    const int64_t a_n = g2 * g2 * (mid > D ? mid : D), a_pool = gh * gh * E;
+    float* a = (float*)malloc(sizeof(float) * (size_t)(a_n > a_pool ? a_n : a_pool));
+    float* bb = (float*)malloc(sizeof(float) * (size_t)(g4 * g4 * D));
+    float* c = (float*)malloc(sizeof(float) * (size_t)(g4 * g4 * D));
+    int rc = -1;
+    if (!a || !bb || !c || grid % 2) goto done;
+    /* scale 0 */
+    or_deconv2x2(x, grid, grid, E, w->s0_dc1_w, w->s0_dc1_b, mid, a, threads);
+    or_gelu_erf(a, a, g2 * g2 * mid);
+    or_deconv2x2(a, (int)g2, (int)g2, mid, w->s0_dc2_w, w->s0_dc2_b, D, bb, threads);
+    or_conv2d(bb, (int)g4, (int)g4, D, w->s0_c1_w, w->s0_c1_b, D, 1, c, threads);
+    or_conv2d(c, (int)g4, (int)g4, D, w->s0_c3_w, w->s0_c3_b, D, 3, out[0], threads);
+    /* scale 1 */
+    or_deconv2x2(x, grid, grid, E, w->s1_dc_w, w->s1_dc_b, mid, a, threads);
+    or_conv2d(a, (int)g2, (int)g2, mid, w->s1_c1_w, w->s1_c1_b, D, 1, c, threads);
+    or_conv2d(c, (int)g2, (int)g2, D, w->s1_c3_w, w->s1_c3_b, D, 3, out[1], threads);
+    /* scale 2 */
+    or_conv2d(x, grid, grid, E, w->s2_c1_w, w->s2_c1_b, D, 1, c, threads);
+    or_conv2d(c, grid, grid, D, w->s2_c3_w, w->s2_c3_b, D, 3, out[2], threads);
+    /* scale 3 */
+    or_maxpool2x2(x, grid, grid, E, a);
+    or_conv2d(a, (int)gh, (int)gh, E, w->s3_c1_w, w->s3_c1_b, D, 1, c, threads);
+    or_conv2d(c, (int)gh, (int)gh, D, w->s3_c3_w, w->s3_c3_b, D, 3, out[3], threads);
+    rc = 0;
+done:
+    free(a);
+    free(bb);
+    free(c);
+    return rc;
+}

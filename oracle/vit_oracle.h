@@ -89,6 +89,38 @@ int or_vit_block(const or_vit_block_weights* wts, const float* x_in, float* x_ou
 int or_vit_prefix(const float* image, int img, int patch, const float* kernel, const float* pos, int pos_grid,
                   const float* ln_w, const float* ln_b, int E, float* out, int threads);
 
+/* ---- SimpleFPN neck (src/models/sam3/vision.hpp:307-366) ----------------
+ * Feature maps are pixel-major rows of C floats: pixel (x, y) of a W x H
+ * map at row y*W + x (ggml ne = {C, W, H}).  Sums in double. */
+
+/* ConvTranspose2d k=2 s=2 (sam3_deconv_2x2, src/models/sam3/ops.hpp:96-121):
+ * out[(2y+ky)*2W + 2x+kx][co] = b[co] + sum_ci w[kx + 2*(ky + 2*(co + Cout*ci))] * in[y*W+x][ci]
+ * (weight ggml {2, 2, Cout, Cin}); b may be NULL. */
+void or_deconv2x2(const float* in, int W, int H, int Cin, const float* w, const float* b, int Cout, float* out,
+                  int threads);
+/* Conv2d stride 1, k x k, zero padding k/2 (sam3_conv_2d, ops.hpp:71-94):
+ * out[y*W+x][co] = b[co] + sum w[kx + k*(ky + k*(ci + Cin*co))] * in[(y+ky-p)*W + x+kx-p][ci]
+ * (weight ggml {k, k, Cin, Cout}). */
+void or_conv2d(const float* in, int W, int H, int Cin, const float* w, const float* b, int Cout, int k, float* out,
+               int threads);
+/* ggml_pool_2d MAX 2x2 stride 2 (W, H even). */
+void or_maxpool2x2(const float* in, int W, int H, int C, float* out);
+
+typedef struct {
+    /* scale 0: deconv (E -> mid), GELU, deconv (mid -> D), 1x1, 3x3 */
+    const float *s0_dc1_w, *s0_dc1_b, *s0_dc2_w, *s0_dc2_b, *s0_c1_w, *s0_c1_b, *s0_c3_w, *s0_c3_b;
+    /* scale 1: deconv (E -> mid), 1x1 (mid -> D), 3x3 */
+    const float *s1_dc_w, *s1_dc_b, *s1_c1_w, *s1_c1_b, *s1_c3_w, *s1_c3_b;
+    /* scale 2: 1x1 (E -> D), 3x3 */
+    const float *s2_c1_w, *s2_c1_b, *s2_c3_w, *s2_c3_b;
+    /* scale 3: maxpool, 1x1 (E -> D), 3x3 */
+    const float *s3_c1_w, *s3_c1_b, *s3_c3_w, *s3_c3_b;
+} or_neck_weights;
+
+/* sam3_build_neck_graph on the ViT output x (grid x grid rows of E): out[i]
+ * are (4, 2, 1, 0.5) x grid maps of D channels. */
+int or_neck(const or_neck_weights* w, const float* x, int grid, int E, int mid, int D, float* out[4], int threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -493,7 +493,7 @@ int samhip_get_rows(samhip_context* ctx, const samhip_tensor* src, const samhip_
 int samhip_quantize_rows(samhip_context* ctx, int32_t type, const float* src, size_t src_row_stride, void* dst,
                          int64_t rows, int64_t k, int32_t q8_rounding) {
     if (!ctx || !src || !dst || rows <= 0 || k <= 0) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: invalid argument");
-    if (type != T_Q8_0 && type != T_Q8_K && type != T_Q4_K && type != T_Q5_K && type != T_Q6_K)
+    if (type != T_F16 && type != T_Q8_0 && type != T_Q8_K && type != T_Q4_K && type != T_Q5_K && type != T_Q6_K)
         return fail(SAMHIP_ERR_UNSUPPORTED, "quantize_rows: unsupported type %d", type);
     if (k % block_elems(type)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: k must be a multiple of %d", block_elems(type));
     if (src_row_stride < size_t(4 * k) || src_row_stride % 4 || reinterpret_cast<uintptr_t>(src) % 4)
@@ -502,8 +502,12 @@ int samhip_quantize_rows(samhip_context* ctx, int32_t type, const float* src, si
         return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: unknown Q8 rounding");
     if ((type == T_Q8_K) && reinterpret_cast<uintptr_t>(dst) % 4) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: Q8_K dst must be 4-byte aligned");
     if (rows > (int64_t(1) << 30) || k > (int64_t(1) << 24)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: too large");
+    if (type == T_F16 && reinterpret_cast<uintptr_t>(dst) % 2)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: F16 dst must be 2-byte aligned");
     if (int rc = set_device(ctx)) return rc;
-    if (type == T_Q8_0 || type == T_Q8_K)
+    if (type == T_F16)
+        launch_cast_f16(src, int64_t(src_row_stride / 4), int(rows), int(k), static_cast<_Float16*>(dst), ctx->stream);
+    else if (type == T_Q8_0 || type == T_Q8_K)
         launch_quantize_act(type, src, int64_t(src_row_stride / 4), int(rows), int(k), dst,
                             q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->stream);
     else
@@ -515,7 +519,10 @@ int samhip_quantize_rows(samhip_context* ctx, int32_t type, const float* src, si
 int samhip_dequantize_rows(samhip_context* ctx, int32_t type, const void* src, size_t src_row_stride, float* dst,
                            int64_t rows, int64_t k) {
     if (!ctx || !src || !dst || rows <= 0 || k <= 0) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "dequantize_rows: invalid argument");
-    if (!is_weight_type(type) && type != T_Q8_K) return fail(SAMHIP_ERR_UNSUPPORTED, "dequantize_rows: unsupported type %d", type);
+    if (!is_weight_type(type) && type != T_Q8_K && type != T_F16)
+        return fail(SAMHIP_ERR_UNSUPPORTED, "dequantize_rows: unsupported type %d", type);
+    if (type == T_F16 && (k % 32 || reinterpret_cast<uintptr_t>(src) % 2 || src_row_stride % 2))
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "dequantize_rows: F16 rows must be 32-value groups, 2-byte aligned");
     if (k % block_elems(type) || src_row_stride < row_bytes(type, k))
         return fail(SAMHIP_ERR_INVALID_ARGUMENT, "dequantize_rows: invalid row shape");
     if (rows > (int64_t(1) << 30) || k > (int64_t(1) << 24)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "dequantize_rows: too large");

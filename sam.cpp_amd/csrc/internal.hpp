@@ -13,6 +13,9 @@ void launch_stage_rows(int mode, bool aligned, const float* x, int64_t x_stride,
 void launch_quantize_act(int type, const float* x, int64_t x_stride, int rows, int K, void* dst, int x86,
                          hipStream_t stream);
 
+// F32 -> F16 rows, packed (ggml_cast to F16).
+void launch_cast_f16(const float* x, int64_t x_stride, int rows, int K, _Float16* dst, hipStream_t stream);
+
 // Q4_K / Q5_K / Q6_K weight rows in ggml wire format (ggml_quantize_chunk).
 void launch_quantize_weights(int type, const float* x, int64_t x_stride, int rows, int K, void* dst,
                              hipStream_t stream);

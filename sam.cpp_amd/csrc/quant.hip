@@ -495,6 +495,21 @@ void launch_stage_rows(int mode, bool aligned, const float* x, int64_t x_stride,
 #undef SAMHIP_STAGE
 }
 
+// F32 -> F16 rows (ggml_cast to F16: round to nearest even, overflow to inf).
+__global__ __launch_bounds__(256) void cast_f16_kernel(const float* __restrict__ x, int64_t x_stride, int rows, int K,
+                                                       _Float16* __restrict__ dst) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= int64_t(rows) * K) return;
+    const int64_t r = i / K, c = i - r * K;
+    dst[i] = (_Float16)x[r * x_stride + c];
+}
+
+void launch_cast_f16(const float* x, int64_t x_stride, int rows, int K, _Float16* dst, hipStream_t stream) {
+    const int64_t n = int64_t(rows) * K;
+    hipLaunchKernelGGL(cast_f16_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, x, x_stride, rows, K,
+                       dst);
+}
+
 void launch_quantize_act(int type, const float* x, int64_t x_stride, int rows, int K, void* dst, int x86,
                          hipStream_t stream) {
     const dim3 grid((rows + 3) / 4), block(256);

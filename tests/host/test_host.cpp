@@ -7,6 +7,7 @@
 // (tests/api/test_contracts.cpp:327-339, tests/models/test_image_cli.cpp:25-65,
 // tests/runtime/ggml/test_quantization.cpp:105-175), extended to HIP.
 #include "sam_hip.hpp"
+#include "feature_cache.hpp"
 #include "ggml_oracle.h"
 
 #include <cmath>
@@ -204,6 +205,60 @@ void test_no_device() {
     CHECK(throws<std::runtime_error>([] { sam::HipBackend::make(0); }, "no visible devices"));
 }
 
+// Feature-cache snapshots without a device: the reference's HostTensor
+// checks (src/runtime/ggml/host_tensor.hpp:36-91).
+void test_feature_cache_cpu() {
+    using namespace sam;
+    // exact host decode of hand-made Q8_0 blocks: d = 0.5, codes -3 and 127
+    std::vector<uint8_t> blk(34, 0);
+    blk[0] = 0x00;
+    blk[1] = 0x38;   // 0.5 in binary16
+    blk[2] = uint8_t(int8_t(-3));
+    blk[33] = 127;
+    std::vector<uint8_t> two = blk;
+    two.insert(two.end(), blk.begin(), blk.end());
+    const HipHostTensor q = HipHostTensor::from_bytes(SAMHIP_TYPE_Q8_0, 1, 64, two);
+    const std::vector<float> f = q.as_f32();
+    CHECK(f.size() == 64 && f[0] == -1.5f && f[1] == 0.f && f[31] == 63.5f && f[32] == -1.5f && f[63] == 63.5f);
+    // flattening allowed, a different row layout is not
+    q.validate_shape(64, 1, 1, 1);
+    CHECK(throws<std::invalid_argument>([&] { q.validate_shape(32, 2, 1, 1); }, "row layout"));
+    CHECK(throws<std::invalid_argument>([&] { q.validate_shape(64, 2, 1, 1); }, "row layout"));
+    CHECK(throws<std::invalid_argument>([&] { q.validate_shape(64, 0, 1, 1); }, "dimension"));
+    // non-finite or negative scales are rejected
+    for (uint16_t bad : {uint16_t(0x7c00), uint16_t(0x7e00), uint16_t(0xb800)}) {
+        std::vector<uint8_t> b = two;
+        b[34] = uint8_t(bad & 0xff);
+        b[35] = uint8_t(bad >> 8);
+        CHECK(throws<std::runtime_error>([&] { HipHostTensor::from_bytes(SAMHIP_TYPE_Q8_0, 1, 64, b); },
+                                         "non-finite or invalid"));
+    }
+    // F16: every element is checked; -2 and a subnormal decode exactly
+    std::vector<uint8_t> h(64, 0);
+    h[0] = 0x00, h[1] = 0xc0;   // -2
+    h[2] = 0x01, h[3] = 0x00;   // 2^-24
+    const std::vector<float> hf = HipHostTensor::from_bytes(SAMHIP_TYPE_F16, 1, 32, h).as_f32();
+    CHECK(hf[0] == -2.f && hf[1] == std::ldexp(1.f, -24) && hf[2] == 0.f);
+    h[62] = 0x00, h[63] = 0x7c;   // +inf
+    CHECK(throws<std::runtime_error>([&] { HipHostTensor::from_bytes(SAMHIP_TYPE_F16, 1, 32, h); }, "non-finite"));
+    // half_to_float agrees with the oracle's conversion on every binary16 value
+    bool same = true;
+    for (uint32_t b = 0; b < 65536; ++b) {
+        const float a = half_to_float(uint16_t(b)), o = or_fp16_to_fp32(uint16_t(b));
+        uint32_t x, y;
+        std::memcpy(&x, &a, 4);
+        std::memcpy(&y, &o, 4);
+        same = same && (x == y || (std::isnan(a) && std::isnan(o)));
+    }
+    CHECK(same);
+    // wrong sizes and types
+    CHECK(throws<std::runtime_error>([&] { HipHostTensor::from_bytes(SAMHIP_TYPE_Q8_0, 1, 64, blk); }, "layout"));
+    CHECK(throws<std::runtime_error>([&] { HipHostTensor::from_bytes(SAMHIP_TYPE_Q4_K, 1, 256, {}); }, "type"));
+    CHECK(feature_cache_level_type(2, SAMHIP_TYPE_Q8_0) == SAMHIP_TYPE_F32);
+    CHECK(feature_cache_level_type(1, SAMHIP_TYPE_Q8_0) == SAMHIP_TYPE_Q8_0);
+    CHECK(feature_cache_level_type(2, SAMHIP_TYPE_F16) == SAMHIP_TYPE_F16);
+}
+
 // ---------------------------------------------------------------------------
 
 double max_row_rel_l2(const std::vector<float>& y, const std::vector<float>& ref, int m, int n) {
@@ -306,6 +361,44 @@ void test_gpu() {
     }, "activation width"));
 
     for (void* p : {d_w, d_e, d_xs, d_xt, d_ys, d_yt, d_ids, d_rows}) backend.free(p);
+
+    // feature caches of a neck-level map (144 x 144 x 256): device cast,
+    // host snapshot, re-upload with device decode
+    const int64_t fr = 144 * 144, fc = 256;
+    std::vector<float> feat(size_t(fr * fc));
+    or_rng_normal(9, 0.f, 2.f, feat.data(), int64_t(feat.size()));
+    feat[5] = 1e6f;   // beyond F16 range in a row that Q8_0 still represents
+    void* d_feat = backend.alloc(feat.size() * 4);
+    void* d_back = backend.alloc(feat.size() * 4);
+    backend.upload(d_feat, feat.data(), feat.size() * 4);
+    // Q8_0: bytes equal the oracle's x86 quantizer, decode equals to_float
+    const HipHostTensor q8 = HipHostTensor::capture(backend, static_cast<float*>(d_feat), fr, fc, SAMHIP_TYPE_Q8_0);
+    std::vector<uint8_t> ref_q(q8.size_bytes());
+    or_quantize_q8_0(feat.data(), ref_q.data(), fr, fc, OR_Q8_ROUND_X86);
+    CHECK(q8.bytes() == ref_q);
+    std::vector<float> ref_f(feat.size());
+    or_dequantize(OR_Q8_0, ref_q.data(), ref_f.data(), fr, fc);
+    CHECK(q8.as_f32() == ref_f);
+    q8.upload_f32(backend, static_cast<float*>(d_back));
+    std::vector<float> back(feat.size());
+    backend.download(back.data(), d_back, back.size() * 4);
+    CHECK(back == ref_f);
+    q8.validate_shape(fc, 144, 144, 1);
+    // F16: round to nearest even per value; the 1e6 overflows and is rejected
+    CHECK(throws<std::runtime_error>([&] {
+        HipHostTensor::capture(backend, static_cast<float*>(d_feat), fr, fc, SAMHIP_TYPE_F16);
+    }, "non-finite"));
+    feat[5] = 3.f;
+    backend.upload(d_feat, feat.data(), feat.size() * 4);
+    const HipHostTensor f16 = HipHostTensor::capture(backend, static_cast<float*>(d_feat), fr, fc, SAMHIP_TYPE_F16);
+    std::vector<uint16_t> ref_h(feat.size());
+    or_fp32_to_fp16_rows(feat.data(), ref_h.data(), int64_t(feat.size()));
+    CHECK(std::memcmp(f16.bytes().data(), ref_h.data(), f16.size_bytes()) == 0);
+    f16.upload_f32(backend, static_cast<float*>(d_back));
+    backend.download(back.data(), d_back, back.size() * 4);
+    CHECK(back == f16.as_f32());
+    backend.free(d_feat);
+    backend.free(d_back);
 }
 
 }  // namespace
@@ -319,6 +412,7 @@ int main(int argc, char** argv) {
             test_policy();
             test_status_mapping_without_device();
             test_no_device();
+            test_feature_cache_cpu();
         } else if (mode == "--gpu") {
             test_gpu();
         } else {

@@ -108,6 +108,21 @@ def test_dequantize_bit_exact(gpu_ctx, oracle, qtype):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+def test_f16_cast_round_trip_bit_exact(gpu_ctx, samhip):
+    """ggml_cast F32 -> F16 (the F16 feature cache) and back: round to
+    nearest even, overflow to +-inf, subnormals kept, against numpy."""
+    say("case f16 cast")
+    rng = np.random.default_rng(25)
+    x = (rng.standard_normal((37, 256)) * 3).astype(np.float32)
+    x[0, :6] = [65504.0, 65520.0, -1e9, 2.0 ** -20, 6.1e-5, -0.0]
+    x[1, :4] = np.float32(1) + np.float32(2.0 ** -11) * np.array([1, 3, 1.5, 2.5], np.float32)   # ties
+    got = gpu_ctx.quantize(samhip.F16, x)
+    ref = x.astype(np.float16)
+    assert np.array_equal(got.view(np.uint16).reshape(ref.shape), ref.view(np.uint16))
+    back = gpu_ctx.dequantize(samhip.F16, got, 256)
+    assert np.array_equal(back.view(np.uint32), ref.astype(np.float32).view(np.uint32))
+
+
 @pytest.mark.parametrize("qtype", [0, 8, 12, 14])
 def test_get_rows(gpu_ctx, oracle, samhip, qtype):
     say("case get_rows", qtype)

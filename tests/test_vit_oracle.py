@@ -168,3 +168,80 @@ def test_block_composition(oracle, ws):
     # linear moves a row by ~1e-4 of its norm
     assert rel.max() < 5e-4, rel.max()
     assert np.median(rel) < 1e-5
+
+
+# ---- SimpleFPN neck ----------------------------------------------------------
+
+def np_deconv(x, W, H, w, b, cout):
+    """ConvTranspose2d k=2 s=2 in float64 (PyTorch semantics; weight ggml {2,2,Cout,Cin} = torch [Cin][Cout][2][2])."""
+    cin = x.shape[1]
+    wt = w.reshape(cin, cout, 2, 2).astype(np.float64)           # [ci][co][ky][kx]
+    img = x.reshape(H, W, cin).astype(np.float64)
+    out = np.einsum("yxc,cokl->ykxlo", img, wt).reshape(2 * H, 2 * W, cout)
+    return (out + (0 if b is None else b)).reshape(-1, cout)
+
+
+def np_conv(x, W, H, w, b, cout, k):
+    """Conv2d stride 1, padding k//2, in float64 (weight ggml {k,k,Cin,Cout} = torch [Cout][Cin][k][k])."""
+    cin, p = x.shape[1], k // 2
+    wt = w.reshape(cout, cin, k, k).astype(np.float64)
+    img = np.pad(x.reshape(H, W, cin).astype(np.float64), ((p, p), (p, p), (0, 0)))
+    out = np.zeros((H, W, cout))
+    for ky in range(k):
+        for kx in range(k):
+            out += img[ky:ky + H, kx:kx + W] @ wt[:, :, ky, kx].T
+    return (out + (0 if b is None else b)).reshape(-1, cout)
+
+
+def test_deconv_conv_pool_against_float64(oracle):
+    rng = np.random.default_rng(12)
+    W, H, cin, cout = 6, 4, 12, 8
+    x = rng.standard_normal((W * H, cin)).astype(np.float32)
+    wd = rng.standard_normal(2 * 2 * cout * cin).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32)
+    assert np.abs(oracle.deconv2x2(x, W, H, wd, b, cout) - np_deconv(x, W, H, wd, b, cout)).max() < 1e-5
+    for k in (1, 3):
+        wc = rng.standard_normal(k * k * cin * cout).astype(np.float32)
+        assert np.abs(oracle.conv2d(x, W, H, wc, b, cout, k) - np_conv(x, W, H, wc, b, cout, k)).max() < 1e-5
+    # a 3x3 kernel with only the centre tap equals the 1x1 convolution
+    w1 = rng.standard_normal(cin * cout).astype(np.float32)
+    w3 = np.zeros((cout, cin, 3, 3), np.float32)
+    w3[:, :, 1, 1] = w1.reshape(cout, cin)
+    assert np.array_equal(oracle.conv2d(x, W, H, w3.ravel(), b, cout, 3), oracle.conv2d(x, W, H, w1, b, cout, 1))
+    p = oracle.maxpool2x2(x, W, H)
+    assert np.array_equal(p, x.reshape(H // 2, 2, W // 2, 2, cin).max(axis=(1, 3)).reshape(-1, cin))
+
+
+def neck_weights(rng, E, mid, D):
+    def r(*shape, s=0.05):
+        return (rng.standard_normal(shape) * s).astype(np.float32).ravel()
+    return {"s0_dc1_w": r(E, mid, 2, 2), "s0_dc1_b": r(mid), "s0_dc2_w": r(mid, D, 2, 2), "s0_dc2_b": r(D),
+            "s0_c1_w": r(D, D), "s0_c1_b": r(D), "s0_c3_w": r(D, D, 3, 3), "s0_c3_b": r(D),
+            "s1_dc_w": r(E, mid, 2, 2), "s1_dc_b": r(mid), "s1_c1_w": r(D, mid), "s1_c1_b": r(D),
+            "s1_c3_w": r(D, D, 3, 3), "s1_c3_b": r(D), "s2_c1_w": r(D, E), "s2_c1_b": r(D),
+            "s2_c3_w": r(D, D, 3, 3), "s2_c3_b": r(D), "s3_c1_w": r(D, E), "s3_c1_b": r(D),
+            "s3_c3_w": r(D, D, 3, 3), "s3_c3_b": r(D)}
+
+
+def test_neck_composition(oracle):
+    """or_neck equals the reference graph's order of the pinned pieces."""
+    rng = np.random.default_rng(13)
+    grid, E, mid, D = 4, 16, 12, 8
+    w = neck_weights(rng, E, mid, D)
+    x = rng.standard_normal((grid * grid, E)).astype(np.float32)
+    outs = oracle.neck(w, x, grid, E, mid, D)
+    g = grid
+    s0 = np_deconv(x, g, g, w["s0_dc1_w"], w["s0_dc1_b"], mid)
+    s0 = (0.5 * s0 * (1 + erf(s0 / np.sqrt(2))))
+    s0 = np_deconv(s0, 2 * g, 2 * g, w["s0_dc2_w"], w["s0_dc2_b"], D)
+    s0 = np_conv(s0, 4 * g, 4 * g, w["s0_c1_w"], w["s0_c1_b"], D, 1)
+    s0 = np_conv(s0, 4 * g, 4 * g, w["s0_c3_w"], w["s0_c3_b"], D, 3)
+    s1 = np_deconv(x, g, g, w["s1_dc_w"], w["s1_dc_b"], mid)
+    s1 = np_conv(np_conv(s1, 2 * g, 2 * g, w["s1_c1_w"], w["s1_c1_b"], D, 1), 2 * g, 2 * g, w["s1_c3_w"],
+                 w["s1_c3_b"], D, 3)
+    s2 = np_conv(np_conv(x, g, g, w["s2_c1_w"], w["s2_c1_b"], D, 1), g, g, w["s2_c3_w"], w["s2_c3_b"], D, 3)
+    xp = x.reshape(g // 2, 2, g // 2, 2, E).max(axis=(1, 3)).reshape(-1, E)
+    s3 = np_conv(np_conv(xp, g // 2, g // 2, w["s3_c1_w"], w["s3_c1_b"], D, 1), g // 2, g // 2, w["s3_c3_w"],
+                 w["s3_c3_b"], D, 3)
+    for got, ref in zip(outs, (s0, s1, s2, s3)):
+        assert np.abs(got - ref).max() < 1e-4 * max(1.0, np.abs(ref).max())
