@@ -216,6 +216,39 @@ typedef struct samhip_vit_prefix_desc {
  * fp16 operands), tiled position embedding, ln_pre. */
 int samhip_vit_prefix(samhip_context* ctx, const samhip_vit_prefix_desc* prefix, const float* image, float* x);
 
+/* One scale of the SimpleFPN neck (sam3_neck_scale,
+ * src/models/sam3/architecture.hpp:87-96): device F32 weights in their ggml
+ * layouts, transposed convolutions {2, 2, Cout, Cin}, convolutions
+ * {k, k, Cin, Cout}, biases [Cout].  Scale 0 uses every field; scale 1 no
+ * deconv2; scales 2 and 3 neither deconvolution. */
+typedef struct samhip_neck_scale {
+    const float *deconv1_w, *deconv1_b;
+    const float *deconv2_w, *deconv2_b;
+    const float *conv1x1_w, *conv1x1_b;
+    const float *conv3x3_w, *conv3x3_b;
+} samhip_neck_scale;
+
+typedef struct samhip_vit_neck_desc {
+    int32_t version;                    /* SAMHIP_ABI_VERSION */
+    int32_t grid, embed, mid, dim;      /* SAM 3: 72, 1024, 512 (deconvolution width), 256 (neck_dim) */
+    /* im2col columns of the 1x1 and 3x3 convolutions (the runtime's
+     * convolution_columns_type, src/models/sam3/ops.hpp:68-84):
+     * SAMHIP_TYPE_F32 keeps F32 accuracy (split fp16 operands),
+     * SAMHIP_TYPE_F16 rounds both operands to fp16.  The transposed
+     * convolutions are F32-accurate either way (ops.hpp:107-108). */
+    int32_t columns_type;
+    samhip_neck_scale scales[4];
+} samhip_vit_neck_desc;
+
+/* sam3_build_neck_graph (src/models/sam3/vision.hpp:307-366) on the ViT
+ * output x (device F32 [grid*grid][embed], 16-byte aligned): level i, when
+ * its pointer is non-NULL, receives the (4, 2, 1, 1/2) x grid map as device
+ * F32 [side*side][dim] (pixel rows, 16-byte aligned).  A NULL level is not
+ * computed (the image path outputs levels 0-2, execution.hpp:73-83).
+ * embed, mid and dim must be multiples of 4; level 3 needs an even grid. */
+int samhip_vit_neck(samhip_context* ctx, const samhip_vit_neck_desc* neck, const float* x, float* level0,
+                    float* level1, float* level2, float* level3);
+
 /* Pieces of the same graph as single operators.
  * GGML_OP_NORM followed by the gain/bias of sam3_layer_norm
  * (src/models/sam3/ops.hpp:56-66): y = ggml_norm(x, eps) * w + b over rows of

@@ -75,8 +75,9 @@ def lib():
         L.or_vit_prefix.argtypes = [P, I, I, P, P, I, P, P, I, P, I]
         L.or_deconv2x2.argtypes = [P, I, I, I, P, P, I, P, I]
         L.or_conv2d.argtypes = [P, I, I, I, P, P, I, I, P, I]
+        L.or_conv2d_cols.argtypes = [P, I, I, I, P, P, I, I, I, P, I]
         L.or_maxpool2x2.argtypes = [P, I, I, I, P]
-        L.or_neck.argtypes = [ctypes.POINTER(NeckWeights), P, I, I, I, I, ctypes.POINTER(P), I]
+        L.or_neck.argtypes = [ctypes.POINTER(NeckWeights), P, I, I, I, I, I, ctypes.POINTER(P), I]
         _lib = L
     return _lib
 
@@ -275,12 +276,12 @@ def deconv2x2(x, W, H, w, b, cout, threads=0):
     return out
 
 
-def conv2d(x, W, H, w, b, cout, k, threads=0):
-    """x: [H*W][Cin]; w: ggml {k, k, Cin, Cout} flat."""
+def conv2d(x, W, H, w, b, cout, k, threads=0, columns_f16=False):
+    """x: [H*W][Cin]; w: ggml {k, k, Cin, Cout} flat; columns_f16 rounds both operands to fp16."""
     x = _f32(x)
     out = np.empty((W * H, cout), np.float32)
-    lib().or_conv2d(_ptr(x), W, H, x.shape[1], _ptr(_f32(w)), None if b is None else _ptr(_f32(b)), cout, k,
-                    _ptr(out), threads)
+    lib().or_conv2d_cols(_ptr(x), W, H, x.shape[1], _ptr(_f32(w)), None if b is None else _ptr(_f32(b)), cout, k,
+                         int(columns_f16), _ptr(out), threads)
     return out
 
 
@@ -291,13 +292,14 @@ def maxpool2x2(x, W, H):
     return out
 
 
-def neck(weights, x, grid, E, mid, D, threads=0):
-    """weights: dict of NECK_FIELDS numpy arrays (ggml layouts); returns the 4 maps."""
-    keep = {n: _f32(weights[n]) for n in NECK_FIELDS}
-    s = NeckWeights(*[_ptr(keep[n]) for n in NECK_FIELDS])
-    outs = [np.empty(((4 * grid) ** 2, D), np.float32), np.empty(((2 * grid) ** 2, D), np.float32),
-            np.empty((grid * grid, D), np.float32), np.empty(((grid // 2) ** 2, D), np.float32)]
-    arr = (ctypes.c_void_p * 4)(*[_ptr(o) for o in outs])
-    if lib().or_neck(ctypes.byref(s), _ptr(_f32(x)), grid, E, mid, D, arr, threads):
+def neck(weights, x, grid, E, mid, D, threads=0, columns_f16=False, levels=(0, 1, 2, 3)):
+    """weights: dict of NECK_FIELDS numpy arrays (ggml layouts; those of
+    skipped levels may be absent); returns the 4 maps (None when skipped)."""
+    keep = {n: _f32(weights[n]) for n in NECK_FIELDS if n in weights}
+    s = NeckWeights(*[_ptr(keep[n]) if n in keep else None for n in NECK_FIELDS])
+    sides = (4 * grid, 2 * grid, grid, grid // 2)
+    outs = [np.empty((sides[i] ** 2, D), np.float32) if i in levels else None for i in range(4)]
+    arr = (ctypes.c_void_p * 4)(*[None if o is None else _ptr(o) for o in outs])
+    if lib().or_neck(ctypes.byref(s), _ptr(_f32(x)), grid, E, mid, D, int(columns_f16), arr, threads):
         raise ValueError("oracle neck rejected its arguments")
     return outs

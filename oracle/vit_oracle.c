@@ -283,8 +283,17 @@ void or_deconv2x2(const float* in, int W, int H, int Cin, const float* w, const 
     }
 }
 
+static inline double conv_operand(float v, int columns_f16) {
+    return columns_f16 ? (double)or_fp16_to_fp32(or_fp32_to_fp16(v)) : (double)v;
+}
+
 void or_conv2d(const float* in, int W, int H, int Cin, const float* w, const float* b, int Cout, int k, float* out,
                int threads) {
+    or_conv2d_cols(in, W, H, Cin, w, b, Cout, k, 0, out, threads);
+}
+
+void or_conv2d_cols(const float* in, int W, int H, int Cin, const float* w, const float* b, int Cout, int k,
+                    int columns_f16, float* out, int threads) {
     const int pad = k / 2;
     use_threads(threads);
 #pragma omp parallel for schedule(static)
@@ -300,7 +309,8 @@ void or_conv2d(const float* in, int W, int H, int Cin, const float* w, const flo
                     if (ix < 0 || ix >= W) continue;
                     const float* ir = in + ((int64_t)iy * W + ix) * Cin;
                     for (int ci = 0; ci < Cin; ++ci)
-                        s += (double)w[kx + k * (ky + k * (ci + (int64_t)Cin * co))] * (double)ir[ci];
+                        s += conv_operand(w[kx + k * (ky + k * (ci + (int64_t)Cin * co))], columns_f16) *
+                             conv_operand(ir[ci], columns_f16);
                 }
             }
             out[p * Cout + co] = (float)s + (b ? b[co] : 0.f);
@@ -323,31 +333,42 @@ void or_maxpool2x2(const float* in, int W, int H, int C, float* out) {
 }
 
 /* sam3_build_neck_graph (src/models/sam3/vision.hpp:307-366). */
-int or_neck(const or_neck_weights* w, const float* x, int grid, int E, int mid, int D, float* out[4], int threads) {
+int or_neck(const or_neck_weights* w, const float* x, int grid, int E, int mid, int D, int columns_f16, float* out[4],
+            int threads) {
+    const int cf = columns_f16;
     const int64_t g = grid, g2 = 2 * g, g4 = 4 * g, gh = g / 2;
     const int64_t a_n = g2 * g2 * (mid > D ? mid : D), a_pool = gh * gh * E;
     float* a = (float*)malloc(sizeof(float) * (size_t)(a_n > a_pool ? a_n : a_pool));
     float* bb = (float*)malloc(sizeof(float) * (size_t)(g4 * g4 * D));
     float* c = (float*)malloc(sizeof(float) * (size_t)(g4 * g4 * D));
     int rc = -1;
-    if (!a || !bb || !c || grid % 2) goto done;
+    if (!a || !bb || !c) goto done;
+    if (out[3] && grid % 2) goto done;
     /* scale 0 */
-    or_deconv2x2(x, grid, grid, E, w->s0_dc1_w, w->s0_dc1_b, mid, a, threads);
-    or_gelu_erf(a, a, g2 * g2 * mid);
-    or_deconv2x2(a, (int)g2, (int)g2, mid, w->s0_dc2_w, w->s0_dc2_b, D, bb, threads);
-    or_conv2d(bb, (int)g4, (int)g4, D, w->s0_c1_w, w->s0_c1_b, D, 1, c, threads);
-    or_conv2d(c, (int)g4, (int)g4, D, w->s0_c3_w, w->s0_c3_b, D, 3, out[0], threads);
+    if (out[0]) {
+        or_deconv2x2(x, grid, grid, E, w->s0_dc1_w, w->s0_dc1_b, mid, a, threads);
+        or_gelu_erf(a, a, g2 * g2 * mid);
+        or_deconv2x2(a, (int)g2, (int)g2, mid, w->s0_dc2_w, w->s0_dc2_b, D, bb, threads);
+        or_conv2d_cols(bb, (int)g4, (int)g4, D, w->s0_c1_w, w->s0_c1_b, D, 1, cf, c, threads);
+        or_conv2d_cols(c, (int)g4, (int)g4, D, w->s0_c3_w, w->s0_c3_b, D, 3, cf, out[0], threads);
+    }
     /* scale 1 */
-    or_deconv2x2(x, grid, grid, E, w->s1_dc_w, w->s1_dc_b, mid, a, threads);
-    or_conv2d(a, (int)g2, (int)g2, mid, w->s1_c1_w, w->s1_c1_b, D, 1, c, threads);
-    or_conv2d(c, (int)g2, (int)g2, D, w->s1_c3_w, w->s1_c3_b, D, 3, out[1], threads);
+    if (out[1]) {
+        or_deconv2x2(x, grid, grid, E, w->s1_dc_w, w->s1_dc_b, mid, a, threads);
+        or_conv2d_cols(a, (int)g2, (int)g2, mid, w->s1_c1_w, w->s1_c1_b, D, 1, cf, c, threads);
+        or_conv2d_cols(c, (int)g2, (int)g2, D, w->s1_c3_w, w->s1_c3_b, D, 3, cf, out[1], threads);
+    }
     /* scale 2 */
-    or_conv2d(x, grid, grid, E, w->s2_c1_w, w->s2_c1_b, D, 1, c, threads);
-    or_conv2d(c, grid, grid, D, w->s2_c3_w, w->s2_c3_b, D, 3, out[2], threads);
+    if (out[2]) {
+        or_conv2d_cols(x, grid, grid, E, w->s2_c1_w, w->s2_c1_b, D, 1, cf, c, threads);
+        or_conv2d_cols(c, grid, grid, D, w->s2_c3_w, w->s2_c3_b, D, 3, cf, out[2], threads);
+    }
     /* scale 3 */
-    or_maxpool2x2(x, grid, grid, E, a);
-    or_conv2d(a, (int)gh, (int)gh, E, w->s3_c1_w, w->s3_c1_b, D, 1, c, threads);
-    or_conv2d(c, (int)gh, (int)gh, D, w->s3_c3_w, w->s3_c3_b, D, 3, out[3], threads);
+    if (out[3]) {
+        or_maxpool2x2(x, grid, grid, E, a);
+        or_conv2d_cols(a, (int)gh, (int)gh, E, w->s3_c1_w, w->s3_c1_b, D, 1, cf, c, threads);
+        or_conv2d_cols(c, (int)gh, (int)gh, D, w->s3_c3_w, w->s3_c3_b, D, 3, cf, out[3], threads);
+    }
     rc = 0;
 done:
     free(a);

@@ -103,6 +103,12 @@ void or_deconv2x2(const float* in, int W, int H, int Cin, const float* w, const 
  * (weight ggml {k, k, Cin, Cout}). */
 void or_conv2d(const float* in, int W, int H, int Cin, const float* w, const float* b, int Cout, int k, float* out,
                int threads);
+/* The same with F16 im2col columns when columns_f16 != 0: each input value
+ * and each kernel value enters the product rounded to fp16 (the F16
+ * convolution_columns_type, ops.hpp:68-84, whose product narrows the kernel
+ * to the columns' type). */
+void or_conv2d_cols(const float* in, int W, int H, int Cin, const float* w, const float* b, int Cout, int k,
+                    int columns_f16, float* out, int threads);
 /* ggml_pool_2d MAX 2x2 stride 2 (W, H even). */
 void or_maxpool2x2(const float* in, int W, int H, int C, float* out);
 
@@ -118,8 +124,10 @@ typedef struct {
 } or_neck_weights;
 
 /* sam3_build_neck_graph on the ViT output x (grid x grid rows of E): out[i]
- * are (4, 2, 1, 0.5) x grid maps of D channels. */
-int or_neck(const or_neck_weights* w, const float* x, int grid, int E, int mid, int D, float* out[4], int threads);
+ * are (4, 2, 1, 0.5) x grid maps of D channels; a NULL out[i] is skipped.
+ * Returns nonzero for an odd grid with out[3] requested. */
+int or_neck(const or_neck_weights* w, const float* x, int grid, int E, int mid, int D, int columns_f16, float* out[4],
+            int threads);
 
 #ifdef __cplusplus
 }

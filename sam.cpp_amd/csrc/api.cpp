@@ -878,6 +878,185 @@ int samhip_vit_prefix(samhip_context* ctx, const samhip_vit_prefix_desc* d, cons
     });
 }
 
+int samhip_vit_neck(samhip_context* ctx, const samhip_vit_neck_desc* d, const float* x, float* level0, float* level1,
+                    float* level2, float* level3) {
+    if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "vit_neck");
+    if (!d || !x) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_neck: null argument");
+    if (d->version != SAMHIP_ABI_VERSION) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_neck: descriptor version");
+    if (d->columns_type != T_F32 && d->columns_type != T_F16)
+        return fail(SAMHIP_ERR_UNSUPPORTED, "vit_neck: columns type must be F32 or F16");
+    float* level[4] = {level0, level1, level2, level3};
+    const int64_t g = d->grid, E = d->embed, mid = d->mid, D = d->dim;
+    if (g <= 0 || g > 4096 || E <= 0 || mid <= 0 || D <= 0 || E > 8192 || mid > 8192 || D > 8192 || E % 4 ||
+        mid % 4 || D % 4)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT,
+                    "vit_neck: grid (1..4096) and channel counts (multiples of 4, at most 8192) out of range");
+    if (level[3] && g % 2) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_neck: level 3 needs an even grid");
+    if (reinterpret_cast<uintptr_t>(x) % 16) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_neck: 16-byte alignment");
+    for (float* p : level)
+        if (reinterpret_cast<uintptr_t>(p) % 16) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_neck: 16-byte alignment");
+    const samhip_neck_scale* sc = d->scales;
+    auto convs = [](const samhip_neck_scale& s) { return s.conv1x1_w && s.conv1x1_b && s.conv3x3_w && s.conv3x3_b; };
+    if ((level[0] && !(convs(sc[0]) && sc[0].deconv1_w && sc[0].deconv1_b && sc[0].deconv2_w && sc[0].deconv2_b)) ||
+        (level[1] && !(convs(sc[1]) && sc[1].deconv1_w && sc[1].deconv1_b)) || (level[2] && !convs(sc[2])) ||
+        (level[3] && !convs(sc[3])))
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_neck: null weight pointer for a requested level");
+    if (!level[0] && !level[1] && !level[2] && !level[3]) return SAMHIP_OK;
+    if (int rc = set_device(ctx)) return rc;
+
+    // Operand rows: split columns are 3 parts of kp halves, F16 columns one.
+    const bool f16 = d->columns_type == T_F16;
+    const int64_t parts = f16 ? 1 : 3;
+    auto kpad = [](int64_t k) { return (k + 127) / 128 * 128; };
+    const int64_t T = g * g, T2 = 4 * T, T4 = 16 * T, kpE = kpad(E), kpM = kpad(mid), kpD = kpad(D),
+                  kp9 = kpad(9 * D);
+    constexpr int64_t kMaxOperand = 0x7fffffff;   // 32-bit buffer offsets of the GEMM
+    auto chunk_rows = [&](int64_t rows, int64_t lda) {
+        return std::min(rows, std::max<int64_t>(256, kMaxOperand / (lda * 2) / 256 * 256));
+    };
+    // (rows, row halves) of every convolution operand this call builds
+    std::vector<std::pair<int64_t, int64_t>> conv_ops;
+    const bool need_ax = level[0] || level[1] || (level[2] && !f16);
+    if (level[0]) {
+        conv_ops.push_back({T4, parts * kpD});
+        conv_ops.push_back({T4, parts * kp9});
+    }
+    if (level[1]) {
+        conv_ops.push_back({T2, parts * kpM});
+        conv_ops.push_back({T2, parts * kp9});
+    }
+    if (level[2]) {
+        if (f16) conv_ops.push_back({T, kpE});
+        conv_ops.push_back({T, parts * kp9});
+    }
+    if (level[3]) {
+        conv_ops.push_back({T / 4, parts * kpE});
+        conv_ops.push_back({T / 4, parts * kp9});
+    }
+    // whole-map products: the split ViT output and the second deconvolution's input
+    if ((need_ax && T * 3 * kpE * 2 > kMaxOperand) || (level[0] && T2 * 3 * kpM * 2 > kMaxOperand))
+        return fail(SAMHIP_ERR_UNSUPPORTED, "vit_neck: map too large for one transposed-convolution product");
+    int64_t at_halves = level[0] ? T2 * 3 * kpM : 0, max_rows = level[0] ? T2 : 0;
+    for (auto [rows, lda] : conv_ops) {
+        at_halves = std::max(at_halves, chunk_rows(rows, lda) * lda);
+        max_rows = std::max(max_rows, chunk_rows(rows, lda));
+    }
+    const int64_t wb_halves = std::max({4 * mid * 3 * kpE, 4 * D * 3 * kpM, D * parts * kp9, D * parts * kpE,
+                                        D * parts * kpM, D * parts * kpD});
+    const int64_t t1_floats = std::max({level[0] || level[1] ? T2 * mid : 0, T * D, T / 4 * D});
+    const int64_t t2_floats = level[0] ? T4 * D : T2 * D;
+    Carve c;
+    const size_t o_ax = c.take(need_ax ? size_t(T * 3 * kpE) * 2 : 0), o_rsx = c.take(size_t(T) * 4),
+                 o_at = c.take(size_t(at_halves) * 2), o_rst = c.take(size_t(max_rows) * 4),
+                 o_wb = c.take(size_t(wb_halves) * 2), o_cs = c.take(size_t(4 * std::max(mid, D)) * 4),
+                 o_t1 = c.take(size_t(t1_floats) * 4), o_t2 = c.take(size_t(t2_floats) * 4),
+                 o_t3 = c.take(level[0] ? size_t(T4 * D) * 4 : 0);
+    if (int rc = ensure_work(ctx, c.used)) return rc;
+    uint8_t* wk = static_cast<uint8_t*>(ctx->work);
+    _Float16* ax = reinterpret_cast<_Float16*>(wk + o_ax);
+    float* rsx = reinterpret_cast<float*>(wk + o_rsx);
+    _Float16* at = reinterpret_cast<_Float16*>(wk + o_at);
+    float* rst = reinterpret_cast<float*>(wk + o_rst);
+    _Float16* wb = reinterpret_cast<_Float16*>(wk + o_wb);
+    float* cs = reinterpret_cast<float*>(wk + o_cs);
+    float* t1 = reinterpret_cast<float*>(wk + o_t1);
+    float* t2 = reinterpret_cast<float*>(wk + o_t2);
+    float* t3 = reinterpret_cast<float*>(wk + o_t3);
+
+    auto columns = [&](int src, bool split, const float* in, int64_t W, int64_t H, int64_t C, int64_t kp,
+                       int64_t row0, int64_t rows, _Float16* a, float* rs) -> int {
+        return traced(ctx, "neck_columns", T_F32, rows, 0, kp, [&]() -> int {
+            launch_neck_columns(src, split, in, int(W), int(H), int(C), int(kp), row0, int(rows), a, rs, ctx->stream);
+            HIP_TRY(hipGetLastError(), "neck columns launch");
+            return SAMHIP_OK;
+        });
+    };
+    auto weights = [&](bool deconv, bool split, const float* w, int k, int64_t cin, int64_t cout, int64_t kp) -> int {
+        return traced(ctx, "neck_weights", T_F32, deconv ? 4 * cout : cout, 0, kp, [&]() -> int {
+            launch_neck_weights(deconv, split, w, k, int(cin), int(cout), int(kp), wb, cs, ctx->stream);
+            HIP_TRY(hipGetLastError(), "neck weights launch");
+            return SAMHIP_OK;
+        });
+    };
+    auto gemm = [&](const char* name, const _Float16* a, int64_t lda, const float* rs, float* y, int64_t ldy,
+                    int64_t M, int64_t N, const Epilogue& ep) -> int {
+        if (!gemm_f16_supported(int(M), int(N), int(lda), lda, lda))
+            return fail(SAMHIP_ERR_UNSUPPORTED, "vit_neck: product %lld x %lld x %lld out of range", (long long)M,
+                        (long long)N, (long long)lda);
+        return traced(ctx, name, T_F32, M, N, lda, [&]() -> int {
+            if (!launch_gemm_f16_epi(a, lda, rs, wb, lda, y, ldy, int(M), int(N), int(lda), ctx->cus, ep, ctx->stream))
+                return fail(SAMHIP_ERR_UNSUPPORTED, "vit_neck: no GEMM variant");
+            HIP_TRY(hipGetLastError(), "neck gemm launch");
+            return SAMHIP_OK;
+        });
+    };
+    // k x k convolution (stride 1, padding k/2) of a W x H map of C channels
+    // into D channels; NECK_POOL convolves the 2x2 max pool of the map.  With
+    // split columns a 1x1 convolution of the ViT output reuses its operand.
+    auto conv = [&](const char* name, int src, const float* in, int64_t W, int64_t H, int64_t C, const float* w,
+                    const float* b, int k, float* out) -> int {
+        const int64_t K = src == NECK_IM2COL3 ? 9 * C : C, kp = kpad(K), lda = parts * kp;
+        const int64_t rows = src == NECK_POOL ? (W / 2) * (H / 2) : W * H, step = chunk_rows(rows, lda);
+        if (int rc = weights(false, !f16, w, k, C, D, kp)) return rc;
+        Epilogue ep;
+        ep.bias = b;
+        ep.col_scale = cs;
+        if (!f16 && in == x && src == NECK_ROWS) return gemm(name, ax, lda, rsx, out, D, rows, D, ep);
+        for (int64_t r0 = 0; r0 < rows; r0 += step) {
+            const int64_t n = std::min(step, rows - r0);
+            if (int rc = columns(src, !f16, in, W, H, C, kp, r0, n, at, rst)) return rc;
+            if (int rc = gemm(name, at, lda, rst, out + r0 * D, D, n, D, ep)) return rc;
+        }
+        return SAMHIP_OK;
+    };
+    // 2x2 stride-2 transposed convolution of split rows of a W x W map
+    auto deconv = [&](const _Float16* a, const float* rs, int64_t W, int64_t cin, const float* w, const float* b,
+                      int64_t cout, bool gelu, float* out) -> int {
+        const int64_t kp = kpad(cin);
+        if (int rc = weights(true, true, w, 2, cin, cout, kp)) return rc;
+        Epilogue ep;
+        ep.bias = b;
+        ep.col_scale = cs;
+        ep.shuffle_w = int(W);
+        ep.shuffle_c = int(cout);
+        ep.gelu = gelu;
+        return gemm("neck_deconv", a, 3 * kp, rs, out, cout, W * W, 4 * cout, ep);
+    };
+
+    int rc = SAMHIP_OK;
+    if (need_ax && (rc = columns(NECK_ROWS, true, x, g, g, E, kpE, 0, T, ax, rsx))) return rc;
+    if (level[0]) {
+        const samhip_neck_scale& s = sc[0];
+        if ((rc = deconv(ax, rsx, g, E, s.deconv1_w, s.deconv1_b, mid, true, t1)) ||
+            (rc = columns(NECK_ROWS, true, t1, 2 * g, 2 * g, mid, kpM, 0, T2, at, rst)) ||
+            (rc = deconv(at, rst, 2 * g, mid, s.deconv2_w, s.deconv2_b, D, false, t2)) ||
+            (rc = conv("neck_conv1x1", NECK_ROWS, t2, 4 * g, 4 * g, D, s.conv1x1_w, s.conv1x1_b, 1, t3)) ||
+            (rc = conv("neck_conv3x3", NECK_IM2COL3, t3, 4 * g, 4 * g, D, s.conv3x3_w, s.conv3x3_b, 3, level[0])))
+            return rc;
+    }
+    if (level[1]) {
+        const samhip_neck_scale& s = sc[1];
+        if ((rc = deconv(ax, rsx, g, E, s.deconv1_w, s.deconv1_b, mid, false, t1)) ||
+            (rc = conv("neck_conv1x1", NECK_ROWS, t1, 2 * g, 2 * g, mid, s.conv1x1_w, s.conv1x1_b, 1, t2)) ||
+            (rc = conv("neck_conv3x3", NECK_IM2COL3, t2, 2 * g, 2 * g, D, s.conv3x3_w, s.conv3x3_b, 3, level[1])))
+            return rc;
+    }
+    if (level[2]) {
+        const samhip_neck_scale& s = sc[2];
+        if ((rc = conv("neck_conv1x1", NECK_ROWS, x, g, g, E, s.conv1x1_w, s.conv1x1_b, 1, t1)) ||
+            (rc = conv("neck_conv3x3", NECK_IM2COL3, t1, g, g, D, s.conv3x3_w, s.conv3x3_b, 3, level[2])))
+            return rc;
+    }
+    if (level[3]) {
+        const samhip_neck_scale& s = sc[3];
+        if ((rc = conv("neck_conv1x1", NECK_POOL, x, g, g, E, s.conv1x1_w, s.conv1x1_b, 1, t1)) ||
+            (rc = conv("neck_conv3x3", NECK_IM2COL3, t1, g / 2, g / 2, D, s.conv3x3_w, s.conv3x3_b, 3, level[3])))
+            return rc;
+    }
+    return SAMHIP_OK;
+}
+
 int samhip_trace_begin(samhip_context* ctx, const char* kernel_filter) {
     if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
     SAMHIP_NOT_WHILE_CAPTURING(ctx, "trace_begin");

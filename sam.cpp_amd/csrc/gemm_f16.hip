@@ -14,6 +14,7 @@
 // Both keep one barrier per BK stage.  The epilogue goes through LDS so that
 // each lane stores 16 contiguous bytes of Y.
 #include "internal.hpp"
+#include "q8stage.hpp"
 
 namespace samhip {
 
@@ -42,7 +43,8 @@ __device__ __forceinline__ void tile_order(int bid, int nblocks, int tiles_m, in
 // 16-byte row segments scaled by their row's 2^e.  (Staging the row scales
 // in LDS at kernel start measured up to 35 % slower on the long-K shapes.)
 // Epilogue flags (EPI template bits) for Epilogue fields.
-constexpr int EPI_BIAS = 1, EPI_RES = 4, EPI_REMAP = 8, EPI_PACK = 16;
+constexpr int EPI_BIAS = 1, EPI_RES = 4, EPI_REMAP = 8, EPI_PACK = 16, EPI_COLSCALE = 32, EPI_SHUFFLE = 64,
+              EPI_GELU = 128;
 
 template <int FM, int FN, int ES>
 __device__ __forceinline__ void store_tile(floatx16 (&acc)[FM][FN], const float* row_scale, float* slab, int lane,
@@ -94,10 +96,22 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
     const int c4 = lane % C4, r0 = lane / C4;
     const int n = col0 + 4 * c4;
     const bool full = n + 3 < N;
-    floatx4 bias{0.f, 0.f, 0.f, 0.f};
+    // transposed-convolution scatter: the lane's 4 columns share one tap
+    int ycol = n, sky = 0, skx = 0;
+    if (EPI & EPI_SHUFFLE) {
+        const int tap = n / ep.shuffle_c;
+        ycol = n - tap * ep.shuffle_c;
+        sky = tap >> 1;
+        skx = tap & 1;
+    }
+    floatx4 bias{0.f, 0.f, 0.f, 0.f}, cs{1.f, 1.f, 1.f, 1.f};
     if (EPI & EPI_BIAS)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) bias[q] = (full || n + q < N) ? ep.bias[n + q] : 0.f;
+        for (int q = 0; q < 4; ++q) bias[q] = (full || n + q < N) ? ep.bias[ycol + q] : 0.f;
+    if (EPI & EPI_COLSCALE)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) cs[q] = (full || n + q < N) ? ep.col_scale[n + q] : 0.f;
+    const float inv_sw = (EPI & EPI_SHUFFLE) ? 1.0f / float(ep.shuffle_w) : 0.f;
     // packed outputs: the wave's 64-aligned column block lies in one part and
     // one head (embed is a multiple of 64)
     const int part = (EPI & EPI_PACK) ? n / ep.embed : 0;
@@ -123,6 +137,15 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
                 dst[t] = (int64_t(w) * ep.heads * ep.np + tok) * 64;
                 if (part < 2 && ep.freqs)
                     fq[t] = *reinterpret_cast<const floatx4*>(ep.freqs + (int64_t(tok) * 32 + ((n & 63) >> 1)) * 2);
+            } else if (EPI & EPI_SHUFFLE) {
+                // input pixel (x, y) = (m % shuffle_w, m / shuffle_w) by a float
+                // reciprocal and one correction
+                const int sw = ep.shuffle_w;
+                int y = int(float(m) * inv_sw);
+                y += (y + 1) * sw <= m;
+                y -= y * sw > m;
+                const int x = m - y * sw;
+                dst[t] = live ? int64_t(2 * y + sky) * 2 * sw + 2 * x + skx : 0;
             } else {
                 dst[t] = (EPI & EPI_REMAP) ? (live ? int64_t(ep.row_map[m]) : 0) : int64_t(m);
             }
@@ -156,7 +179,9 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 float u = raw[q] * sc[t];
+                if (EPI & EPI_COLSCALE) u = u * cs[q];
                 if (EPI & EPI_BIAS) u = u + bias[q];
+                if (EPI & EPI_GELU) u = gelu_erf(u);
                 if (EPI & EPI_RES) u = res[t][q] + u;
                 v[q] = u;
             }
@@ -178,7 +203,7 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
                     half4_t{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
                 continue;
             }
-            float* yp = Y + dst[t] * ldy + n;
+            float* yp = Y + dst[t] * ldy + ycol;
             if (vec_ok && full) {
                 *reinterpret_cast<floatx4*>(yp) = v;
             } else {
@@ -743,7 +768,8 @@ template <int BM, int BN, int WM, int WN>
 bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
                 int64_t ldy, int M, int N, int K, bool spread, const Epilogue& ep, hipStream_t stream) {
     const int flags = (ep.bias ? EPI_BIAS : 0) | (ep.res ? EPI_RES : 0) | (ep.row_map ? EPI_REMAP : 0) |
-                      (ep.pack[0] ? EPI_PACK : 0);
+                      (ep.pack[0] ? EPI_PACK : 0) | (ep.col_scale ? EPI_COLSCALE : 0) |
+                      (ep.shuffle_c > 0 ? EPI_SHUFFLE : 0) | (ep.gelu ? EPI_GELU : 0);
     switch (flags) {
         case 0: launch_pipe<BM, BN, 64, 2, WM, WN, 0>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream, ep); break;
         case EPI_BIAS:
@@ -760,6 +786,18 @@ bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16*
         case EPI_BIAS | EPI_RES | EPI_REMAP:
             launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_RES | EPI_REMAP>(a, lda, rs, b, ldb, y, ldy, M, N, K,
                                                                               spread, stream, ep);
+            break;
+        case EPI_BIAS | EPI_COLSCALE:
+            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_COLSCALE>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread,
+                                                                       stream, ep);
+            break;
+        case EPI_BIAS | EPI_COLSCALE | EPI_SHUFFLE:
+            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_COLSCALE | EPI_SHUFFLE>(a, lda, rs, b, ldb, y, ldy, M, N,
+                                                                                     K, spread, stream, ep);
+            break;
+        case EPI_BIAS | EPI_COLSCALE | EPI_SHUFFLE | EPI_GELU:
+            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_COLSCALE | EPI_SHUFFLE | EPI_GELU>(
+                a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream, ep);
             break;
         default: return false;   // combinations the encoder does not use
     }

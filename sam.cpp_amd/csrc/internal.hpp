@@ -58,11 +58,20 @@ struct Epilogue {
     const float* freqs = nullptr;
     int embed = 0, per = 0, np = 0, heads = 0;
     float q_scale = 1.f;
+    // Per-column scale (multiplies with the row scale before the bias).
+    const float* col_scale = nullptr;
+    // 2x2 stride-2 transposed convolution: column n = tap*shuffle_c + c
+    // (tap = 2*ky + kx) of input pixel m = y*shuffle_w + x goes to row
+    // (2y+ky)*2*shuffle_w + 2x+kx, column c of Y (ldy = shuffle_c); the bias
+    // is indexed by c.
+    int shuffle_w = 0, shuffle_c = 0;
+    bool gelu = false;   // ggml_gelu_erf after the bias
 };
 // Same product as launch_gemm_f16 with the shape's picked configuration and
 // the epilogue; returns the configuration's name, or nullptr for an
 // epilogue combination without a kernel (bias; bias + res; bias + res +
-// row_map; bias + pack; or none are built).
+// row_map; bias + pack; bias + col_scale; bias + col_scale + shuffle (+ gelu);
+// or none are built).
 const char* launch_gemm_f16_epi(const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
                                 int64_t ldb, float* y, int64_t ldy, int M, int N, int K, int cus, const Epilogue& ep,
                                 hipStream_t stream);
@@ -91,6 +100,29 @@ void launch_attention(const _Float16* qh, const _Float16* kh, const _Float16* vt
 void launch_patch_columns(const float* image, int img, int patch, _Float16* a, float* row_scale, int kp,
                           hipStream_t stream);
 void launch_patch_kernel(const float* kernel, int E, int patch, _Float16* w, int kp, hipStream_t stream);
+
+// SimpleFPN neck operands (neck.hip).  A rows: output row r of a chunk
+// starting at row0 reads its K values from x (pixel rows of C floats, a W x
+// H map) as
+//   NECK_ROWS   : pixel row0 + r                                 (K = C)
+//   NECK_POOL   : max over the 2x2 block of output pixel row0 + r (K = C,
+//                 output map W/2 x H/2)
+//   NECK_IM2COL3: column tap*C + c = pixel (y+ky-1, x+kx-1) channel c,
+//                 zero outside the map, tap = 3*ky + kx          (K = 9 C)
+// and writes, for split, [hi | hi | lo] of v * 2^-e (e from the row's
+// largest magnitude, hi = fp16, lo = fp16 of the remainder, row_scale = 2^e;
+// rows of 3*kp halves), else fp16(v) (row_scale 1, rows of kp halves).
+// Columns K..kp-1 are zero.  C is a multiple of 4.
+constexpr int NECK_ROWS = 0, NECK_POOL = 1, NECK_IM2COL3 = 2;
+void launch_neck_columns(int src, bool split, const float* x, int W, int H, int C, int kp, int64_t row0, int rows,
+                         _Float16* a, float* row_scale, hipStream_t stream);
+// B rows from ggml convolution weights:
+//   conv   {k, k, Cin, Cout}: row co, column tap*Cin + ci (tap = k*ky + kx)
+//   deconv {2, 2, Cout, Cin}: row tap*Cout + co (tap = 2*ky + kx), column ci
+// split: [hi | lo | hi] of w * 2^-e per row (col_scale = 2^e), else
+// fp16(w) (col_scale 1).
+void launch_neck_weights(bool deconv, bool split, const float* w, int k, int cin, int cout, int kp, _Float16* b,
+                         float* col_scale, hipStream_t stream);
 
 // The producing graph node folded into a tall product's activation staging:
 // PRE_GELU stages gelu_erf(x) (ggml_gelu_erf), PRE_LAYER_NORM stages

@@ -61,6 +61,22 @@ class VitBlockDesc(ctypes.Structure):
                [(n, ctypes.c_void_p) for n in ("qkv_b", "proj_b", "fc1_b", "fc2_b", "freqs_cis")]
 
 
+NECK_SCALE_FIELDS = ("deconv1_w", "deconv1_b", "deconv2_w", "deconv2_b", "conv1x1_w", "conv1x1_b", "conv3x3_w",
+                     "conv3x3_b")
+
+
+class NeckScale(ctypes.Structure):
+    """samhip_neck_scale."""
+    _fields_ = [(n, ctypes.c_void_p) for n in NECK_SCALE_FIELDS]
+
+
+class VitNeckDesc(ctypes.Structure):
+    """samhip_vit_neck_desc."""
+    _fields_ = [("version", ctypes.c_int32), ("grid", ctypes.c_int32), ("embed", ctypes.c_int32),
+                ("mid", ctypes.c_int32), ("dim", ctypes.c_int32), ("columns_type", ctypes.c_int32),
+                ("scales", NeckScale * 4)]
+
+
 class VitPrefixDesc(ctypes.Structure):
     """samhip_vit_prefix_desc."""
     _fields_ = [("version", ctypes.c_int32), ("image_size", ctypes.c_int32), ("patch", ctypes.c_int32),
@@ -95,6 +111,7 @@ SIGNATURES = {
     "samhip_graph_destroy": ([_P], None),
     "samhip_vit_block": ([_P, ctypes.POINTER(VitBlockDesc), _P], _I),
     "samhip_vit_prefix": ([_P, ctypes.POINTER(VitPrefixDesc), _P, _P], _I),
+    "samhip_vit_neck": ([_P, ctypes.POINTER(VitNeckDesc), _P, _P, _P, _P, _P], _I),
     "samhip_layer_norm": ([_P, _P, _P, _I64, _I64, _P, _P, ctypes.c_float], _I),
     "samhip_flash_attn": ([_P, _P, _P, _P, _I64, _P, _I64, _I64, _I32, _I32, ctypes.c_float], _I),
 }
@@ -403,6 +420,41 @@ class VitPrefix:
 
     def forward(self, image_buf, x_buf):
         check(lib().samhip_vit_prefix(self.ctx.handle, ctypes.byref(self.desc), image_buf.ptr, x_buf.ptr))
+
+    def free(self):
+        for b in self.buffers.values():
+            b.free()
+        self.buffers = {}
+
+
+class VitNeck:
+    """The SimpleFPN neck weights on the device.  `scales` is a list of 4
+    dicts keyed by NECK_SCALE_FIELDS (ggml layouts, absent keys unused);
+    columns_type F32 (F32-accurate) or F16 (fp16 im2col operands)."""
+
+    def __init__(self, ctx, scales, grid, embed, mid, dim, columns_type=F32):
+        self.ctx = ctx
+        self.buffers = {}
+        d = VitNeckDesc()
+        d.version = ABI_VERSION
+        d.grid, d.embed, d.mid, d.dim, d.columns_type = grid, embed, mid, dim, columns_type
+        for i, sc in enumerate(scales):
+            for n in NECK_SCALE_FIELDS:
+                if sc.get(n) is not None:
+                    b = ctx.upload(np.ascontiguousarray(sc[n], np.float32))
+                    self.buffers[(i, n)] = b
+                    setattr(d.scales[i], n, b.ptr)
+        self.desc = d
+        self.grid, self.dim = grid, dim
+
+    def level_rows(self, level):
+        side = (4 * self.grid) >> level
+        return side * side
+
+    def forward(self, x_buf, levels):
+        """levels: 4 device buffers (or None) of level_rows(i) x dim floats."""
+        ptrs = [None if b is None else b.ptr for b in levels]
+        check(lib().samhip_vit_neck(self.ctx.handle, ctypes.byref(self.desc), x_buf.ptr, *ptrs))
 
     def free(self):
         for b in self.buffers.values():

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 from scipy.special import erf
 
-from tests.vit_fixtures import axial_rope_table, block_weights
+from tests.vit_fixtures import axial_rope_table, block_weights, neck_scales, neck_weights
 
 
 def np_layer_norm(x, w=None, b=None, eps=1e-5):
@@ -208,19 +208,14 @@ def test_deconv_conv_pool_against_float64(oracle):
     w3 = np.zeros((cout, cin, 3, 3), np.float32)
     w3[:, :, 1, 1] = w1.reshape(cout, cin)
     assert np.array_equal(oracle.conv2d(x, W, H, w3.ravel(), b, cout, 3), oracle.conv2d(x, W, H, w1, b, cout, 1))
+    # F16 columns: the same convolution of fp16-rounded operands
+    wc = rng.standard_normal(9 * cin * cout).astype(np.float32)
+    got = oracle.conv2d(x, W, H, wc, b, cout, 3, columns_f16=True)
+    ref = np_conv(x.astype(np.float16).astype(np.float32), W, H, wc.astype(np.float16).astype(np.float32), b, cout, 3)
+    assert np.abs(got - ref).max() < 1e-5
+    assert np.abs(got - oracle.conv2d(x, W, H, wc, b, cout, 3)).max() > 1e-4   # the rounding is visible
     p = oracle.maxpool2x2(x, W, H)
     assert np.array_equal(p, x.reshape(H // 2, 2, W // 2, 2, cin).max(axis=(1, 3)).reshape(-1, cin))
-
-
-def neck_weights(rng, E, mid, D):
-    def r(*shape, s=0.05):
-        return (rng.standard_normal(shape) * s).astype(np.float32).ravel()
-    return {"s0_dc1_w": r(E, mid, 2, 2), "s0_dc1_b": r(mid), "s0_dc2_w": r(mid, D, 2, 2), "s0_dc2_b": r(D),
-            "s0_c1_w": r(D, D), "s0_c1_b": r(D), "s0_c3_w": r(D, D, 3, 3), "s0_c3_b": r(D),
-            "s1_dc_w": r(E, mid, 2, 2), "s1_dc_b": r(mid), "s1_c1_w": r(D, mid), "s1_c1_b": r(D),
-            "s1_c3_w": r(D, D, 3, 3), "s1_c3_b": r(D), "s2_c1_w": r(D, E), "s2_c1_b": r(D),
-            "s2_c3_w": r(D, D, 3, 3), "s2_c3_b": r(D), "s3_c1_w": r(D, E), "s3_c1_b": r(D),
-            "s3_c3_w": r(D, D, 3, 3), "s3_c3_b": r(D)}
 
 
 def test_neck_composition(oracle):
@@ -245,3 +240,25 @@ def test_neck_composition(oracle):
                  w["s3_c3_b"], D, 3)
     for got, ref in zip(outs, (s0, s1, s2, s3)):
         assert np.abs(got - ref).max() < 1e-4 * max(1.0, np.abs(ref).max())
+
+
+def test_neck_scales_mapping():
+    w = neck_weights(np.random.default_rng(0), 8, 8, 4)
+    s = neck_scales(w)
+    assert s[0]["deconv2_w"] is w["s0_dc2_w"] and s[1]["deconv1_b"] is w["s1_dc_b"]
+    assert s[3]["conv3x3_w"] is w["s3_c3_w"] and "deconv1_w" not in s[2]
+    assert sum(len(x) for x in s) == len(w)
+
+
+def test_neck_skips_levels(oracle):
+    rng = np.random.default_rng(14)
+    grid, E, mid, D = 4, 16, 12, 8
+    w = neck_weights(rng, E, mid, D)
+    x = rng.standard_normal((grid * grid, E)).astype(np.float32)
+    full = oracle.neck(w, x, grid, E, mid, D)
+    part = oracle.neck(w, x, grid, E, mid, D, levels=(1, 2))
+    assert part[0] is None and part[3] is None
+    assert np.array_equal(part[1], full[1]) and np.array_equal(part[2], full[2])
+    with pytest.raises(ValueError):
+        oracle.neck(w, x[:9], 3, E, mid, D)   # level 3 of an odd grid
+    assert oracle.neck(w, x[:9], 3, E, mid, D, levels=(2,))[2].shape == (9, D)

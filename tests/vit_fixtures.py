@@ -45,3 +45,29 @@ def block_weights(oracle, E, mlp, heads, tokens_rope, rope_w, seed, types=None):
     w["norm2_b"] = (0.05 * rng.standard_normal(E)).astype(np.float32)
     w["freqs"] = axial_rope_table(rope_w, tokens_rope // rope_w, hd)
     return w
+
+
+def neck_weights(rng, E, mid, D, scale=0.05):
+    """SimpleFPN weights in ggml layouts (flat), keyed as the oracle's
+    or_neck_weights: deconvolutions {2, 2, Cout, Cin}, convolutions
+    {k, k, Cin, Cout} (numpy shapes are the reversed ggml dims)."""
+    def r(*shape):
+        return (rng.standard_normal(shape) * scale).astype(np.float32).ravel()
+    return {"s0_dc1_w": r(E, mid, 2, 2), "s0_dc1_b": r(mid), "s0_dc2_w": r(mid, D, 2, 2), "s0_dc2_b": r(D),
+            "s0_c1_w": r(D, D), "s0_c1_b": r(D), "s0_c3_w": r(D, D, 3, 3), "s0_c3_b": r(D),
+            "s1_dc_w": r(E, mid, 2, 2), "s1_dc_b": r(mid), "s1_c1_w": r(D, mid), "s1_c1_b": r(D),
+            "s1_c3_w": r(D, D, 3, 3), "s1_c3_b": r(D), "s2_c1_w": r(D, E), "s2_c1_b": r(D),
+            "s2_c3_w": r(D, D, 3, 3), "s2_c3_b": r(D), "s3_c1_w": r(D, E), "s3_c1_b": r(D),
+            "s3_c3_w": r(D, D, 3, 3), "s3_c3_b": r(D)}
+
+
+_NECK_SCALE_KEYS = {"dc1": "deconv1", "dc": "deconv1", "dc2": "deconv2", "c1": "conv1x1", "c3": "conv3x3"}
+
+
+def neck_scales(weights):
+    """The oracle-keyed neck weights as 4 per-scale dicts (samhip_neck_scale fields)."""
+    scales = [{}, {}, {}, {}]
+    for name, value in weights.items():
+        level, part, kind = name.split("_")
+        scales[int(level[1])][f"{_NECK_SCALE_KEYS[part]}_{kind}"] = value
+    return scales
