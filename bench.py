@@ -346,7 +346,16 @@ def text_stream(args, sh, ctx, fmt):
 
 
 ENC = {"E": 1024, "HEADS": 16, "MLP": 4736, "GRID": 72, "WINDOW": 24, "IMG": 1008, "PATCH": 14, "POS_GRID": 24,
-       "DEPTH": 32, "GLOBAL": (7, 15, 23, 31)}
+       "DEPTH": 32, "GLOBAL": (7, 15, 23, 31), "NECK_MID": 512, "NECK_DIM": 256}
+
+
+def neck_flops(grid, E, mid, D):
+    """Algorithmic flops of neck levels 0-2 (2 per multiply-add)."""
+    T = grid * grid
+    mac = (T * E * 4 * mid + 4 * T * mid * 4 * D + 16 * T * D * D + 16 * T * 9 * D * D   # level 0
+           + T * E * 4 * mid + 4 * T * mid * D + 4 * T * 9 * D * D                      # level 1
+           + T * E * D + T * 9 * D * D)                                                 # level 2
+    return 2.0 * mac
 
 
 def axial_rope_table(width, height, hd, theta=10000.0):
@@ -363,9 +372,11 @@ def axial_rope_table(width, height, hd, theta=10000.0):
 class Encoder:
     """A random-init SAM 3 vision encoder on the device (1008 px, 72x72
     tokens, width 1024, 32 pre-LN blocks, 16 heads, MLP 4736, window 24 with
-    global attention in blocks 7/15/23/31): qkv/proj/fc1 in the K-quant
-    `qt`, fc2 in Q8_0 (4736-wide rows), norms/biases/embeddings F32.  Linear
-    weights N(0, 0.02^2) packed on the device by samhip_quantize_rows."""
+    global attention in blocks 7/15/23/31) and its SimpleFPN neck (mid 512,
+    dim 256; levels 0-2 as the image path outputs them, F32 columns):
+    qkv/proj/fc1 in the K-quant `qt`, fc2 in Q8_0 (4736-wide rows),
+    norms/biases/embeddings/neck F32.  Linear weights N(0, 0.02^2) packed on
+    the device by samhip_quantize_rows."""
 
     def __init__(self, sh, ctx, qt, seed=0):
         import ctypes
@@ -410,6 +421,24 @@ class Encoder:
                                    e["PATCH"], E, e["POS_GRID"])
         self.image = ctx.upload(np.random.default_rng(seed + 1).standard_normal((3, e["IMG"], e["IMG"]), dtype=np.float32))
         self.x = ctx.alloc(G * G * E * 4)
+        mid, D = e["NECK_MID"], e["NECK_DIM"]
+        nr = np.random.default_rng(seed + 2)
+
+        def nw(*shape):
+            return (nr.standard_normal(shape, dtype=np.float32) * 0.02).ravel()
+        # oracle-keyed (or_neck_weights) host copies, ggml layouts
+        self.neck_host = {"s0_dc1_w": nw(E, mid, 2, 2), "s0_dc1_b": nw(mid), "s0_dc2_w": nw(mid, D, 2, 2),
+                          "s0_dc2_b": nw(D), "s0_c1_w": nw(D, D), "s0_c1_b": nw(D), "s0_c3_w": nw(D, D, 3, 3),
+                          "s0_c3_b": nw(D), "s1_dc_w": nw(E, mid, 2, 2), "s1_dc_b": nw(mid), "s1_c1_w": nw(D, mid),
+                          "s1_c1_b": nw(D), "s1_c3_w": nw(D, D, 3, 3), "s1_c3_b": nw(D), "s2_c1_w": nw(D, E),
+                          "s2_c1_b": nw(D), "s2_c3_w": nw(D, D, 3, 3), "s2_c3_b": nw(D)}
+        keys = {"dc1": "deconv1", "dc": "deconv1", "dc2": "deconv2", "c1": "conv1x1", "c3": "conv3x3"}
+        scales = [{}, {}, {}, {}]
+        for name, v in self.neck_host.items():
+            lv, part, kind = name.split("_")
+            scales[int(lv[1])][f"{keys[part]}_{kind}"] = v
+        self.neck = sh.VitNeck(ctx, scales, G, E, mid, D, sh.F32)
+        self.levels = [ctx.alloc(self.neck.level_rows(i) * D * 4) for i in range(3)] + [None]
         self.flops = self._flops()
 
     def _flops(self):
@@ -419,12 +448,15 @@ class Encoder:
         att_w = 4.0 * T * (e["WINDOW"] ** 2) * E          # QK^T and PV over each token's window
         att_g = 4.0 * T * T * E
         kp = -(-3 * e["PATCH"] ** 2 // 128) * 128
-        return 2.0 * T * E * 3 * kp + sum(lin + (att_g if i in e["GLOBAL"] else att_w) for i in range(e["DEPTH"]))
+        return (2.0 * T * E * 3 * kp + sum(lin + (att_g if i in e["GLOBAL"] else att_w) for i in range(e["DEPTH"]))
+                + neck_flops(e["GRID"], E, e["NECK_MID"], e["NECK_DIM"]))
 
-    def forward(self):
+    def forward(self, neck=True):
         self.prefix.forward(self.image, self.x)
         for d in self.blocks:
             self.sh.check(self.sh.lib().samhip_vit_block(self.ctx.handle, self.ctypes.byref(d), self.x.ptr))
+        if neck:
+            self.neck.forward(self.x, self.levels)
 
     def host_block(self, i):
         """Block i's weights as numpy arrays (device bytes downloaded) for the oracle."""
@@ -480,16 +512,26 @@ def encoder_cpu_baseline(enc, seconds_cap=60.0):
                  rng.standard_normal((e["POS_GRID"], e["POS_GRID"], E)).astype(np.float32) * 0.1, e["POS_GRID"],
                  np.ones(E, np.float32), np.zeros(E, np.float32), E, threads)
     times["prefix"] = time.perf_counter() - t0
+    # the neck on a 24 x 24 crop of the 72 x 72 map (every level's cost is
+    # proportional to its pixels), scaled by 9
+    crop = x.reshape(G, G, E)[:24, :24].reshape(-1, E)
+    t0 = time.perf_counter()
+    O.neck(enc.neck_host, crop, 24, E, e["NECK_MID"], e["NECK_DIM"], threads, levels=(0, 1, 2))
+    times["neck"] = (time.perf_counter() - t0) * (G / 24) ** 2
     n_glob = len(e["GLOBAL"])
-    per_image = times["prefix"] + (e["DEPTH"] - n_glob) * times["windowed"] + n_glob * times.get("global", times["windowed"])
+    per_image = (times["prefix"] + (e["DEPTH"] - n_glob) * times["windowed"]
+                 + n_glob * times.get("global", times["windowed"]) + times["neck"])
     return {"value": round(per_image * 1e3, 1), "unit": "ms/image", "cores": threads, "kind": "port",
             "sample": f"prefix {times['prefix']:.2f} s + one windowed block {times['windowed']:.2f} s + one global "
                       f"block {times.get('global', float('nan')):.2f} s, extrapolated to 28 windowed + 4 global "
-                      f"blocks; oracle/vit_oracle.c (native Q8 linears, exact-softmax attention), OpenMP"}
+                      f"blocks, + neck levels 0-2 on a 24x24 crop x 9 ({times['neck']:.2f} s); "
+                      f"oracle/vit_oracle.c (native Q8 linears, exact-softmax attention, F32 convolutions), OpenMP"}
 
 
 def encoder_measure(sh, ctx, enc, warmup, iters):
-    """ms/image of the forward (prefix + 32 blocks) and its kernel breakdown."""
+    """ms/image of the image encode (prefix + 32 blocks + neck levels 0-2,
+    as the reference's image path runs it), its kernel breakdown, and
+    ms/image of the ViT alone (prefix + 32 blocks)."""
     for _ in range(warmup):
         enc.forward()
     ctx.synchronize()
@@ -501,6 +543,11 @@ def encoder_measure(sh, ctx, enc, warmup, iters):
         enc.forward()
     ctx.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / iters
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        enc.forward(neck=False)
+    ctx.synchronize()
+    enc.vit_ms = (time.perf_counter() - t0) * 1e3 / iters
     by = {}
     for name, wt, m, n, k, kms in prof:
         by.setdefault(name, []).append((m, n, k, kms))
@@ -525,8 +572,10 @@ def encoder_workload(args, sh, ctx):
         "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
         "config": {"workload": f"SAM 3 vision encoder forward, 1008x1008x3 image, 72x72 tokens, width 1024, 32 blocks "
                                f"(window 24, global 7/15/23/31), 16 heads, MLP 4736; {sh.TYPE_NAMES[qt]} qkv/proj/fc1, "
-                               f"q8_0 fc2; random-init weights", "batch": 1, "parallelism": "single-gpu"},
+                               f"q8_0 fc2; SimpleFPN neck levels 0-2 (F32 columns); random-init weights", "batch": 1,
+                   "parallelism": "single-gpu"},
         "tflops_effective": round(enc.flops / (ms * 1e-3) / 1e12, 2),
+        "vit_ms_per_image": round(enc.vit_ms, 3),
         "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(ach / PEAK_FP16_TFLOPS, 4), "traffic": None, "kernel": "vit_fc1 (fp16 GEMM + bias + GELU)",
                      "shape": {"M": m_, "N": n_, "K": k_}, "launch_ms": round(fc1_ms, 5)},
@@ -712,10 +761,11 @@ def main():
         enc_ms, _, breakdown = encoder_measure(sh, ctx, enc, 3, 10)
         result["vision_encoder"] = {
             "ms_per_image": round(enc_ms, 3), "images_per_s": round(1e3 / enc_ms, 2),
+            "vit_ms_per_image": round(enc.vit_ms, 3),
             "tflops_effective": round(enc.flops / (enc_ms * 1e-3) / 1e12, 2),
             "config": "1008x1008x3 image, 72x72 tokens, width 1024, 32 blocks (window 24, global 7/15/23/31), "
-                      "16 heads, MLP 4736; Q4_K qkv/proj/fc1, Q8_0 fc2; random-init weights; batch 1; 3 warmup + "
-                      "10 timed forwards",
+                      "16 heads, MLP 4736; Q4_K qkv/proj/fc1, Q8_0 fc2; SimpleFPN neck levels 0-2 (F32 columns); "
+                      "random-init weights; batch 1; 3 warmup + 10 timed forwards",
             "kernel_ms_per_image": breakdown}
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")

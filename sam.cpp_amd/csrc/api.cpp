@@ -905,53 +905,67 @@ int samhip_vit_neck(samhip_context* ctx, const samhip_vit_neck_desc* d, const fl
     if (!level[0] && !level[1] && !level[2] && !level[3]) return SAMHIP_OK;
     if (int rc = set_device(ctx)) return rc;
 
-    // Operand rows: split columns are 3 parts of kp halves, F16 columns one.
+    // Operands.  Split (F32 columns) A rows are stored [hi | lo] and read as
+    // [hi | hi | lo] (A_REPEAT) against B rows [hi | lo | hi]; F16 columns
+    // are one fp16 part.  A 3x3 convolution over a map of 128k channels
+    // gathers its im2col rows from the map's own operand rows (A_CONV3, one
+    // power-of-two scale for the whole map); other channel counts build the
+    // im2col rows.
     const bool f16 = d->columns_type == T_F16;
-    const int64_t parts = f16 ? 1 : 3;
+    const int64_t parts = f16 ? 1 : 3, stored = f16 ? 1 : 2;
     auto kpad = [](int64_t k) { return (k + 127) / 128 * 128; };
     const int64_t T = g * g, T2 = 4 * T, T4 = 16 * T, kpE = kpad(E), kpM = kpad(mid), kpD = kpad(D),
                   kp9 = kpad(9 * D);
+    const bool gather3 = D % 128 == 0;
     constexpr int64_t kMaxOperand = 0x7fffffff;   // 32-bit buffer offsets of the GEMM
     auto chunk_rows = [&](int64_t rows, int64_t lda) {
         return std::min(rows, std::max<int64_t>(256, kMaxOperand / (lda * 2) / 256 * 256));
     };
-    // (rows, row halves) of every convolution operand this call builds
+    // (rows, stored row halves) of every A operand built into `at`: 1x1 and
+    // pooled inputs in chunks, 3x3 inputs whole (gathered) or in chunks
     std::vector<std::pair<int64_t, int64_t>> conv_ops;
     const bool need_ax = level[0] || level[1] || (level[2] && !f16);
+    auto add3 = [&](int64_t rows) {
+        conv_ops.push_back(gather3 ? std::make_pair(rows, stored * D)
+                                   : std::make_pair(chunk_rows(rows, stored * kp9), stored * kp9));
+    };
     if (level[0]) {
-        conv_ops.push_back({T4, parts * kpD});
-        conv_ops.push_back({T4, parts * kp9});
+        conv_ops.push_back({chunk_rows(T4, stored * kpD), stored * kpD});
+        add3(T4);
     }
     if (level[1]) {
-        conv_ops.push_back({T2, parts * kpM});
-        conv_ops.push_back({T2, parts * kp9});
+        conv_ops.push_back({chunk_rows(T2, stored * kpM), stored * kpM});
+        add3(T2);
     }
     if (level[2]) {
         if (f16) conv_ops.push_back({T, kpE});
-        conv_ops.push_back({T, parts * kp9});
+        add3(T);
     }
     if (level[3]) {
-        conv_ops.push_back({T / 4, parts * kpE});
-        conv_ops.push_back({T / 4, parts * kp9});
+        conv_ops.push_back({chunk_rows(T / 4, stored * kpE), stored * kpE});
+        add3(T / 4);
     }
-    // whole-map products: the split ViT output and the second deconvolution's input
-    if ((need_ax && T * 3 * kpE * 2 > kMaxOperand) || (level[0] && T2 * 3 * kpM * 2 > kMaxOperand))
-        return fail(SAMHIP_ERR_UNSUPPORTED, "vit_neck: map too large for one transposed-convolution product");
-    int64_t at_halves = level[0] ? T2 * 3 * kpM : 0, max_rows = level[0] ? T2 : 0;
+    // whole-map operands: the split ViT output, the second deconvolution's
+    // input and the gathered 3x3 inputs
+    if ((need_ax && T * 2 * kpE * 2 > kMaxOperand) || (level[0] && T2 * 2 * kpM * 2 > kMaxOperand) ||
+        (gather3 && (level[0] ? T4 : T2) * stored * D * 2 > kMaxOperand))
+        return fail(SAMHIP_ERR_UNSUPPORTED, "vit_neck: map too large for one product");
+    int64_t at_halves = level[0] ? T2 * 2 * kpM : 0, max_rows = level[0] ? T2 : 0;
     for (auto [rows, lda] : conv_ops) {
-        at_halves = std::max(at_halves, chunk_rows(rows, lda) * lda);
-        max_rows = std::max(max_rows, chunk_rows(rows, lda));
+        at_halves = std::max(at_halves, rows * lda);
+        max_rows = std::max(max_rows, rows);
     }
     const int64_t wb_halves = std::max({4 * mid * 3 * kpE, 4 * D * 3 * kpM, D * parts * kp9, D * parts * kpE,
                                         D * parts * kpM, D * parts * kpD});
     const int64_t t1_floats = std::max({level[0] || level[1] ? T2 * mid : 0, T * D, T / 4 * D});
     const int64_t t2_floats = level[0] ? T4 * D : T2 * D;
+    const int64_t part_floats = std::max<int64_t>(1024, (std::max(E, mid) + 63) / 64 * 4 * std::max(mid, D));
     Carve c;
-    const size_t o_ax = c.take(need_ax ? size_t(T * 3 * kpE) * 2 : 0), o_rsx = c.take(size_t(T) * 4),
+    const size_t o_ax = c.take(need_ax ? size_t(T * 2 * kpE) * 2 : 0), o_rsx = c.take(size_t(T) * 4),
                  o_at = c.take(size_t(at_halves) * 2), o_rst = c.take(size_t(max_rows) * 4),
                  o_wb = c.take(size_t(wb_halves) * 2), o_cs = c.take(size_t(4 * std::max(mid, D)) * 4),
-                 o_t1 = c.take(size_t(t1_floats) * 4), o_t2 = c.take(size_t(t2_floats) * 4),
-                 o_t3 = c.take(level[0] ? size_t(T4 * D) * 4 : 0);
+                 o_part = c.take(size_t(part_floats) * 4), o_t1 = c.take(size_t(t1_floats) * 4),
+                 o_t2 = c.take(size_t(t2_floats) * 4), o_t3 = c.take(level[0] ? size_t(T4 * D) * 4 : 0);
     if (int rc = ensure_work(ctx, c.used)) return rc;
     uint8_t* wk = static_cast<uint8_t*>(ctx->work);
     _Float16* ax = reinterpret_cast<_Float16*>(wk + o_ax);
@@ -960,6 +974,7 @@ int samhip_vit_neck(samhip_context* ctx, const samhip_vit_neck_desc* d, const fl
     float* rst = reinterpret_cast<float*>(wk + o_rst);
     _Float16* wb = reinterpret_cast<_Float16*>(wk + o_wb);
     float* cs = reinterpret_cast<float*>(wk + o_cs);
+    float* part = reinterpret_cast<float*>(wk + o_part);
     float* t1 = reinterpret_cast<float*>(wk + o_t1);
     float* t2 = reinterpret_cast<float*>(wk + o_t2);
     float* t3 = reinterpret_cast<float*>(wk + o_t3);
@@ -974,39 +989,65 @@ int samhip_vit_neck(samhip_context* ctx, const samhip_vit_neck_desc* d, const fl
     };
     auto weights = [&](bool deconv, bool split, const float* w, int k, int64_t cin, int64_t cout, int64_t kp) -> int {
         return traced(ctx, "neck_weights", T_F32, deconv ? 4 * cout : cout, 0, kp, [&]() -> int {
-            launch_neck_weights(deconv, split, w, k, int(cin), int(cout), int(kp), wb, cs, ctx->stream);
+            launch_neck_weights(deconv, split, w, k, int(cin), int(cout), int(kp), wb, cs, part, ctx->stream);
             HIP_TRY(hipGetLastError(), "neck weights launch");
             return SAMHIP_OK;
         });
     };
-    auto gemm = [&](const char* name, const _Float16* a, int64_t lda, const float* rs, float* y, int64_t ldy,
-                    int64_t M, int64_t N, const Epilogue& ep) -> int {
-        if (!gemm_f16_supported(int(M), int(N), int(lda), lda, lda))
+    // product of A (M rows of lda stored halves, read as K columns) with the
+    // prepared B rows (K halves each)
+    auto gemm = [&](const char* name, const _Float16* a, int64_t lda, int64_t K, const float* rs, float* y,
+                    int64_t ldy, int64_t M, int64_t N, const Epilogue& ep, const AOperand& op) -> int {
+        if (!gemm_f16_supported(int(M), int(N), int(K), lda, K))
             return fail(SAMHIP_ERR_UNSUPPORTED, "vit_neck: product %lld x %lld x %lld out of range", (long long)M,
-                        (long long)N, (long long)lda);
-        return traced(ctx, name, T_F32, M, N, lda, [&]() -> int {
-            if (!launch_gemm_f16_epi(a, lda, rs, wb, lda, y, ldy, int(M), int(N), int(lda), ctx->cus, ep, ctx->stream))
+                        (long long)N, (long long)K);
+        return traced(ctx, name, T_F32, M, N, K, [&]() -> int {
+            if (!launch_gemm_f16_epi(a, lda, rs, wb, K, y, ldy, int(M), int(N), int(K), ctx->cus, ep, ctx->stream, op))
                 return fail(SAMHIP_ERR_UNSUPPORTED, "vit_neck: no GEMM variant");
             HIP_TRY(hipGetLastError(), "neck gemm launch");
             return SAMHIP_OK;
         });
+    };
+    auto repeat = [&](int64_t kp) {
+        AOperand op;
+        if (!f16) {
+            op.mode = A_REPEAT;
+            op.part = int(kp);
+        }
+        return op;
     };
     // k x k convolution (stride 1, padding k/2) of a W x H map of C channels
     // into D channels; NECK_POOL convolves the 2x2 max pool of the map.  With
     // split columns a 1x1 convolution of the ViT output reuses its operand.
     auto conv = [&](const char* name, int src, const float* in, int64_t W, int64_t H, int64_t C, const float* w,
                     const float* b, int k, float* out) -> int {
-        const int64_t K = src == NECK_IM2COL3 ? 9 * C : C, kp = kpad(K), lda = parts * kp;
-        const int64_t rows = src == NECK_POOL ? (W / 2) * (H / 2) : W * H, step = chunk_rows(rows, lda);
-        if (int rc = weights(false, !f16, w, k, C, D, kp)) return rc;
         Epilogue ep;
         ep.bias = b;
         ep.col_scale = cs;
-        if (!f16 && in == x && src == NECK_ROWS) return gemm(name, ax, lda, rsx, out, D, rows, D, ep);
+        if (src == NECK_IM2COL3 && gather3) {
+            const int64_t K = parts * 9 * C, rows = W * H;
+            if (int rc = weights(false, !f16, w, k, C, D, 9 * C)) return rc;
+            int rc = traced(ctx, "neck_columns", T_F32, rows, 0, C, [&]() -> int {
+                launch_neck_pixels(!f16, in, rows, int(C), at, rst, part, ctx->stream);
+                HIP_TRY(hipGetLastError(), "neck pixels launch");
+                return SAMHIP_OK;
+            });
+            if (rc) return rc;
+            AOperand op;
+            op.mode = A_CONV3;
+            op.part = int(C);
+            op.width = int(W);
+            op.height = int(H);
+            return gemm(name, at, stored * C, K, rst, out, D, rows, D, ep, op);
+        }
+        const int64_t kp = kpad(src == NECK_IM2COL3 ? 9 * C : C), lda = stored * kp;
+        const int64_t rows = src == NECK_POOL ? (W / 2) * (H / 2) : W * H, step = chunk_rows(rows, lda);
+        if (int rc = weights(false, !f16, w, k, C, D, kp)) return rc;
+        if (!f16 && in == x && src == NECK_ROWS) return gemm(name, ax, lda, parts * kp, rsx, out, D, rows, D, ep, repeat(kp));
         for (int64_t r0 = 0; r0 < rows; r0 += step) {
             const int64_t n = std::min(step, rows - r0);
             if (int rc = columns(src, !f16, in, W, H, C, kp, r0, n, at, rst)) return rc;
-            if (int rc = gemm(name, at, lda, rst, out + r0 * D, D, n, D, ep)) return rc;
+            if (int rc = gemm(name, at, lda, parts * kp, rst, out + r0 * D, D, n, D, ep, repeat(kp))) return rc;
         }
         return SAMHIP_OK;
     };
@@ -1021,7 +1062,10 @@ int samhip_vit_neck(samhip_context* ctx, const samhip_vit_neck_desc* d, const fl
         ep.shuffle_w = int(W);
         ep.shuffle_c = int(cout);
         ep.gelu = gelu;
-        return gemm("neck_deconv", a, 3 * kp, rs, out, cout, W * W, 4 * cout, ep);
+        AOperand op;
+        op.mode = A_REPEAT;
+        op.part = int(kp);
+        return gemm("neck_deconv", a, 2 * kp, 3 * kp, rs, out, cout, W * W, 4 * cout, ep, op);
     };
 
     int rc = SAMHIP_OK;

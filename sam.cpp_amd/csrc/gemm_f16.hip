@@ -492,12 +492,12 @@ __global__ __launch_bounds__(256) void gemm_f16_dma_kernel(const _Float16* __res
 // independent 32x32 accumulators per wave (8 waves: two per SIMD).
 // ---------------------------------------------------------------------------
 
-template <int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI = 0>
+template <int BM, int BN, int BK, int STAGES, int WM, int WN, int EPI = 0, int AM = A_PLAIN>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_pipe_kernel(const _Float16* __restrict__ A, int64_t lda,
                                                             const float* __restrict__ row_scale,
                                                             const _Float16* __restrict__ B, int64_t ldb,
                                                             float* Y, int64_t ldy, int M, int N, int K,
-                                                            int tiles_m, int tiles_n, Epilogue ep) {
+                                                            int tiles_m, int tiles_n, Epilogue ep, AOperand op) {
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int NW = WM * WN;
     constexpr int CPR = BK / 8, RB = BK * 2;
@@ -530,11 +530,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_pipe_kernel(const _Floa
     const __amdgpu_buffer_rsrc_t rb_desc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(B), 0, b_bytes, RSRC_WORD3);
 
     uint32_t a_off[A_PER_WAVE], b_off[B_PER_WAVE];
+    int a_taps[A_PER_WAVE];   // A_CONV3: bit 3*ky+kx set when that neighbour lies in the map
 #pragma unroll
     for (int i = 0; i < A_PER_WAVE; ++i) {
         const int blk = wave * A_PER_WAVE + i, r = blk * RPB + lane / CPR, slot = lane % CPR;
         const int kc = slot ^ swz<CPR>(r);
         a_off[i] = m0 + r < M ? uint32_t((int64_t(m0 + r) * lda + 8 * kc) * 2) : a_bytes;
+        if (AM == A_CONV3) {
+            const int m = m0 + r, y = m / op.width, x = m - y * op.width;
+            int taps = 0;
+#pragma unroll
+            for (int t = 0; t < 9; ++t) {
+                const int yy = y + t / 3 - 1, xx = x + t % 3 - 1;
+                taps |= (m < M && yy >= 0 && yy < op.height && xx >= 0 && xx < op.width) ? 1 << t : 0;
+            }
+            a_taps[i] = taps;
+        }
     }
 #pragma unroll
     for (int i = 0; i < B_PER_WAVE; ++i) {
@@ -545,11 +556,26 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_pipe_kernel(const _Floa
     auto issue = [&](int s) {
         uint8_t* st = lds + (s % STAGES) * STAGE_BYTES;
         const int koff = s * RB;
+        if (AM == A_CONV3) {
+            // the stage's BK columns lie in one (part, tap) block of `part`
+            // channels: one signed byte step from each lane's own pixel
+            const int k = s * BK, span = 9 * op.part;
+            const int p = k / span, rem = k - p * span, tap = rem / op.part, c0 = rem - tap * op.part;
+            const int step = (((tap / 3 - 1) * op.width + tap % 3 - 1) * int(lda) + (p == 2 ? op.part : 0) + c0) * 2;
 #pragma unroll
-        for (int i = 0; i < A_PER_WAVE; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ra_desc, (__attribute__((address_space(3))) void*)(st + (wave * A_PER_WAVE + i) * 1024), 16,
-                a_off[i], koff, 0, 0);
+            for (int i = 0; i < A_PER_WAVE; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    ra_desc, (__attribute__((address_space(3))) void*)(st + (wave * A_PER_WAVE + i) * 1024), 16,
+                    (a_taps[i] >> tap) & 1 ? uint32_t(int(a_off[i]) + step) : a_bytes, 0, 0, 0);
+        } else {
+            // A_REPEAT: logical columns [part, 2 part) re-read the hi half
+            const int akoff = (AM == A_REPEAT && s * BK >= op.part) ? koff - op.part * 2 : koff;
+#pragma unroll
+            for (int i = 0; i < A_PER_WAVE; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    ra_desc, (__attribute__((address_space(3))) void*)(st + (wave * A_PER_WAVE + i) * 1024), 16,
+                    a_off[i], akoff, 0, 0);
+        }
 #pragma unroll
         for (int i = 0; i < B_PER_WAVE; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -663,13 +689,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_pipe_kernel(const _Floa
 // idle (the dispatcher fills a CU before moving on).
 constexpr size_t spread_pad(size_t static_lds) { return static_lds > 82944 ? 0 : 82944 - static_lds; }
 
-template <int BM, int BN, int BK, int STAGES, int WM = 2, int WN = 2, int EPI = 0>
+template <int BM, int BN, int BK, int STAGES, int WM = 2, int WN = 2, int EPI = 0, int AM = A_PLAIN>
 void launch_pipe(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
-                 int64_t ldy, int M, int N, int K, bool spread, hipStream_t stream, const Epilogue& ep = Epilogue{}) {
+                 int64_t ldy, int M, int N, int K, bool spread, hipStream_t stream, const Epilogue& ep = Epilogue{},
+                 const AOperand& op = AOperand{}) {
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const size_t pad = spread ? spread_pad(size_t(STAGES) * (BM + BN) * BK * 2) : 0;
-    hipLaunchKernelGGL((gemm_f16_pipe_kernel<BM, BN, BK, STAGES, WM, WN, EPI>), dim3(unsigned(tiles_m * tiles_n)),
-                       dim3(64 * WM * WN), pad, stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n, ep);
+    hipLaunchKernelGGL((gemm_f16_pipe_kernel<BM, BN, BK, STAGES, WM, WN, EPI, AM>), dim3(unsigned(tiles_m * tiles_n)),
+                       dim3(64 * WM * WN), pad, stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n, ep, op);
 }
 
 template <int BM, int BN, int BK, int STAGES>
@@ -766,52 +793,54 @@ int gemm_f16_pick(int /*M*/, int N, int /*K*/) {
 // 4x2 waves) with each epilogue the vision encoder uses.
 template <int BM, int BN, int WM, int WN>
 bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
-                int64_t ldy, int M, int N, int K, bool spread, const Epilogue& ep, hipStream_t stream) {
+                int64_t ldy, int M, int N, int K, bool spread, const Epilogue& ep, const AOperand& op,
+                hipStream_t stream) {
     const int flags = (ep.bias ? EPI_BIAS : 0) | (ep.res ? EPI_RES : 0) | (ep.row_map ? EPI_REMAP : 0) |
                       (ep.pack[0] ? EPI_PACK : 0) | (ep.col_scale ? EPI_COLSCALE : 0) |
                       (ep.shuffle_c > 0 ? EPI_SHUFFLE : 0) | (ep.gelu ? EPI_GELU : 0);
-    switch (flags) {
-        case 0: launch_pipe<BM, BN, 64, 2, WM, WN, 0>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream, ep); break;
-        case EPI_BIAS:
-            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream, ep);
-            break;
-        case EPI_BIAS | EPI_RES:
-            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_RES>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream,
-                                                                  ep);
-            break;
-        case EPI_BIAS | EPI_PACK:
-            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_PACK>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream,
-                                                                   ep);
-            break;
-        case EPI_BIAS | EPI_RES | EPI_REMAP:
-            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_RES | EPI_REMAP>(a, lda, rs, b, ldb, y, ldy, M, N, K,
-                                                                              spread, stream, ep);
-            break;
-        case EPI_BIAS | EPI_COLSCALE:
-            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_COLSCALE>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread,
-                                                                       stream, ep);
-            break;
-        case EPI_BIAS | EPI_COLSCALE | EPI_SHUFFLE:
-            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_COLSCALE | EPI_SHUFFLE>(a, lda, rs, b, ldb, y, ldy, M, N,
-                                                                                     K, spread, stream, ep);
-            break;
-        case EPI_BIAS | EPI_COLSCALE | EPI_SHUFFLE | EPI_GELU:
-            launch_pipe<BM, BN, 64, 2, WM, WN, EPI_BIAS | EPI_COLSCALE | EPI_SHUFFLE | EPI_GELU>(
-                a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream, ep);
-            break;
-        default: return false;   // combinations the encoder does not use
-    }
+#define SAMHIP_EPI(E, AMODE)                                                                                     \
+    launch_pipe<BM, BN, 64, 2, WM, WN, E, AMODE>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream, ep, op); \
     return true;
+    constexpr int BC = EPI_BIAS | EPI_COLSCALE;
+    if (op.mode == A_PLAIN) {
+        switch (flags) {
+            case 0: SAMHIP_EPI(0, A_PLAIN)
+            case EPI_BIAS: SAMHIP_EPI(EPI_BIAS, A_PLAIN)
+            case EPI_BIAS | EPI_RES: SAMHIP_EPI(EPI_BIAS | EPI_RES, A_PLAIN)
+            case EPI_BIAS | EPI_PACK: SAMHIP_EPI(EPI_BIAS | EPI_PACK, A_PLAIN)
+            case EPI_BIAS | EPI_RES | EPI_REMAP: SAMHIP_EPI(EPI_BIAS | EPI_RES | EPI_REMAP, A_PLAIN)
+            case BC: SAMHIP_EPI(BC, A_PLAIN)
+            default: return false;
+        }
+    }
+    if (op.mode == A_REPEAT) {
+        switch (flags) {
+            case BC: SAMHIP_EPI(BC, A_REPEAT)
+            case BC | EPI_SHUFFLE: SAMHIP_EPI(BC | EPI_SHUFFLE, A_REPEAT)
+            case BC | EPI_SHUFFLE | EPI_GELU: SAMHIP_EPI(BC | EPI_SHUFFLE | EPI_GELU, A_REPEAT)
+            default: return false;
+        }
+    }
+    if (op.mode == A_CONV3 && flags == BC) {
+        SAMHIP_EPI(BC, A_CONV3)
+    }
+#undef SAMHIP_EPI
+    return false;   // combinations the encoder does not use
 }
 
 const char* launch_gemm_f16_epi(const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
                                 int64_t ldb, float* y, int64_t ldy, int M, int N, int K, int cus, const Epilogue& ep,
-                                hipStream_t stream) {
+                                hipStream_t stream, const AOperand& op) {
+    // (128x256 tiles for the neck's N = 256 products measured 4 % slower on
+    // the largest, M = 82944, K = 6912, than the picked 256x128)
     const int cfg = gemm_f16_pick(M, N, K);
     const Cfg& c = kConfigs[cfg];
     const bool spread = int64_t((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) <= cus;
-    const bool ok = cfg == 20 ? launch_epi<256, 256, 2, 4>(a, lda, row_scale, b, ldb, y, ldy, M, N, K, spread, ep, stream)
-                              : launch_epi<256, 128, 4, 2>(a, lda, row_scale, b, ldb, y, ldy, M, N, K, spread, ep, stream);
+    if (op.mode != A_PLAIN && (op.part % (op.mode == A_CONV3 ? 128 : 64) || op.part <= 0)) return nullptr;
+    if (op.mode == A_CONV3 && (op.width <= 0 || op.height <= 0 || int64_t(op.width) * op.height != M)) return nullptr;
+    const bool ok = cfg == 20
+        ? launch_epi<256, 256, 2, 4>(a, lda, row_scale, b, ldb, y, ldy, M, N, K, spread, ep, op, stream)
+        : launch_epi<256, 128, 4, 2>(a, lda, row_scale, b, ldb, y, ldy, M, N, K, spread, ep, op, stream);
     return ok ? c.name : nullptr;
 }
 

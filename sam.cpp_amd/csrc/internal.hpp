@@ -67,14 +67,32 @@ struct Epilogue {
     int shuffle_w = 0, shuffle_c = 0;
     bool gelu = false;   // ggml_gelu_erf after the bias
 };
+// How the A tile loader reads row m, logical column k (K columns) of A:
+//   A_PLAIN : A[m][k] (lda halves per row);
+//   A_REPEAT: split rows stored [hi | lo] (part halves each, lda = 2*part)
+//             read as [hi | hi | lo] (K = 3*part);
+//   A_CONV3 : a 3x3, stride-1, zero-padded convolution gathered from pixel
+//             rows of a width x height map: A rows hold [v] or [hi | lo] of
+//             `part` channels each (lda = part or 2*part); logical column
+//             k = ((p*9 + tap)*part + c) reads physical part (p == 2) of
+//             pixel (y+ky-1, x+kx-1), tap = 3*ky + kx, zero outside the map
+//             (K = 9*part for one part, 27*part for [hi | hi | lo]).
+// part is a multiple of 64 (of 128 for A_CONV3).
+constexpr int A_PLAIN = 0, A_REPEAT = 1, A_CONV3 = 2;
+struct AOperand {
+    int mode = A_PLAIN;
+    int part = 0;
+    int width = 0, height = 0;
+};
 // Same product as launch_gemm_f16 with the shape's picked configuration and
 // the epilogue; returns the configuration's name, or nullptr for an
-// epilogue combination without a kernel (bias; bias + res; bias + res +
-// row_map; bias + pack; bias + col_scale; bias + col_scale + shuffle (+ gelu);
-// or none are built).
+// epilogue / operand combination without a kernel (plain A with: bias;
+// bias + res; bias + res + row_map; bias + pack; bias + col_scale; or none;
+// repeated A with bias + col_scale (+ shuffle (+ gelu)); gathered A with
+// bias + col_scale are built).
 const char* launch_gemm_f16_epi(const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
                                 int64_t ldb, float* y, int64_t ldy, int M, int N, int K, int cus, const Epilogue& ep,
-                                hipStream_t stream);
+                                hipStream_t stream, const AOperand& op = AOperand{});
 
 // SAM 3 vision-encoder kernels (vit.hip).
 // Layer norm over rows of E floats (E a multiple of 256): y[dst(r)] =
@@ -109,20 +127,28 @@ void launch_patch_kernel(const float* kernel, int E, int patch, _Float16* w, int
 //                 output map W/2 x H/2)
 //   NECK_IM2COL3: column tap*C + c = pixel (y+ky-1, x+kx-1) channel c,
 //                 zero outside the map, tap = 3*ky + kx          (K = 9 C)
-// and writes, for split, [hi | hi | lo] of v * 2^-e (e from the row's
-// largest magnitude, hi = fp16, lo = fp16 of the remainder, row_scale = 2^e;
-// rows of 3*kp halves), else fp16(v) (row_scale 1, rows of kp halves).
+// and writes, for split, [hi | lo] of v * 2^-e (e from the row's largest
+// magnitude, hi = fp16, lo = fp16 of the remainder, row_scale = 2^e; rows of
+// 2*kp halves, read as A_REPEAT), else fp16(v) (row_scale 1, rows of kp
+// halves).
 // Columns K..kp-1 are zero.  C is a multiple of 4.
 constexpr int NECK_ROWS = 0, NECK_POOL = 1, NECK_IM2COL3 = 2;
 void launch_neck_columns(int src, bool split, const float* x, int W, int H, int C, int kp, int64_t row0, int rows,
                          _Float16* a, float* row_scale, hipStream_t stream);
+// Operand rows of a whole map (rows pixels of C floats, C a multiple of 4)
+// for A_CONV3: split [hi | lo] of v * 2^-e with one e from the map's largest
+// magnitude (row_scale = 2^e on every row; `partial` holds 1024 floats),
+// else fp16(v) (row_scale 1).
+void launch_neck_pixels(bool split, const float* x, int64_t rows, int C, _Float16* a, float* row_scale,
+                        float* partial, hipStream_t stream);
 // B rows from ggml convolution weights:
 //   conv   {k, k, Cin, Cout}: row co, column tap*Cin + ci (tap = k*ky + kx)
 //   deconv {2, 2, Cout, Cin}: row tap*Cout + co (tap = 2*ky + kx), column ci
 // split: [hi | lo | hi] of w * 2^-e per row (col_scale = 2^e), else
-// fp16(w) (col_scale 1).
+// fp16(w) (col_scale 1).  Transposed convolutions are always split and use
+// `partial` (ceil(Cin/64) * 4 * Cout floats) for their row maxima.
 void launch_neck_weights(bool deconv, bool split, const float* w, int k, int cin, int cout, int kp, _Float16* b,
-                         float* col_scale, hipStream_t stream);
+                         float* col_scale, float* partial, hipStream_t stream);
 
 // The producing graph node folded into a tall product's activation staging:
 // PRE_GELU stages gelu_erf(x) (ggml_gelu_erf), PRE_LAYER_NORM stages

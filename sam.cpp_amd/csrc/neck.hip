@@ -8,13 +8,16 @@
 //     of im2col rows (tap-major, channel-minor) with the rearranged kernel.
 // F32 columns keep F32 accuracy with split operands: a value v scaled by a
 // power of two 2^-e is hi + lo with hi = fp16(v 2^-e), lo = fp16(v 2^-e -
-// hi); A rows [hi | hi | lo] against B rows [hi | lo | hi] sum hi*hi + hi*lo
-// + lo*hi in F32, and the epilogue multiplies by the row's and the
-// column's 2^e.  F16 columns are plain fp16 operands without scaling.
+// hi); A rows stored [hi | lo] and read as [hi | hi | lo] against B rows
+// [hi | lo | hi] sum hi*hi + hi*lo + lo*hi in F32, and the epilogue
+// multiplies by the row's and the column's 2^e.  F16 columns are plain fp16
+// operands without scaling.  A 3x3 convolution over 128k channels does not
+// build im2col rows: the product gathers them from the map's own operand
+// rows (scaled by one exponent for the whole map).
 //
-// Both operand builders give one wave to one output row: a first pass finds
-// the row's largest magnitude (split only), a second reads the values again
-// (from cache) and writes the halves.
+// The activation builder gives one wave to one output row: a first pass
+// finds the row's largest magnitude (split only), a second reads the values
+// again (from cache) and writes the halves.
 #include "internal.hpp"
 #include "q8stage.hpp"
 
@@ -65,7 +68,7 @@ __global__ __launch_bounds__(256) void neck_columns_kernel(const float* __restri
         e = row_exponent(wave_max(amax));
     }
     const float down = exp2i(-e);
-    _Float16* row = a + int64_t(r) * (SPLIT ? 3 : 1) * kp;
+    _Float16* row = a + int64_t(r) * (SPLIT ? 2 : 1) * kp;
     for (int c = 4 * lane; c < kp; c += 256) {
         const floatx4 v = c < K ? neck_fetch<SRC>(x, W, H, C, p, oy, ox, c) : floatx4{0.f, 0.f, 0.f, 0.f};
         if (SPLIT) {
@@ -77,8 +80,7 @@ __global__ __launch_bounds__(256) void neck_columns_kernel(const float* __restri
                 lo[i] = (_Float16)(s - (float)hi[i]);
             }
             *reinterpret_cast<half4_t*>(row + c) = hi;
-            *reinterpret_cast<half4_t*>(row + kp + c) = hi;
-            *reinterpret_cast<half4_t*>(row + 2 * kp + c) = lo;
+            *reinterpret_cast<half4_t*>(row + kp + c) = lo;
         } else {
             *reinterpret_cast<half4_t*>(row + c) = half4_t{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
         }
@@ -86,36 +88,93 @@ __global__ __launch_bounds__(256) void neck_columns_kernel(const float* __restri
     if (lane == 0) row_scale[r] = exp2i(e);
 }
 
-template <bool DECONV>
-__device__ __forceinline__ float neck_weight(const float* __restrict__ w, int k, int cin, int cout, int n, int c) {
-    if (DECONV) {   // ggml {2, 2, Cout, Cin}: row n = tap*Cout + co, column ci
-        const int tap = n / cout, co = n - tap * cout;
-        return w[(tap & 1) + 2 * ((tap >> 1) + 2 * (co + int64_t(cout) * c))];
+// Operand rows of a whole map for the gathered 3x3 convolution: the map's
+// largest magnitude (block maxima into `partial`, then combined by every
+// block of the second kernel) gives one power-of-two scale, and each pixel
+// row of C values becomes [hi | lo] (split) or [fp16] (unscaled).
+__global__ __launch_bounds__(256) void neck_absmax_kernel(const float* __restrict__ x, int64_t n4,
+                                                          float* __restrict__ partial) {
+    __shared__ float part[4];
+    float amax = 0.f;
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n4; i += int64_t(gridDim.x) * 256) {
+        const floatx4 v = load4f(x + 4 * i);
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
     }
-    // ggml {k, k, Cin, Cout}: row co = n, column tap*Cin + ci
-    const int tap = c / cin, ci = c - tap * cin, ky = tap / k, kx = tap - k * ky;
-    return w[kx + k * (ky + k * (ci + int64_t(cin) * n))];
+    amax = wave_max(amax);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    if (threadIdx.x == 0) partial[blockIdx.x] = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
 }
 
-template <bool DECONV, bool SPLIT>
-__global__ __launch_bounds__(256) void neck_weights_kernel(const float* __restrict__ w, int k, int cin, int cout,
-                                                           int kp, _Float16* __restrict__ b,
-                                                           float* __restrict__ col_scale) {
+template <bool SPLIT>
+__global__ __launch_bounds__(256) void neck_pixels_kernel(const float* __restrict__ x, int64_t rows, int C,
+                                                          const float* __restrict__ partial, int nparts,
+                                                          _Float16* __restrict__ a, float* __restrict__ row_scale) {
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
-    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int rows = DECONV ? 4 * cout : cout, K = DECONV ? cin : k * k * cin;
-    if (n >= rows) return;
+    __shared__ float part[4];
     int e = 0;
     if (SPLIT) {
         float amax = 0.f;
-        for (int c = lane; c < K; c += 64) amax = fmaxf(amax, fabsf(neck_weight<DECONV>(w, k, cin, cout, n, c)));
-        e = row_exponent(wave_max(amax));
+        for (int i = threadIdx.x; i < nparts; i += 256) amax = fmaxf(amax, partial[i]);
+        amax = wave_max(amax);
+        if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = amax;
+        __syncthreads();
+        e = row_exponent(fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3])));
+    }
+    const float down = exp2i(-e), up = exp2i(e);
+    const int c4 = C / 4;
+    const int64_t n4 = rows * c4;
+    for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n4; i += int64_t(gridDim.x) * 256) {
+        const int64_t p = i / c4;
+        const int c = int(i - p * c4) * 4;
+        const floatx4 v = load4f(x + 4 * i);
+        if (SPLIT) {
+            half4_t hi, lo;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float s = v[q] * down;
+                hi[q] = (_Float16)s;
+                lo[q] = (_Float16)(s - (float)hi[q]);
+            }
+            *reinterpret_cast<half4_t*>(a + p * 2 * C + c) = hi;
+            *reinterpret_cast<half4_t*>(a + p * 2 * C + C + c) = lo;
+        } else {
+            *reinterpret_cast<half4_t*>(a + p * C + c) =
+                half4_t{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+        }
+        if (c == 0) row_scale[p] = up;
+    }
+}
+
+// Convolution kernel {k, k, Cin, Cout} -> B row co, column tap*Cin + ci
+// (tap = k*ky + kx).  One workgroup per row: the row's k*k*Cin source
+// values are contiguous (ci-major, taps inner), read coalesced for the
+// magnitude pass and re-read from cache, k*k apart, for the permuted write.
+template <bool SPLIT>
+__global__ __launch_bounds__(256) void neck_conv_weights_kernel(const float* __restrict__ w, int kk, int cin, int kp,
+                                                                _Float16* __restrict__ b,
+                                                                float* __restrict__ col_scale) {
+#pragma clang fp contract(off)
+    __shared__ float part[4];
+    const int co = blockIdx.x, t = threadIdx.x, K = kk * cin;
+    const float* src = w + int64_t(co) * K;
+    int e = 0;
+    if (SPLIT) {
+        float amax = 0.f;
+        for (int c = t; c < K; c += 256) amax = fmaxf(amax, fabsf(src[c]));
+        amax = wave_max(amax);
+        if ((t & 63) == 0) part[t >> 6] = amax;
+        __syncthreads();
+        e = row_exponent(fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3])));
     }
     const float down = exp2i(-e);
-    _Float16* row = b + int64_t(n) * (SPLIT ? 3 : 1) * kp;
-    for (int c = lane; c < kp; c += 64) {
-        const float v = c < K ? neck_weight<DECONV>(w, k, cin, cout, n, c) : 0.f;
+    _Float16* row = b + int64_t(co) * (SPLIT ? 3 : 1) * kp;
+    for (int c = t; c < kp; c += 256) {
+        float v = 0.f;
+        if (c < K) {
+            const int tap = c / cin, ci = c - tap * cin;
+            v = src[int64_t(ci) * kk + tap];
+        }
         if (SPLIT) {
             const float s = v * down;
             const _Float16 hi = (_Float16)s, lo = (_Float16)(s - (float)hi);
@@ -126,7 +185,69 @@ __global__ __launch_bounds__(256) void neck_weights_kernel(const float* __restri
             row[c] = (_Float16)v;
         }
     }
-    if (lane == 0) col_scale[n] = exp2i(e);
+    if (t == 0) col_scale[co] = exp2i(e);
+}
+
+// Transposed-convolution kernel {2, 2, Cout, Cin}: as a matrix S[ci][j]
+// with j = 4*co + tap (tap = 2*ky + kx) it becomes B row n(j) = tap*Cout +
+// co, column ci.  64 x 64 tiles of S: the first pass leaves each tile's
+// column maxima in `partial` [Cin/64][4 Cout], the second combines a
+// column's partials into its power-of-two scale and transposes the tile
+// through LDS, so that both the reads of S and the writes of B are
+// contiguous.
+__device__ __forceinline__ int deconv_row(int j, int cout) { return (j & 3) * cout + (j >> 2); }
+
+__global__ __launch_bounds__(256) void neck_deconv_max_kernel(const float* __restrict__ w, int cin, int cout,
+                                                              float* __restrict__ partial) {
+    __shared__ float part[4][64];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const int J = 4 * cout, j = blockIdx.x * 64 + tx, ci0 = blockIdx.y * 64;
+    float amax = 0.f;
+    if (j < J)
+#pragma unroll 4
+        for (int r = ty; r < 64; r += 4)
+            if (ci0 + r < cin) amax = fmaxf(amax, fabsf(w[int64_t(ci0 + r) * J + j]));
+    part[ty][tx] = amax;
+    __syncthreads();
+    if (ty == 0 && j < J)
+        partial[int64_t(blockIdx.y) * J + j] = fmaxf(fmaxf(part[0][tx], part[1][tx]), fmaxf(part[2][tx], part[3][tx]));
+}
+
+__global__ __launch_bounds__(256) void neck_deconv_pack_kernel(const float* __restrict__ w, int cin, int cout, int kp,
+                                                               const float* __restrict__ partial,
+                                                               _Float16* __restrict__ b, float* __restrict__ col_scale) {
+#pragma clang fp contract(off)
+    __shared__ float tile[64][65];
+    __shared__ float down[64];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const int J = 4 * cout, j0 = blockIdx.x * 64, ci0 = blockIdx.y * 64, tiles = (cin + 63) / 64;
+#pragma unroll 4
+    for (int r = ty; r < 64; r += 4) {
+        const int ci = ci0 + r, j = j0 + tx;
+        tile[r][tx] = (ci < cin && j < J) ? w[int64_t(ci) * J + j] : 0.f;
+    }
+    if (ty == 0) {
+        const int j = j0 + tx;
+        float amax = 0.f;
+        if (j < J)
+            for (int t = 0; t < tiles; ++t) amax = fmaxf(amax, partial[int64_t(t) * J + j]);
+        const int e = row_exponent(amax);
+        down[tx] = exp2i(-e);
+        if (blockIdx.y == 0 && j < J) col_scale[deconv_row(j, cout)] = exp2i(e);
+    }
+    __syncthreads();
+    const int ci = ci0 + tx;
+#pragma unroll 4
+    for (int jj = ty; jj < 64; jj += 4) {
+        const int j = j0 + jj;
+        if (j >= J) break;
+        const float s = tile[tx][jj] * down[jj];
+        const _Float16 hi = (_Float16)s, lo = (_Float16)(s - (float)hi);
+        _Float16* row = b + int64_t(deconv_row(j, cout)) * 3 * kp;
+        row[ci] = hi;
+        row[kp + ci] = lo;
+        row[2 * kp + ci] = hi;
+    }
 }
 
 }  // namespace
@@ -148,18 +269,36 @@ void launch_neck_columns(int src, bool split, const float* x, int W, int H, int 
 #undef SAMHIP_NECK_COLUMNS
 }
 
+void launch_neck_pixels(bool split, const float* x, int64_t rows, int C, _Float16* a, float* row_scale,
+                        float* partial, hipStream_t stream) {
+    const int64_t n4 = rows * (C / 4);
+    const int blocks = int(std::min<int64_t>(1024, (n4 + 255) / 256));
+    if (split) {
+        hipLaunchKernelGGL(neck_absmax_kernel, dim3(unsigned(blocks)), dim3(256), 0, stream, x, n4, partial);
+        hipLaunchKernelGGL(neck_pixels_kernel<true>, dim3(unsigned(blocks)), dim3(256), 0, stream, x, rows, C, partial,
+                           blocks, a, row_scale);
+    } else {
+        hipLaunchKernelGGL(neck_pixels_kernel<false>, dim3(unsigned(blocks)), dim3(256), 0, stream, x, rows, C,
+                           partial, 0, a, row_scale);
+    }
+}
+
 void launch_neck_weights(bool deconv, bool split, const float* w, int k, int cin, int cout, int kp, _Float16* b,
-                         float* col_scale, hipStream_t stream) {
-    const int rows = deconv ? 4 * cout : cout;
-    const dim3 grid(unsigned((rows + 3) / 4)), block(256);
-    if (deconv && split)
-        hipLaunchKernelGGL((neck_weights_kernel<true, true>), grid, block, 0, stream, w, k, cin, cout, kp, b, col_scale);
-    else if (deconv)
-        hipLaunchKernelGGL((neck_weights_kernel<true, false>), grid, block, 0, stream, w, k, cin, cout, kp, b, col_scale);
-    else if (split)
-        hipLaunchKernelGGL((neck_weights_kernel<false, true>), grid, block, 0, stream, w, k, cin, cout, kp, b, col_scale);
+                         float* col_scale, float* partial, hipStream_t stream) {
+    if (deconv) {   // always split (the transposed convolutions stay F32-accurate)
+        const unsigned jt = unsigned((4 * cout + 63) / 64);
+        hipLaunchKernelGGL(neck_deconv_max_kernel, dim3(jt, unsigned((cin + 63) / 64)), dim3(256), 0, stream, w, cin,
+                           cout, partial);
+        hipLaunchKernelGGL(neck_deconv_pack_kernel, dim3(jt, unsigned(kp / 64)), dim3(256), 0, stream, w, cin, cout,
+                           kp, partial, b, col_scale);
+        return;
+    }
+    if (split)
+        hipLaunchKernelGGL(neck_conv_weights_kernel<true>, dim3(unsigned(cout)), dim3(256), 0, stream, w, k * k, cin,
+                           kp, b, col_scale);
     else
-        hipLaunchKernelGGL((neck_weights_kernel<false, false>), grid, block, 0, stream, w, k, cin, cout, kp, b, col_scale);
+        hipLaunchKernelGGL(neck_conv_weights_kernel<false>, dim3(unsigned(cout)), dim3(256), 0, stream, w, k * k, cin,
+                           kp, b, col_scale);
 }
 
 }  // namespace samhip

@@ -457,3 +457,33 @@ def test_capture_needs_reserved_staging(samhip, oracle):
         ctx.capture_end().destroy()
     finally:
         ctx.close()
+
+
+# ---- mixed per-module formats, batch of 8 images (M = 8 x 5184) ------------
+
+def test_mul_mat_batch8_mixed_formats(gpu_ctx, oracle, samhip):
+    """One forward's worth of products with the format switching per module:
+    vision qkv/proj Q6_K, fc1 Q5_K, fc2 Q8_0 (4736-wide rows cannot hold
+    K-quant super-blocks, src/models/sam3/weights.hpp:159-160), text and
+    decoder linears Q8_0, interleaved on one context.  Sampled rows against
+    the oracle's native path (1e-3), and every image's rows bit-identical to
+    the same image run alone (the products are row-independent)."""
+    m1, batch = 5184, 8
+    steps = [("qkv", samhip.Q6_K, 1024, 3072, m1 * batch), ("text fc1", samhip.Q8_0, 1024, 4096, 32),
+             ("proj", samhip.Q6_K, 1024, 1024, m1 * batch), ("fc1", samhip.Q5_K, 1024, 4736, m1 * batch),
+             ("decoder fc1", samhip.Q8_0, 256, 2048, 200), ("fc2", samhip.Q8_0, 4736, 1024, m1 * batch)]
+    for i, (name, qtype, k, n, m) in enumerate(steps):
+        say("case batch8", name, qtype, m)
+        w = gpu_ctx.quantize(qtype, (np.random.default_rng(10 + i).standard_normal((n, k)) * 0.02).astype(np.float32),
+                             samhip.ROUND_REF)
+        x = np.random.default_rng(20 + i).standard_normal((m, k)).astype(np.float32)
+        y = gpu_ctx.matmul(qtype, w, x)
+        rows = np.unique(np.concatenate([np.arange(0, m, 331), [m - 1]]))
+        r = max_row_rel_l2(y[rows], oracle.mul_mat_native(qtype, w, x[rows]))
+        say("  row rel L2", r)
+        assert r <= ROW_REL_L2, name
+        if m == m1 * batch:
+            for img in (0, 5, 7):
+                alone = gpu_ctx.matmul(qtype, w, x[img * m1:(img + 1) * m1])
+                assert np.array_equal(alone, y[img * m1:(img + 1) * m1]), (name, img)
+        del x, y
