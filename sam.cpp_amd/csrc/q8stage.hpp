@@ -87,17 +87,17 @@ __device__ __forceinline__ int min32_lanes(int v) {
 }
 typedef float floatx8 __attribute__((ext_vector_type(8)));
 
-// The fp16 operand of 8 consecutive activations held by each lane; lanes
+// The Q8 block codes of 8 consecutive activations held by each lane; lanes
 // 4g..4g+3 hold one Q8_0 block, lanes 32h..32h+31 one Q8_K block.  Every
 // lane of the wave must call it (cross-lane reductions); lanes past the
-// row's end hold zeros.  `down` = 2^-e.  X86 selects the Q8_0 rounding of
-// ggml's x86-64 from_float (scale 127/amax, ties to even) over the
-// reference quantize_row_q8_0_ref (scale 1/d, ties away from zero).
+// row's end hold zeros.  d is the block's decoded scale (the stored fp16 for
+// Q8_0), q[i] the integer codes in [-127, 127].  X86 selects the Q8_0
+// rounding of ggml's x86-64 from_float (scale 127/amax, ties to even) over
+// the reference quantize_row_q8_0_ref (scale 1/d, ties away from zero).
 template <int MODE, bool X86>
-__device__ __forceinline__ half8 quant8(const floatx8& v, int lane, float down) {
+__device__ __forceinline__ void quant8_codes(const floatx8& v, int lane, float& d, float (&q)[8]) {
 #pragma clang fp contract(off)
-    float d = 0.f;
-    float q[8];
+    d = 0.f;
     if (MODE == T_Q8_0) {
         float amax = 0.f;
 #pragma unroll
@@ -113,8 +113,8 @@ __device__ __forceinline__ half8 quant8(const floatx8& v, int lane, float down) 
             const float s = v[i] * inv;
             q[i] = X86 ? __builtin_rintf(s) : __builtin_roundf(s);
         }
-    } else if (MODE == T_Q8_K) {
-        // first element of largest magnitude in the 256-value block
+    } else {
+        // Q8_K: first element of largest magnitude in the 256-value block
         const int base = 8 * (lane & 31);
         float la = 0.f, ls = 0.f;
         int li = 1 << 20;
@@ -136,9 +136,24 @@ __device__ __forceinline__ half8 quant8(const floatx8& v, int lane, float down) 
             for (int i = 0; i < 8; ++i) q[i] = 0.f;
         }
     }
+}
+
+// The fp16 MFMA operand of the same 8 activations:
+//   Q8 modes: fp16(d * q * down);  F16 mode: fp16(x * down)
+// with `down` = 2^-e.
+template <int MODE, bool X86>
+__device__ __forceinline__ half8 quant8(const floatx8& v, int lane, float down) {
+#pragma clang fp contract(off)
     half8 o;
+    if (MODE == T_F16) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = MODE == T_F16 ? (_Float16)(v[i] * down) : (_Float16)((d * q[i]) * down);
+        for (int i = 0; i < 8; ++i) o[i] = (_Float16)(v[i] * down);
+        return o;
+    }
+    float d, q[8];
+    quant8_codes<MODE, X86>(v, lane, d, q);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (_Float16)((d * q[i]) * down);
     return o;
 }
 
