@@ -762,6 +762,8 @@ const Cfg kConfigs[] = {
     {"gemm_f16pipe_128x128x64_s3_w2x4", launch_pipe_plain<128, 128, 64, 3, 2, 4>, 128, 128, 64},
     {"gemm_f16pipe_128x256x64_s2_w2x4", launch_pipe_plain<128, 256, 64, 2, 2, 4>, 128, 256, 64},
     {"gemm_f16pipe_128x128x128_s2_w2x4", launch_pipe_plain<128, 128, 128, 2, 2, 4>, 128, 128, 128},
+    {"gemm_f16pipe_192x128x64_s2_w2x4", launch_pipe_plain<192, 128, 64, 2, 2, 4>, 192, 128, 64},
+    {"gemm_f16pipe_192x128x64_s2_w2x2", launch_pipe_plain<192, 128, 64, 2, 2, 2>, 192, 128, 64},
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -778,19 +780,27 @@ bool gemm_f16_supported(int M, int N, int K, int64_t lda, int64_t ldb) {
     return K % 128 == 0 && int64_t(M) * lda * 2 < 0x7fffffff && int64_t(N) * ldb * 2 < 0x7fffffff;
 }
 
-// Tile choice from a measured sweep of the configurations on the SAM 3 linear
-// shapes at M = 5184 tokens on MI355X (kernel time, HIP events, random
-// operands; differences below ~3 % are within run-to-run noise).  Eight-wave
-// workgroups (two waves per SIMD of one workgroup) win on every shape:
-//   N >= 2048 (qkv 3072, fc1 4736)        -> 256x256x64, 2 stages, 2x4 waves (733-773 / 668-685 TFLOP/s)
-//   N <= 1024 (proj 1024, fc2 4736->1024, fusion/decoder widths)
-//                                          -> 256x128x64, 2 stages, 4x2 waves (452 proj, 706-713 fc2)
-int gemm_f16_pick(int /*M*/, int N, int /*K*/) {
-    return N >= 2048 ? 20 : 22;
+// Tile choice from measured sweeps on MI355X (kernel time, HIP events,
+// random operands; differences below ~3 % are within run-to-run noise).
+// Eight-wave workgroups win on every shape; what decides between the two
+// remaining tiles is how evenly the grid fills the CUs.  256x256 tiles
+// (2x4 waves, one workgroup per CU) are the most efficient per tile but
+// come in coarse waves; 192x128 tiles (2x4 waves, 80 KB of LDS: two
+// workgroups per CU) balance better.  256x256 is taken when its tiles fill
+// at least 80 % of the CU waves they occupy:
+//   M = 5184:  qkv N 3072 (252 tiles) 42.8 us vs 46.3; fc1 N 4736 (399
+//              tiles) 72.9 vs 61.2 -> 192x128; N 1024 K 1024 / 4736 (proj,
+//              fc2) 22.1 / 65.7 us with 192x128 vs 23.7 / 70.3 with 256x128;
+//   M = 41472: N 3072 377 vs 408, N 4736 557 vs 579, N 1024 K 4736 495 vs
+//              528 -> 256x256; N 1024 K 1024 117 vs 115.
+int gemm_f16_pick(int M, int N, int /*K*/, int cus) {
+    const int64_t tiles = int64_t((M + 255) / 256) * ((N + 255) / 256);
+    const int64_t waves = (tiles + cus - 1) / cus;
+    return tiles * 10 >= waves * cus * 8 ? 20 : 30;
 }
 
-// The picked configurations (20: 256x256x64 on 2x4 waves, 22: 256x128x64 on
-// 4x2 waves) with each epilogue the vision encoder uses.
+// The picked configurations (20: 256x256x64 on 2x4 waves, 30: 192x128x64 on
+// 2x4 waves) with each epilogue and operand mode the encoder uses.
 template <int BM, int BN, int WM, int WN>
 bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
                 int64_t ldy, int M, int N, int K, bool spread, const Epilogue& ep, const AOperand& op,
@@ -831,22 +841,20 @@ bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16*
 const char* launch_gemm_f16_epi(const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
                                 int64_t ldb, float* y, int64_t ldy, int M, int N, int K, int cus, const Epilogue& ep,
                                 hipStream_t stream, const AOperand& op) {
-    // (128x256 tiles for the neck's N = 256 products measured 4 % slower on
-    // the largest, M = 82944, K = 6912, than the picked 256x128)
-    const int cfg = gemm_f16_pick(M, N, K);
+    const int cfg = gemm_f16_pick(M, N, K, cus);
     const Cfg& c = kConfigs[cfg];
     const bool spread = int64_t((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) <= cus;
     if (op.mode != A_PLAIN && (op.part % (op.mode == A_CONV3 ? 128 : 64) || op.part <= 0)) return nullptr;
     if (op.mode == A_CONV3 && (op.width <= 0 || op.height <= 0 || int64_t(op.width) * op.height != M)) return nullptr;
     const bool ok = cfg == 20
         ? launch_epi<256, 256, 2, 4>(a, lda, row_scale, b, ldb, y, ldy, M, N, K, spread, ep, op, stream)
-        : launch_epi<256, 128, 4, 2>(a, lda, row_scale, b, ldb, y, ldy, M, N, K, spread, ep, op, stream);
+        : launch_epi<192, 128, 2, 4>(a, lda, row_scale, b, ldb, y, ldy, M, N, K, spread, ep, op, stream);
     return ok ? c.name : nullptr;
 }
 
 const char* launch_gemm_f16(int cfg, const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
                             int64_t ldb, float* y, int64_t ldy, int M, int N, int K, int cus, hipStream_t stream) {
-    if (cfg < 0 || cfg >= kNumConfigs || K % kConfigs[cfg].bk) cfg = gemm_f16_pick(M, N, K);
+    if (cfg < 0 || cfg >= kNumConfigs || K % kConfigs[cfg].bk) cfg = gemm_f16_pick(M, N, K, cus);
     const Cfg& c = kConfigs[cfg];
     const int64_t tiles = int64_t((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
     c.launch(a, lda, row_scale, b, ldb, y, ldy, M, N, K, tiles <= cus, stream);

@@ -34,7 +34,7 @@ void launch_dequant_w_f16(int wtype, const void* w, int64_t w_stride, int N, int
 int gemm_f16_config_count();
 bool gemm_f16_supported(int M, int N, int K, int64_t lda, int64_t ldb);
 const char* gemm_f16_config_name(int cfg);
-int gemm_f16_pick(int M, int N, int K);
+int gemm_f16_pick(int M, int N, int K, int cus);
 // `cus`: compute units of the device; grids with at most that many tiles run
 // one workgroup per CU.
 const char* launch_gemm_f16(int cfg, const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,

@@ -104,13 +104,14 @@ __device__ __forceinline__ void stage8_row(const float* __restrict__ x, int64_t 
     }
 }
 
-// Long rows (K up to 512*CH, CH > 4) in Q8 modes: instead of holding the
-// whole row in registers (80 values per lane at K = 4736, which left two
-// waves per SIMD), each 512-value chunk is loaded, passed through PRE, and
-// quantized to its Q8 blocks at once; the codes (int8) and block scales go
-// to the wave's LDS slab and the row maximum is kept running.  Once the row
-// exponent is known the codes come back from LDS as fp16(d * q * 2^-e), the
-// same values stage8_row writes.  X is read once.
+// Long rows (K up to 512*CH, CH > 4) through erf-GELU in Q8 modes: instead
+// of holding the whole row in registers (80 values per lane at K = 4736 and
+// the GELU's temporaries, which left two waves per SIMD), each 512-value
+// chunk is loaded, passed through PRE and quantized to its Q8 blocks at
+// once; the codes (int8) and block scales go to the wave's LDS slab and the
+// row maximum is kept running.  Once the row exponent is known the codes
+// come back from LDS as fp16(d * q * 2^-e), the same values stage8_row
+// writes.  X is read once.
 template <int CH>
 constexpr int stage_lds_bytes() { return CH * 512 + CH * 16 * 4; }
 
@@ -211,7 +212,10 @@ __global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ x, 
                                                    _Float16* __restrict__ a, int64_t lda, float* __restrict__ row_scale,
                                                    int stage_blocks, const uint8_t* __restrict__ W, int64_t w_stride,
                                                    int N, _Float16* __restrict__ wout, int64_t ldo, RowPre pre) {
-    constexpr bool SLAB = CH > 4 && MODE != T_F16 && PRE != PRE_LAYER_NORM;
+    // (without a PRE the register path keeps 4-5 waves per SIMD with every
+    // load of the row in flight at once, and measured 40 us against 47 for
+    // the slab at K = 4736)
+    constexpr bool SLAB = CH > 4 && MODE != T_F16 && PRE == PRE_GELU;
     __shared__ __attribute__((aligned(16))) uint8_t slabs[SLAB ? 4 * stage_lds_bytes<CH>() : 16];
     if (int(blockIdx.x) < stage_blocks) {
         const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
