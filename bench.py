@@ -83,7 +83,8 @@ def kernel_symbol(variant):
     gemm_f16_{BM}x{BN}x{BK}_w{WM}x{WN} -> gemm_f16_kernel<BM, BN, WM, WN, BK>,
     gemm_f16dma_{BM}x{BN}x{BK}_s{S}    -> gemm_f16_dma_kernel<BM, BN, BK, S>,
     gemm_f16pipe_{BM}x{BN}x{BK}_s{S}[_w{WM}x{WN}]
-                                       -> gemm_f16_pipe_kernel<BM, BN, BK, S, WM, WN> (2x2 waves by default).
+                                       -> gemm_f16_pipe_kernel<BM, BN, BK, S, WM, WN, 0, 0> (2x2 waves by
+                                          default; plain epilogue and A operand).
     Returns (symbol, threads per workgroup, BM, BN) or None."""
     import re
     m = re.fullmatch(r"gemm_f16_(\d+)x(\d+)x(\d+)_w(\d+)x(\d+)", variant)
@@ -98,7 +99,7 @@ def kernel_symbol(variant):
     if m:
         bm, bn, bk, st = map(int, m.groups()[:4])
         wm, wn = (int(m.group(5)), int(m.group(6))) if m.group(5) else (2, 2)
-        return f"gemm_f16_pipe_kernel<{bm}, {bn}, {bk}, {st}, {wm}, {wn}>", 64 * wm * wn, bm, bn
+        return f"gemm_f16_pipe_kernel<{bm}, {bn}, {bk}, {st}, {wm}, {wn}, 0, 0>", 64 * wm * wn, bm, bn
     return None
 
 
@@ -209,10 +210,12 @@ def summarize_profiles(d, commands):
                 "8 forwards: 2 warmup, 5 timed, 1 traced)", commands["encoder"],
                 "kernel_stats_vision_encoder_1008px_q4_k.md",
                 note="`quantize_weights_kernel` and `quantize_act_kernel` pack the random-init weights once at set-up; "
-                     "every other kernel runs 8 times per block (or per image for the prefix).  Template arguments: "
-                     "`prep_kernel<mode, chunks, x86, weight type, pre>` (pre 1 = erf-GELU, 2 = layer norm), "
-                     "`gemm_f16_pipe_kernel<BM, BN, BK, stages, waves M, waves N, epilogue>` (epilogue bits 1 bias, "
-                     "4 residual, 8 window unpartition, 16 packed attention operands).")
+                     "every other kernel runs 8 times per block (or per image for the prefix and the neck).  Template "
+                     "arguments: `prep_kernel<mode, chunks, x86, weight type, pre>` (pre 1 = erf-GELU, 2 = layer "
+                     "norm), `gemm_f16_pipe_kernel<BM, BN, BK, stages, waves M, waves N, epilogue, A operand>` "
+                     "(epilogue bits 1 bias, 4 residual, 8 window unpartition, 16 packed attention operands, 32 "
+                     "column scale, 64 transposed-convolution scatter, 128 erf-GELU; A operand 0 rows, 1 split rows "
+                     "read as [hi | hi | lo], 2 gathered 3x3 convolution).")
 
     lines = ["# HBM traffic per dispatch, SAM 3 ViT linear sweep at M=5184", "",
              "Commands (from the repository root, `cd /tmp && export TMPDIR=/tmp` first):", "", "```",
