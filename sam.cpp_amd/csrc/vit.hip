@@ -403,8 +403,9 @@ void launch_zero_pad(_Float16* qh, _Float16* kh, _Float16* vh, int B, int H, int
 void launch_attention(const _Float16* qh, const _Float16* kh, const _Float16* vh, float* out, int64_t ldo, int B,
                       int H, int N, hipStream_t stream) {
     const int np = (N + 63) / 64 * 64;
-    // 128-query workgroups: measured on the SAM 3 shapes against 64 and 192
-    // (windowed 34 / 42 / 41 us, global 206 / 294 / 267 us)
+    // 128-query workgroups: measured on the SAM 3 shapes against 64, 96 and
+    // 192 (windowed 34 / 42 / 35 / 41 us, global 206 / 294 / 213 / 267 us;
+    // 96 tiles 576 and 5184 queries exactly and still loses)
     hipLaunchKernelGGL(attention_kernel<4>, dim3(unsigned((np + 127) / 128), unsigned(H), unsigned(B)), dim3(256), 0,
                        stream, qh, kh, vh, out, ldo, H, N, np);
 }
