@@ -11,9 +11,16 @@
 //                                  check the device bytes equal the file's and
 //                                  run each as Y = X W^T with M random rows,
 //                                  against the oracle's native product
+//   gguf_tool encode   <file> <image.f32> <out prefix> [f32|f16]
+//                                  load vit.* / neck.det.* onto device 0, run
+//                                  the image encoder (sam.cpp_amd/host/
+//                                  vision_encoder.hpp) on the raw F32 planes
+//                                  and write the ViT output <prefix>.features.f32
+//                                  and <prefix>.level<i>.f32 per neck level
 // A rejected file prints {"error": "<message>"} and exits with status 3.
 #include "gguf_reader.hpp"
 #include "ggml_oracle.h"
+#include "vision_encoder.hpp"
 
 #include <cmath>
 #include <cstdio>
@@ -168,11 +175,72 @@ int gpu(const std::string& path, int64_t m) {
     return 0;
 }
 
+int encode(const std::string& path, const std::string& image_path, const std::string& prefix, bool f16) {
+    sam::GgufReader r(path);
+    const sam::VisionParameters p = sam::VisionParameters::read(r);
+    sam::HipBackend backend = sam::HipBackend::make(0, sam::HipComputeMode::Q8Native);
+    sam::DeviceWeights weights(backend);
+    weights.load(r, [](const sam::GgufTensorInfo& t) {
+        return t.name.rfind("vit.", 0) == 0 || t.name.rfind("neck.det.", 0) == 0;
+    });
+    sam::HipVisionEncoder encoder(backend, weights, p, f16 ? SAMHIP_TYPE_F16 : SAMHIP_TYPE_F32);
+    const size_t image_floats = size_t(3) * p.image_size * p.image_size;
+    std::vector<float> image(image_floats);
+    FILE* f = std::fopen(image_path.c_str(), "rb");
+    if (!f || std::fread(image.data(), 4, image_floats, f) != image_floats) {
+        if (f) std::fclose(f);
+        throw std::runtime_error("cannot read the image planes");
+    }
+    std::fclose(f);
+    void* dimage = backend.alloc(image_floats * 4);
+    backend.upload(dimage, image.data(), image_floats * 4);
+    const bool level3 = weights.has("neck.det.3.conv_1x1.weight");
+    float* levels[4] = {nullptr, nullptr, nullptr, nullptr};
+    for (int i = 0; i < (level3 ? 4 : 3); ++i) {
+        const size_t side = size_t(encoder.level_side(i));
+        levels[i] = static_cast<float*>(backend.alloc(side * side * size_t(p.neck_dim) * 4));
+    }
+    encoder.encode(static_cast<const float*>(dimage), levels);
+    backend.synchronize();
+    {
+        const size_t n = size_t(p.grid()) * p.grid() * size_t(p.embed);
+        std::vector<float> x(n);
+        backend.download(x.data(), encoder.features(), n * 4);
+        const std::string name = prefix + ".features.f32";
+        FILE* o = std::fopen(name.c_str(), "wb");
+        if (!o || std::fwrite(x.data(), 4, n, o) != n) {
+            if (o) std::fclose(o);
+            throw std::runtime_error("cannot write " + name);
+        }
+        std::fclose(o);
+    }
+    std::printf("{\"loaded\": %zu, \"grid\": %d, \"dim\": %d, \"levels\": [", weights.count(), p.grid(),
+                p.neck_dim);
+    for (int i = 0; i < 4 && levels[i]; ++i) {
+        const size_t side = size_t(encoder.level_side(i)), n = side * side * size_t(p.neck_dim);
+        std::vector<float> out(n);
+        backend.download(out.data(), levels[i], n * 4);
+        const std::string name = prefix + ".level" + std::to_string(i) + ".f32";
+        FILE* o = std::fopen(name.c_str(), "wb");
+        if (!o || std::fwrite(out.data(), 4, n, o) != n) {
+            if (o) std::fclose(o);
+            throw std::runtime_error("cannot write " + name);
+        }
+        std::fclose(o);
+        std::printf("%s%zu", i ? ", " : "", side);
+        backend.free(levels[i]);
+    }
+    std::printf("]}\n");
+    backend.free(dimage);
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
     if (argc < 3) {
-        std::fprintf(stderr, "usage: gguf_tool inspect|contract|profile <file> | gpu <file> <M>\n");
+        std::fprintf(stderr, "usage: gguf_tool inspect|contract|profile <file> | gpu <file> <M> | "
+                             "encode <file> <image.f32> <out prefix> [f32|f16]\n");
         return 2;
     }
     const std::string mode = argv[1], path = argv[2];
@@ -181,6 +249,8 @@ int main(int argc, char** argv) {
         if (mode == "contract") return contract(path);
         if (mode == "profile") return profile(path);
         if (mode == "gpu" && argc > 3) return gpu(path, std::atoll(argv[3]));
+        if (mode == "encode" && argc > 4)
+            return encode(path, argv[3], argv[4], argc > 5 && std::string(argv[5]) == "f16");
         std::fprintf(stderr, "unknown mode %s\n", mode.c_str());
         return 2;
     } catch (const std::exception& e) {

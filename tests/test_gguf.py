@@ -11,6 +11,7 @@ checkpoint with ViT-shaped linears and checks the device bytes and products.
 """
 
 import json
+import struct
 import os
 import subprocess
 
@@ -330,3 +331,123 @@ def test_gguf_upload_and_products(tmp_path, oracle, kq, file_type, profile_name)
             print(p, flush=True)
             assert p["bytes_equal"], p
             assert p["max_row_rel_l2"] <= 1e-3, p
+
+
+# ---------------------------------------------------------------------------
+# The image encoder from a converted checkpoint
+# ---------------------------------------------------------------------------
+
+def _encoder_checkpoint(oracle, tmp_path):
+    """A SAM 3-structured checkpoint at reduced size (168 px, patch 14 ->
+    12 x 12 tokens, width 256, 4 heads, 2 blocks with block 1 global, MLP
+    512, window 6, neck 64 -> 32): the reference's tensor names and ggml
+    shapes (src/models/sam3/tensors.hpp:96-163) and sam3.vision.* metadata.
+    Returns the path, the image, and the host weights for the oracle."""
+    from tests.vit_fixtures import axial_rope_table, block_weights, neck_weights
+    img, patch, E, heads, mlp, ws, D, mid, blocks, glob = 168, 14, 256, 4, 512, 6, 32, 64, 2, [1]
+    G, pg = img // patch, img // patch // 3
+    rng = np.random.default_rng(21)
+    f32 = lambda a: np.ascontiguousarray(a, np.float32)
+    kernel = f32(rng.standard_normal((E, 3, patch, patch)) * 0.02)
+    pos = f32(rng.standard_normal((pg, pg, E)) * 0.1)
+    lw, lb = f32(1 + 0.1 * rng.standard_normal(E)), f32(0.05 * rng.standard_normal(E))
+    T = [("vit.patch_embed.proj.weight", (patch, patch, 3, E), gg.GGML_F32, kernel.tobytes()),
+         ("vit.pos_embed", (E, pg, pg), gg.GGML_F32, pos.tobytes()),
+         ("vit.ln_pre.weight", (E,), gg.GGML_F32, lw.tobytes()), ("vit.ln_pre.bias", (E,), gg.GGML_F32, lb.tobytes())]
+    bw = []
+    for i in range(blocks):
+        g = i in glob
+        w = block_weights(oracle, E, mlp, heads, G * G if g else ws * ws, G if g else ws, 30 + i,
+                          {"qkv": oracle.Q4_K, "proj": oracle.Q4_K, "fc1": oracle.Q4_K, "fc2": oracle.Q8_0})
+        bw.append(w)
+        p = f"vit.blocks.{i}"
+        for n, k, nn in (("attn.qkv", E, 3 * E), ("attn.proj", E, E), ("mlp.lin1", E, mlp), ("mlp.lin2", mlp, E)):
+            key = {"attn.qkv": "qkv", "attn.proj": "proj", "mlp.lin1": "fc1", "mlp.lin2": "fc2"}[n]
+            gt = {oracle.Q4_K: gg.GGML_Q4_K, oracle.Q8_0: gg.GGML_Q8_0}[w[key + "_type"]]
+            T.append((f"{p}.{n}.weight", (k, nn), gt, w[key + "_w"].tobytes()))
+            T.append((f"{p}.{n}.bias", (nn,), gg.GGML_F32, f32(w[key + "_b"]).tobytes()))
+        for n in ("norm1", "norm2"):
+            T.append((f"{p}.{n}.weight", (E,), gg.GGML_F32, f32(w[n + "_w"]).tobytes()))
+            T.append((f"{p}.{n}.bias", (E,), gg.GGML_F32, f32(w[n + "_b"]).tobytes()))
+        T.append((f"{p}.attn.freqs_cis", (2, 32, w["freqs"].shape[0]), gg.GGML_F32, f32(w["freqs"]).tobytes()))
+    nw = neck_weights(rng, E, mid, D, scale=1.0 / np.sqrt(E))
+    names = {"s0_dc1": ("0.dconv_2x2_0", (2, 2, mid, E)), "s0_dc2": ("0.dconv_2x2_1", (2, 2, D, mid)),
+             "s0_c1": ("0.conv_1x1", (1, 1, D, D)), "s0_c3": ("0.conv_3x3", (3, 3, D, D)),
+             "s1_dc": ("1.dconv_2x2", (2, 2, mid, E)), "s1_c1": ("1.conv_1x1", (1, 1, mid, D)),
+             "s1_c3": ("1.conv_3x3", (3, 3, D, D)), "s2_c1": ("2.conv_1x1", (1, 1, E, D)),
+             "s2_c3": ("2.conv_3x3", (3, 3, D, D)), "s3_c1": ("3.conv_1x1", (1, 1, E, D)),
+             "s3_c3": ("3.conv_3x3", (3, 3, D, D))}
+    for key, (n, shape) in names.items():
+        T.append((f"neck.det.{n}.weight", shape, gg.GGML_F32, f32(nw[key + "_w"]).tobytes()))
+        T.append((f"neck.det.{n}.bias", (shape[2] if "dconv" in n else shape[3],), gg.GGML_F32,
+                  f32(nw[key + "_b"]).tobytes()))
+    kv = [("general.architecture", gg.STRING, "sam3"), ("sam3.vision.image_size", gg.U32, img),
+          ("sam3.vision.patch_size", gg.U32, patch), ("sam3.vision.embedding_length", gg.U32, E),
+          ("sam3.vision.block_count", gg.U32, blocks), ("sam3.vision.attention.head_count", gg.U32, heads),
+          ("sam3.vision.feed_forward_length", gg.U32, mlp), ("sam3.vision.window_size", gg.U32, ws),
+          ("sam3.vision.global_attention_blocks", gg.ARRAY, (gg.U32, glob)),
+          ("sam3.neck.embedding_length", gg.U32, D)]
+    path = write(tmp_path, gg.gguf_bytes(kv, T))
+    image = f32(np.random.default_rng(22).standard_normal((3, img, img)))
+    host = {"img": img, "patch": patch, "E": E, "heads": heads, "mlp": mlp, "ws": ws, "D": D, "mid": mid,
+            "glob": glob, "G": G, "pg": pg, "kernel": kernel, "pos": pos, "lw": lw, "lb": lb, "blocks": bw,
+            "neck": nw}
+    return path, image, host
+
+
+def _row_rel(got, ref):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    return np.linalg.norm(got - ref, axis=1) / np.maximum(np.linalg.norm(ref, axis=1), 1e-30)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("columns", ["f32", "f16"])
+def test_image_encoder_from_checkpoint(tmp_path, oracle, columns):
+    """The image encoder wired from a converted checkpoint's tensors
+    (sam.cpp_amd/host/vision_encoder.hpp): its ViT output against the
+    oracle's prefix and blocks on the same weights (native Q8 linears:
+    median 2e-3, max 6e-3 per row over the two blocks, inside the one-block
+    bar of tests/test_gpu_vit.py; measured 6e-4 / 9e-4), and its neck levels
+    against the
+    oracle's neck applied to that same ViT output (F32 columns 5e-6; F16
+    columns median 3e-5, max 1e-3, as tests/test_gpu_neck.py)."""
+    path, image, h = _encoder_checkpoint(oracle, tmp_path)
+    image_path = str(tmp_path / "image.f32")
+    image.tofile(image_path)
+    prefix = str(tmp_path / "out")
+    print(f"image encoder from checkpoint ({columns} columns)", flush=True)
+    out = tool("encode", path, image_path, prefix, columns, timeout=120)
+    assert out.returncode == 0, out.stdout + out.stderr
+    res = json.loads(out.stdout)
+    G, E, D = h["G"], h["E"], h["D"]
+    assert res["grid"] == G and res["dim"] == D and res["levels"] == [4 * G, 2 * G, G, G // 2]
+    x = np.fromfile(prefix + ".features.f32", np.float32).reshape(G * G, E)
+    ref = oracle.vit_prefix(image, h["patch"], h["kernel"], h["pos"], h["pg"], h["lw"], h["lb"], E)
+    for i, w in enumerate(h["blocks"]):
+        ref = oracle.vit_block(w, ref, G, G, E, h["heads"], h["mlp"], 0 if i in h["glob"] else h["ws"])
+    rel = _row_rel(x, ref)
+    print(f"  ViT output: median {np.median(rel):.3g} max {rel.max():.3g}", flush=True)
+    assert np.median(rel) < 2e-3 and rel.max() < 6e-3
+    levels = oracle.neck(h["neck"], x, G, E, h["mid"], D, columns_f16=columns == "f16")
+    for i, lref in enumerate(levels):
+        got = np.fromfile(prefix + f".level{i}.f32", np.float32).reshape(-1, D)
+        rel = _row_rel(got, lref)
+        print(f"  level {i}: median {np.median(rel):.3g} max {rel.max():.3g}", flush=True)
+        if columns == "f32":
+            assert rel.max() < 5e-6, i
+        else:
+            assert np.median(rel) < (3e-5 if i < 2 else 2e-6) and rel.max() < 1e-3, i
+
+
+def test_image_encoder_parameters_rejected(tmp_path, oracle):
+    """VisionParameters checks the metadata before any device work: a
+    non-64 head width is refused with the reference's message family."""
+    path, image, h = _encoder_checkpoint(oracle, tmp_path)
+    data = open(path, "rb").read()
+    key = b"sam3.vision.attention.head_count"
+    at = data.index(key) + len(key) + 4        # u32 value type, then the value
+    bad = data[:at] + struct.pack("<I", 8) + data[at + 4:]
+    p2 = tmp_path / "bad.gguf"
+    p2.write_bytes(bad)
+    out = tool("encode", str(p2), str(tmp_path / "none.f32"), str(tmp_path / "o"))
+    assert out.returncode == 3 and "unsupported SAM 3 image encoder parameters" in out.stdout, out.stdout
