@@ -533,8 +533,9 @@ def encoder_cpu_baseline(enc, seconds_cap=60.0):
 
 def encoder_measure(sh, ctx, enc, warmup, iters):
     """ms/image of the image encode (prefix + 32 blocks + neck levels 0-2,
-    as the reference's image path runs it), its kernel breakdown, and
-    ms/image of the ViT alone (prefix + 32 blocks)."""
+    as the reference's image path runs it, F32-accurate attention), its
+    kernel breakdown, ms/image of the ViT alone (prefix + 32 blocks) and of
+    the encode with fp16 attention operands."""
     for _ in range(warmup):
         enc.forward()
     ctx.synchronize()
@@ -551,6 +552,18 @@ def encoder_measure(sh, ctx, enc, warmup, iters):
         enc.forward(neck=False)
     ctx.synchronize()
     enc.vit_ms = (time.perf_counter() - t0) * 1e3 / iters
+    # the same encode with fp16 attention operands (attention_type F16)
+    for d in enc.blocks:
+        d.attention_type = sh.F16
+    enc.forward()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        enc.forward()
+    ctx.synchronize()
+    enc.fp16_attention_ms = (time.perf_counter() - t0) * 1e3 / iters
+    for d in enc.blocks:
+        d.attention_type = sh.F32
     by = {}
     for name, wt, m, n, k, kms in prof:
         by.setdefault(name, []).append((m, n, k, kms))
@@ -579,6 +592,7 @@ def encoder_workload(args, sh, ctx):
                    "parallelism": "single-gpu"},
         "tflops_effective": round(enc.flops / (ms * 1e-3) / 1e12, 2),
         "vit_ms_per_image": round(enc.vit_ms, 3),
+        "fp16_attention_ms_per_image": round(enc.fp16_attention_ms, 3),
         "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(ach / PEAK_FP16_TFLOPS, 4), "traffic": None, "kernel": "vit_fc1 (fp16 GEMM + bias + GELU)",
                      "shape": {"M": m_, "N": n_, "K": k_}, "launch_ms": round(fc1_ms, 5)},
@@ -765,6 +779,7 @@ def main():
         result["vision_encoder"] = {
             "ms_per_image": round(enc_ms, 3), "images_per_s": round(1e3 / enc_ms, 2),
             "vit_ms_per_image": round(enc.vit_ms, 3),
+            "fp16_attention_ms_per_image": round(enc.fp16_attention_ms, 3),
             "tflops_effective": round(enc.flops / (enc_ms * 1e-3) / 1e12, 2),
             "config": "1008x1008x3 image, 72x72 tokens, width 1024, 32 blocks (window 24, global 7/15/23/31), "
                       "16 heads, MLP 4736; Q4_K qkv/proj/fc1, Q8_0 fc2; SimpleFPN neck levels 0-2 (F32 columns); "

@@ -196,6 +196,10 @@ typedef struct samhip_vit_block_desc {
     const float *qkv_b, *proj_b, *fc1_b, *fc2_b;      /* device F32 [N] */
     const float* freqs_cis;                           /* device F32 [tokens per window (or grid)][head_dim/2][2]
                                                          (cos, sin); NULL = no RoPE */
+    int32_t attention_type;                           /* SAMHIP_TYPE_F32 (0, default): F32-accurate attention, as
+                                                         the reference's GGML_PREC_F32 (src/runtime/ggml/
+                                                         graph.hpp:64), split fp16 operands at three times the
+                                                         MFMA work; SAMHIP_TYPE_F16: fp16 operands */
 } samhip_vit_block_desc;
 
 /* sam3_vit_block_forward (src/models/sam3/vision.hpp:152-243): x (device F32
@@ -255,7 +259,8 @@ int samhip_vit_neck(samhip_context* ctx, const samhip_vit_neck_desc* neck, const
  * n floats (n a multiple of 256, at most 2048; w, b may be NULL). */
 int samhip_layer_norm(samhip_context* ctx, const float* x, float* y, int64_t rows, int64_t n, const float* w,
                       const float* b, float eps);
-/* GGML_OP_FLASH_ATTN_EXT without mask (src/models/sam3/vision.hpp:214-218):
+/* GGML_OP_FLASH_ATTN_EXT without mask (src/models/sam3/vision.hpp:214-218),
+ * F32-accurate (GGML_PREC_F32):
  * per batch and head, out = softmax(scale * Q K^T) V over n tokens.  q, k, v
  * (device F32) rows b*n + t with stride ld floats, head h at columns
  * h*head_dim; out rows of heads*head_dim floats.  head_dim must be 64. */

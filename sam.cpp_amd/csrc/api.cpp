@@ -705,22 +705,26 @@ int samhip_flash_attn(samhip_context* ctx, const float* q, const float* k, const
         if (reinterpret_cast<uintptr_t>(p) % 16) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "flash_attn: 16-byte alignment");
     if (!std::isfinite(scale)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "flash_attn: scale");
     if (int rc = set_device(ctx)) return rc;
+    // F32-accurate, as the reference requests GGML_PREC_F32 for every
+    // FLASH_ATTN_EXT node (src/runtime/ggml/graph.hpp:64)
     const int64_t np = (n + 63) / 64 * 64;
     const size_t packed = size_t(batches) * heads * np * 64 * 2;
     Carve c;
-    const size_t oq = c.take(packed), ok = c.take(packed), ov = c.take(packed);
+    size_t off[6];
+    for (size_t& o : off) o = c.take(packed);
     if (int rc = ensure_work(ctx, c.used)) return rc;
     uint8_t* wb = static_cast<uint8_t*>(ctx->work);
-    _Float16 *qh = reinterpret_cast<_Float16*>(wb + oq), *kh = reinterpret_cast<_Float16*>(wb + ok),
-             *vt = reinterpret_cast<_Float16*>(wb + ov);
+    AttnOperands ops;
+    _Float16** parts[6] = {&ops.q, &ops.k, &ops.v, &ops.ql, &ops.kl, &ops.vl};
+    for (int i = 0; i < 6; ++i) *parts[i] = reinterpret_cast<_Float16*>(wb + off[i]);
     int rc = traced(ctx, "vit_pack_qkv", T_F32, batches * n, heads * 64, 0, [&]() -> int {
-        launch_pack_qkv(q, k, v, ld, nullptr, scale, qh, kh, vt, int(batches), heads, int(n), ctx->stream);
+        launch_pack_qkv(q, k, v, ld, nullptr, scale, ops, int(batches), heads, int(n), ctx->stream);
         HIP_TRY(hipGetLastError(), "pack launch");
         return SAMHIP_OK;
     });
     if (rc) return rc;
     return traced(ctx, "vit_attention", T_F32, batches * n, heads * 64, n, [&]() -> int {
-        launch_attention(qh, kh, vt, out, int64_t(heads) * 64, int(batches), heads, int(n), ctx->stream);
+        launch_attention(ops, out, int64_t(heads) * 64, int(batches), heads, int(n), ctx->stream);
         HIP_TRY(hipGetLastError(), "attention launch");
         return SAMHIP_OK;
     });
@@ -746,6 +750,9 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
         if (int rc = weight_check(*w.t, w.k, w.n, GW * GH, w.name)) return rc;
     if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(d->freqs_cis) % 16)
         return fail(SAMHIP_ERR_INVALID_ARGUMENT, "vit_block: x and freqs_cis must be 16-byte aligned");
+    if (d->attention_type != T_F32 && d->attention_type != T_F16)
+        return fail(SAMHIP_ERR_UNSUPPORTED, "vit_block: attention type must be F32 or F16");
+    const bool precise = d->attention_type == T_F32;
     if (int rc = set_device(ctx)) return rc;
 
     const int64_t T = GW * GH, per = WS > 0 ? WS * WS : T, B = T / per, np = (per + 63) / 64 * 64;
@@ -754,14 +761,16 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
     const size_t o_ln = c.take(size_t(T * E) * 4), o_x1 = c.take(size_t(T * E) * 4),
                  o_h1 = c.take(size_t(T * MLP) * 4);
     const size_t packed = size_t(B * H * np * 64) * 2;
-    const size_t o_qh = c.take(packed), o_kh = c.take(packed), o_vt = c.take(packed);
+    size_t o_ops[6];
+    for (int i = 0; i < (precise ? 6 : 3); ++i) o_ops[i] = c.take(packed);
     if (int rc = ensure_work(ctx, c.used)) return rc;
     uint8_t* wb = static_cast<uint8_t*>(ctx->work);
     float* ln = reinterpret_cast<float*>(wb + o_ln);
     float* x1 = reinterpret_cast<float*>(wb + o_x1);
     float* h1 = reinterpret_cast<float*>(wb + o_h1);
-    _Float16 *qh = reinterpret_cast<_Float16*>(wb + o_qh), *kh = reinterpret_cast<_Float16*>(wb + o_kh),
-             *vt = reinterpret_cast<_Float16*>(wb + o_vt);
+    AttnOperands ops;
+    _Float16** parts[6] = {&ops.q, &ops.k, &ops.v, &ops.ql, &ops.kl, &ops.vl};
+    for (int i = 0; i < (precise ? 6 : 3); ++i) *parts[i] = reinterpret_cast<_Float16*>(wb + o_ops[i]);
     const int iT = int(T);
 
     // attention half: LN1 folded into the qkv staging (rows leave in window
@@ -780,9 +789,12 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
     // attention operands (RoPE on q and k, q times 1/8)
     Epilogue e_qkv;
     e_qkv.bias = d->qkv_b;
-    e_qkv.pack[0] = qh;
-    e_qkv.pack[1] = kh;
-    e_qkv.pack[2] = vt;
+    e_qkv.pack[0] = ops.q;
+    e_qkv.pack[1] = ops.k;
+    e_qkv.pack[2] = ops.v;
+    e_qkv.pack_lo[0] = ops.ql;
+    e_qkv.pack_lo[1] = ops.kl;
+    e_qkv.pack_lo[2] = ops.vl;
     e_qkv.freqs = d->freqs_cis;
     e_qkv.embed = int(E);
     e_qkv.per = int(per);
@@ -793,14 +805,14 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
     if (rc) return rc;
     if (np != per) {
         rc = traced(ctx, "vit_zero_pad", T_F32, T, E, per, [&]() -> int {
-            launch_zero_pad(qh, kh, vt, int(B), int(H), int(per), ctx->stream);
+            launch_zero_pad(ops, int(B), int(H), int(per), ctx->stream);
             HIP_TRY(hipGetLastError(), "zero pad launch");
             return SAMHIP_OK;
         });
         if (rc) return rc;
     }
     rc = traced(ctx, "vit_attention", T_F32, T, E, per, [&]() -> int {
-        launch_attention(qh, kh, vt, ln, E, int(B), int(H), int(per), ctx->stream);
+        launch_attention(ops, ln, E, int(B), int(H), int(per), ctx->stream);
         HIP_TRY(hipGetLastError(), "attention launch");
         return SAMHIP_OK;
     });

@@ -44,7 +44,7 @@ __device__ __forceinline__ void tile_order(int bid, int nblocks, int tiles_m, in
 // in LDS at kernel start measured up to 35 % slower on the long-K shapes.)
 // Epilogue flags (EPI template bits) for Epilogue fields.
 constexpr int EPI_BIAS = 1, EPI_RES = 4, EPI_REMAP = 8, EPI_PACK = 16, EPI_COLSCALE = 32, EPI_SHUFFLE = 64,
-              EPI_GELU = 128;
+              EPI_GELU = 128, EPI_PACK_LO = 512;
 
 template <int FM, int FN, int ES>
 __device__ __forceinline__ void store_tile(floatx16 (&acc)[FM][FN], const float* row_scale, float* slab, int lane,
@@ -199,8 +199,12 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
 #pragma unroll
                     for (int q = 0; q < 4; ++q) v[q] = v[q] * ep.q_scale;
                 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-                *reinterpret_cast<half4_t*>(ep.pack[part] + dst[t] + head_off) =
-                    half4_t{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+                const half4_t hv{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+                *reinterpret_cast<half4_t*>(ep.pack[part] + dst[t] + head_off) = hv;
+                if ((EPI & EPI_PACK_LO) && ep.pack_lo[part])
+                    *reinterpret_cast<half4_t*>(ep.pack_lo[part] + dst[t] + head_off) =
+                        half4_t{(_Float16)(v[0] - (float)hv[0]), (_Float16)(v[1] - (float)hv[1]),
+                                (_Float16)(v[2] - (float)hv[2]), (_Float16)(v[3] - (float)hv[3])};
                 continue;
             }
             float* yp = Y + dst[t] * ldy + ycol;
@@ -807,7 +811,8 @@ bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16*
                 hipStream_t stream) {
     const int flags = (ep.bias ? EPI_BIAS : 0) | (ep.res ? EPI_RES : 0) | (ep.row_map ? EPI_REMAP : 0) |
                       (ep.pack[0] ? EPI_PACK : 0) | (ep.col_scale ? EPI_COLSCALE : 0) |
-                      (ep.shuffle_c > 0 ? EPI_SHUFFLE : 0) | (ep.gelu ? EPI_GELU : 0);
+                      (ep.shuffle_c > 0 ? EPI_SHUFFLE : 0) | (ep.gelu ? EPI_GELU : 0) |
+                      (ep.pack_lo[0] ? EPI_PACK_LO : 0);
 #define SAMHIP_EPI(E, AMODE)                                                                                     \
     launch_pipe<BM, BN, 64, 2, WM, WN, E, AMODE>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream, ep, op); \
     return true;
@@ -818,6 +823,7 @@ bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16*
             case EPI_BIAS: SAMHIP_EPI(EPI_BIAS, A_PLAIN)
             case EPI_BIAS | EPI_RES: SAMHIP_EPI(EPI_BIAS | EPI_RES, A_PLAIN)
             case EPI_BIAS | EPI_PACK: SAMHIP_EPI(EPI_BIAS | EPI_PACK, A_PLAIN)
+            case EPI_BIAS | EPI_PACK | EPI_PACK_LO: SAMHIP_EPI(EPI_BIAS | EPI_PACK | EPI_PACK_LO, A_PLAIN)
             case EPI_BIAS | EPI_RES | EPI_REMAP: SAMHIP_EPI(EPI_BIAS | EPI_RES | EPI_REMAP, A_PLAIN)
             case BC: SAMHIP_EPI(BC, A_PLAIN)
             default: return false;

@@ -45,6 +45,14 @@ const char* launch_gemm_f16(int cfg, const _Float16* a, int64_t lda, const float
 //   v = rs[m] * acc;  v += bias[n];  y[d] = res[d] + v
 // where d is the output row: m itself, or row_map[m] (the grid row that a
 // window-order row returns to, ggml_win_unpart).  res may alias y.
+// Per-head attention operands [B*H][Np][64] fp16 (hi), and for the
+// F32-accurate attention their remainders fp16(v - hi) (lo, all three;
+// else null).
+struct AttnOperands {
+    _Float16 *q = nullptr, *k = nullptr, *v = nullptr;
+    _Float16 *ql = nullptr, *kl = nullptr, *vl = nullptr;
+};
+
 struct Epilogue {
     const float* bias = nullptr;
     const float* res = nullptr;   // row stride = ldy
@@ -55,6 +63,7 @@ struct Epilogue {
     // d] in fp16, q and k rotated by freqs[t] (complex RoPE, products
     // rounded before the add), q multiplied by q_scale.
     _Float16* pack[3] = {nullptr, nullptr, nullptr};
+    _Float16* pack_lo[3] = {nullptr, nullptr, nullptr};   // with pack: fp16(v - fp16(v)) too
     const float* freqs = nullptr;
     int embed = 0, per = 0, np = 0, heads = 0;
     float q_scale = 1.f;
@@ -102,16 +111,18 @@ const char* launch_gemm_f16_epi(const _Float16* a, int64_t lda, const float* row
 void launch_layer_norm(const float* x, const float* add, int add_grid, int gw, int gh, int ws, const float* w,
                        const float* b, float eps, float* y, int rows, int E, hipStream_t stream);
 // q/k/v rows (row b*N + n, stride ld floats, head h at columns h*64) ->
-// Qh [B][H][Np][64] (RoPE, times q_scale), Kh (RoPE), Vh, fp16, Np = N
-// rounded up to 64 with zero padding; freqs (nullable): [N][32][2] (cos, sin).
+// per-head operands [B][H][Np][64] fp16: Q (RoPE, times q_scale), K (RoPE),
+// V, Np = N rounded up to 64 with zero padding; freqs (nullable):
+// [N][32][2] (cos, sin).  With the lo pointers set each value v is also
+// written as fp16(v - fp16(v)), for the F32-accurate attention.
 void launch_pack_qkv(const float* q, const float* k, const float* v, int64_t ld, const float* freqs, float q_scale,
-                     _Float16* qh, _Float16* kh, _Float16* vh, int B, int H, int N, hipStream_t stream);
-// Zero the padding rows [N, Np) of the three packed operands.
-void launch_zero_pad(_Float16* qh, _Float16* kh, _Float16* vh, int B, int H, int N, hipStream_t stream);
+                     const AttnOperands& o, int B, int H, int N, hipStream_t stream);
+// Zero the padding rows [N, Np) of the packed operands.
+void launch_zero_pad(const AttnOperands& o, int B, int H, int N, hipStream_t stream);
 // softmax(Q K^T) V per (batch, head) on the packed operands (head dim 64);
-// out row b*N + n, columns h*64.. (row stride ldo floats).
-void launch_attention(const _Float16* qh, const _Float16* kh, const _Float16* vt, float* out, int64_t ldo, int B,
-                      int H, int N, hipStream_t stream);
+// out row b*N + n, columns h*64.. (row stride ldo floats).  F32-accurate
+// (split operands, three products each) when o carries the lo parts.
+void launch_attention(const AttnOperands& o, float* out, int64_t ldo, int B, int H, int N, hipStream_t stream);
 // Patch convolution operands as split fp16: A [T][3*Kp] = [hi | hi | lo] of
 // the image patches, W [E][3*Kp] = [hi | lo | hi] of the kernel rows, so
 // A W^T = hi*hi + hi*lo + lo*hi (F32-accurate); Kp = 3*p*p rounded up to 128.

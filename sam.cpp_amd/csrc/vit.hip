@@ -99,8 +99,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float* __restrict
 __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                        const float* __restrict__ v, int64_t ld,
                                                        const float* __restrict__ freqs, float q_scale,
-                                                       _Float16* __restrict__ qh, _Float16* __restrict__ kh,
-                                                       _Float16* __restrict__ vh, int H, int N, int Np) {
+                                                       AttnOperands o_, int H, int N, int Np) {
     const int n0 = blockIdx.x * 64, h = blockIdx.y, b = blockIdx.z;
     const int t = threadIdx.x, tok = t >> 2, d0 = 16 * (t & 3);
     const int n = n0 + tok;
@@ -135,30 +134,43 @@ __global__ __launch_bounds__(256) void pack_qkv_kernel(const float* __restrict__
 #pragma unroll
             for (int j = 0; j < 16; ++j) xs[j] = 0.f;
         }
-        half8 lo, hi;
+        half8 h0, h1;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            lo[j] = (_Float16)xs[j];
-            hi[j] = (_Float16)xs[8 + j];
+            h0[j] = (_Float16)xs[j];
+            h1[j] = (_Float16)xs[8 + j];
         }
-        half8* o = reinterpret_cast<half8*>((which == 0 ? qh : which == 1 ? kh : vh) + dst);
-        o[0] = lo;
-        o[1] = hi;
+        half8* o = reinterpret_cast<half8*>((which == 0 ? o_.q : which == 1 ? o_.k : o_.v) + dst);
+        o[0] = h0;
+        o[1] = h1;
+        _Float16* lo = which == 0 ? o_.ql : which == 1 ? o_.kl : o_.vl;
+        if (lo) {   // remainders for the split products
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                h0[j] = (_Float16)(xs[j] - (float)h0[j]);
+                h1[j] = (_Float16)(xs[8 + j] - (float)h1[j]);
+            }
+            half8* ol = reinterpret_cast<half8*>(lo + dst);
+            ol[0] = h0;
+            ol[1] = h1;
+        }
     }
 }
 
 // Zero rows [N, Np) of packed operands [B*H][Np][64] (the padding of the
 // last key tile when the qkv product wrote the packed rows itself).
-__global__ __launch_bounds__(256) void zero_pad_kernel(_Float16* __restrict__ qh, _Float16* __restrict__ kh,
-                                                       _Float16* __restrict__ vh, int N, int Np) {
+__global__ __launch_bounds__(256) void zero_pad_kernel(AttnOperands o, int N, int Np) {
     const int64_t bh = blockIdx.y;
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;   // 8-half chunk of the pad rows
     if (i >= int64_t(Np - N) * 8) return;
     const int64_t off = (bh * Np + N) * 64 + 8 * i;
     const half8 z{0, 0, 0, 0, 0, 0, 0, 0};
-    *reinterpret_cast<half8*>(qh + off) = z;
-    *reinterpret_cast<half8*>(kh + off) = z;
-    *reinterpret_cast<half8*>(vh + off) = z;
+    *reinterpret_cast<half8*>(o.q + off) = z;
+    *reinterpret_cast<half8*>(o.k + off) = z;
+    *reinterpret_cast<half8*>(o.v + off) = z;
+    if (o.ql) *reinterpret_cast<half8*>(o.ql + off) = z;
+    if (o.kl) *reinterpret_cast<half8*>(o.kl + off) = z;
+    if (o.vl) *reinterpret_cast<half8*>(o.vl + off) = z;
 }
 
 // ---------------------------------------------------------------------------
@@ -170,42 +182,58 @@ __global__ __launch_bounds__(256) void zero_pad_kernel(_Float16* __restrict__ qh
 // l^32), and O^T = V^T P^T with P^T used as the B operand straight from the
 // S^T accumulator registers (the K index of both operands is the same
 // permutation of the tile's keys).
+// PRECISE: every operand is split, v = hi + lo (lo = fp16(v - hi)), and each
+// product sums hi*hi + lo*hi + hi*lo, with the weights P split the same way
+// in registers: the scores and the output carry ~22 bits, as the reference
+// computes attention in F32 (GGML_PREC_F32 on every FLASH_ATTN_EXT node,
+// src/runtime/ggml/graph.hpp:64), at three times the MFMA work.
 // ---------------------------------------------------------------------------
 constexpr int K_STRIDE = 72;   // halves per LDS key row (144 B: conflict-free 16-byte reads)
 constexpr int V_STRIDE = 68;   // halves per LDS d row (136 B: conflict-free 8-byte reads)
 constexpr float LOG2E = 1.44269504088896340736f;
 
-template <int QW>   // waves per workgroup, 32 queries each
-__global__ __launch_bounds__(64 * QW) void attention_kernel(const _Float16* __restrict__ qh, const _Float16* __restrict__ kh,
-                                                        const _Float16* __restrict__ vh, float* __restrict__ out,
-                                                        int64_t ldo, int H, int N, int Np) {
-    __shared__ __attribute__((aligned(16))) _Float16 ks[2][64 * K_STRIDE];
-    __shared__ __attribute__((aligned(16))) _Float16 vs[2][64 * V_STRIDE];
+// LEVEL 0: fp16 operands; 1: split scores; 2: split scores and output.
+template <int QW, int LEVEL>   // waves per workgroup (32 queries each), precision level
+__global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, float* __restrict__ out, int64_t ldo,
+                                                            int H, int N, int Np) {
+    constexpr bool PRECISE = LEVEL > 0;         // split scores
+    constexpr bool PRECISE_PV = LEVEL > 1;      // split weights and values too
+    constexpr int P = PRECISE ? 2 : 1;          // parts of Q and K: hi (and lo)
+    constexpr int PV = PRECISE_PV ? 2 : 1;      // parts of V
+    __shared__ __attribute__((aligned(16))) _Float16 ks[P][2][64 * K_STRIDE];
+    __shared__ __attribute__((aligned(16))) _Float16 vs[PV][2][64 * V_STRIDE];
     const int h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 31, hh = lane >> 5;
     const int64_t bh = int64_t(b) * H + h;
-    const _Float16* Q = qh + bh * Np * 64;
-    const _Float16* Kg = kh + bh * Np * 64;
-    const _Float16* Vg = vh + bh * Np * 64;
+    const _Float16* Qg[2] = {op.q + bh * Np * 64, PRECISE ? op.ql + bh * Np * 64 : nullptr};
+    const _Float16* Kg[2] = {op.k + bh * Np * 64, PRECISE ? op.kl + bh * Np * 64 : nullptr};
+    const _Float16* Vg[2] = {op.v + bh * Np * 64, PRECISE_PV ? op.vl + bh * Np * 64 : nullptr};
     const int q0 = blockIdx.x * (32 * QW) + wave * 32;
     const int qrow = min(q0 + li, Np - 1);
 
-    half8 qf[4];
+    half8 qf[P][4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const half8*>(Q + int64_t(qrow) * 64 + 16 * s + 8 * hh);
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            qf[p][s] = *reinterpret_cast<const half8*>(Qg[p] + int64_t(qrow) * 64 + 16 * s + 8 * hh);
 
     // tile loads: thread t moves 16-byte chunks t, t + 64*QW, ... of each
     // 512-chunk tile
     constexpr int NT = 64 * QW, LPT = (512 + NT - 1) / NT;
-    half8 kreg[LPT], vreg[LPT];
+    half8 kreg[P][LPT], vreg[PV][LPT];
     auto gload = [&](int kb) {
 #pragma unroll
         for (int i = 0; i < LPT; ++i) {
             const int idx = tid + NT * i, r = idx >> 3, c = idx & 7;
             if (512 % NT == 0 || idx < 512) {
-                kreg[i] = *reinterpret_cast<const half8*>(Kg + int64_t(kb * 64 + r) * 64 + 8 * c);
-                vreg[i] = *reinterpret_cast<const half8*>(Vg + int64_t(kb * 64 + r) * 64 + 8 * c);
+#pragma unroll
+                for (int p = 0; p < P; ++p)
+                    kreg[p][i] = *reinterpret_cast<const half8*>(Kg[p] + int64_t(kb * 64 + r) * 64 + 8 * c);
+#pragma unroll
+                for (int p = 0; p < PV; ++p)
+                    vreg[p][i] = *reinterpret_cast<const half8*>(Vg[p] + int64_t(kb * 64 + r) * 64 + 8 * c);
             }
         }
     };
@@ -214,10 +242,13 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(const _Float16* __re
         for (int i = 0; i < LPT; ++i) {
             const int idx = tid + NT * i, r = idx >> 3, c = idx & 7;
             if (512 % NT != 0 && idx >= 512) continue;
-            *reinterpret_cast<half8*>(&ks[buf][r * K_STRIDE + 8 * c]) = kreg[i];
+#pragma unroll
+            for (int p = 0; p < P; ++p) *reinterpret_cast<half8*>(&ks[p][buf][r * K_STRIDE + 8 * c]) = kreg[p][i];
             // key r, dims 8c..8c+7 -> column r of V^T rows 8c..8c+7
 #pragma unroll
-            for (int j = 0; j < 8; ++j) vs[buf][(8 * c + j) * V_STRIDE + r] = vreg[i][j];
+            for (int p = 0; p < PV; ++p)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) vs[p][buf][(8 * c + j) * V_STRIDE + r] = vreg[p][i][j];
         }
     };
 
@@ -233,16 +264,25 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(const _Float16* __re
     for (int kb = 0; kb < nkb; ++kb) {
         const int buf = kb & 1;
         if (kb + 1 < nkb) gload(kb + 1);
-        const _Float16* kt = ks[buf];
         floatx16 s0, s1;
 #pragma unroll
         for (int r = 0; r < 16; ++r) s0[r] = s1[r] = 0.f;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
+            const _Float16* kt = ks[0][buf];
             const half8 a0 = *reinterpret_cast<const half8*>(kt + li * K_STRIDE + 16 * s + 8 * hh);
             const half8 a1 = *reinterpret_cast<const half8*>(kt + (32 + li) * K_STRIDE + 16 * s + 8 * hh);
-            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qf[s], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qf[s], s1, 0, 0, 0);
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qf[0][s], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qf[0][s], s1, 0, 0, 0);
+            if (PRECISE) {
+                const _Float16* kl = ks[P - 1][buf];
+                const half8 l0 = *reinterpret_cast<const half8*>(kl + li * K_STRIDE + 16 * s + 8 * hh);
+                const half8 l1 = *reinterpret_cast<const half8*>(kl + (32 + li) * K_STRIDE + 16 * s + 8 * hh);
+                s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(l0, qf[0][s], s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(l1, qf[0][s], s1, 0, 0, 0);
+                s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qf[P - 1][s], s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qf[P - 1][s], s1, 0, 0, 0);
+            }
         }
         // keys past N (only in the last tile)
         const int kbase = kb * 64;
@@ -282,26 +322,45 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(const _Float16* __re
             ps += s0[r] + s1[r];
         }
         lsum = lsum + ps;
-        half8 pf[4];
+        half8 pf[PV][4];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            pf[0][j] = (_Float16)s0[j];
-            pf[1][j] = (_Float16)s0[8 + j];
-            pf[2][j] = (_Float16)s1[j];
-            pf[3][j] = (_Float16)s1[8 + j];
+            pf[0][0][j] = (_Float16)s0[j];
+            pf[0][1][j] = (_Float16)s0[8 + j];
+            pf[0][2][j] = (_Float16)s1[j];
+            pf[0][3][j] = (_Float16)s1[8 + j];
+            if (PRECISE_PV) {
+                pf[PV - 1][0][j] = (_Float16)(s0[j] - (float)pf[0][0][j]);
+                pf[PV - 1][1][j] = (_Float16)(s0[8 + j] - (float)pf[0][1][j]);
+                pf[PV - 1][2][j] = (_Float16)(s1[j] - (float)pf[0][2][j]);
+                pf[PV - 1][3][j] = (_Float16)(s1[8 + j] - (float)pf[0][3][j]);
+            }
         }
-        const _Float16* vtile = vs[buf];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        // V^T fragments of part p for 16-key step u
+        auto vfrag = [&](int p, int u, half8& a0, half8& a1) {
+            const _Float16* vtile = vs[p][buf];
             const int kofs = 32 * (u >> 1) + 16 * (u & 1) + 4 * hh;
             const half4 a_lo0 = *reinterpret_cast<const half4*>(vtile + li * V_STRIDE + kofs);
             const half4 a_hi0 = *reinterpret_cast<const half4*>(vtile + li * V_STRIDE + kofs + 8);
             const half4 a_lo1 = *reinterpret_cast<const half4*>(vtile + (32 + li) * V_STRIDE + kofs);
             const half4 a_hi1 = *reinterpret_cast<const half4*>(vtile + (32 + li) * V_STRIDE + kofs + 8);
-            const half8 a0 = __builtin_shufflevector(a_lo0, a_hi0, 0, 1, 2, 3, 4, 5, 6, 7);
-            const half8 a1 = __builtin_shufflevector(a_lo1, a_hi1, 0, 1, 2, 3, 4, 5, 6, 7);
-            o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, pf[u], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, pf[u], o1, 0, 0, 0);
+            a0 = __builtin_shufflevector(a_lo0, a_hi0, 0, 1, 2, 3, 4, 5, 6, 7);
+            a1 = __builtin_shufflevector(a_lo1, a_hi1, 0, 1, 2, 3, 4, 5, 6, 7);
+        };
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            half8 a0, a1;
+            vfrag(0, u, a0, a1);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, pf[0][u], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, pf[0][u], o1, 0, 0, 0);
+            if (PRECISE_PV) {
+                o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, pf[PV - 1][u], o0, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, pf[PV - 1][u], o1, 0, 0, 0);
+                half8 l0, l1;
+                vfrag(PV - 1, u, l0, l1);
+                o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(l0, pf[0][u], o0, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(l1, pf[0][u], o1, 0, 0, 0);
+            }
         }
         if (kb + 1 < nkb) {
             sstore(buf ^ 1);
@@ -386,28 +445,33 @@ void launch_layer_norm(const float* x, const float* add, int add_grid, int gw, i
 }
 
 void launch_pack_qkv(const float* q, const float* k, const float* v, int64_t ld, const float* freqs, float q_scale,
-                     _Float16* qh, _Float16* kh, _Float16* vh, int B, int H, int N, hipStream_t stream) {
+                     const AttnOperands& o, int B, int H, int N, hipStream_t stream) {
     const int np = (N + 63) / 64 * 64;
     hipLaunchKernelGGL(pack_qkv_kernel, dim3(unsigned(np / 64), unsigned(H), unsigned(B)), dim3(256), 0, stream, q, k,
-                       v, ld, freqs, q_scale, qh, kh, vh, H, N, np);
+                       v, ld, freqs, q_scale, o, H, N, np);
 }
 
-void launch_zero_pad(_Float16* qh, _Float16* kh, _Float16* vh, int B, int H, int N, hipStream_t stream) {
+void launch_zero_pad(const AttnOperands& o, int B, int H, int N, hipStream_t stream) {
     const int np = (N + 63) / 64 * 64;
     if (np == N) return;
     const int64_t chunks = int64_t(np - N) * 8;
-    hipLaunchKernelGGL(zero_pad_kernel, dim3(unsigned((chunks + 255) / 256), unsigned(B * H)), dim3(256), 0, stream,
-                       qh, kh, vh, N, np);
+    hipLaunchKernelGGL(zero_pad_kernel, dim3(unsigned((chunks + 255) / 256), unsigned(B * H)), dim3(256), 0, stream, o,
+                       N, np);
 }
 
-void launch_attention(const _Float16* qh, const _Float16* kh, const _Float16* vh, float* out, int64_t ldo, int B,
-                      int H, int N, hipStream_t stream) {
+void launch_attention(const AttnOperands& o, float* out, int64_t ldo, int B, int H, int N, hipStream_t stream) {
     const int np = (N + 63) / 64 * 64;
     // 128-query workgroups: measured on the SAM 3 shapes against 64, 96 and
     // 192 (windowed 34 / 42 / 35 / 41 us, global 206 / 294 / 213 / 267 us;
     // 96 tiles 576 and 5184 queries exactly and still loses)
-    hipLaunchKernelGGL(attention_kernel<4>, dim3(unsigned((np + 127) / 128), unsigned(H), unsigned(B)), dim3(256), 0,
-                       stream, qh, kh, vh, out, ldo, H, N, np);
+    const dim3 grid(unsigned((np + 127) / 128), unsigned(H), unsigned(B));
+    // (splitting the scores alone, level 1, measured 6e-4 relative error per
+    // output row at 2.8 ms per SAM 3 image against 5e-6 at 3.9 ms for level 2
+    // and 4e-3 at 1.9 ms for level 0)
+    if (o.ql && o.kl && o.vl)
+        hipLaunchKernelGGL((attention_kernel<4, 2>), grid, dim3(256), 0, stream, o, out, ldo, H, N, np);
+    else
+        hipLaunchKernelGGL((attention_kernel<4, 0>), grid, dim3(256), 0, stream, o, out, ldo, H, N, np);
 }
 
 void launch_patch_columns(const float* image, int img, int patch, _Float16* a, float* row_scale, int kp,

@@ -64,8 +64,11 @@ public:
     // `weights` must hold the vit.* and neck.det.* tensors: F32 norms, biases,
     // embeddings, RoPE tables and neck convolutions; packed Q8_0 / K-quant
     // linears.  They stay owned by `weights`, which must outlive this object.
+    // columns_type: the neck's 1x1/3x3 operands (F32-accurate or F16);
+    // attention_type: the ViT attention (F32-accurate, as the reference's
+    // GGML_PREC_F32, or fp16 operands).
     HipVisionEncoder(HipBackend& backend, const DeviceWeights& weights, VisionParameters params,
-                     int32_t columns_type = SAMHIP_TYPE_F32)
+                     int32_t columns_type = SAMHIP_TYPE_F32, int32_t attention_type = SAMHIP_TYPE_F32)
         : be_(&backend), p_(std::move(params)) {
         p_.validate();
         const int E = p_.embed, G = p_.grid(), pg = p_.pos_grid(), D = p_.neck_dim;
@@ -101,6 +104,7 @@ public:
             d.fc1_b = f32(weights, b + ".mlp.lin1.bias", {p_.mlp});
             d.fc2_w = linear(weights, b + ".mlp.lin2.weight", p_.mlp, E);
             d.fc2_b = f32(weights, b + ".mlp.lin2.bias", {E});
+            d.attention_type = attention_type;
             const int tokens = global ? G * G : p_.window * p_.window;
             d.freqs_cis = f32(weights, b + ".attn.freqs_cis", {2, 32, tokens});
             blocks_.push_back(d);

@@ -58,7 +58,8 @@ class VitBlockDesc(ctypes.Structure):
                 ("window", ctypes.c_int32)] + \
                [(n, ctypes.c_void_p) for n in ("norm1_w", "norm1_b", "norm2_w", "norm2_b")] + \
                [(n, Tensor) for n in ("qkv_w", "proj_w", "fc1_w", "fc2_w")] + \
-               [(n, ctypes.c_void_p) for n in ("qkv_b", "proj_b", "fc1_b", "fc2_b", "freqs_cis")]
+               [(n, ctypes.c_void_p) for n in ("qkv_b", "proj_b", "fc1_b", "fc2_b", "freqs_cis")] + \
+               [("attention_type", ctypes.c_int32)]
 
 
 NECK_SCALE_FIELDS = ("deconv1_w", "deconv1_b", "deconv2_w", "deconv2_b", "conv1x1_w", "conv1x1_b", "conv3x3_w",
@@ -373,12 +374,13 @@ class VitBlock:
     produced for the oracle: norm*_w/b, {qkv,proj,fc1,fc2}_{type,w,b},
     freqs) and its samhip_vit_block descriptor."""
 
-    def __init__(self, ctx, weights, embed, heads, mlp, grid_w, grid_h, window):
+    def __init__(self, ctx, weights, embed, heads, mlp, grid_w, grid_h, window, attention_type=F32):
         self.ctx = ctx
         self.buffers = {}
         d = VitBlockDesc()
         d.version = ABI_VERSION
         d.embed, d.heads, d.mlp, d.grid_w, d.grid_h, d.window = embed, heads, mlp, grid_w, grid_h, window
+        d.attention_type = attention_type
         for n in ("norm1_w", "norm1_b", "norm2_w", "norm2_b", "qkv_b", "proj_b", "fc1_b", "fc2_b"):
             self.buffers[n] = ctx.upload(np.ascontiguousarray(weights[n], np.float32))
             setattr(d, n, self.buffers[n].ptr)
