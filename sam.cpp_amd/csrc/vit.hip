@@ -174,9 +174,9 @@ __global__ __launch_bounds__(256) void zero_pad_kernel(AttnOperands o, int N, in
 }
 
 // ---------------------------------------------------------------------------
-// Attention.  Workgroup: 32 queries per wave, 4 or 6 waves, one (batch, head);
-// 64-key tiles of K [key][d] and V (stored [key][d], transposed on its way
-// into LDS as V^T [d][key]) double-buffered in LDS.
+// Attention.  Workgroup: 32 queries per wave, 4 waves, one (batch, head);
+// 64-key tiles of K and V, both [key][d], double-buffered in LDS; the
+// V^T fragments are read transposed (ds_read_b64_tr_b16).
 // Each wave computes S^T = K Q^T (lane: query l%32, 16 keys per 32-key
 // tile), so the softmax statistics of a query sit in one lane pair (l,
 // l^32), and O^T = V^T P^T with P^T used as the B operand straight from the
@@ -188,8 +188,19 @@ __global__ __launch_bounds__(256) void zero_pad_kernel(AttnOperands o, int N, in
 // computes attention in F32 (GGML_PREC_F32 on every FLASH_ATTN_EXT node,
 // src/runtime/ggml/graph.hpp:64), at three times the MFMA work.
 // ---------------------------------------------------------------------------
-constexpr int K_STRIDE = 72;   // halves per LDS key row (144 B: conflict-free 16-byte reads)
-constexpr int V_STRIDE = 68;   // halves per LDS d row (136 B: conflict-free 8-byte reads)
+constexpr int K_STRIDE = 72;   // halves per LDS key row of K and V (144 B: conflict-free 16-byte reads)
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives
+// element (i % 4) of the 8-byte rows that lanes 4j + i/4 address, j = 0..3
+// (lane layout measured on gfx950).  With lane r of a group addressing
+// V[key0 + r/4][d0 + 4 (r % 4)] of a key-major tile, lane i holds
+// V[key0 + j][d0 + i], j = 0..3: four consecutive keys of one column.
+__device__ __forceinline__ half4 ds_read_tr(const _Float16* p) {
+    const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)(p));
+    return __builtin_bit_cast(half4, v);
+}
 constexpr float LOG2E = 1.44269504088896340736f;
 
 // LEVEL 0: fp16 operands; 1: split scores; 2: split scores and output.
@@ -201,7 +212,7 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
     constexpr int P = PRECISE ? 2 : 1;          // parts of Q and K: hi (and lo)
     constexpr int PV = PRECISE_PV ? 2 : 1;      // parts of V
     __shared__ __attribute__((aligned(16))) _Float16 ks[P][2][64 * K_STRIDE];
-    __shared__ __attribute__((aligned(16))) _Float16 vs[PV][2][64 * V_STRIDE];
+    __shared__ __attribute__((aligned(16))) _Float16 vs[PV][2][64 * K_STRIDE];
     const int h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 31, hh = lane >> 5;
@@ -244,11 +255,8 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
             if (512 % NT != 0 && idx >= 512) continue;
 #pragma unroll
             for (int p = 0; p < P; ++p) *reinterpret_cast<half8*>(&ks[p][buf][r * K_STRIDE + 8 * c]) = kreg[p][i];
-            // key r, dims 8c..8c+7 -> column r of V^T rows 8c..8c+7
 #pragma unroll
-            for (int p = 0; p < PV; ++p)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) vs[p][buf][(8 * c + j) * V_STRIDE + r] = vreg[p][i][j];
+            for (int p = 0; p < PV; ++p) *reinterpret_cast<half8*>(&vs[p][buf][r * K_STRIDE + 8 * c]) = vreg[p][i];
         }
     };
 
@@ -336,14 +344,15 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
                 pf[PV - 1][3][j] = (_Float16)(s1[8 + j] - (float)pf[0][3][j]);
             }
         }
-        // V^T fragments of part p for 16-key step u
+        // V^T fragments of part p for 16-key step u (lane: dim l%32 of each
+        // 32-dim half, keys kofs + 0..3 and kofs + 8..11, the P^T order),
+        // read transposed out of the key-major tile
         auto vfrag = [&](int p, int u, half8& a0, half8& a1) {
-            const _Float16* vtile = vs[p][buf];
             const int kofs = 32 * (u >> 1) + 16 * (u & 1) + 4 * hh;
-            const half4 a_lo0 = *reinterpret_cast<const half4*>(vtile + li * V_STRIDE + kofs);
-            const half4 a_hi0 = *reinterpret_cast<const half4*>(vtile + li * V_STRIDE + kofs + 8);
-            const half4 a_lo1 = *reinterpret_cast<const half4*>(vtile + (32 + li) * V_STRIDE + kofs);
-            const half4 a_hi1 = *reinterpret_cast<const half4*>(vtile + (32 + li) * V_STRIDE + kofs + 8);
+            const _Float16* at = vs[p][buf] + (kofs + ((lane & 15) >> 2)) * K_STRIDE + 16 * ((lane >> 4) & 1) +
+                                 4 * (lane & 3);
+            const half4 a_lo0 = ds_read_tr(at), a_hi0 = ds_read_tr(at + 8 * K_STRIDE);
+            const half4 a_lo1 = ds_read_tr(at + 32), a_hi1 = ds_read_tr(at + 8 * K_STRIDE + 32);
             a0 = __builtin_shufflevector(a_lo0, a_hi0, 0, 1, 2, 3, 4, 5, 6, 7);
             a1 = __builtin_shufflevector(a_lo1, a_hi1, 0, 1, 2, 3, 4, 5, 6, 7);
         };
