@@ -188,7 +188,10 @@ __global__ __launch_bounds__(256) void zero_pad_kernel(AttnOperands o, int N, in
 // computes attention in F32 (GGML_PREC_F32 on every FLASH_ATTN_EXT node,
 // src/runtime/ggml/graph.hpp:64), at three times the MFMA work.
 // ---------------------------------------------------------------------------
-constexpr int K_STRIDE = 72;   // halves per LDS key row of K and V (144 B: conflict-free 16-byte reads)
+constexpr int RSRC_WORD3 = 0x00020000;   // raw buffer, 32-bit data format
+
+// s_waitcnt vmcnt(0), expcnt/lgkmcnt left at their maximum (gfx9 encoding)
+__device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x70 | 0xF00); }
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
@@ -197,7 +200,7 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 // (lane layout measured on gfx950).  With lane r of a group addressing
 // V[key0 + r/4][d0 + 4 (r % 4)] of a key-major tile, lane i holds
 // V[key0 + j][d0 + i], j = 0..3: four consecutive keys of one column.
-__device__ __forceinline__ half4 ds_read_tr(const _Float16* p) {
+__device__ __forceinline__ half4 ds_read_tr(const uint8_t* p) {
     const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)(p));
     return __builtin_bit_cast(half4, v);
 }
@@ -207,19 +210,20 @@ constexpr float LOG2E = 1.44269504088896340736f;
 template <int QW, int LEVEL>   // waves per workgroup (32 queries each), precision level
 __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, float* __restrict__ out, int64_t ldo,
                                                             int H, int N, int Np) {
+#if defined(__HIP_DEVICE_COMPILE__)   // LDS-DMA builtins exist only in the device pass
     constexpr bool PRECISE = LEVEL > 0;         // split scores
     constexpr bool PRECISE_PV = LEVEL > 1;      // split weights and values too
     constexpr int P = PRECISE ? 2 : 1;          // parts of Q and K: hi (and lo)
     constexpr int PV = PRECISE_PV ? 2 : 1;      // parts of V
-    __shared__ __attribute__((aligned(16))) _Float16 ks[P][2][64 * K_STRIDE];
-    __shared__ __attribute__((aligned(16))) _Float16 vs[PV][2][64 * K_STRIDE];
+    static_assert(QW == 4, "the tile loads assume 4 waves");
+    constexpr int TB = 64 * 128;   // bytes of one 64-key tile of one part
+    __shared__ __attribute__((aligned(1024))) uint8_t ktile[P][2][TB];
+    __shared__ __attribute__((aligned(1024))) uint8_t vtile[PV][2][TB];
     const int h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 31, hh = lane >> 5;
     const int64_t bh = int64_t(b) * H + h;
     const _Float16* Qg[2] = {op.q + bh * Np * 64, PRECISE ? op.ql + bh * Np * 64 : nullptr};
-    const _Float16* Kg[2] = {op.k + bh * Np * 64, PRECISE ? op.kl + bh * Np * 64 : nullptr};
-    const _Float16* Vg[2] = {op.v + bh * Np * 64, PRECISE_PV ? op.vl + bh * Np * 64 : nullptr};
     const int q0 = blockIdx.x * (32 * QW) + wave * 32;
     const int qrow = min(q0 + li, Np - 1);
 
@@ -230,33 +234,40 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
         for (int s = 0; s < 4; ++s)
             qf[p][s] = *reinterpret_cast<const half8*>(Qg[p] + int64_t(qrow) * 64 + 16 * s + 8 * hh);
 
-    // tile loads: thread t moves 16-byte chunks t, t + 64*QW, ... of each
-    // 512-chunk tile
-    constexpr int NT = 64 * QW, LPT = (512 + NT - 1) / NT;
-    half8 kreg[P][LPT], vreg[PV][LPT];
-    auto gload = [&](int kb) {
+    // K and V tiles go straight from HBM into LDS (buffer_load ... lds): a
+    // tile's 512 16-byte chunks, two per lane; the chunk landing in slot c of
+    // row r is the row's chunk c ^ (r & 7), so that the fragment reads of 32
+    // rows at one column spread over the banks.
+    const uint32_t bytes = uint32_t(Np) * 128;
+    __amdgpu_buffer_rsrc_t kr[P], vr[PV];
 #pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int idx = tid + NT * i, r = idx >> 3, c = idx & 7;
-            if (512 % NT == 0 || idx < 512) {
+    for (int p = 0; p < P; ++p)
+        kr[p] = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>((p ? op.kl : op.k) + bh * Np * 64), 0, bytes,
+                                                  RSRC_WORD3);
 #pragma unroll
-                for (int p = 0; p < P; ++p)
-                    kreg[p][i] = *reinterpret_cast<const half8*>(Kg[p] + int64_t(kb * 64 + r) * 64 + 8 * c);
+    for (int p = 0; p < PV; ++p)
+        vr[p] = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>((p ? op.vl : op.v) + bh * Np * 64), 0, bytes,
+                                                  RSRC_WORD3);
+    uint32_t goff[2];
 #pragma unroll
-                for (int p = 0; p < PV; ++p)
-                    vreg[p][i] = *reinterpret_cast<const half8*>(Vg[p] + int64_t(kb * 64 + r) * 64 + 8 * c);
-            }
-        }
-    };
-    auto sstore = [&](int buf) {
+    for (int i = 0; i < 2; ++i) {
+        const int id = wave * 128 + i * 64 + lane, r = id >> 3, c = id & 7;
+        goff[i] = uint32_t(r * 128 + ((c ^ (r & 7)) << 4));
+    }
+    auto issue = [&](int kb, int buf) {
+        const int koff = kb * TB;
 #pragma unroll
-        for (int i = 0; i < LPT; ++i) {
-            const int idx = tid + NT * i, r = idx >> 3, c = idx & 7;
-            if (512 % NT != 0 && idx >= 512) continue;
+        for (int i = 0; i < 2; ++i) {
 #pragma unroll
-            for (int p = 0; p < P; ++p) *reinterpret_cast<half8*>(&ks[p][buf][r * K_STRIDE + 8 * c]) = kreg[p][i];
+            for (int p = 0; p < P; ++p)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    kr[p], (__attribute__((address_space(3))) void*)(ktile[p][buf] + (wave * 128 + i * 64) * 16), 16,
+                    goff[i], koff, 0, 0);
 #pragma unroll
-            for (int p = 0; p < PV; ++p) *reinterpret_cast<half8*>(&vs[p][buf][r * K_STRIDE + 8 * c]) = vreg[p][i];
+            for (int p = 0; p < PV; ++p)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    vr[p], (__attribute__((address_space(3))) void*)(vtile[p][buf] + (wave * 128 + i * 64) * 16), 16,
+                    goff[i], koff, 0, 0);
         }
     };
 
@@ -266,26 +277,28 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
     float mrun = -__builtin_inff(), lsum = 0.f;
     const int nkb = Np / 64;
 
-    gload(0);
-    sstore(0);
+    issue(0, 0);
+    wait_vmcnt0();
     __syncthreads();
     for (int kb = 0; kb < nkb; ++kb) {
         const int buf = kb & 1;
-        if (kb + 1 < nkb) gload(kb + 1);
+        if (kb + 1 < nkb) issue(kb + 1, buf ^ 1);   // that buffer's reads ended at the last barrier
         floatx16 s0, s1;
 #pragma unroll
         for (int r = 0; r < 16; ++r) s0[r] = s1[r] = 0.f;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-            const _Float16* kt = ks[0][buf];
-            const half8 a0 = *reinterpret_cast<const half8*>(kt + li * K_STRIDE + 16 * s + 8 * hh);
-            const half8 a1 = *reinterpret_cast<const half8*>(kt + (32 + li) * K_STRIDE + 16 * s + 8 * hh);
+            // rows li and 32 + li, chunk 2s + hh (same swizzle: (32 + li) & 7 == li & 7)
+            const int kofs0 = li * 128 + (((2 * s + hh) ^ (li & 7)) << 4);
+            const uint8_t* kt = ktile[0][buf];
+            const half8 a0 = *reinterpret_cast<const half8*>(kt + kofs0);
+            const half8 a1 = *reinterpret_cast<const half8*>(kt + kofs0 + 32 * 128);
             s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qf[0][s], s0, 0, 0, 0);
             s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, qf[0][s], s1, 0, 0, 0);
             if (PRECISE) {
-                const _Float16* kl = ks[P - 1][buf];
-                const half8 l0 = *reinterpret_cast<const half8*>(kl + li * K_STRIDE + 16 * s + 8 * hh);
-                const half8 l1 = *reinterpret_cast<const half8*>(kl + (32 + li) * K_STRIDE + 16 * s + 8 * hh);
+                const uint8_t* kl = ktile[P - 1][buf];
+                const half8 l0 = *reinterpret_cast<const half8*>(kl + kofs0);
+                const half8 l1 = *reinterpret_cast<const half8*>(kl + kofs0 + 32 * 128);
                 s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(l0, qf[0][s], s0, 0, 0, 0);
                 s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(l1, qf[0][s], s1, 0, 0, 0);
                 s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, qf[P - 1][s], s0, 0, 0, 0);
@@ -348,11 +361,13 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
         // 32-dim half, keys kofs + 0..3 and kofs + 8..11, the P^T order),
         // read transposed out of the key-major tile
         auto vfrag = [&](int p, int u, half8& a0, half8& a1) {
-            const int kofs = 32 * (u >> 1) + 16 * (u & 1) + 4 * hh;
-            const _Float16* at = vs[p][buf] + (kofs + ((lane & 15) >> 2)) * K_STRIDE + 16 * ((lane >> 4) & 1) +
-                                 4 * (lane & 3);
-            const half4 a_lo0 = ds_read_tr(at), a_hi0 = ds_read_tr(at + 8 * K_STRIDE);
-            const half4 a_lo1 = ds_read_tr(at + 32), a_hi1 = ds_read_tr(at + 8 * K_STRIDE + 32);
+            const int row = 32 * (u >> 1) + 16 * (u & 1) + 4 * hh + ((lane & 15) >> 2);
+            const int cg = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1), sw = row & 7;   // rows row, row + 8 alike
+            const uint8_t* at = vtile[p][buf] + row * 128 + 8 * (lane & 1);
+            const half4 a_lo0 = ds_read_tr(at + ((cg ^ sw) << 4));
+            const half4 a_hi0 = ds_read_tr(at + 8 * 128 + ((cg ^ sw) << 4));
+            const half4 a_lo1 = ds_read_tr(at + (((cg + 4) ^ sw) << 4));
+            const half4 a_hi1 = ds_read_tr(at + 8 * 128 + (((cg + 4) ^ sw) << 4));
             a0 = __builtin_shufflevector(a_lo0, a_hi0, 0, 1, 2, 3, 4, 5, 6, 7);
             a1 = __builtin_shufflevector(a_lo1, a_hi1, 0, 1, 2, 3, 4, 5, 6, 7);
         };
@@ -372,7 +387,7 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
             }
         }
         if (kb + 1 < nkb) {
-            sstore(buf ^ 1);
+            wait_vmcnt0();   // this wave's loads of the next tile landed
             __syncthreads();
         }
     }
@@ -389,6 +404,7 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
                 floatx4{o1[4 * g] * inv, o1[4 * g + 1] * inv, o1[4 * g + 2] * inv, o1[4 * g + 3] * inv};
         }
     }
+#endif
 }
 
 // ---------------------------------------------------------------------------
