@@ -74,6 +74,7 @@ struct samhip_context {
     int tall_m = 256;
     int gemm_cfg = -1;
     bool fused_skinny = true;   // SAMHIP_FUSED_SKINNY=0 routes M <= 128 through staging + the skinny kernel
+    int strip_skinny = 1;       // SAMHIP_STRIP_SKINNY: 0 never, 1 where preferred, 2 every M <= 32 product
     int fused_max_splits = 16;  // SAMHIP_FUSED_MAX_SPLITS: cap on the fused kernel's K splits
     samhip_exec_info info{};
     // per-launch event trace (samhip_trace_begin / samhip_trace_end)
@@ -269,6 +270,7 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
     // kernel-variant forcing for tuning runs (SAMHIP_* environment variables)
     ctx->tall_m = std::max(1, env_int("SAMHIP_TALL_M", ctx->tall_m));
     ctx->fused_skinny = env_int("SAMHIP_FUSED_SKINNY", 1) != 0;
+    ctx->strip_skinny = env_int("SAMHIP_STRIP_SKINNY", 1);
     ctx->fused_max_splits = std::max(1, env_int("SAMHIP_FUSED_MAX_SPLITS", 16));
     const int cfg = env_int("SAMHIP_GEMM_CONFIG", -1);
     ctx->gemm_cfg = (cfg >= 0 && cfg < gemm_f16_config_count()) ? cfg : -1;
@@ -363,6 +365,28 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     const int K = int(w->ne[0]), N = int(w->ne[1]), M = int(x->ne[1]);
     if (int rc = set_device(ctx)) return rc;
     const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K);
+    if (!tall && M <= kStripMaxM && ctx->fused_skinny && ctx->strip_skinny &&
+        (ctx->strip_skinny == 2 || strip_skinny_preferred(w->type, K))) {
+        // one launch per product (and a reduce when K > 1024): activation
+        // packing in registers, weight decode and product
+        const FusedPlan plan = strip_skinny_plan(M, N, K);
+        if (int rc = ensure_staging(ctx, std::max<size_t>(plan.part_bytes, 256))) return rc;
+        const char* variant = strip_skinny_variant(w->type);
+        if (!variant) return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no kernel for weight type %d", w->type);
+        int rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
+            launch_strip_skinny(w->type, ctx->compute == SAMHIP_COMPUTE_F16, static_cast<const float*>(x->data),
+                                int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
+                                int64_t(y->nb[1] / 4), static_cast<float*>(ctx->staging), M, N, K,
+                                ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->stream);
+            HIP_TRY(hipGetLastError(), "strip skinny launch");
+            return SAMHIP_OK;
+        });
+        if (rc) return rc;
+        ctx->info.mul_mat_calls++;
+        ctx->info.skinny_launches++;
+        std::snprintf(ctx->info.kernel_variant, sizeof(ctx->info.kernel_variant), "%s", variant);
+        return SAMHIP_OK;
+    }
     if (!tall && M <= kFusedMaxM && ctx->fused_skinny) {
         // one launch: activation packing, weight decode and product
         const FusedPlan plan = fused_skinny_plan(M, N, K, ctx->fused_max_splits);

@@ -207,24 +207,10 @@ __global__ __launch_bounds__(512) void fused_skinny_kernel(const float* __restri
         const int cb = WT == T_Q8_0 ? 34 * steps : CB;
         const int64_t off = int64_t(c) * CB;
 
-        // 1. packed weight bytes: each wave copies 16 rows of its tile with
-        //    coalesced dword loads (two rows per pass), and the first
-        //    activation rows are issued before any wait
-        constexpr int DPR = (CB + 2 + 3) / 4;   // dwords a row can span
-        constexpr int RI = (DPR + 31) / 32;
-        uint32_t wreg[8][RI];
-#pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            const int r = 16 * kh + 2 * p + h;
-            const uintptr_t g = reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + r, N - 1)) * w_stride + off);
-            const uint32_t* src = reinterpret_cast<const uint32_t*>(g & ~uintptr_t(3));
-            const int ndw = int(((g & 3) + cb + 3) >> 2);
-#pragma unroll
-            for (int q = 0; q < RI; ++q) {
-                const int d = col + 32 * q;
-                wreg[p][q] = d < ndw ? src[d] : 0u;
-            }
-        }
+        // 1. the activation rows are requested first (loads return in issue
+        //    order, so they are packed while the weights are in flight),
+        //    then the packed weight bytes: each wave copies 16 rows of its
+        //    tile with coalesced dword loads (two rows per pass)
         auto load_x = [&](int pass) -> floatx8 {
             const int r = pass * 16 + wave * 2 + h;
             const int k = kc + 8 * col;
@@ -244,13 +230,21 @@ __global__ __launch_bounds__(512) void fused_skinny_kernel(const float* __restri
         floatx8 xv[2 * MT];
 #pragma unroll
         for (int p = 0; p < 2 * MT; ++p) xv[p] = load_x(p);
+        constexpr int DPR = (CB + 2 + 3) / 4;   // dwords a row can span
+        constexpr int RI = (DPR + 31) / 32;
+        uint32_t wreg[8][RI];
 #pragma unroll
-        for (int p = 0; p < 8; ++p)
+        for (int p = 0; p < 8; ++p) {
+            const int r = 16 * kh + 2 * p + h;
+            const uintptr_t g = reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + r, N - 1)) * w_stride + off);
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(g & ~uintptr_t(3));
+            const int ndw = int(((g & 3) + cb + 3) >> 2);
 #pragma unroll
             for (int q = 0; q < RI; ++q) {
                 const int d = col + 32 * q;
-                if (d < WDW) Ws[tile][(16 * kh + 2 * p + h) * WDW + d] = wreg[p][q];
+                wreg[p][q] = d < ndw ? src[d] : 0u;
             }
+        }
 
         // 2. activation chunk -> fp16 operand (two rows per wave per pass)
 #pragma unroll
@@ -265,6 +259,13 @@ __global__ __launch_bounds__(512) void fused_skinny_kernel(const float* __restri
             *reinterpret_cast<half8*>(&As[r * ALD + 8 * col]) = o;
             if (col == 0) escale[r] = exp2i(e);
         }
+#pragma unroll
+        for (int p = 0; p < 8; ++p)
+#pragma unroll
+            for (int q = 0; q < RI; ++q) {
+                const int d = col + 32 * q;
+                if (d < WDW) Ws[tile][(16 * kh + 2 * p + h) * WDW + d] = wreg[p][q];
+            }
         __syncthreads();
 
         // 3. products of this wave's K steps of the chunk
@@ -328,7 +329,9 @@ __global__ __launch_bounds__(512) void fused_skinny_kernel(const float* __restri
         }
 }
 
-// Y[m][n] = sum over q = 0 .. S-1 of part[q][m][n], in that order.
+// Y[m][n] = sum over q = 0 .. S-1 of part[q][m][n], in that order.  Up to
+// 16 partials are loaded at once (one memory latency instead of S: the
+// loads are issued before the first add).
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, float* __restrict__ Y,
                                                             int64_t ldy, int M, int N, int S) {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
@@ -336,16 +339,238 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     const int m = int(i / N), n = int(i % N);
     const int64_t plane = int64_t(M) * N;
     float v = 0.f;
-    int q = 0;
-    for (; q + 8 <= S; q += 8) {   // eight independent loads in flight, added in split order
-        float t[8];
+    for (int q = 0; q < S; q += 16) {
+        float t[16];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) t[j] = part[(q + j) * plane + i];
+        for (int j = 0; j < 16; ++j) t[j] = q + j < S ? part[(q + j) * plane + i] : 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v += t[j];
+        for (int j = 0; j < 16; ++j)
+            if (q + j < S) v += t[j];
     }
-    for (; q < S; ++q) v += part[q * plane + i];
     Y[int64_t(m) * ldy + n] = v;
+}
+
+// ---------------------------------------------------------------------------
+// Strip path for M <= 32 (the text encoder's 32 tokens): one workgroup per
+// 32-row strip of W and group of four 256-wide K chunks; 16 waves, wave w
+// taking two 32-wide steps (quarter w % 4) of chunk w / 4.  A lane holds
+// the 16 activations of one row that its A fragments need (row l % 32,
+// values 16 (l / 32) .. +15 of each step), so the Q8 blocks are formed in
+// registers (Q8_0: one exchange between lanes l and l ^ 32 per block; Q8_K:
+// the four quarters' maxima meet in LDS), and the weights are decoded from
+// the lane's own loads: no LDS staging before the products.  Activations
+// are requested before weights (loads return in issue order), so packing
+// runs while the weights are in flight.  The 16 partial tiles meet in LDS
+// and are added in a fixed order; with more than four chunks the groups go
+// to `part` and splitk_reduce_kernel adds them.  Every workgroup packs the
+// activations it uses: VALU time per workgroup in place of a second launch
+// and a round trip of partial sums through memory.
+// ---------------------------------------------------------------------------
+
+// The Q8 codes and block scale of a lane's 2 steps x 16 activations.
+template <int MODE, bool X86>
+__device__ __forceinline__ void strip_q8_0(const floatx4 (&xv)[2][4], float (&d)[2], float (&q)[2][16],
+                                           float& rmax) {
+#pragma clang fp contract(off)
+    rmax = 0.f;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(xv[s][i >> 2][i & 3]));
+        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+        rmax = fmaxf(rmax, amax);
+        const float dd = amax / 127.f;
+        float inv;
+        if (X86) inv = amax != 0.f ? 127.f / amax : 0.f;
+        else inv = dd != 0.f ? 1.f / dd : 0.f;
+        d[s] = half_bits_to_float(float_to_half_bits(dd));   // stored fp16 scale
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float t = xv[s][i >> 2][i & 3] * inv;
+            q[s][i] = X86 ? __builtin_rintf(t) : __builtin_roundf(t);
+        }
+    }
+}
+
+template <int WT, int MODE, bool X86, bool XVEC>
+__global__ __launch_bounds__(1024) void strip_skinny_kernel(const float* __restrict__ X, int64_t ldx,
+                                                            const uint8_t* __restrict__ W, int64_t w_stride,
+                                                            float* __restrict__ Y, int64_t ldy,
+                                                            float* __restrict__ part, int M, int N, int K, int RG) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) float red[16][16 * 64];   // the waves' partial tiles
+    __shared__ __attribute__((aligned(16))) float escale[16][32];     // 2^e per wave and row
+    __shared__ float cand_a[16][32], cand_s[16][32];                  // Q8_K: quarter maxima per row
+    __shared__ int cand_i[16][32];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 31, h = lane >> 5;
+    const int rg = blockIdx.x % RG, sp = blockIdx.x / RG;
+    const int n0 = rg * 32;
+    const int nchunks = (K + 255) / 256;
+    const int c = 4 * sp + (wave >> 2), s0 = 2 * (wave & 3);
+    const bool active = c < nchunks;
+    const int kc = 256 * min(c, nchunks - 1);
+    const int steps = min(8, (K - kc) / 32);
+
+    // activations first: row `col` (clamped in bounds, zeroed past M); steps
+    // past the chunk's end repeat its last step and are zeroed
+    const bool live = col < M && active;
+    const float* xr = X + int64_t(col < M ? col : 0) * ldx + kc + 16 * h;
+    floatx4 xv[2][4];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const float* xs = xr + 32 * min(s0 + s, steps - 1);
+        const bool use = live && s0 + s < steps;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            floatx4 v;
+            if (XVEC) {
+                v = load4f(xs + 4 * j);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = xs[4 * j + i];
+            }
+            xv[s][j] = use ? v : floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    // this lane's weight pieces (row n0 + col clamped in bounds)
+    const uint8_t* wr = W + int64_t(min(n0 + col, N - 1)) * w_stride;
+    const int st0 = kc / 32 + min(s0, steps - 1), st1 = kc / 32 + min(s0 + 1, steps - 1);
+    WeightPiece<WT> wp0, wp1;
+    wp0.load(wr, st0, h);
+    wp1.load(wr, st1, h);
+
+    // the fp16 operand: fp16(d * q * 2^-e), or fp16(x * 2^-e) in F16 mode
+    half8 alo[2], ahi[2];
+    float rmax = 0.f, dk[2] = {0.f, 0.f}, q[2][16];
+    if (MODE == T_Q8_0) {
+        strip_q8_0<MODE, X86>(xv, dk, q, rmax);
+    } else if (MODE == T_Q8_K) {
+        // the first element of largest magnitude of the 256-value block
+        // (value index 32 s + 16 h + i of the chunk)
+        float la = 0.f, ls = 0.f;
+        int li = 1 << 20;
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float v = xv[s][i >> 2][i & 3], t = fabsf(v);
+                if (t > la) { la = t; ls = v; li = 32 * (s0 + s) + 16 * h + i; }
+            }
+        const float pa = __shfl_xor(la, 32, 64), ps = __shfl_xor(ls, 32, 64);
+        const int pi = __shfl_xor(li, 32, 64);
+        if (pa > la || (pa == la && pi < li)) { la = pa; ls = ps; li = pi; }
+        if (h == 0) {
+            cand_a[wave][col] = la;
+            cand_s[wave][col] = ls;
+            cand_i[wave][col] = li;
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) rmax = fmaxf(rmax, fabsf(xv[s][i >> 2][i & 3]));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+    }
+    if (MODE == T_Q8_K) {
+        __syncthreads();
+        const int g = wave & ~3;   // the chunk's four quarters, in value order
+        float la = cand_a[g][col], ls = cand_s[g][col];
+        int li = cand_i[g][col];
+#pragma unroll
+        for (int t = 1; t < 4; ++t) {
+            const float a = cand_a[g + t][col];
+            const int i = cand_i[g + t][col];
+            if (a > la || (a == la && i < li)) { la = a; ls = cand_s[g + t][col]; li = i; }
+        }
+        rmax = la;
+        if (la != 0.f) {
+            const float iscale = -127.f / ls;
+            dk[0] = dk[1] = 1.f / iscale;
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) q[s][i] = fminf(127.f, __builtin_rintf(iscale * xv[s][i >> 2][i & 3]));
+        } else {
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) q[s][i] = 0.f;
+        }
+    }
+    const int e = row_exponent(rmax);
+    const float down = exp2i(-e);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (MODE == T_F16) {
+                alo[s][i] = (_Float16)(xv[s][i >> 2][i & 3] * down);
+                ahi[s][i] = (_Float16)(xv[s][2 + (i >> 2)][i & 3] * down);
+            } else {
+                // d * q is exact in F32 for Q8_0 (11 x 8 bits); for Q8_K the
+                // one rounding of (d * 2^-e) * q equals that of d * q
+                const float sd = dk[s] * down;
+                alo[s][i] = (_Float16)(q[s][i] * sd);
+                ahi[s][i] = (_Float16)(q[s][8 + i] * sd);
+            }
+        }
+    if (h == 0) escale[wave][col] = exp2i(e);
+
+    floatx16 a0, a1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) a0[r] = a1[r] = 0.f;
+    {
+        _Float16 wv[16];
+        wp0.dequant(st0, h, wv);
+        a0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[0], (half8{wv[0], wv[1], wv[2], wv[3], wv[4], wv[5], wv[6], wv[7]}), a0, 0, 0, 0);
+        a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[0], (half8{wv[8], wv[9], wv[10], wv[11], wv[12], wv[13], wv[14], wv[15]}), a1, 0, 0, 0);
+        wp1.dequant(st1, h, wv);
+        a0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[1], (half8{wv[0], wv[1], wv[2], wv[3], wv[4], wv[5], wv[6], wv[7]}), a0, 0, 0, 0);
+        a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[1], (half8{wv[8], wv[9], wv[10], wv[11], wv[12], wv[13], wv[14], wv[15]}), a1, 0, 0, 0);
+    }
+    // accumulator element r is activation row 8 (r / 4) + 4 h + r % 4
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+        const floatx4 sc = *reinterpret_cast<const floatx4*>(&escale[wave][8 * qd + 4 * h]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave][(4 * qd + i) * 64 + lane] = (a0[4 * qd + i] + a1[4 * qd + i]) * sc[i];
+    }
+    __syncthreads();
+    // wave w adds the 16 tiles' element (m, n), m = 2 w + h, n = n0 + col
+    const int m = 2 * wave + h, n = n0 + col;
+    const int ri = (4 * (m >> 3) + (m & 3)) * 64 + col + 32 * ((m >> 2) & 1);
+    float v = 0.f;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) v += red[t][ri];
+    float* out = part ? part + int64_t(sp) * M * N : Y;
+    const int64_t ld = part ? int64_t(N) : ldy;
+    if (m < M && n < N) out[int64_t(m) * ld + n] = v;
+}
+
+template <int WT, int MODE, bool X86>
+void launch_strip_mode(bool xvec, const float* x, int64_t ldx, const uint8_t* w, int64_t w_stride, float* y,
+                       int64_t ldy, float* part, int M, int N, int K, int RG, int S, hipStream_t stream) {
+    const dim3 grid(unsigned(RG * S)), block(1024);
+    if (xvec)
+        hipLaunchKernelGGL((strip_skinny_kernel<WT, MODE, X86, true>), grid, block, 0, stream, x, ldx, w, w_stride, y,
+                           ldy, part, M, N, K, RG);
+    else
+        hipLaunchKernelGGL((strip_skinny_kernel<WT, MODE, X86, false>), grid, block, 0, stream, x, ldx, w, w_stride,
+                           y, ldy, part, M, N, K, RG);
+}
+
+template <int WT>
+void launch_strip_wt(bool f16, int x86, bool xvec, const float* x, int64_t ldx, const uint8_t* w, int64_t w_stride,
+                     float* y, int64_t ldy, float* part, int M, int N, int K, int RG, int S, hipStream_t stream) {
+    constexpr int Q = WT == T_Q8_0 ? T_Q8_0 : T_Q8_K;
+    if (f16)
+        launch_strip_mode<WT, T_F16, false>(xvec, x, ldx, w, w_stride, y, ldy, part, M, N, K, RG, S, stream);
+    else if (Q == T_Q8_0 && x86)
+        launch_strip_mode<WT, Q, true>(xvec, x, ldx, w, w_stride, y, ldy, part, M, N, K, RG, S, stream);
+    else
+        launch_strip_mode<WT, Q, false>(xvec, x, ldx, w, w_stride, y, ldy, part, M, N, K, RG, S, stream);
 }
 
 template <int WT, int MODE, bool X86, int MT>
@@ -434,6 +659,49 @@ FusedPlan fused_skinny_plan(int M, int N, int K, int max_splits) {
     p.splits = (nchunks + p.cps - 1) / p.cps;
     p.part_bytes = p.splits > 1 ? size_t(p.splits) * size_t(M) * size_t(N) * 4 : 0;
     return p;
+}
+
+FusedPlan strip_skinny_plan(int M, int N, int K) {
+    FusedPlan p{};
+    p.rg = (N + 31) / 32;
+    const int nchunks = (K + 255) / 256;
+    p.cps = 4;
+    p.splits = (nchunks + 3) / 4;
+    p.part_bytes = p.splits > 1 ? size_t(p.splits) * size_t(M) * size_t(N) * 4 : 0;
+    (void)M;
+    return p;
+}
+
+const char* strip_skinny_variant(int wtype) {
+    switch (wtype) {
+        case T_Q8_0: return "skinny_strip_q8_0";
+        case T_Q4_K: return "skinny_strip_q4_k";
+        case T_Q5_K: return "skinny_strip_q5_k";
+        case T_Q6_K: return "skinny_strip_q6_k";
+        default: return nullptr;
+    }
+}
+
+const char* launch_strip_skinny(int wtype, bool f16, const float* x, int64_t ldx, const void* w, int64_t w_stride,
+                                float* y, int64_t ldy, float* part, int M, int N, int K, int x86, hipStream_t stream) {
+    if (M < 1 || M > kStripMaxM || N < 1 || K < 32 || K % 32) return nullptr;
+    const FusedPlan p = strip_skinny_plan(M, N, K);
+    const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    float* pt = p.splits > 1 ? part : nullptr;
+    switch (wtype) {
+        case T_Q8_0: launch_strip_wt<T_Q8_0>(f16, x86, xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, p.rg, p.splits, stream); break;
+        case T_Q4_K: launch_strip_wt<T_Q4_K>(f16, x86, xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, p.rg, p.splits, stream); break;
+        case T_Q5_K: launch_strip_wt<T_Q5_K>(f16, x86, xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, p.rg, p.splits, stream); break;
+        case T_Q6_K: launch_strip_wt<T_Q6_K>(f16, x86, xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, p.rg, p.splits, stream); break;
+        default: return nullptr;
+    }
+    if (p.splits > 1) {
+        const int64_t outs = int64_t(M) * N;
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(unsigned((outs + 255) / 256)), dim3(256), 0, stream, part, y, ldy,
+                           M, N, p.splits);
+    }
+    return strip_skinny_variant(wtype);
 }
 
 const char* fused_skinny_variant(int wtype) {

@@ -269,7 +269,7 @@ def test_mul_mat_tall_path_tails(gpu_ctx, f16_ctx, oracle, qtype):
 
 
 SKINNY_CASES = [(1, 96, 256), (32, 257, 1024), (33, 300, 512), (64, 64, 256), (65, 33, 256), (201, 256, 512),
-                (255, 70, 256), (32, 4096, 1024), (201, 2048, 256)]
+                (255, 70, 256), (32, 4096, 1024), (201, 2048, 256), (32, 1024, 4096), (17, 100, 800)]
 
 
 @pytest.mark.parametrize("qtype", TYPES)
@@ -312,6 +312,42 @@ def test_mul_mat_fused_split_k_deterministic(gpu_ctx, f16_ctx, oracle, samhip, q
         assert np.array_equal(first, again)
     yf = f16_ctx.matmul(qtype, w, x, w_row_offset=n, w_rows=n)
     _check_product(oracle, qtype, w[n:], x, first, yf)
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_mul_mat_strip_path(gpu_ctx, samhip, oracle, monkeypatch, qtype):
+    """M <= 32 takes the strip kernel where it is preferred (Q8_0, K <= 1024;
+    SAMHIP_STRIP_SKINNY=2 forces it for every weight type and K, with a
+    split-K reduce past K = 1024): repeated calls give identical bits, and
+    the fused kernel (SAMHIP_STRIP_SKINNY=0), which forms the same fp16
+    operands, agrees to F32 summation-order rounding."""
+    say("case strip path", qtype)
+    rng = np.random.default_rng(45)
+    monkeypatch.setenv("SAMHIP_STRIP_SKINNY", "2")
+    strip = samhip.Context(0)
+    monkeypatch.setenv("SAMHIP_STRIP_SKINNY", "0")
+    fused = samhip.Context(0)
+    try:
+        for m, n, k in ((32, 4096, 1024), (32, 1024, 4096), (9, 70, 512)):
+            w = oracle.quantize(qtype, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            first = strip.matmul(qtype, w, x)
+            assert strip.query().kernel_variant.startswith(b"skinny_strip")
+            default = gpu_ctx.matmul(qtype, w, x)
+            preferred = qtype == 8 and k <= 1024
+            assert gpu_ctx.query().kernel_variant.startswith(b"skinny_strip" if preferred else b"skinny_fused")
+            if preferred:
+                assert np.array_equal(first, default)
+            assert np.array_equal(first, strip.matmul(qtype, w, x))
+            other = fused.matmul(qtype, w, x)
+            assert fused.query().kernel_variant.startswith(b"skinny_fused")
+            err = float(np.max(np.abs(first - other)) / np.max(np.abs(other)))
+            print(f"  strip vs fused m{m} n{n} k{k}: max {err:.2e}", flush=True)
+            assert err <= 1e-5
+            assert max_row_rel_l2(first, oracle.mul_mat_native(qtype, w, x)) <= ROW_REL_L2
+    finally:
+        strip.close()
+        fused.close()
 
 
 @pytest.mark.parametrize("qtype", [8, 12])
