@@ -352,198 +352,141 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 
 // ---------------------------------------------------------------------------
 // Strip path for M <= 32 (the text encoder's 32 tokens): one workgroup per
-// 32-row strip of W and group of four 256-wide K chunks; 16 waves, wave w
-// taking two 32-wide steps (quarter w % 4) of chunk w / 4.  A lane holds
-// the 16 activations of one row that its A fragments need (row l % 32,
-// values 16 (l / 32) .. +15 of each step), so the Q8 blocks are formed in
-// registers (Q8_0: one exchange between lanes l and l ^ 32 per block; Q8_K:
-// the four quarters' maxima meet in LDS), and the weights are decoded from
-// the lane's own loads: no LDS staging before the products.  Activations
-// are requested before weights (loads return in issue order), so packing
-// runs while the weights are in flight.  The 16 partial tiles meet in LDS
-// and are added in a fixed order; with more than four chunks the groups go
-// to `part` and splitk_reduce_kernel adds them.  Every workgroup packs the
-// activations it uses: VALU time per workgroup in place of a second launch
-// and a round trip of partial sums through memory.
+// 32-row strip of W and group of four 256-wide K chunks, 16 waves, so that
+// a product with K <= 1024 is one launch with no partial sums in memory.
+//  * the waves copy the strip's packed bytes for the group with coalesced
+//    dword loads into LDS (odd dword row stride: conflict-free piece reads);
+//  * the four waves of chunk q pack its 32 activation rows (two rows per
+//    wave per pass, 8 values per lane, requested before the weights) into
+//    the fp16 operand with quant8 under a power-of-two scale per row and
+//    chunk, as the fused kernel does;
+//  * wave w runs steps 2 (w % 4) and 2 (w % 4) + 1 of chunk w / 4 (weights
+//    decoded from LDS), scales by 2^e, and the 16 partial tiles are added in
+//    LDS in a fixed order.
+// With more than four chunks the groups go to `part` and
+// splitk_reduce_kernel adds them.  Every workgroup packs the activation
+// chunks it uses: VALU time per workgroup in place of a second launch and a
+// round trip of partial sums through memory.
 // ---------------------------------------------------------------------------
-
-// The Q8 codes and block scale of a lane's 2 steps x 16 activations.
-template <int MODE, bool X86>
-__device__ __forceinline__ void strip_q8_0(const floatx4 (&xv)[2][4], float (&d)[2], float (&q)[2][16],
-                                           float& rmax) {
-#pragma clang fp contract(off)
-    rmax = 0.f;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        float amax = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(xv[s][i >> 2][i & 3]));
-        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-        rmax = fmaxf(rmax, amax);
-        const float dd = amax / 127.f;
-        float inv;
-        if (X86) inv = amax != 0.f ? 127.f / amax : 0.f;
-        else inv = dd != 0.f ? 1.f / dd : 0.f;
-        d[s] = half_bits_to_float(float_to_half_bits(dd));   // stored fp16 scale
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float t = xv[s][i >> 2][i & 3] * inv;
-            q[s][i] = X86 ? __builtin_rintf(t) : __builtin_roundf(t);
-        }
-    }
-}
+template <int WT>
+constexpr int strip_wdw() { return ((4 * chunk_bytes<WT>() + 2 + 3) / 4) | 1; }
 
 template <int WT, int MODE, bool X86, bool XVEC>
 __global__ __launch_bounds__(1024) void strip_skinny_kernel(const float* __restrict__ X, int64_t ldx,
                                                             const uint8_t* __restrict__ W, int64_t w_stride,
                                                             float* __restrict__ Y, int64_t ldy,
                                                             float* __restrict__ part, int M, int N, int K, int RG) {
-#pragma clang fp contract(off)
-    __shared__ __attribute__((aligned(16))) float red[16][16 * 64];   // the waves' partial tiles
-    __shared__ __attribute__((aligned(16))) float escale[16][32];     // 2^e per wave and row
-    __shared__ float cand_a[16][32], cand_s[16][32];                  // Q8_K: quarter maxima per row
-    __shared__ int cand_i[16][32];
+    constexpr int CB = chunk_bytes<WT>();
+    constexpr int WDW = strip_wdw<WT>();
+    constexpr int RI = (WDW + 31) / 32;
+    // activation tiles of the four chunks; afterwards the 16 partial tiles
+    __shared__ __attribute__((aligned(16))) _Float16 As[4][32 * ALD];
+    __shared__ __attribute__((aligned(16))) uint32_t Ws[32 * WDW];
+    __shared__ __attribute__((aligned(16))) float escale[4][32];
+    static_assert(4 * 32 * ALD * 2 >= 16 * 16 * 64 * 4, "partial tiles must fit the activation tiles");
+    float* red = reinterpret_cast<float*>(&As[0][0]);
+
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 31, h = lane >> 5;
     const int rg = blockIdx.x % RG, sp = blockIdx.x / RG;
     const int n0 = rg * 32;
     const int nchunks = (K + 255) / 256;
-    const int c = 4 * sp + (wave >> 2), s0 = 2 * (wave & 3);
+    const int cq = wave >> 2, c = 4 * sp + cq;   // this wave's chunk
     const bool active = c < nchunks;
-    const int kc = 256 * min(c, nchunks - 1);
-    const int steps = min(8, (K - kc) / 32);
 
-    // activations first: row `col` (clamped in bounds, zeroed past M); steps
-    // past the chunk's end repeat its last step and are zeroed
-    const bool live = col < M && active;
-    const float* xr = X + int64_t(col < M ? col : 0) * ldx + kc + 16 * h;
-    floatx4 xv[2][4];
+    // 1. activations of chunk cq, rows 8 (w % 4) + 2 p + h, then the packed bytes
+    const int kc = 256 * c;
+    floatx8 xv[4];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-        const float* xs = xr + 32 * min(s0 + s, steps - 1);
-        const bool use = live && s0 + s < steps;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            floatx4 v;
+    for (int p = 0; p < 4; ++p) {
+        const int r = 8 * (wave & 3) + 2 * p + h, k = kc + 8 * col;
+        floatx8 v{0, 0, 0, 0, 0, 0, 0, 0};
+        if (active && r < M && k < K) {
+            const float* xr = X + int64_t(r) * ldx + k;
             if (XVEC) {
-                v = load4f(xs + 4 * j);
+                const floatx4 lo = load4f(xr), hi = load4f(xr + 4);
+                v = floatx8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) v[i] = xs[4 * j + i];
+                for (int i = 0; i < 8; ++i) v[i] = xr[i];
             }
-            xv[s][j] = use ? v : floatx4{0.f, 0.f, 0.f, 0.f};
         }
+        xv[p] = v;
     }
-    // this lane's weight pieces (row n0 + col clamped in bounds)
-    const uint8_t* wr = W + int64_t(min(n0 + col, N - 1)) * w_stride;
-    const int st0 = kc / 32 + min(s0, steps - 1), st1 = kc / 32 + min(s0 + 1, steps - 1);
-    WeightPiece<WT> wp0, wp1;
-    wp0.load(wr, st0, h);
-    wp1.load(wr, st1, h);
+    const int64_t off = int64_t(4 * sp) * CB;   // the group's first byte in a row
+    const int gb = WT == T_Q8_0 ? 34 * min(32, K / 32 - 32 * sp) : CB * min(4, nchunks - 4 * sp);
+    const int wr = 2 * wave + h;                  // the row this lane copies
+    const uintptr_t g = reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + wr, N - 1)) * w_stride + off);
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(g & ~uintptr_t(3));
+    const int ndw = int(((g & 3) + gb + 3) >> 2);
+    uint32_t wreg[RI];
+#pragma unroll
+    for (int i = 0; i < RI; ++i) {
+        const int d = col + 32 * i;
+        wreg[i] = d < ndw ? src[d] : 0u;
+    }
 
-    // the fp16 operand: fp16(d * q * 2^-e), or fp16(x * 2^-e) in F16 mode
-    half8 alo[2], ahi[2];
-    float rmax = 0.f, dk[2] = {0.f, 0.f}, q[2][16];
-    if (MODE == T_Q8_0) {
-        strip_q8_0<MODE, X86>(xv, dk, q, rmax);
-    } else if (MODE == T_Q8_K) {
-        // the first element of largest magnitude of the 256-value block
-        // (value index 32 s + 16 h + i of the chunk)
-        float la = 0.f, ls = 0.f;
-        int li = 1 << 20;
+    // 2. the fp16 operand (two rows per pass), then the weight bytes to LDS
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
+    for (int p = 0; p < 4; ++p) {
+        const int r = 8 * (wave & 3) + 2 * p + h;
+        float rmax = 0.f;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float v = xv[s][i >> 2][i & 3], t = fabsf(v);
-                if (t > la) { la = t; ls = v; li = 32 * (s0 + s) + 16 * h + i; }
-            }
-        const float pa = __shfl_xor(la, 32, 64), ps = __shfl_xor(ls, 32, 64);
-        const int pi = __shfl_xor(li, 32, 64);
-        if (pa > la || (pa == la && pi < li)) { la = pa; ls = ps; li = pi; }
-        if (h == 0) {
-            cand_a[wave][col] = la;
-            cand_s[wave][col] = ls;
-            cand_i[wave][col] = li;
-        }
-    } else {
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) rmax = fmaxf(rmax, fabsf(xv[s][i >> 2][i & 3]));
-        rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+        for (int i = 0; i < 8; ++i) rmax = fmaxf(rmax, fabsf(xv[p][i]));
+        rmax = max32_lanes(rmax);
+        const int e = row_exponent(rmax);
+        const half8 o = quant8<MODE, X86>(xv[p], lane, exp2i(-e));
+        *reinterpret_cast<half8*>(&As[cq][r * ALD + 8 * col]) = o;
+        if (col == 0) escale[cq][r] = exp2i(e);
     }
-    if (MODE == T_Q8_K) {
-        __syncthreads();
-        const int g = wave & ~3;   // the chunk's four quarters, in value order
-        float la = cand_a[g][col], ls = cand_s[g][col];
-        int li = cand_i[g][col];
 #pragma unroll
-        for (int t = 1; t < 4; ++t) {
-            const float a = cand_a[g + t][col];
-            const int i = cand_i[g + t][col];
-            if (a > la || (a == la && i < li)) { la = a; ls = cand_s[g + t][col]; li = i; }
-        }
-        rmax = la;
-        if (la != 0.f) {
-            const float iscale = -127.f / ls;
-            dk[0] = dk[1] = 1.f / iscale;
-#pragma unroll
-            for (int s = 0; s < 2; ++s)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) q[s][i] = fminf(127.f, __builtin_rintf(iscale * xv[s][i >> 2][i & 3]));
-        } else {
-#pragma unroll
-            for (int s = 0; s < 2; ++s)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) q[s][i] = 0.f;
-        }
+    for (int i = 0; i < RI; ++i) {
+        const int d = col + 32 * i;
+        if (d < WDW) Ws[wr * WDW + d] = wreg[i];
     }
-    const int e = row_exponent(rmax);
-    const float down = exp2i(-e);
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            if (MODE == T_F16) {
-                alo[s][i] = (_Float16)(xv[s][i >> 2][i & 3] * down);
-                ahi[s][i] = (_Float16)(xv[s][2 + (i >> 2)][i & 3] * down);
-            } else {
-                // d * q is exact in F32 for Q8_0 (11 x 8 bits); for Q8_K the
-                // one rounding of (d * 2^-e) * q equals that of d * q
-                const float sd = dk[s] * down;
-                alo[s][i] = (_Float16)(q[s][i] * sd);
-                ahi[s][i] = (_Float16)(q[s][8 + i] * sd);
-            }
-        }
-    if (h == 0) escale[wave][col] = exp2i(e);
+    __syncthreads();
 
+    // 3. this wave's two steps of its chunk
     floatx16 a0, a1;
 #pragma unroll
     for (int r = 0; r < 16; ++r) a0[r] = a1[r] = 0.f;
-    {
-        _Float16 wv[16];
-        wp0.dequant(st0, h, wv);
-        a0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[0], (half8{wv[0], wv[1], wv[2], wv[3], wv[4], wv[5], wv[6], wv[7]}), a0, 0, 0, 0);
-        a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[0], (half8{wv[8], wv[9], wv[10], wv[11], wv[12], wv[13], wv[14], wv[15]}), a1, 0, 0, 0);
-        wp1.dequant(st1, h, wv);
-        a0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[1], (half8{wv[0], wv[1], wv[2], wv[3], wv[4], wv[5], wv[6], wv[7]}), a0, 0, 0, 0);
-        a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[1], (half8{wv[8], wv[9], wv[10], wv[11], wv[12], wv[13], wv[14], wv[15]}), a1, 0, 0, 0);
+    if (active) {
+        const int steps = min(8, (K - kc) / 32);
+        const LdsRow wrow{&Ws[col * WDW], int((reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + col, N - 1)) * w_stride) +
+                                               uintptr_t(off)) & 3)};
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int s = 2 * (wave & 3) + t;
+            if (s >= steps) break;
+            WeightPiece<WT> wp;
+            wp.load(wrow, 8 * cq + s, h);
+            _Float16 wv[16];
+            wp.dequant(8 * cq + s, h, wv);
+            const half8 b_lo{wv[0], wv[1], wv[2], wv[3], wv[4], wv[5], wv[6], wv[7]};
+            const half8 b_hi{wv[8], wv[9], wv[10], wv[11], wv[12], wv[13], wv[14], wv[15]};
+            const half8* ap = reinterpret_cast<const half8*>(&As[cq][col * ALD + 32 * s + 16 * h]);
+            a0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ap[0], b_lo, a0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ap[1], b_hi, a1, 0, 0, 0);
+        }
     }
+    floatx16 acc;
     // accumulator element r is activation row 8 (r / 4) + 4 h + r % 4
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) {
-        const floatx4 sc = *reinterpret_cast<const floatx4*>(&escale[wave][8 * qd + 4 * h]);
+        const floatx4 sc = *reinterpret_cast<const floatx4*>(&escale[cq][8 * qd + 4 * h]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) red[wave][(4 * qd + i) * 64 + lane] = (a0[4 * qd + i] + a1[4 * qd + i]) * sc[i];
+        for (int i = 0; i < 4; ++i) acc[4 * qd + i] = (a0[4 * qd + i] + a1[4 * qd + i]) * sc[i];
     }
+    __syncthreads();   // the activation tiles are read; their LDS takes the partial tiles
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
     __syncthreads();
     // wave w adds the 16 tiles' element (m, n), m = 2 w + h, n = n0 + col
     const int m = 2 * wave + h, n = n0 + col;
     const int ri = (4 * (m >> 3) + (m & 3)) * 64 + col + 32 * ((m >> 2) & 1);
     float v = 0.f;
 #pragma unroll
-    for (int t = 0; t < 16; ++t) v += red[t][ri];
+    for (int t = 0; t < 16; ++t) v += red[t * 16 * 64 + ri];
     float* out = part ? part + int64_t(sp) * M * N : Y;
     const int64_t ld = part ? int64_t(N) : ldy;
     if (m < M && n < N) out[int64_t(m) * ld + n] = v;
