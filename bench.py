@@ -348,6 +348,132 @@ def text_stream(args, sh, ctx, fmt):
     }
 
 
+DET_D, DET_FFN, DET_LAYERS = 256, 2048, 6
+DET_M = {"img": 5184, "prompt": 33, "query": 201}
+
+
+def detector_plan():
+    """The linears of the fusion encoder (src/models/sam3/fusion_encoder.hpp:46-145) and of the DETR
+    decoder (src/models/sam3/detector.hpp:343-479), 6 layers each, D = 256, FFN 2048.  Entries:
+    (label, weight key, weight rows, row offset, N, K, activation key).  q/k/v are row-offset views of
+    the fused [3D, D] in-projections, as the reference takes them with ggml_view_2d."""
+    D, F = DET_D, DET_FFN
+    plan = []
+    for l in range(DET_LAYERS):
+        f = f"fenc{l}"
+        for i, (part, src) in enumerate((("q", "img"), ("k", "img"), ("v", "img"))):
+            plan.append((f"{f}.sa_{part}", f"{f}.sa_in", 3 * D, i * D, D, D, (src, D)))
+        plan.append((f"{f}.sa_out", f"{f}.sa_out", D, 0, D, D, ("img", D)))
+        for i, (part, src) in enumerate((("q", "img"), ("k", "prompt"), ("v", "prompt"))):
+            plan.append((f"{f}.ca_{part}", f"{f}.ca_in", 3 * D, i * D, D, D, (src, D)))
+        plan.append((f"{f}.ca_out", f"{f}.ca_out", D, 0, D, D, ("img", D)))
+        plan.append((f"{f}.fc1", f"{f}.fc1", F, 0, F, D, ("img", D)))
+        plan.append((f"{f}.fc2", f"{f}.fc2", D, 0, D, F, ("img", F)))
+    for l in range(DET_LAYERS):
+        d = f"ddec{l}"
+        for i, part in enumerate("qkv"):
+            plan.append((f"{d}.sa_{part}", f"{d}.sa_in", 3 * D, i * D, D, D, ("query", D)))
+        plan.append((f"{d}.sa_out", f"{d}.sa_out", D, 0, D, D, ("query", D)))
+        for ca, kv in (("ca_text", "prompt"), ("ca_img", "img")):
+            for i, (part, src) in enumerate((("q", "query"), ("k", kv), ("v", kv))):
+                plan.append((f"{d}.{ca}_{part}", f"{d}.{ca}_in", 3 * D, i * D, D, D, (src, D)))
+            plan.append((f"{d}.{ca}_out", f"{d}.{ca}_out", D, 0, D, D, ("query", D)))
+        plan.append((f"{d}.fc1", f"{d}.fc1", F, 0, F, D, ("query", D)))
+        plan.append((f"{d}.fc2", f"{d}.fc2", D, 0, D, F, ("query", F)))
+    return plan
+
+
+def detector_stream(args, sh, ctx, fmt):
+    """Config 3's fusion and decoder half: the 6 fusion-encoder and 6 decoder layers' linears (image
+    tokens M = 5184, prompt tokens M = 33, queries M = 201; D = 256, FFN 2048), every layer with its
+    own weights and the q/k/v products on row-offset views of the fused in-projections, 144 mul_mat
+    per step replayed as one HIP graph.  One JSON line: algorithmic bytes (packed W + F32 X + F32 Y)
+    per second over the stream, its TOPS, per-shape times, and the dominant kernel's roofline."""
+    qt = {"q8_0": sh.Q8_0, "q4_k": sh.Q4_K, "q5_k": sh.Q5_K, "q6_k": sh.Q6_K}[fmt]
+    log("preparing fusion/decoder stream weights")
+    plan = detector_plan()
+    rng = np.random.default_rng(3)
+    xbuf = {(src, k): ctx.upload(rng.standard_normal((DET_M[src], k)).astype(np.float32))
+            for src, k in sorted({p[6] for p in plan})}
+    wbuf = {}
+    for _, key, rows, _, _, k, _ in plan:
+        if key in wbuf:
+            continue
+        wf = ctx.upload((np.random.default_rng(len(wbuf)).standard_normal((rows, k)) * 0.02).astype(np.float32))
+        wq = ctx.alloc(rows * sh.row_bytes(qt, k))
+        ctx.quantize_rows(qt, wf.ptr, 4 * k, wq.ptr, rows, k, sh.ROUND_REF)
+        ctx.synchronize()
+        wf.free()
+        wbuf[key] = wq
+    ops, alg_bytes, flops = [], 0, 0
+    for label, key, rows, off, n, k, (src, _) in plan:
+        m, rb = DET_M[src], sh.row_bytes(qt, k)
+        yb = ctx.alloc(m * n * 4)
+        w = sh.tensor(qt, k, n, wbuf[key].ptr + off * rb, nb1=rb)
+        x = sh.tensor(sh.F32, k, m, xbuf[(src, k)].ptr)
+        y = sh.tensor(sh.F32, n, m, yb.ptr)
+        if not sh.lib().samhip_supports_mul_mat(w, x, y):
+            raise RuntimeError(f"unsupported product {label}")
+        ops.append((label, m, n, k, w, x, y, yb))
+        alg_bytes += n * rb + m * k * 4 + m * n * 4
+        flops += 2 * m * n * k
+
+    def step():
+        for _, _, _, _, w, x, y, _ in ops:
+            ctx.mul_mat(w, x, y)
+
+    for _ in range(args.warmup):
+        step()
+    ctx.trace_begin()
+    step()
+    prof = ctx.trace_end(capacity=4 * len(ops) + 16)
+    ctx.synchronize()
+    ctx.capture_begin()
+    step()
+    graph = ctx.capture_end()
+    graph.launch()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        graph.launch()
+    ctx.synchronize()
+    elapsed = time.perf_counter() - t0
+    graph.destroy()
+    # per (M, N, K) shape: launches and event time per step
+    shapes = {}
+    for name, _, m, n, k, ms in prof:
+        e = shapes.setdefault((m, n, k), {"M": m, "N": n, "K": k, "ms": 0.0, "kernels": {}})
+        e["ms"] += ms
+        e["kernels"][name] = e["kernels"].get(name, 0) + 1
+    per_kernel = {}
+    for name, _, m, n, k, ms in prof:
+        per_kernel[name] = per_kernel.get(name, 0.0) + ms
+    dom = max(per_kernel, key=per_kernel.get)
+    dom_recs = [(m, n, k, ms) for name, _, m, n, k, ms in prof if name == dom]
+    rb_of = {k: sh.row_bytes(qt, k) for k in (DET_D, DET_FFN)}
+    dom_bytes = sum(n * rb_of[k] + m * k * 4 + m * n * 4 for m, n, k, _ in dom_recs)
+    dom_ms = sum(r[3] for r in dom_recs)
+    ach = dom_bytes / (dom_ms * 1e-3) / 1e9
+    for b in list(wbuf.values()) + list(xbuf.values()) + [o[7] for o in ops]:
+        b.free()
+    return {
+        "metric": "fusion/decoder linear stream algorithmic GB/s (D=256, 6+6 layers)",
+        "value": round(alg_bytes * args.steps / elapsed / 1e9, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(elapsed * 1e3 / args.steps, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": f"SAM 3 fusion encoder + decoder linear stream, {fmt.upper()} weights, image tokens "
+                               f"M=5184, prompt M=33, queries M=201, {len(ops)} mul_mat per step",
+                   "parallelism": "single-gpu"},
+        "tops": round(flops * args.steps / elapsed / 1e12, 2),
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(ach / PEAK_HBM_GBPS, 4), "traffic": None, "kernel": dom,
+                     "launches": len(dom_recs), "launch_ms": round(dom_ms / len(dom_recs), 5)},
+        "shapes": sorted(({**e, "ms": round(e["ms"], 4)} for e in shapes.values()), key=lambda e: -e["ms"]),
+        "replay": "one HIP graph launch per step (samhip_capture_begin/end)",
+        "device": ctx.query().device_name.decode(),
+    }
+
+
 ENC = {"E": 1024, "HEADS": 16, "MLP": 4736, "GRID": 72, "WINDOW": 24, "IMG": 1008, "PATCH": 14, "POS_GRID": 24,
        "DEPTH": 32, "GLOBAL": (7, 15, 23, 31), "NECK_MID": 512, "NECK_DIM": 256}
 
@@ -618,7 +744,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--trace", choices=["dominant", "all", "none"], default="dominant",
                     help="launches bracketed by HIP events inside the timed region")
-    ap.add_argument("--workload", choices=["vit", "text", "encoder"], default="vit",
+    ap.add_argument("--workload", choices=["vit", "text", "encoder", "detector"], default="vit",
                     help="vit: the ViT linear sweep (headline, with the encoder's ms/image beside it); text: the "
                          "M=32 text-encoder linear stream; encoder: the vision encoder forward alone")
     ap.add_argument("--format", choices=["q8_0", "q4_k", "q5_k", "q6_k"], default=None,
@@ -647,6 +773,11 @@ def main():
     ctx = sh.Context(0, compute, sh.ROUND_X86)
     if args.workload == "text":
         result = text_stream(args, sh, ctx, args.format or "q8_0")
+        ctx.close()
+        print(json.dumps(result), flush=True)
+        return
+    if args.workload == "detector":
+        result = detector_stream(args, sh, ctx, args.format or "q8_0")
         ctx.close()
         print(json.dumps(result), flush=True)
         return

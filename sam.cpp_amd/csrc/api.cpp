@@ -73,7 +73,7 @@ struct samhip_context {
     int cus = 256;             // compute units of the device
     int tall_m = 256;
     int gemm_cfg = -1;
-    bool fused_skinny = true;   // SAMHIP_FUSED_SKINNY=0 routes M <= 128 through staging + the skinny kernel
+    bool fused_skinny = true;   // SAMHIP_FUSED_SKINNY=0 routes M < 256 through staging + the skinny kernel
     int strip_skinny = 1;       // SAMHIP_STRIP_SKINNY: 0 never, 1 where preferred, 2 every M <= 32 product
     int fused_max_splits = 16;  // SAMHIP_FUSED_MAX_SPLITS: cap on the fused kernel's K splits
     samhip_exec_info info{};

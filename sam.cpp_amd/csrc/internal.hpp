@@ -195,11 +195,11 @@ const char* skinny_variant(int wtype, int M, int N);
 const char* launch_skinny(int wtype, const _Float16* a, int64_t lda, const float* row_scale, const void* w,
                           int64_t w_stride, float* y, int64_t ldy, int M, int N, int K, hipStream_t stream);
 
-// Fused skinny products (M <= kFusedMaxM): activation packing, weight decode
-// and product in one launch; when the K range is split over workgroups their
-// partial sums go through `part` (FusedPlan::part_bytes) and a second, small
-// launch adds them.
-constexpr int kFusedMaxM = 128;
+// Fused skinny products (M <= kFusedMaxM, in blocks of 128 activation rows):
+// activation packing, weight decode and product in one launch; when the K
+// range is split over workgroups their partial sums go through `part`
+// (FusedPlan::part_bytes) and a second, small launch adds them.
+constexpr int kFusedMaxM = 256;
 struct FusedPlan {
     int rg, splits, cps;
     size_t part_bytes;

@@ -140,9 +140,10 @@ void launch_wt(const _Float16* a, int64_t lda, const float* rs, const uint8_t* w
 }
 
 // ---------------------------------------------------------------------------
-// Fused path for M <= 128: one launch per product (two when K is split).  A
-// workgroup of 8 waves owns 128 weight rows (a 32-row tile per wave pair)
-// and a range of 256-wide K chunks.  Per chunk:
+// Fused path for M <= 256: one launch per product (two when K is split).  A
+// workgroup of 8 waves owns 128 weight rows (a 32-row tile per wave pair),
+// a block of up to 128 activation rows (the decoder's 201 queries take two
+// blocks along the grid) and a range of 256-wide K chunks.  Per chunk:
 //  * the waves copy the packed bytes of their tiles with coalesced dword
 //    loads into LDS (rows padded to an odd dword count, so the per-lane piece
 //    reads of one column are bank-conflict free);
@@ -175,7 +176,7 @@ __global__ __launch_bounds__(512) void fused_skinny_kernel(const float* __restri
                                                            const uint8_t* __restrict__ W, int64_t w_stride,
                                                            float* __restrict__ Y, int64_t ldy,
                                                            float* __restrict__ part, int M, int N, int K, int RG,
-                                                           int cps) {
+                                                           int S, int cps) {
     constexpr int WDW = wrow_dw<WT>();
     constexpr int CB = chunk_bytes<WT>();
     // the activation tile; after the last chunk it holds the K-half partial sums
@@ -186,11 +187,16 @@ __global__ __launch_bounds__(512) void fused_skinny_kernel(const float* __restri
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tile = wave & 3, kh = wave >> 2;   // 32-row tile, half of the chunk's K steps
-    const int rg = blockIdx.x % RG, sp = blockIdx.x / RG;
+    const int rg = blockIdx.x % RG, sp = (blockIdx.x / RG) % S, mb = blockIdx.x / (RG * S);
     const int n0 = rg * FROWS + 32 * tile;
     const int col = lane & 31, h = lane >> 5;
     const int nchunks = (K + CHUNK - 1) / CHUNK;
     const int c0 = sp * cps, c1 = min(nchunks, c0 + cps);
+    // this workgroup's block of MT * 32 activation rows
+    const int m0 = mb * (MT * 32), Mall = M;
+    X += int64_t(m0) * ldx;
+    Y += int64_t(m0) * ldy;
+    M = min(M - m0, MT * 32);
 
     // this lane's weight row (for its pieces) and its byte shift in LDS
     const uint8_t* my_row = W + int64_t(min(n0 + col, N - 1)) * w_stride;
@@ -317,7 +323,7 @@ __global__ __launch_bounds__(512) void fused_skinny_kernel(const float* __restri
 
     // S == 1: the product; otherwise this split's partial sums
     const int n = n0 + col;
-    float* out = part ? part + int64_t(sp) * M * N : Y;
+    float* out = part ? part + (int64_t(sp) * Mall + m0) * N : Y;
     const int64_t ld = part ? int64_t(N) : ldy;
 #pragma unroll
     for (int t = 0; t < MT; ++t)
@@ -520,13 +526,14 @@ template <int WT, int MODE, bool X86, int MT>
 void launch_fused_mt(const float* x, int64_t ldx, bool xvec, const uint8_t* w, int64_t w_stride, float* y,
                      int64_t ldy, float* part, int M, int N, int K, int RG, int S, int cps, int x86,
                      hipStream_t stream) {
-    const dim3 grid(unsigned(RG * S)), block(512);
+    const int MB = (M + MT * 32 - 1) / (MT * 32);
+    const dim3 grid(unsigned(RG * S * MB)), block(512);
     if (xvec)
         hipLaunchKernelGGL((fused_skinny_kernel<WT, MODE, X86, MT, true>), grid, block, 0, stream, x, ldx, w, w_stride,
-                           y, ldy, part, M, N, K, RG, cps);
+                           y, ldy, part, M, N, K, RG, S, cps);
     else
         hipLaunchKernelGGL((fused_skinny_kernel<WT, MODE, X86, MT, false>), grid, block, 0, stream, x, ldx, w, w_stride,
-                           y, ldy, part, M, N, K, RG, cps);
+                           y, ldy, part, M, N, K, RG, S, cps);
 }
 
 template <int WT, int MODE, bool X86>
@@ -596,8 +603,10 @@ namespace samhip {
 FusedPlan fused_skinny_plan(int M, int N, int K, int max_splits) {
     FusedPlan p{};
     p.rg = (N + FROWS - 1) / FROWS;
+    const int mb = (M + 127) / 128;   // blocks of up to 128 activation rows
+    const int groups = p.rg * mb;
     const int nchunks = (K + CHUNK - 1) / CHUNK;
-    const int S = std::min(std::min(nchunks, std::max(1, max_splits)), std::max(1, (256 + p.rg - 1) / p.rg));
+    const int S = std::min(std::min(nchunks, std::max(1, max_splits)), std::max(1, (256 + groups - 1) / groups));
     p.cps = (nchunks + S - 1) / S;
     p.splits = (nchunks + p.cps - 1) / p.cps;
     p.part_bytes = p.splits > 1 ? size_t(p.splits) * size_t(M) * size_t(N) * 4 : 0;

@@ -269,15 +269,17 @@ def test_mul_mat_tall_path_tails(gpu_ctx, f16_ctx, oracle, qtype):
 
 
 SKINNY_CASES = [(1, 96, 256), (32, 257, 1024), (33, 300, 512), (64, 64, 256), (65, 33, 256), (201, 256, 512),
-                (255, 70, 256), (32, 4096, 1024), (201, 2048, 256), (32, 1024, 4096), (17, 100, 800)]
+                (255, 70, 256), (32, 4096, 1024), (201, 2048, 256), (32, 1024, 4096), (17, 100, 800),
+                (201, 256, 2048), (250, 300, 1024)]
 
 
 @pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("shape", SKINNY_CASES, ids=lambda s: "m%d_n%d_k%d" % s)
 def test_mul_mat_skinny_shapes(gpu_ctx, f16_ctx, oracle, samhip, qtype, shape):
-    """M < 256 takes the register-decode skinny kernel: the text encoder's
-    M = 32, text K/V M = 33, decoder queries M = 201 and the M / N tails
-    around them, with a strided activation on every other case."""
+    """M < 256 takes the strip or fused kernel (blocks of 128 activation
+    rows, split K with a reduce): the text encoder's M = 32, text K/V
+    M = 33, decoder queries M = 201 and the M / N tails around them, with a
+    strided activation on every other case."""
     m, n, k = shape
     if qtype != 8 and k % 256:
         pytest.skip("K-quant rows need K % 256 == 0")
@@ -352,7 +354,7 @@ def test_mul_mat_strip_path(gpu_ctx, samhip, oracle, monkeypatch, qtype):
 
 @pytest.mark.parametrize("qtype", [8, 12])
 def test_mul_mat_skinny_unfused_path(samhip, oracle, monkeypatch, qtype):
-    """SAMHIP_FUSED_SKINNY=0 routes M <= 128 through activation staging and
+    """SAMHIP_FUSED_SKINNY=0 routes M < 256 through activation staging and
     the register-decode skinny kernel; both paths agree with the oracle."""
     say("case skinny unfused", qtype)
     monkeypatch.setenv("SAMHIP_FUSED_SKINNY", "0")
