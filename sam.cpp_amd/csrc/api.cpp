@@ -452,7 +452,7 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
             });
             if (rc) return rc;
         }
-        const int cfg = ctx->gemm_cfg >= 0 ? ctx->gemm_cfg : gemm_f16_pick(M, N, K, ctx->cus);
+        const int cfg = ctx->gemm_cfg >= 0 ? ctx->gemm_cfg : gemm_f16_pick_plain(M, N, K, ctx->cus);
         variant = gemm_f16_config_name(cfg);
         rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
             launch_gemm_f16(cfg, a, K, rs, wh, K, static_cast<float*>(y->data), int64_t(y->nb[1] / 4), M, N, K,

@@ -803,6 +803,19 @@ int gemm_f16_pick(int M, int N, int /*K*/, int cus) {
     return tiles * 10 >= waves * cus * 8 ? 20 : 30;
 }
 
+// Plain products (mul_mat) also take 128x128x64 tiles on 2x4 waves (three
+// stages) when even 192x128 tiles would leave half the CUs idle: M = 5184,
+// N = 256 (the fusion / decoder image-token products) 9.5 vs 10.9 us at
+// K = 256 and 23.5 vs 29.3 us at K = 2048; N = 2048 stays 192x128 (17.3 vs
+// 22.1 us).
+int gemm_f16_pick_plain(int M, int N, int K, int cus) {
+    constexpr int kSmall = 27;
+    const int64_t tiles = int64_t((M + 191) / 192) * ((N + 127) / 128);
+    if (2 * tiles <= cus && kConfigs[kSmall].bm == 128 && kConfigs[kSmall].bn == 128 && K % kConfigs[kSmall].bk == 0)
+        return kSmall;
+    return gemm_f16_pick(M, N, K, cus);
+}
+
 // The picked configurations (20: 256x256x64 on 2x4 waves, 30: 192x128x64 on
 // 2x4 waves) with each epilogue and operand mode the encoder uses.
 template <int BM, int BN, int WM, int WN>

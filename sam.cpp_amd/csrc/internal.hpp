@@ -35,6 +35,8 @@ int gemm_f16_config_count();
 bool gemm_f16_supported(int M, int N, int K, int64_t lda, int64_t ldb);
 const char* gemm_f16_config_name(int cfg);
 int gemm_f16_pick(int M, int N, int K, int cus);
+// gemm_f16_pick plus 128x128 tiles for small grids (plain products only).
+int gemm_f16_pick_plain(int M, int N, int K, int cus);
 // `cus`: compute units of the device; grids with at most that many tiles run
 // one workgroup per CU.
 const char* launch_gemm_f16(int cfg, const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
