@@ -37,6 +37,8 @@ PROFILE_COMMANDS = {
             "python3 bench.py --workload text --steps 10 --warmup 2",
     "encoder": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/encoder -o bench -- "
                "python3 bench.py --workload encoder --steps 5 --warmup 2 --no-cpu-baseline",
+    "detector": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/detector -o bench -- "
+                "python3 bench.py --workload detector --steps 10 --warmup 2",
     "fetch": "rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/fetch -o bench -- "
              "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-encoder",
     "write": "rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/write -o bench -- "
@@ -206,6 +208,10 @@ def summarize_profiles(d, commands):
                 "kernel_stats_vit_sweep_m5184.md")
     stats_table("text", "Kernel time, SAM 3 text-encoder linear stream at M=32 (97 mul_mat per step, Q8_0)",
                 commands["text"], "kernel_stats_text_stream_m32_q8_0.md")
+    if os.path.isdir(os.path.join(d, "detector")):
+        stats_table("detector", "Kernel time, SAM 3 fusion encoder + decoder linear stream (144 mul_mat per step, "
+                    "Q8_0; image tokens M=5184, prompt M=33, queries M=201)", commands["detector"],
+                    "kernel_stats_detector_stream_q8_0.md")
     stats_table("encoder", "Kernel time, SAM 3 vision encoder forward at 1008 px (Q4_K qkv/proj/fc1, Q8_0 fc2; "
                 "8 forwards: 2 warmup, 5 timed, 1 traced)", commands["encoder"],
                 "kernel_stats_vision_encoder_1008px_q4_k.md",
