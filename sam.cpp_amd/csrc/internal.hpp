@@ -204,6 +204,7 @@ const char* launch_skinny(int wtype, const _Float16* a, int64_t lda, const float
 constexpr int kFusedMaxM = 256;
 struct FusedPlan {
     int rg, splits, cps;
+    int mt;               // 32-row activation tiles per row block (fused kernel)
     size_t part_bytes;
 };
 FusedPlan fused_skinny_plan(int M, int N, int K, int max_splits);

@@ -538,9 +538,9 @@ void launch_fused_mt(const float* x, int64_t ldx, bool xvec, const uint8_t* w, i
 
 template <int WT, int MODE, bool X86>
 void launch_fused_mode(const float* x, int64_t ldx, bool xvec, const uint8_t* w, int64_t w_stride, float* y,
-                       int64_t ldy, float* part, int M, int N, int K, int RG, int S, int cps, int x86,
+                       int64_t ldy, float* part, int M, int N, int K, int RG, int S, int cps, int MT, int x86,
                        hipStream_t stream) {
-    switch ((M + 31) / 32) {
+    switch (MT) {
         case 1: launch_fused_mt<WT, MODE, X86, 1>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, x86, stream); break;
         case 2: launch_fused_mt<WT, MODE, X86, 2>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, x86, stream); break;
         case 3: launch_fused_mt<WT, MODE, X86, 3>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, x86, stream); break;
@@ -550,15 +550,15 @@ void launch_fused_mode(const float* x, int64_t ldx, bool xvec, const uint8_t* w,
 
 template <int WT>
 void launch_fused_wt(bool f16, const float* x, int64_t ldx, bool xvec, const uint8_t* w, int64_t w_stride, float* y,
-                     int64_t ldy, float* part, int M, int N, int K, int RG, int S, int cps, int x86,
+                     int64_t ldy, float* part, int M, int N, int K, int RG, int S, int cps, int MT, int x86,
                      hipStream_t stream) {
     constexpr int Q = WT == T_Q8_0 ? T_Q8_0 : T_Q8_K;
     if (f16)
-        launch_fused_mode<WT, T_F16, false>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, x86, stream);
+        launch_fused_mode<WT, T_F16, false>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, MT, x86, stream);
     else if (Q == T_Q8_0 && x86)
-        launch_fused_mode<WT, Q, true>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, x86, stream);
+        launch_fused_mode<WT, Q, true>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, MT, x86, stream);
     else
-        launch_fused_mode<WT, Q, false>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, x86, stream);
+        launch_fused_mode<WT, Q, false>(x, ldx, xvec, w, w_stride, y, ldy, part, M, N, K, RG, S, cps, MT, x86, stream);
 }
 
 }  // namespace
@@ -603,7 +603,12 @@ namespace samhip {
 FusedPlan fused_skinny_plan(int M, int N, int K, int max_splits) {
     FusedPlan p{};
     p.rg = (N + FROWS - 1) / FROWS;
-    const int mb = (M + 127) / 128;   // blocks of up to 128 activation rows
+    // rows per block: up to 128, fewer while the grid would have fewer than
+    // 64 (row group, row block) workgroups (the decoder's 201 queries on 256
+    // weight rows: 7 blocks of 32 rows, 6.6 us per product instead of 13.5)
+    p.mt = std::min(4, (M + 31) / 32);
+    while (p.mt > 1 && int64_t(p.rg) * ((M + 32 * p.mt - 1) / (32 * p.mt)) < 64) p.mt /= 2;
+    const int mb = (M + 32 * p.mt - 1) / (32 * p.mt);
     const int groups = p.rg * mb;
     const int nchunks = (K + CHUNK - 1) / CHUNK;
     const int S = std::min(std::min(nchunks, std::max(1, max_splits)), std::max(1, (256 + groups - 1) / groups));
@@ -674,10 +679,10 @@ const char* launch_fused_skinny(int wtype, bool f16, const float* x, int64_t ldx
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     switch (wtype) {
-        case T_Q8_0: launch_fused_wt<T_Q8_0>(f16, x, ldx, xvec, wb, w_stride, y, ldy, p.splits > 1 ? part : nullptr, M, N, K, p.rg, p.splits, p.cps, x86, stream); break;
-        case T_Q4_K: launch_fused_wt<T_Q4_K>(f16, x, ldx, xvec, wb, w_stride, y, ldy, p.splits > 1 ? part : nullptr, M, N, K, p.rg, p.splits, p.cps, x86, stream); break;
-        case T_Q5_K: launch_fused_wt<T_Q5_K>(f16, x, ldx, xvec, wb, w_stride, y, ldy, p.splits > 1 ? part : nullptr, M, N, K, p.rg, p.splits, p.cps, x86, stream); break;
-        case T_Q6_K: launch_fused_wt<T_Q6_K>(f16, x, ldx, xvec, wb, w_stride, y, ldy, p.splits > 1 ? part : nullptr, M, N, K, p.rg, p.splits, p.cps, x86, stream); break;
+        case T_Q8_0: launch_fused_wt<T_Q8_0>(f16, x, ldx, xvec, wb, w_stride, y, ldy, p.splits > 1 ? part : nullptr, M, N, K, p.rg, p.splits, p.cps, p.mt, x86, stream); break;
+        case T_Q4_K: launch_fused_wt<T_Q4_K>(f16, x, ldx, xvec, wb, w_stride, y, ldy, p.splits > 1 ? part : nullptr, M, N, K, p.rg, p.splits, p.cps, p.mt, x86, stream); break;
+        case T_Q5_K: launch_fused_wt<T_Q5_K>(f16, x, ldx, xvec, wb, w_stride, y, ldy, p.splits > 1 ? part : nullptr, M, N, K, p.rg, p.splits, p.cps, p.mt, x86, stream); break;
+        case T_Q6_K: launch_fused_wt<T_Q6_K>(f16, x, ldx, xvec, wb, w_stride, y, ldy, p.splits > 1 ? part : nullptr, M, N, K, p.rg, p.splits, p.cps, p.mt, x86, stream); break;
         default: return nullptr;
     }
     if (p.splits > 1) {
