@@ -178,6 +178,51 @@ __device__ __forceinline__ void stage8_row_lds(const float* __restrict__ x, int6
     }
 }
 
+// Rows of up to 5120 values with no producing node folded in: two waves per
+// row (values [0, 2560) and [2560, K)), the row maximum combined through LDS,
+// so each wave holds half the row in registers and the workgroup stages two
+// rows.  Every wave of the workgroup must call it (one barrier).
+template <int MODE, bool X86>
+__device__ __forceinline__ void stage8_half_row(const float* __restrict__ x, int64_t x_stride, int m, int M, int K,
+                                                _Float16* __restrict__ a, int64_t lda, float* __restrict__ row_scale,
+                                                int lane, int wave, float* pair_max) {
+    constexpr int CHH = 5;
+    const int half = wave & 1;
+    const bool live = m < M;
+    const float* xr = x + int64_t(live ? m : 0) * x_stride;
+    floatx8 v[CHH];
+#pragma unroll
+    for (int c = 0; c < CHH; ++c) {
+        const int k = 2560 * half + 512 * c + 8 * lane;
+        if (live && k < K) {
+            const floatx4 lo = load4f(xr + k), hi = load4f(xr + k + 4);
+            v[c] = floatx8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        } else {
+            v[c] = floatx8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+    }
+    float rmax = 0.f;
+#pragma unroll
+    for (int c = 0; c < CHH; ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) rmax = fmaxf(rmax, fabsf(v[c][i]));
+    const float r32 = max32_lanes(rmax);
+    rmax = fmaxf(r32, __shfl_xor(r32, 32, 64));
+    if (lane == 0) pair_max[wave] = rmax;
+    __syncthreads();
+    rmax = fmaxf(pair_max[wave & ~1], pair_max[wave | 1]);
+    const int e = row_exponent(rmax);
+    const float down = exp2i(-e);
+    if (live && half == 0 && lane == 0) row_scale[m] = exp2i(e);
+    _Float16* ar = a + int64_t(live ? m : 0) * lda;
+#pragma unroll
+    for (int c = 0; c < CHH; ++c) {
+        const int k = 2560 * half + 512 * c + 8 * lane;
+        const half8 o = quant8<MODE, X86>(v[c], lane, down);
+        if (live && k < K) *reinterpret_cast<half8*>(ar + k) = o;
+    }
+}
+
 template <int MODE, int CH, bool X86>
 __global__ __launch_bounds__(256) void stage8_kernel(const float* __restrict__ x, int64_t x_stride, int M, int K,
                                                      _Float16* __restrict__ a, int64_t lda,
@@ -212,12 +257,22 @@ __global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ x, 
                                                    _Float16* __restrict__ a, int64_t lda, float* __restrict__ row_scale,
                                                    int stage_blocks, const uint8_t* __restrict__ W, int64_t w_stride,
                                                    int N, _Float16* __restrict__ wout, int64_t ldo, RowPre pre) {
-    // (without a PRE the register path keeps 4-5 waves per SIMD with every
-    // load of the row in flight at once, and measured 40 us against 47 for
-    // the slab at K = 4736)
+    // (without a PRE, rows past 2048 values go to two waves each: 53 VGPRs
+    // instead of 97, 39 us at K = 4736 against 41 for one wave per row and
+    // 47 for the slab)
     constexpr bool SLAB = CH > 4 && MODE != T_F16 && PRE == PRE_GELU;
+    constexpr bool PAIR = CH > 4 && PRE == PRE_NONE;   // two waves per row, two rows per workgroup
     __shared__ __attribute__((aligned(16))) uint8_t slabs[SLAB ? 4 * stage_lds_bytes<CH>() : 16];
-    if (int(blockIdx.x) < stage_blocks) {
+    if constexpr (PAIR) {
+        if (int(blockIdx.x) < stage_blocks) {
+            __shared__ float pair_max[4];
+            const int wave = threadIdx.x >> 6;
+            stage8_half_row<MODE, X86>(x, x_stride, blockIdx.x * 2 + (wave >> 1), M, K, a, lda, row_scale,
+                                       threadIdx.x & 63, wave, pair_max);
+            return;
+        }
+    }
+    if (!PAIR && int(blockIdx.x) < stage_blocks) {
         const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
         if (m < M) {
             if constexpr (SLAB)
@@ -492,12 +547,14 @@ bool launch_prep(int mode, int wtype, const float* x, int64_t x_stride, int M, i
     if (pre.kind == PRE_LAYER_NORM && (!pre.w || !pre.b || reinterpret_cast<uintptr_t>(pre.w) % 16 ||
                                        reinterpret_cast<uintptr_t>(pre.b) % 16 || K % 8))
         return false;
-    const int sb = (M + 3) / 4;
     const int64_t db = (int64_t(N) * (K / 32) * 2 + 255) / 256;
-    const dim3 grid(unsigned(sb + db)), block(256);
+    const dim3 block(256);
     const uint8_t* wb = static_cast<const uint8_t*>(w);
 #define SAMHIP_PREP(MODE, CH, X86, WT)                                                                               \
     do {                                                                                                             \
+        /* staging workgroups: four rows each, two for long rows with no PRE */                                    \
+        const int sb = (CH > 4 && pre.kind == PRE_NONE) ? (M + 1) / 2 : (M + 3) / 4;                                  \
+        const dim3 grid(unsigned(sb + db));                                                                          \
         if (pre.kind == PRE_GELU)                                                                                    \
             hipLaunchKernelGGL((prep_kernel<MODE, CH, X86, WT, PRE_GELU>), grid, block, 0, stream, x, x_stride, M, K, \
                                a, lda, row_scale, sb, wb, w_stride, N, wout, ldo, pre);                              \
