@@ -104,85 +104,15 @@ __device__ __forceinline__ void stage8_row(const float* __restrict__ x, int64_t 
     }
 }
 
-// Long rows (K up to 512*CH, CH > 4) through erf-GELU in Q8 modes: instead
-// of holding the whole row in registers (80 values per lane at K = 4736 and
-// the GELU's temporaries, which left two waves per SIMD), each 512-value
-// chunk is loaded, passed through PRE and quantized to its Q8 blocks at
-// once; the codes (int8) and block scales go to the wave's LDS slab and the
-// row maximum is kept running.  Once the row exponent is known the codes
-// come back from LDS as fp16(d * q * 2^-e), the same values stage8_row
-// writes.  X is read once.
-template <int CH>
-constexpr int stage_lds_bytes() { return CH * 512 + CH * 16 * 4; }
-
-template <int MODE, int CH, bool X86, int PRE>
-__device__ __forceinline__ void stage8_row_lds(const float* __restrict__ x, int64_t x_stride, int m, int K,
-                                               _Float16* __restrict__ a, int64_t lda, float* __restrict__ row_scale,
-                                               int lane, uint8_t* slab) {
-    static_assert(MODE == T_Q8_0 || MODE == T_Q8_K, "Q8 modes only");
-    const float* xr = x + int64_t(m) * x_stride;
-    uint8_t* codes = slab;                                        // [CH * 512] int8
-    float* ds = reinterpret_cast<float*>(slab + CH * 512);        // [CH * 16] block scales
-    float rmax = 0.f;
-    // the next chunk's loads are in flight while this one is quantized
-    auto fetch = [&](int c) {
-        const int k = 512 * c + 8 * lane;
-        floatx8 v{0, 0, 0, 0, 0, 0, 0, 0};
-        if (c < CH && k < K) {
-            const floatx4 lo = load4f(xr + k), hi = load4f(xr + k + 4);
-            v = floatx8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-        return v;
-    };
-    floatx8 next = fetch(0);
-    for (int c = 0; c < CH; ++c) {
-        floatx8 v = next;
-        next = fetch(c + 1);
-        if (PRE == PRE_GELU)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = gelu_erf(v[i]);   // gelu(0) = 0 keeps the padding
-#pragma unroll
-        for (int i = 0; i < 8; ++i) rmax = fmaxf(rmax, fabsf(v[i]));
-        float d, q[8];
-        quant8_codes<MODE, X86>(v, lane, d, q);
-        uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            w0 |= (uint32_t(int(q[i])) & 0xffu) << (8 * i);
-            w1 |= (uint32_t(int(q[i + 4])) & 0xffu) << (8 * i);
-        }
-        *reinterpret_cast<uint2*>(codes + 512 * c + 8 * lane) = uint2{w0, w1};
-        if (MODE == T_Q8_0 && (lane & 3) == 0) ds[16 * c + lane / 4] = d;
-        if (MODE == T_Q8_K && (lane & 31) == 0) ds[16 * c + lane / 32] = d;
-    }
-    const float r32 = max32_lanes(rmax);
-    rmax = fmaxf(r32, __shfl_xor(r32, 32, 64));
-    const int e = row_exponent(rmax);
-    const float down = exp2i(-e);
-    if (lane == 0) row_scale[m] = exp2i(e);
-    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the slab is written
-    __builtin_amdgcn_wave_barrier();
-    _Float16* ar = a + int64_t(m) * lda;
-    for (int c = 0; c < CH; ++c) {
-        const int k = 512 * c + 8 * lane;
-        if (k >= K) break;
-        const uint2 w = *reinterpret_cast<const uint2*>(codes + 512 * c + 8 * lane);
-        const float d = ds[16 * c + (MODE == T_Q8_0 ? lane / 4 : lane / 32)];
-        half8 o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            o[i] = (_Float16)((d * float(int8_t(w.x >> (8 * i)))) * down);
-            o[i + 4] = (_Float16)((d * float(int8_t(w.y >> (8 * i)))) * down);
-        }
-        *reinterpret_cast<half8*>(ar + k) = o;
-    }
-}
-
-// Rows of up to 5120 values with no producing node folded in: two waves per
-// row (values [0, 2560) and [2560, K)), the row maximum combined through LDS,
-// so each wave holds half the row in registers and the workgroup stages two
-// rows.  Every wave of the workgroup must call it (one barrier).
-template <int MODE, bool X86>
+// Rows of up to 5120 values (fc2's 4736), optionally through erf-GELU: two
+// waves per row (values [0, 2560) and [2560, K)), the row maximum combined
+// through LDS, so each wave holds half the row in registers and the
+// workgroup stages two rows.  Every wave of the workgroup must call it (one
+// barrier).  Measured against the alternatives at K = 4736: 39 us without
+// a PRE (one wave per row, 97 VGPRs: 41 us), 42 us with the erf-GELU (a
+// chunked pass parking the Q8 codes in LDS until the row maximum is known:
+// 43-44 us).
+template <int MODE, bool X86, int PRE>
 __device__ __forceinline__ void stage8_half_row(const float* __restrict__ x, int64_t x_stride, int m, int M, int K,
                                                 _Float16* __restrict__ a, int64_t lda, float* __restrict__ row_scale,
                                                 int lane, int wave, float* pair_max) {
@@ -201,6 +131,11 @@ __device__ __forceinline__ void stage8_half_row(const float* __restrict__ x, int
             v[c] = floatx8{0, 0, 0, 0, 0, 0, 0, 0};
         }
     }
+    if (PRE == PRE_GELU)
+#pragma unroll
+        for (int c = 0; c < CHH; ++c)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[c][i] = gelu_erf(v[c][i]);   // gelu(0) = 0 keeps the padding
     float rmax = 0.f;
 #pragma unroll
     for (int c = 0; c < CHH; ++c)
@@ -257,17 +192,13 @@ __global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ x, 
                                                    _Float16* __restrict__ a, int64_t lda, float* __restrict__ row_scale,
                                                    int stage_blocks, const uint8_t* __restrict__ W, int64_t w_stride,
                                                    int N, _Float16* __restrict__ wout, int64_t ldo, RowPre pre) {
-    // (without a PRE, rows past 2048 values go to two waves each: 53 VGPRs
-    // instead of 97, 39 us at K = 4736 against 41 for one wave per row and
-    // 47 for the slab)
-    constexpr bool SLAB = CH > 4 && MODE != T_F16 && PRE == PRE_GELU;
-    constexpr bool PAIR = CH > 4 && PRE == PRE_NONE;   // two waves per row, two rows per workgroup
-    __shared__ __attribute__((aligned(16))) uint8_t slabs[SLAB ? 4 * stage_lds_bytes<CH>() : 16];
+    // rows past 2048 values without a layer norm: two waves per row
+    constexpr bool PAIR = CH > 4 && (PRE == PRE_NONE || PRE == PRE_GELU);
     if constexpr (PAIR) {
         if (int(blockIdx.x) < stage_blocks) {
             __shared__ float pair_max[4];
             const int wave = threadIdx.x >> 6;
-            stage8_half_row<MODE, X86>(x, x_stride, blockIdx.x * 2 + (wave >> 1), M, K, a, lda, row_scale,
+            stage8_half_row<MODE, X86, PRE>(x, x_stride, blockIdx.x * 2 + (wave >> 1), M, K, a, lda, row_scale,
                                        threadIdx.x & 63, wave, pair_max);
             return;
         }
@@ -275,11 +206,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ x, 
     if (!PAIR && int(blockIdx.x) < stage_blocks) {
         const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
         if (m < M) {
-            if constexpr (SLAB)
-                stage8_row_lds<MODE, CH, X86, PRE>(x, x_stride, m, K, a, lda, row_scale, threadIdx.x & 63,
-                                                   slabs + (threadIdx.x >> 6) * stage_lds_bytes<CH>());
-            else
-                stage8_row<MODE, CH, X86, PRE>(x, x_stride, m, K, a, lda, row_scale, threadIdx.x & 63, pre);
+            stage8_row<MODE, CH, X86, PRE>(x, x_stride, m, K, a, lda, row_scale, threadIdx.x & 63, pre);
         }
         return;
     }
@@ -553,7 +480,7 @@ bool launch_prep(int mode, int wtype, const float* x, int64_t x_stride, int M, i
 #define SAMHIP_PREP(MODE, CH, X86, WT)                                                                               \
     do {                                                                                                             \
         /* staging workgroups: four rows each, two for long rows with no PRE */                                    \
-        const int sb = (CH > 4 && pre.kind == PRE_NONE) ? (M + 1) / 2 : (M + 3) / 4;                                  \
+        const int sb = (CH > 4 && pre.kind != PRE_LAYER_NORM) ? (M + 1) / 2 : (M + 3) / 4;                                  \
         const dim3 grid(unsigned(sb + db));                                                                          \
         if (pre.kind == PRE_GELU)                                                                                    \
             hipLaunchKernelGGL((prep_kernel<MODE, CH, X86, WT, PRE_GELU>), grid, block, 0, stream, x, x_stride, M, K, \
