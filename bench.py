@@ -12,6 +12,7 @@ timed region.  Prints one JSON line.
 """
 
 import argparse
+import collections
 import importlib.util
 import json
 import os
@@ -265,6 +266,39 @@ def cpu_baseline(plan, seconds, rows):
                       f"integer dots), OpenMP"}
 
 
+def stream_cpu_baseline(shape_counts, qt, seconds=10.0):
+    """The oracle's native-quantized CPU path on every distinct (M, N, K) of a
+    linear stream, each timed once per pass, the stream's time being the sum
+    over shapes of time x occurrences; reported as algorithmic GB/s like the
+    GPU line."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as O
+    O.lib()
+    threads = O.max_threads()
+    rb = {k: O.row_bytes(qt, k) for _, _, k in shape_counts}
+    data = {}
+    for m, n, k in shape_counts:
+        w = (np.random.default_rng(0).standard_normal((n, k)) * 0.02).astype(np.float32)
+        data[(m, n, k)] = (O.quantize(qt, w, O.ROUND_REF),
+                           np.random.default_rng(1).standard_normal((m, k)).astype(np.float32))
+    times = {key: 0.0 for key in shape_counts}
+    passes, spent = 0, 0.0
+    while spent < seconds and passes < 20:
+        for key, (w, x) in data.items():
+            t0 = time.perf_counter()
+            O.mul_mat_native(qt, w, x, O.ROUND_X86, threads)
+            dt = time.perf_counter() - t0
+            times[key] += dt
+            spent += dt
+        passes += 1
+    stream_s = sum(times[key] / passes * cnt for key, cnt in shape_counts.items())
+    alg = sum((n * rb[k] + m * k * 4 + m * n * 4) * cnt for (m, n, k), cnt in shape_counts.items())
+    return {"value": round(alg / stream_s / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"each of the {len(shape_counts)} distinct (M, N, K) of the stream timed {passes} times "
+                      f"({spent:.1f} s), weighted by its {sum(shape_counts.values())} occurrences; "
+                      f"oracle/ggml_oracle.c native path, OpenMP"}
+
+
 TEXT_LAYERS = 24
 TEXT_M = 32
 TEXT_SHAPES = [("in_proj", 1024, 3072), ("out_proj", 1024, 1024), ("fc1", 1024, 4096), ("fc2", 4096, 1024)]
@@ -347,6 +381,8 @@ def text_stream(args, sh, ctx, fmt):
                      "shape": {"M": TEXT_M, "N": 4096, "K": 1024}, "launch_ms": round(fc1_ms, 5),
                      "algorithmic_bytes_per_launch": int(fc1_bytes)},
         "eager_ms_per_step": round(eager * 1e3 / args.steps, 4),
+        "cpu_baseline": None if args.no_cpu_baseline else stream_cpu_baseline(
+            collections.Counter((TEXT_M, n, k) for _, k, n in shapes), qt, args.cpu_seconds),
         "replay": "one HIP graph launch per step (samhip_capture_begin/end)",
         "kernel_ms_per_step": round(sum(r[5] for r in kern), 4),
         "stage_ms_per_step": round(sum(r[5] for r in stage), 4),
@@ -475,6 +511,8 @@ def detector_stream(args, sh, ctx, fmt):
                      "frac": round(ach / PEAK_HBM_GBPS, 4), "traffic": None, "kernel": dom,
                      "launches": len(dom_recs), "launch_ms": round(dom_ms / len(dom_recs), 5)},
         "shapes": sorted(({**e, "ms": round(e["ms"], 4)} for e in shapes.values()), key=lambda e: -e["ms"]),
+        "cpu_baseline": None if args.no_cpu_baseline else stream_cpu_baseline(
+            collections.Counter((DET_M[p[6][0]], p[4], p[5]) for p in plan), qt, args.cpu_seconds),
         "replay": "one HIP graph launch per step (samhip_capture_begin/end)",
         "device": ctx.query().device_name.decode(),
     }
