@@ -374,10 +374,11 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
         const char* variant = strip_skinny_variant(w->type);
         if (!variant) return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no kernel for weight type %d", w->type);
         int rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
-            launch_strip_skinny(w->type, ctx->compute == SAMHIP_COMPUTE_F16, static_cast<const float*>(x->data),
-                                int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
-                                int64_t(y->nb[1] / 4), static_cast<float*>(ctx->staging), M, N, K,
-                                ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->stream);
+            if (!launch_strip_skinny(w->type, ctx->compute == SAMHIP_COMPUTE_F16, static_cast<const float*>(x->data),
+                                     int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
+                                     int64_t(y->nb[1] / 4), static_cast<float*>(ctx->staging), M, N, K,
+                                     ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->stream))
+                return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no strip kernel for this shape");
             HIP_TRY(hipGetLastError(), "strip skinny launch");
             return SAMHIP_OK;
         });
@@ -394,10 +395,12 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
         const char* variant = fused_skinny_variant(w->type);
         if (!variant) return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no kernel for weight type %d", w->type);
         int rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
-            launch_fused_skinny(w->type, ctx->compute == SAMHIP_COMPUTE_F16, static_cast<const float*>(x->data),
-                                int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
-                                int64_t(y->nb[1] / 4), static_cast<float*>(ctx->staging), M, N, K,
-                                ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->fused_max_splits, ctx->stream);
+            if (!launch_fused_skinny(w->type, ctx->compute == SAMHIP_COMPUTE_F16, static_cast<const float*>(x->data),
+                                     int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
+                                     int64_t(y->nb[1] / 4), static_cast<float*>(ctx->staging), M, N, K,
+                                     ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->fused_max_splits,
+                                     ctx->stream))
+                return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no fused kernel for this shape");
             HIP_TRY(hipGetLastError(), "fused skinny launch");
             return SAMHIP_OK;
         });
@@ -463,16 +466,18 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     } else if (M <= kSkinnyMaxM) {
         variant = skinny_variant(w->type, M, N);
         rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
-            launch_skinny(w->type, a, K, rs, w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
-                          int64_t(y->nb[1] / 4), M, N, K, ctx->stream);
+            if (!launch_skinny(w->type, a, K, rs, w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
+                               int64_t(y->nb[1] / 4), M, N, K, ctx->stream))
+                return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no skinny kernel for this shape");
             HIP_TRY(hipGetLastError(), "skinny launch");
             return SAMHIP_OK;
         });
         if (!rc) ctx->info.skinny_launches++;
     } else {
         rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
-            launch_gemm(w->type, a, K, rs, w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
-                        int64_t(y->nb[1] / 4), M, N, K, ctx->stream);
+            if (!launch_gemm(w->type, a, K, rs, w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
+                             int64_t(y->nb[1] / 4), M, N, K, ctx->stream))
+                return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no GEMM kernel for this shape");
             HIP_TRY(hipGetLastError(), "gemm launch");
             return SAMHIP_OK;
         });
