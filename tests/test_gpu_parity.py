@@ -316,6 +316,24 @@ def test_mul_mat_fused_split_k_deterministic(gpu_ctx, f16_ctx, oracle, samhip, q
     _check_product(oracle, qtype, w[n:], x, first, yf)
 
 
+@pytest.mark.parametrize("qtype", [8, 12])
+def test_mul_mat_fused_in_projection_views(gpu_ctx, f16_ctx, oracle, qtype):
+    """The fusion / decoder q, k, v products: row-offset views of a fused
+    [3D, D] in-projection (D = 256) against the image tokens (M = 5184, tiled
+    GEMM), the decoder queries (M = 201, fused kernel in 32-row blocks) and
+    the prompt tokens (M = 33), each compared in full."""
+    say("case fused in-projection views", qtype)
+    rng = np.random.default_rng(46)
+    d = 256
+    w = oracle.quantize(qtype, (rng.standard_normal((3 * d, d)) * 0.02).astype(np.float32))
+    for m in (5184, 201, 33):
+        x = rng.standard_normal((m, d)).astype(np.float32)
+        for part in range(3):
+            yn = gpu_ctx.matmul(qtype, w, x, w_row_offset=part * d, w_rows=d)
+            yf = f16_ctx.matmul(qtype, w, x, w_row_offset=part * d, w_rows=d)
+            _check_product(oracle, qtype, w[part * d:(part + 1) * d], x, yn, yf)
+
+
 @pytest.mark.parametrize("qtype", TYPES)
 def test_mul_mat_strip_path(gpu_ctx, samhip, oracle, monkeypatch, qtype):
     """M <= 32 takes the strip kernel where it is preferred (Q8_0, K <= 1024;
