@@ -365,6 +365,13 @@ def test_mul_mat_strip_path(gpu_ctx, samhip, oracle, monkeypatch, qtype):
             print(f"  strip vs fused m{m} n{n} k{k}: max {err:.2e}", flush=True)
             assert err <= 1e-5
             assert max_row_rel_l2(first, oracle.mul_mat_native(qtype, w, x)) <= ROW_REL_L2
+        # rows that are not 16-byte aligned (scalar activation loads)
+        m, n, k = 20, 96, 512
+        w = oracle.quantize(qtype, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        y = strip.matmul(qtype, w, x, x_row_stride=k + 1)
+        assert strip.query().kernel_variant.startswith(b"skinny_strip")
+        assert max_row_rel_l2(y, oracle.mul_mat_native(qtype, w, x)) <= ROW_REL_L2
     finally:
         strip.close()
         fused.close()
