@@ -364,7 +364,10 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     if (const char* why = mul_mat_problem(w, x, y)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "mul_mat: %s", why);
     const int K = int(w->ne[0]), N = int(w->ne[1]), M = int(x->ne[1]);
     if (int rc = set_device(ctx)) return rc;
-    const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K);
+    // tall products with a 256x256-sized weight (the fusion / decoder image
+    // tokens' q, k, v, out projections) run the fused kernel: one launch
+    const bool small_w = ctx->fused_skinny && int64_t(N) * K <= kFusedSmallW;
+    const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K) && !small_w;
     if (!tall && M <= kStripMaxM && ctx->fused_skinny && ctx->strip_skinny &&
         (ctx->strip_skinny == 2 || strip_skinny_preferred(w->type, K))) {
         // one launch per product (and a reduce when K > 1024): activation
@@ -388,7 +391,7 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
         std::snprintf(ctx->info.kernel_variant, sizeof(ctx->info.kernel_variant), "%s", variant);
         return SAMHIP_OK;
     }
-    if (!tall && M <= kFusedMaxM && ctx->fused_skinny) {
+    if (!tall && (M <= kFusedMaxM || small_w) && ctx->fused_skinny) {
         // one launch: activation packing, weight decode and product
         const FusedPlan plan = fused_skinny_plan(M, N, K, ctx->fused_max_splits);
         if (int rc = ensure_staging(ctx, std::max<size_t>(plan.part_bytes, 256))) return rc;

@@ -202,6 +202,8 @@ const char* launch_skinny(int wtype, const _Float16* a, int64_t lda, const float
 // range is split over workgroups their partial sums go through `part`
 // (FusedPlan::part_bytes) and a second, small launch adds them.
 constexpr int kFusedMaxM = 256;
+// ... and any M when the weight has at most this many elements
+constexpr int64_t kFusedSmallW = 256 * 256;
 struct FusedPlan {
     int rg, splits, cps;
     int mt;               // 32-row activation tiles per row block (fused kernel)

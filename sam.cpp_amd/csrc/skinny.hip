@@ -606,8 +606,9 @@ FusedPlan fused_skinny_plan(int M, int N, int K, int max_splits) {
     // rows per block: up to 128, fewer while the grid would have fewer than
     // 64 (row group, row block) workgroups (the decoder's 201 queries on 256
     // weight rows: 7 blocks of 32 rows, 6.6 us per product instead of 13.5)
+    const int64_t want = M > 256 ? 256 : 64;
     p.mt = std::min(4, (M + 31) / 32);
-    while (p.mt > 1 && int64_t(p.rg) * ((M + 32 * p.mt - 1) / (32 * p.mt)) < 64) p.mt /= 2;
+    while (p.mt > 1 && int64_t(p.rg) * ((M + 32 * p.mt - 1) / (32 * p.mt)) < want) p.mt /= 2;
     const int mb = (M + 32 * p.mt - 1) / (32 * p.mt);
     const int groups = p.rg * mb;
     const int nchunks = (K + CHUNK - 1) / CHUNK;
@@ -674,7 +675,7 @@ const char* fused_skinny_variant(int wtype) {
 const char* launch_fused_skinny(int wtype, bool f16, const float* x, int64_t ldx, const void* w, int64_t w_stride,
                                 float* y, int64_t ldy, float* part, int M, int N, int K, int x86, int max_splits,
                                 hipStream_t stream) {
-    if (M < 1 || M > kFusedMaxM || N < 1 || K < 32 || K % 32) return nullptr;
+    if (M < 1 || (M > kFusedMaxM && int64_t(N) * K > kFusedSmallW) || N < 1 || K < 32 || K % 32) return nullptr;
     const FusedPlan p = fused_skinny_plan(M, N, K, max_splits);
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
