@@ -75,6 +75,7 @@ struct samhip_context {
     int gemm_cfg = -1;
     bool fused_skinny = true;   // SAMHIP_FUSED_SKINNY=0 routes M < 256 through staging + the skinny kernel
     int strip_skinny = 1;       // SAMHIP_STRIP_SKINNY: 0 never, 1 where preferred, 2 every M <= 32 product
+    int attn_splits = 0;        // SAMHIP_ATTN_SPLITS: key splits of the attention kernel (0: by grid size)
     int fused_max_splits = 16;  // SAMHIP_FUSED_MAX_SPLITS: cap on the fused kernel's K splits
     samhip_exec_info info{};
     // per-launch event trace (samhip_trace_begin / samhip_trace_end)
@@ -271,6 +272,7 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
     ctx->tall_m = std::max(1, env_int("SAMHIP_TALL_M", ctx->tall_m));
     ctx->fused_skinny = env_int("SAMHIP_FUSED_SKINNY", 1) != 0;
     ctx->strip_skinny = env_int("SAMHIP_STRIP_SKINNY", 1);
+    ctx->attn_splits = std::max(0, env_int("SAMHIP_ATTN_SPLITS", 0));
     ctx->fused_max_splits = std::max(1, env_int("SAMHIP_FUSED_MAX_SPLITS", 16));
     const int cfg = env_int("SAMHIP_GEMM_CONFIG", -1);
     ctx->gemm_cfg = (cfg >= 0 && cfg < gemm_f16_config_count()) ? cfg : -1;
@@ -744,8 +746,11 @@ int samhip_flash_attn(samhip_context* ctx, const float* q, const float* k, const
     Carve c;
     size_t off[6];
     for (size_t& o : off) o = c.take(packed);
+    const size_t att_bytes = attention_scratch_bytes(int(batches), heads, int(n), true, ctx->cus, ctx->attn_splits);
+    const size_t o_att = c.take(att_bytes);
     if (int rc = ensure_work(ctx, c.used)) return rc;
     uint8_t* wb = static_cast<uint8_t*>(ctx->work);
+    float* att_scratch = att_bytes ? reinterpret_cast<float*>(wb + o_att) : nullptr;
     AttnOperands ops;
     _Float16** parts[6] = {&ops.q, &ops.k, &ops.v, &ops.ql, &ops.kl, &ops.vl};
     for (int i = 0; i < 6; ++i) *parts[i] = reinterpret_cast<_Float16*>(wb + off[i]);
@@ -756,7 +761,8 @@ int samhip_flash_attn(samhip_context* ctx, const float* q, const float* k, const
     });
     if (rc) return rc;
     return traced(ctx, "vit_attention", T_F32, batches * n, heads * 64, n, [&]() -> int {
-        launch_attention(ops, out, int64_t(heads) * 64, int(batches), heads, int(n), ctx->stream);
+        launch_attention(ops, out, int64_t(heads) * 64, int(batches), heads, int(n), att_scratch, ctx->cus,
+                         ctx->attn_splits, ctx->stream);
         HIP_TRY(hipGetLastError(), "attention launch");
         return SAMHIP_OK;
     });
@@ -795,8 +801,11 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
     const size_t packed = size_t(B * H * np * 64) * 2;
     size_t o_ops[6];
     for (int i = 0; i < (precise ? 6 : 3); ++i) o_ops[i] = c.take(packed);
+    const size_t att_bytes = attention_scratch_bytes(int(B), int(H), int(per), precise, ctx->cus, ctx->attn_splits);
+    const size_t o_att = c.take(att_bytes);
     if (int rc = ensure_work(ctx, c.used)) return rc;
     uint8_t* wb = static_cast<uint8_t*>(ctx->work);
+    float* att_scratch = att_bytes ? reinterpret_cast<float*>(wb + o_att) : nullptr;
     float* ln = reinterpret_cast<float*>(wb + o_ln);
     float* x1 = reinterpret_cast<float*>(wb + o_x1);
     float* h1 = reinterpret_cast<float*>(wb + o_h1);
@@ -844,7 +853,8 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
         if (rc) return rc;
     }
     rc = traced(ctx, "vit_attention", T_F32, T, E, per, [&]() -> int {
-        launch_attention(ops, ln, E, int(B), int(H), int(per), ctx->stream);
+        launch_attention(ops, ln, E, int(B), int(H), int(per), att_scratch, ctx->cus, ctx->attn_splits,
+                         ctx->stream);
         HIP_TRY(hipGetLastError(), "attention launch");
         return SAMHIP_OK;
     });

@@ -124,7 +124,14 @@ void launch_zero_pad(const AttnOperands& o, int B, int H, int N, hipStream_t str
 // softmax(Q K^T) V per (batch, head) on the packed operands (head dim 64);
 // out row b*N + n, columns h*64.. (row stride ldo floats).  F32-accurate
 // (split operands, three products each) when o carries the lo parts.
-void launch_attention(const AttnOperands& o, float* out, int64_t ldo, int B, int H, int N, hipStream_t stream);
+// softmax(Q K^T) V; when the grid is small against the CUs (SAM 3's global
+// blocks), the keys are split over up to 4 workgroups per query block whose
+// partials go through `scratch` (attention_scratch_bytes, 0 = no split) and
+// are merged in split order by a second launch.
+// force > 0 fixes the number of splits (SAMHIP_ATTN_SPLITS).
+size_t attention_scratch_bytes(int B, int H, int N, bool precise, int cus, int force);
+void launch_attention(const AttnOperands& o, float* out, int64_t ldo, int B, int H, int N, float* scratch, int cus,
+                      int force, hipStream_t stream);
 // Patch convolution operands as split fp16: A [T][3*Kp] = [hi | hi | lo] of
 // the image patches, W [E][3*Kp] = [hi | lo | hi] of the kernel rows, so
 // A W^T = hi*hi + hi*lo + lo*hi (F32-accurate); Kp = 3*p*p rounded up to 128.

@@ -14,6 +14,8 @@
 // adds, no contraction).  Built with MFMA results in VGPRs (Makefile): the
 // softmax reads every score, so accumulation registers would cost a copy
 // per value.
+#include <algorithm>
+
 #include "internal.hpp"
 
 #pragma clang fp contract(off)
@@ -209,7 +211,8 @@ constexpr float LOG2E = 1.44269504088896340736f;
 // LEVEL 0: fp16 operands; 1: split scores; 2: split scores and output.
 template <int QW, int LEVEL>   // waves per workgroup (32 queries each), precision level
 __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, float* __restrict__ out, int64_t ldo,
-                                                            int H, int N, int Np) {
+                                                            int H, int N, int Np, int S, float* __restrict__ part_o,
+                                                            float* __restrict__ part_ml) {
 #if defined(__HIP_DEVICE_COMPILE__)   // LDS-DMA builtins exist only in the device pass
     constexpr bool PRECISE = LEVEL > 0;         // split scores
     constexpr bool PRECISE_PV = LEVEL > 1;      // split weights and values too
@@ -219,7 +222,8 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
     constexpr int TB = 64 * 128;   // bytes of one 64-key tile of one part
     __shared__ __attribute__((aligned(1024))) uint8_t ktile[P][2][TB];
     __shared__ __attribute__((aligned(1024))) uint8_t vtile[PV][2][TB];
-    const int h = blockIdx.y, b = blockIdx.z;
+    // grid z = window x key split: split sp takes key tiles [kb0, kb1)
+    const int h = blockIdx.y, b = blockIdx.z / S, sp = blockIdx.z - b * S;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 31, hh = lane >> 5;
     const int64_t bh = int64_t(b) * H + h;
@@ -275,14 +279,15 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
 #pragma unroll
     for (int r = 0; r < 16; ++r) o0[r] = o1[r] = 0.f;
     float mrun = -__builtin_inff(), lsum = 0.f;
-    const int nkb = Np / 64;
+    const int nkb = Np / 64, per_split = (nkb + S - 1) / S;
+    const int kb0 = sp * per_split, kb1 = min(nkb, kb0 + per_split);
 
-    issue(0, 0);
+    issue(kb0, 0);
     wait_vmcnt0();
     __syncthreads();
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int buf = kb & 1;
-        if (kb + 1 < nkb) issue(kb + 1, buf ^ 1);   // that buffer's reads ended at the last barrier
+    for (int kb = kb0; kb < kb1; ++kb) {
+        const int buf = (kb - kb0) & 1;
+        if (kb + 1 < kb1) issue(kb + 1, buf ^ 1);   // that buffer's reads ended at the last barrier
         floatx16 s0, s1;
 #pragma unroll
         for (int r = 0; r < 16; ++r) s0[r] = s1[r] = 0.f;
@@ -386,15 +391,24 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
                 o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(l1, pf[0][u], o1, 0, 0, 0);
             }
         }
-        if (kb + 1 < nkb) {
+        if (kb + 1 < kb1) {
             wait_vmcnt0();   // this wave's loads of the next tile landed
             __syncthreads();
         }
     }
-    const float inv = 1.0f / (lsum + __shfl_xor(lsum, 32, 64));
+    const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+    const float inv = 1.0f / ltot;
     const int qo = q0 + li;
     if (qo < N) {
-        float* orow = out + (int64_t(b) * N + qo) * ldo + h * 64;
+        // one split: the output; several: this split's normalized partial,
+        // its exponent base and weight sum (attention_merge_kernel)
+        float* orow = S == 1 ? out + (int64_t(b) * N + qo) * ldo + h * 64
+                             : part_o + ((int64_t(sp) * gridDim.z / S + b) * N + qo) * (int64_t(H) * 64) + h * 64;
+        if (S > 1 && hh == 0) {
+            float* ml = part_ml + (((int64_t(sp) * gridDim.z / S + b) * N + qo) * H + h) * 2;
+            ml[0] = mrun;
+            ml[1] = ltot;
+        }
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int d0 = 8 * g + 4 * hh;
@@ -484,19 +498,89 @@ void launch_zero_pad(const AttnOperands& o, int B, int H, int N, hipStream_t str
                        N, np);
 }
 
-void launch_attention(const AttnOperands& o, float* out, int64_t ldo, int B, int H, int N, hipStream_t stream) {
+// O = sum_s w_s O_s / sum_s w_s with w_s = l_s exp(m_s - max m): the key
+// splits of one (window, query, head) combined in split order.  One thread
+// per 4 output values.
+__global__ __launch_bounds__(256) void attention_merge_kernel(const float* __restrict__ part_o,
+                                                              const float* __restrict__ part_ml,
+                                                              float* __restrict__ out, int64_t ldo, int rows, int H,
+                                                              int S) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;   // (row, head, 4-value group)
+    if (i >= int64_t(rows) * H * 16) return;
+    const int64_t row = i / (H * 16);
+    const int hg = int(i - row * H * 16), h = hg >> 4, g = hg & 15;
+    const int64_t plane_o = int64_t(rows) * H * 64, plane_ml = int64_t(rows) * H * 2;
+    float mmax = -__builtin_inff();
+    for (int sp = 0; sp < S; ++sp) mmax = fmaxf(mmax, part_ml[sp * plane_ml + (row * H + h) * 2]);
+    floatx4 acc{0.f, 0.f, 0.f, 0.f};
+    float wsum = 0.f;
+    for (int sp = 0; sp < S; ++sp) {
+        const float* ml = part_ml + sp * plane_ml + (row * H + h) * 2;
+        const float w = ml[1] * __builtin_amdgcn_exp2f((ml[0] - mmax) * LOG2E);
+        const floatx4 o = ld4(part_o + sp * plane_o + row * H * 64 + h * 64 + 4 * g);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] = acc[q] + w * o[q];
+        wsum = wsum + w;
+    }
+    const float inv = 1.0f / wsum;
+    *reinterpret_cast<floatx4*>(out + row * ldo + h * 64 + 4 * g) =
+        floatx4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+}
+
+// Key splits for a grid of `wgs` workgroups: the S in 1..4 that needs the
+// fewest rounds of resident workgroups per unit of work (two F32-accurate or
+// four fp16 workgroups per CU), each split keeping at least 8 key tiles.
+int attention_splits(int B, int H, int N, bool precise, int cus, int force) {
+    const int np = (N + 63) / 64 * 64, nkb = np / 64;
+    if (force > 0) {
+        // every split keeps at least one key tile
+        int S = std::max(1, std::min(force, nkb));
+        while (S > 1 && (S - 1) * ((nkb + S - 1) / S) >= nkb) --S;
+        return S;
+    }
+    const int64_t wgs = int64_t((np + 127) / 128) * H * B, slots = int64_t(precise ? 2 : 4) * cus;
+    int best = 1;
+    double best_cost = double((wgs + slots - 1) / slots);
+    for (int s = 2; s <= 4 && nkb >= 8 * s; ++s) {
+        const double cost = double((wgs * s + slots - 1) / slots) / s;
+        if (cost < best_cost * 0.95) {
+            best = s;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
+size_t attention_scratch_bytes(int B, int H, int N, bool precise, int cus, int force) {
+    const int S = attention_splits(B, H, N, precise, cus, force);
+    return S == 1 ? 0 : size_t(S) * B * N * H * (64 + 2) * 4;
+}
+
+void launch_attention(const AttnOperands& o, float* out, int64_t ldo, int B, int H, int N, float* scratch, int cus,
+                      int force, hipStream_t stream) {
     const int np = (N + 63) / 64 * 64;
+    const bool precise = o.ql && o.kl && o.vl;
+    const int S = scratch ? attention_splits(B, H, N, precise, cus, force) : 1;
+    float* part_o = S > 1 ? scratch : nullptr;
+    float* part_ml = S > 1 ? scratch + size_t(S) * B * N * H * 64 : nullptr;
     // 128-query workgroups: measured on the SAM 3 shapes against 64, 96 and
     // 192 (windowed 34 / 42 / 35 / 41 us, global 206 / 294 / 213 / 267 us;
     // 96 tiles 576 and 5184 queries exactly and still loses)
-    const dim3 grid(unsigned((np + 127) / 128), unsigned(H), unsigned(B));
+    const dim3 grid(unsigned((np + 127) / 128), unsigned(H), unsigned(B * S));
     // (splitting the scores alone, level 1, measured 6e-4 relative error per
     // output row at 2.8 ms per SAM 3 image against 5e-6 at 3.9 ms for level 2
     // and 4e-3 at 1.9 ms for level 0)
-    if (o.ql && o.kl && o.vl)
-        hipLaunchKernelGGL((attention_kernel<4, 2>), grid, dim3(256), 0, stream, o, out, ldo, H, N, np);
+    if (precise)
+        hipLaunchKernelGGL((attention_kernel<4, 2>), grid, dim3(256), 0, stream, o, out, ldo, H, N, np, S, part_o,
+                           part_ml);
     else
-        hipLaunchKernelGGL((attention_kernel<4, 0>), grid, dim3(256), 0, stream, o, out, ldo, H, N, np);
+        hipLaunchKernelGGL((attention_kernel<4, 0>), grid, dim3(256), 0, stream, o, out, ldo, H, N, np, S, part_o,
+                           part_ml);
+    if (S > 1) {
+        const int64_t n = int64_t(B) * N * H * 16;
+        hipLaunchKernelGGL(attention_merge_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, part_o,
+                           part_ml, out, ldo, B * N, H, S);
+    }
 }
 
 void launch_patch_columns(const float* image, int img, int patch, _Float16* a, float* row_scale, int kp,

@@ -70,6 +70,30 @@ def test_flash_attn(gpu_ctx, oracle, batches, n, heads):
     assert rel.max() < 1e-5 and np.median(rel) < 2e-6
 
 
+@pytest.mark.parametrize("splits", [2, 3, 4])
+def test_flash_attn_key_splits(samhip, oracle, monkeypatch, splits):
+    """Keys split over several workgroups per query block and merged
+    (SAMHIP_ATTN_SPLITS forces the count, which is cut back so that every
+    split keeps a key tile: 9 tiles at n = 576, a ragged last tile at 1000,
+    a peaked row): the merged result stays F32-accurate."""
+    monkeypatch.setenv("SAMHIP_ATTN_SPLITS", str(splits))
+    ctx = samhip.Context(0)
+    try:
+        for batches, n, heads in ((2, 576, 2), (1, 1000, 3), (1, 130, 1)):
+            rng = np.random.default_rng(n + splits)
+            q, k, v = (rng.standard_normal((batches * n, heads * 64)).astype(np.float32) for _ in range(3))
+            q[0] *= 40   # one query with a dominant key
+            say(f"flash_attn splits={splits} batches={batches} n={n} heads={heads}")
+            got = ctx.flash_attn(q, k, v, batches, heads, 0.125)
+            ref = np.concatenate([oracle.attention(q[b * n:(b + 1) * n], k[b * n:(b + 1) * n],
+                                                   v[b * n:(b + 1) * n], heads, 64, 0.125) for b in range(batches)])
+            rel = row_rel(got.reshape(-1, 64), ref.reshape(-1, 64))
+            say(f"  max {rel.max():.3g} median {np.median(rel):.3g}")
+            assert np.all(np.isfinite(got)) and rel.max() < 1e-5 and np.median(rel) < 2e-6
+    finally:
+        ctx.close()
+
+
 def test_flash_attn_rejects(gpu_ctx, samhip):
     x = np.zeros((64, 128), np.float32)
     with pytest.raises(samhip.SamhipError, match="head_dim"):
