@@ -74,7 +74,7 @@ struct samhip_context {
     int tall_m = 256;
     int gemm_cfg = -1;
     bool fused_skinny = true;   // SAMHIP_FUSED_SKINNY=0 routes M < 256 through staging + the skinny kernel
-    int strip_skinny = 1;       // SAMHIP_STRIP_SKINNY: 0 never, 1 where preferred, 2 every M <= 32 product
+    int strip_skinny = 1;       // SAMHIP_STRIP_SKINNY: 0 never, 1 where preferred, 2 every M < 256 product
     int attn_splits = 0;        // SAMHIP_ATTN_SPLITS: key splits of the attention kernel (0: by grid size)
     int fused_max_splits = 16;  // SAMHIP_FUSED_MAX_SPLITS: cap on the fused kernel's K splits
     samhip_exec_info info{};
@@ -371,7 +371,7 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     const bool small_w = ctx->fused_skinny && int64_t(N) * K <= kFusedSmallW;
     const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K) && !small_w;
     if (!tall && M <= kStripMaxM && ctx->fused_skinny && ctx->strip_skinny &&
-        (ctx->strip_skinny == 2 || strip_skinny_preferred(w->type, K))) {
+        (ctx->strip_skinny == 2 || strip_skinny_preferred(w->type, M, K))) {
         // one launch per product (and a reduce when K > 1024): activation
         // packing in registers, weight decode and product
         const FusedPlan plan = strip_skinny_plan(M, N, K);

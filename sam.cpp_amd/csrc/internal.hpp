@@ -225,11 +225,11 @@ const char* launch_fused_skinny(int wtype, bool f16, const float* x, int64_t ldx
 // Strip skinny products (M <= kStripMaxM): one launch per product while
 // K <= 1024 (four 256-wide chunks per workgroup), plus the split-K reduce
 // beyond; partial sums go through `part` (FusedPlan::part_bytes).
-constexpr int kStripMaxM = 32;
+constexpr int kStripMaxM = 256;   // in blocks of 32 activation rows
 // Where the strip kernel measured faster than the fused one: Q8_0 weights
 // with K <= 1024 (one launch).  K-quant pieces are read with scattered
 // per-lane loads and K > 1024 adds the reduce launch back.
-inline bool strip_skinny_preferred(int wtype, int K) { return wtype == T_Q8_0 && K <= 1024; }
+inline bool strip_skinny_preferred(int wtype, int M, int K) { return wtype == T_Q8_0 && K <= 1024 && M <= 32; }
 FusedPlan strip_skinny_plan(int M, int N, int K);
 const char* strip_skinny_variant(int wtype);
 const char* launch_strip_skinny(int wtype, bool f16, const float* x, int64_t ldx, const void* w, int64_t w_stride,

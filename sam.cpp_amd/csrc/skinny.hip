@@ -357,8 +357,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 }
 
 // ---------------------------------------------------------------------------
-// Strip path for M <= 32 (the text encoder's 32 tokens): one workgroup per
-// 32-row strip of W and group of four 256-wide K chunks, 16 waves, so that
+// Strip path for M < 256 (the text encoder's 32 tokens), in blocks of 32
+// activation rows: one workgroup per 32-row strip of W, row block and group
+// of four 256-wide K chunks, 16 waves, so that
 // a product with K <= 1024 is one launch with no partial sums in memory.
 //  * the waves copy the strip's packed bytes for the group with coalesced
 //    dword loads into LDS (odd dword row stride: conflict-free piece reads);
@@ -381,7 +382,8 @@ template <int WT, int MODE, bool X86, bool XVEC>
 __global__ __launch_bounds__(1024) void strip_skinny_kernel(const float* __restrict__ X, int64_t ldx,
                                                             const uint8_t* __restrict__ W, int64_t w_stride,
                                                             float* __restrict__ Y, int64_t ldy,
-                                                            float* __restrict__ part, int M, int N, int K, int RG) {
+                                                            float* __restrict__ part, int M, int N, int K, int RG,
+                                                            int S) {
     constexpr int CB = chunk_bytes<WT>();
     constexpr int WDW = strip_wdw<WT>();
     constexpr int RI = (WDW + 31) / 32;
@@ -394,10 +396,15 @@ __global__ __launch_bounds__(1024) void strip_skinny_kernel(const float* __restr
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 31, h = lane >> 5;
-    const int rg = blockIdx.x % RG, sp = blockIdx.x / RG;
+    const int rg = blockIdx.x % RG, sp = (blockIdx.x / RG) % S, mb = blockIdx.x / (RG * S);
     const int n0 = rg * 32;
     const int nchunks = (K + 255) / 256;
     const int cq = wave >> 2, c = 4 * sp + cq;   // this wave's chunk
+    // this workgroup's block of 32 activation rows
+    const int m0 = mb * 32, Mall = M;
+    X += int64_t(m0) * ldx;
+    Y += int64_t(m0) * ldy;
+    M = min(M - m0, 32);
     const bool active = c < nchunks;
 
     // 1. activations of chunk cq, rows 8 (w % 4) + 2 p + h, then the packed bytes
@@ -493,7 +500,7 @@ __global__ __launch_bounds__(1024) void strip_skinny_kernel(const float* __restr
     float v = 0.f;
 #pragma unroll
     for (int t = 0; t < 16; ++t) v += red[t * 16 * 64 + ri];
-    float* out = part ? part + int64_t(sp) * M * N : Y;
+    float* out = part ? part + (int64_t(sp) * Mall + m0) * N : Y;
     const int64_t ld = part ? int64_t(N) : ldy;
     if (m < M && n < N) out[int64_t(m) * ld + n] = v;
 }
@@ -501,13 +508,13 @@ __global__ __launch_bounds__(1024) void strip_skinny_kernel(const float* __restr
 template <int WT, int MODE, bool X86>
 void launch_strip_mode(bool xvec, const float* x, int64_t ldx, const uint8_t* w, int64_t w_stride, float* y,
                        int64_t ldy, float* part, int M, int N, int K, int RG, int S, hipStream_t stream) {
-    const dim3 grid(unsigned(RG * S)), block(1024);
+    const dim3 grid(unsigned(RG * S * ((M + 31) / 32))), block(1024);
     if (xvec)
         hipLaunchKernelGGL((strip_skinny_kernel<WT, MODE, X86, true>), grid, block, 0, stream, x, ldx, w, w_stride, y,
-                           ldy, part, M, N, K, RG);
+                           ldy, part, M, N, K, RG, S);
     else
         hipLaunchKernelGGL((strip_skinny_kernel<WT, MODE, X86, false>), grid, block, 0, stream, x, ldx, w, w_stride,
-                           y, ldy, part, M, N, K, RG);
+                           y, ldy, part, M, N, K, RG, S);
 }
 
 template <int WT>

@@ -348,13 +348,13 @@ def test_mul_mat_strip_path(gpu_ctx, samhip, oracle, monkeypatch, qtype):
     monkeypatch.setenv("SAMHIP_STRIP_SKINNY", "0")
     fused = samhip.Context(0)
     try:
-        for m, n, k in ((32, 4096, 1024), (32, 1024, 4096), (9, 70, 512)):
+        for m, n, k in ((32, 4096, 1024), (32, 1024, 4096), (9, 70, 512), (201, 256, 2048), (33, 300, 512)):
             w = oracle.quantize(qtype, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
             x = rng.standard_normal((m, k)).astype(np.float32)
             first = strip.matmul(qtype, w, x)
             assert strip.query().kernel_variant.startswith(b"skinny_strip")
             default = gpu_ctx.matmul(qtype, w, x)
-            preferred = qtype == 8 and k <= 1024
+            preferred = qtype == 8 and k <= 1024 and m <= 32
             assert gpu_ctx.query().kernel_variant.startswith(b"skinny_strip" if preferred else b"skinny_fused")
             if preferred:
                 assert np.array_equal(first, default)
