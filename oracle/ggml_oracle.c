@@ -348,18 +348,28 @@ static void pack_scale_min(const uint8_t ls[8], const uint8_t lm[8], uint8_t pac
     }
 }
 
-/* Shared body of the Q4_K/Q5_K reference quantizers: per 32-element
- * sub-block fit, 6-bit quantized scales/mins, then requantized codes. */
-static void kquant_asym_block(const float* x, uint8_t* header, int nmax, float rmin, int nstep, uint8_t codes[QKK]) {
-    float scales[8], mins[8], weights[32];
+/* First phase of the Q4_K/Q5_K quantizers: each 32-element sub-block fitted
+ * with the weights sqrt(mean x^2) + |x| (scales[j], mins[j] = -min, codes). */
+static void kquant_asym_fit(const float* x, int nmax, float rmin, int nstep, float scales[8], float mins[8],
+                            uint8_t codes[QKK]) {
+    float weights[32];
     uint8_t trial[32];
-    float max_scale = 0, max_min = 0;
     for (int j = 0; j < 8; ++j) {
         float sum_x2 = 0;
         for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
         const float av_x = sqrtf(sum_x2 / 32);
         for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
         scales[j] = fit_scale_min(32, nmax, x + 32 * j, weights, codes + 32 * j, &mins[j], trial, rmin, 0.1f, nstep);
+    }
+}
+
+/* Shared body of the Q4_K/Q5_K reference quantizers: per 32-element
+ * sub-block fit, 6-bit quantized scales/mins, then requantized codes. */
+static void kquant_asym_block(const float* x, uint8_t* header, int nmax, float rmin, int nstep, uint8_t codes[QKK]) {
+    float scales[8], mins[8];
+    float max_scale = 0, max_min = 0;
+    kquant_asym_fit(x, nmax, rmin, nstep, scales, mins, codes);
+    for (int j = 0; j < 8; ++j) {
         if (scales[j] > max_scale) max_scale = scales[j];
         if (mins[j] > max_min) max_min = mins[j];
     }
@@ -480,6 +490,12 @@ static float fit_scale_sym(int n, int nmax, const float* x, int8_t* codes) {
     return scale;
 }
 
+/* First phase of the Q6_K quantizer: each 16-element sub-block fitted
+ * symmetrically (scales[s], codes l + 32). */
+static void q6_k_fit(const float* xb, float scales[16], int8_t codes[QKK]) {
+    for (int s = 0; s < 16; ++s) scales[s] = fit_scale_sym(16, 32, xb + 16 * s, codes + 16 * s);
+}
+
 int or_quantize_q6_k(const float* x, void* y, int64_t rows, int64_t k) {
     if (k <= 0 || k % QKK || rows < 0) return -1;
     const int64_t nb = k / QKK;
@@ -490,8 +506,8 @@ int or_quantize_q6_k(const float* x, void* y, int64_t rows, int64_t k) {
             const float* xb = x + r * k + b * QKK;
             uint8_t* out = (uint8_t*)y + (r * nb + b) * 210;
             float max_scale = 0, max_abs = 0;
+            q6_k_fit(xb, scales, codes);
             for (int s = 0; s < 16; ++s) {
-                scales[s] = fit_scale_sym(16, 32, xb + 16 * s, codes + 16 * s);
                 const float a = fabsf(scales[s]);
                 if (a > max_abs) { max_abs = a; max_scale = scales[s]; }
             }
@@ -524,6 +540,109 @@ int or_quantize_q6_k(const float* x, void* y, int64_t rows, int64_t k) {
                     qh[32 * h + l] = (uint8_t)(((c[l] >> 4) & 3) | (((c[l + 32] >> 4) & 3) << 2) |
                                                (((c[l + 64] >> 4) & 3) << 4) | (((c[l + 96] >> 4) & 3) << 6));
                 }
+            }
+        }
+    }
+    return 0;
+}
+
+int or_kquant_fit(int type, const float* x, float* scales, float* mins, uint8_t* codes) {
+    switch (type) {
+        case OR_Q4_K: kquant_asym_fit(x, 15, -1.f, 20, scales, mins, codes); return 0;
+        case OR_Q5_K: kquant_asym_fit(x, 31, -0.5f, 15, scales, mins, codes); return 0;
+        case OR_Q6_K: q6_k_fit(x, scales, (int8_t*)codes); return 0;
+        default: return -1;
+    }
+}
+
+/* ---- ggml-cuda activation formats --------------------------------------- */
+
+/* quantize_q8_1 (MMVQ right operand, as pinned by tools/validation/
+ * verify_q8_rhs_staging.py:24-83): d = amax/127, q = roundf(x/d) (ties away),
+ * zero block -> zeros; stored half d and half of the original values' sum,
+ * reduced in the 32-lane xor-butterfly order (offsets 16, 8, 4, 2, 1). */
+static void q8_1_block(const float* x, uint8_t* out) {
+    float amax = 0.f;
+    for (int j = 0; j < QK8; ++j) {
+        const float a = fabsf(x[j]);
+        amax = a > amax ? a : amax;
+    }
+    float lanes[QK8];
+    memcpy(lanes, x, sizeof(lanes));
+    for (int off = 16; off > 0; off >>= 1) {
+        float next[QK8];
+        for (int j = 0; j < QK8; ++j) next[j] = lanes[j] + lanes[j ^ off];
+        memcpy(lanes, next, sizeof(lanes));
+    }
+    const float d = amax / 127.f;
+    int8_t* q = (int8_t*)(out + 4);
+    for (int j = 0; j < QK8; ++j) q[j] = (int8_t)(amax == 0.f ? 0.f : roundf(x[j] / d));
+    put_f16(out, d);
+    put_f16(out + 2, lanes[0]);
+}
+
+int or_quantize_q8_1(const float* x, void* y, int64_t rows, int64_t k) {
+    if (k <= 0 || k % QK8 || rows < 0) return -1;
+    const int64_t nb = k / QK8;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t b = 0; b < nb; ++b) q8_1_block(x + r * k + b * QK8, (uint8_t*)y + (r * nb + b) * 36);
+    return 0;
+}
+
+/* The native-activation range rule (cmake/patches/ggml-native-activation.patch:
+ * 148-171, tools/quantize/native_activation.py:24-40): finite values, and
+ * each nonzero 32-value block maximum in [1e-30, 1e30], compared as F32 bit
+ * patterns (no flush of subnormals).  1 when every block passes. */
+int or_q8_rhs_supported(const float* x, int64_t rows, int64_t k) {
+    if (k <= 0 || k % QK8 || rows < 0) return 0;
+    uint32_t lower, upper;
+    const float lo = 1.e-30f, hi = 1.e30f;
+    memcpy(&lower, &lo, 4);
+    memcpy(&upper, &hi, 4);
+    for (int64_t i = 0; i < rows * k; i += QK8) {
+        uint32_t maximum = 0;
+        for (int j = 0; j < QK8; ++j) {
+            uint32_t bits;
+            memcpy(&bits, x + i + j, 4);
+            bits &= 0x7fffffffu;
+            if (bits >= 0x7f800000u) return 0;
+            maximum = bits > maximum ? bits : maximum;
+        }
+        if (maximum > upper || (maximum != 0 && maximum < lower)) return 0;
+    }
+    return 1;
+}
+
+/* quantize_mmq_q8_1 with the D4 layout (ggml-cuda MMQ right operand for
+ * Q8_0 weights, K padded to 512 with zeros; tools/quantize/
+ * native_activation.py:42-62): d_inv = 127/amax (correctly rounded,
+ * cmake/patches/ggml-precise-cuda.patch:627-633), q = roundf(x * d_inv),
+ * stored F32 scale d = 1/d_inv, zero block -> zeros.  Layout [kp/128 tile]
+ * [row][4 F32 scales | 128 codes] = 144 B per row and tile. */
+int64_t or_q8_1_mmq_bytes(int64_t rows, int64_t k) { return (k + 511) / 512 * 4 * rows * 144; }
+
+int or_quantize_q8_1_mmq(const float* x, void* y, int64_t rows, int64_t k) {
+    if (k <= 0 || k % QK8 || rows < 0) return -1;
+    const int64_t kp = (k + 511) / 512 * 512, tiles = kp / 128;
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int64_t t = 0; t < tiles; ++t) {
+            uint8_t* out = (uint8_t*)y + (t * rows + r) * 144;
+            for (int s = 0; s < 4; ++s) {
+                const int64_t k0 = t * 128 + s * 32;
+                float v[QK8];
+                for (int j = 0; j < QK8; ++j) v[j] = k0 + j < k ? x[r * k + k0 + j] : 0.f;
+                float amax = 0.f;
+                for (int j = 0; j < QK8; ++j) amax = fabsf(v[j]) > amax ? fabsf(v[j]) : amax;
+                float d = 0.f;
+                int8_t* q = (int8_t*)(out + 16 + 32 * s);
+                if (amax != 0.f) {
+                    const float d_inv = 127.f / amax;
+                    for (int j = 0; j < QK8; ++j) q[j] = (int8_t)roundf(v[j] * d_inv);
+                    d = 1.f / d_inv;
+                } else {
+                    memset(q, 0, QK8);
+                }
+                memcpy(out + 4 * s, &d, 4);
             }
         }
     }

@@ -70,6 +70,24 @@ int or_quantize_q6_k(const float* x, void* y, int64_t rows, int64_t k);
  * weights (q8_0 uses the reference rounding). Returns bytes written or -1. */
 int64_t or_quantize_chunk(int type, const float* x, void* y, int64_t rows, int64_t k);
 
+/* First phase of the K-quant weight quantizers on one 256-value super-block,
+ * exposed so tests can check it against the published candidate search:
+ * Q4_K/Q5_K: scales[8], mins[8] (= -min >= 0) and codes[256] in [0, nmax]
+ * of the weighted least-squares fit of each 32-element sub-block;
+ * Q6_K: scales[16] and codes[256] (l + 32) of each 16-element sub-block's
+ * symmetric fit (mins unused).  Returns -1 for other types. */
+int or_kquant_fit(int type, const float* x, float* scales, float* mins, uint8_t* codes);
+
+/* ggml-cuda right-operand formats: Q8_1 rows (36 B per 32 values: half d,
+ * half original sum, 32 codes) and the MMQ D4 staging of Q8_0 products
+ * ([ceil(k/512)*4 tiles][rows][144 B]; or_q8_1_mmq_bytes gives the size). */
+int or_quantize_q8_1(const float* x, void* y, int64_t rows, int64_t k);
+int64_t or_q8_1_mmq_bytes(int64_t rows, int64_t k);
+int or_quantize_q8_1_mmq(const float* x, void* y, int64_t rows, int64_t k);
+/* 1 when x is finite with every nonzero 32-value block maximum in
+ * [1e-30, 1e30] (the native activation's fail-closed range rule). */
+int or_q8_rhs_supported(const float* x, int64_t rows, int64_t k);
+
 /* to_float for Q8_0/Q4_K/Q5_K/Q6_K/Q8_K rows. */
 int or_dequantize(int type, const void* x, float* y, int64_t rows, int64_t k);
 

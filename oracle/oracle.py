@@ -14,11 +14,11 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libggml_oracle.so")
 
-F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K = 0, 1, 8, 12, 13, 14, 15
+F32, F16, Q8_0, Q8_1, Q4_K, Q5_K, Q6_K, Q8_K = 0, 1, 8, 9, 12, 13, 14, 15
 ROUND_REF, ROUND_X86 = 0, 1
-BLOCK_ELEMS = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256}
-BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292}
-NAMES = {Q8_0: "q8_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K"}
+BLOCK_ELEMS = {Q8_0: 32, Q8_1: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256}
+BLOCK_BYTES = {Q8_0: 34, Q8_1: 36, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292}
+NAMES = {Q8_0: "q8_0", Q8_1: "q8_1", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K"}
 
 _lib = None
 
@@ -59,6 +59,12 @@ def lib():
         L.or_quantize_chunk.argtypes = [I, P, P, I64, I64]
         L.or_quantize_chunk.restype = I64
         L.or_dequantize.argtypes = [I, P, P, I64, I64]
+        L.or_kquant_fit.argtypes = [I, P, P, P, P]
+        L.or_quantize_q8_1.argtypes = [P, P, I64, I64]
+        L.or_q8_1_mmq_bytes.argtypes = [I64, I64]
+        L.or_q8_1_mmq_bytes.restype = I64
+        L.or_quantize_q8_1_mmq.argtypes = [P, P, I64, I64]
+        L.or_q8_rhs_supported.argtypes = [P, I64, I64]
         L.or_vec_dot.argtypes = [I, P, P, I64]
         L.or_vec_dot.restype = ctypes.c_float
         L.or_mul_mat_native.argtypes = [I, P, ctypes.c_size_t, P, ctypes.c_size_t, P, I64, I64, I64, I, I]
@@ -119,11 +125,42 @@ def quantize(qtype, x, rounding=ROUND_REF):
         rc = lib().or_quantize_q8_0(_ptr(x), _ptr(out), rows, k, rounding)
     elif qtype == Q8_K:
         rc = lib().or_quantize_q8_k(_ptr(x), _ptr(out), rows, k)
+    elif qtype == Q8_1:
+        rc = lib().or_quantize_q8_1(_ptr(x), _ptr(out), rows, k)
     else:
         rc = 0 if lib().or_quantize_chunk(qtype, _ptr(x), _ptr(out), rows, k) == out.size else -1
     if rc:
         raise ValueError("oracle quantize rejected shape")
     return out
+
+
+def kquant_fit(qtype, x256):
+    """First phase of a K-quant weight quantizer on one super-block:
+    (scales, mins, codes) — mins is None for Q6_K."""
+    x = np.ascontiguousarray(x256, np.float32).reshape(256)
+    n = 16 if qtype == Q6_K else 8
+    scales = np.zeros(n, np.float32)
+    mins = np.zeros(n, np.float32)
+    codes = np.zeros(256, np.uint8)
+    if lib().or_kquant_fit(qtype, _ptr(x), _ptr(scales), _ptr(mins), _ptr(codes)):
+        raise ValueError("oracle kquant_fit: not a K-quant type")
+    return scales, (None if qtype == Q6_K else mins), codes
+
+
+def quantize_q8_1_mmq(x):
+    """ggml-cuda MMQ D4 staging: bytes [ceil(k/512)*4][rows][144]."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, k = x.shape
+    out = np.zeros(int(lib().or_q8_1_mmq_bytes(rows, k)), np.uint8)
+    if lib().or_quantize_q8_1_mmq(_ptr(x), _ptr(out), rows, k):
+        raise ValueError("oracle quantize_q8_1_mmq rejected shape")
+    return out
+
+
+def q8_rhs_supported(x):
+    x = np.ascontiguousarray(x, np.float32)
+    rows, k = x.shape
+    return bool(lib().or_q8_rhs_supported(_ptr(x), rows, k))
 
 
 def dequantize(qtype, packed, k):
