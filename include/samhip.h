@@ -38,6 +38,7 @@ enum samhip_type {
     SAMHIP_TYPE_F32 = 0,
     SAMHIP_TYPE_F16 = 1,
     SAMHIP_TYPE_Q8_0 = 8,
+    SAMHIP_TYPE_Q8_1 = 9,
     SAMHIP_TYPE_Q4_K = 12,
     SAMHIP_TYPE_Q5_K = 13,
     SAMHIP_TYPE_Q6_K = 14,
@@ -136,6 +137,15 @@ int samhip_tensor_set(samhip_context* ctx, void* device_dst, const void* host_sr
 int samhip_tensor_get(samhip_context* ctx, void* host_dst, const void* device_src, size_t bytes);
 
 /* --- operators ------------------------------------------------------------ */
+/* The native activation's fail-closed range check for mul_mat (the
+ * reference runs it on every native-activation product,
+ * cmake/patches/ggml-native-activation.patch:148-171): when enabled, a
+ * Q8_NATIVE mul_mat first checks X and returns INVALID_ARGUMENT, computing
+ * nothing, if a value is non-finite or a nonzero 32-value block maximum lies
+ * outside [1e-30, 1e30].  Off by default; the check synchronizes the stream,
+ * so checked products cannot be captured. */
+int samhip_context_set_activation_check(samhip_context* ctx, int enabled);
+
 /* 1 if mul_mat(w, x, y) has a kernel, else 0; asked before execution so an
  * unsupported node is a runtime error, not a crash (ggml_backend_supports_op
  * at src/runtime/ggml/graph.hpp:65-78). */
@@ -157,11 +167,32 @@ int samhip_get_rows(samhip_context* ctx, const samhip_tensor* src, const samhip_
  *         ggml_cast F32 -> Q8_0 of the Q8_0 feature cache,
  *         src/models/sam3/execution.hpp:76-83)
  *   Q8_K: quantize_row_q8_K_ref (CPU activation packing for K weights)
+ *   Q8_1: ggml-cuda's MMVQ right operand (quantize_row_q8_1_cuda, exported by
+ *         the SAM-patched ggml and driven by tools/quantize/
+ *         cuda_q8_rhs_probe.cu:15-20, 74-80): 36-byte blocks of half
+ *         d = amax/127, half sum of the original values (32-lane xor-butterfly
+ *         order), codes roundf(x/d); q8_rounding is ignored
  *   Q4_K, Q5_K, Q6_K: quantize_row_q*_K_ref (ggml_quantize_chunk without
  *         importance weights; tools/quantize/quantize_rows.cpp:210)
  * src rows have `src_row_stride` bytes, dst rows are packed back to back. */
 int samhip_quantize_rows(samhip_context* ctx, int32_t type, const float* src, size_t src_row_stride,
                          void* dst, int64_t rows, int64_t k, int32_t q8_rounding);
+
+/* ggml-cuda's MMQ right operand for Q8_0 weights in the D4 layout
+ * (quantize_mmq_q8_1_cuda as patched at cmake/patches/ggml-precise-cuda.patch:
+ * 622-633; layout tools/quantize/native_activation.py:13-20, 42-62): rows
+ * padded with zeros to a multiple of 512 values, then for 128-value tile t of
+ * row r, dst + (t*rows + r)*144 holds 4 F32 scales 1/d_inv (d_inv = 127/amax
+ * per 32 values, correctly rounded) and the 128 codes roundf(x*d_inv).
+ * Fails closed like sam_q8_rhs_validate
+ * (cmake/patches/ggml-native-activation.patch:148-171): a non-finite value or
+ * a nonzero 32-value block maximum outside [1e-30, 1e30] returns
+ * INVALID_ARGUMENT (dst contents then unspecified).  Synchronizes the
+ * stream; not capturable.  dst must be 4-byte aligned and hold
+ * samhip_q8_1_mmq_bytes(rows, k) bytes. */
+size_t samhip_q8_1_mmq_bytes(int64_t rows, int64_t k);
+int samhip_quantize_rows_q8_1_mmq(samhip_context* ctx, const float* src, size_t src_row_stride, void* dst,
+                                  int64_t rows, int64_t k);
 
 /* ggml to_float on the device for F16/Q8_0/Q4_K/Q5_K/Q6_K/Q8_K rows
  * (bit-exact; F16 rows need k % 32 == 0). */

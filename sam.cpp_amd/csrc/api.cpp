@@ -77,6 +77,7 @@ struct samhip_context {
     int strip_skinny = 1;       // SAMHIP_STRIP_SKINNY: 0 never, 1 where preferred, 2 every M < 256 product
     int attn_splits = 0;        // SAMHIP_ATTN_SPLITS: key splits of the attention kernel (0: by grid size)
     int fused_max_splits = 16;  // SAMHIP_FUSED_MAX_SPLITS: cap on the fused kernel's K splits
+    bool check_activations = false;   // samhip_context_set_activation_check
     samhip_exec_info info{};
     // per-launch event trace (samhip_trace_begin / samhip_trace_end)
     struct TraceRecord {
@@ -361,11 +362,43 @@ int samhip_supports_mul_mat(const samhip_tensor* w, const samhip_tensor* x, cons
     return mul_mat_problem(w, x, y) == nullptr ? 1 : 0;
 }
 
+namespace {
+
+// Reads back the device flag a range check or D4 staging launch raised.
+int read_range_flag(samhip_context* ctx) {
+    int bad = 0;
+    HIP_TRY(hipMemcpyAsync(&bad, ctx->flag, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "hipMemcpyAsync");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (bad)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT,
+                    "native Q8 activations require finite F32 and each nonzero block maximum in [1e-30,1e30]");
+    return SAMHIP_OK;
+}
+
+int check_q8_rhs(samhip_context* ctx, const float* x, int64_t x_stride, int rows, int K) {
+    HIP_TRY(hipMemsetAsync(ctx->flag, 0, sizeof(int), ctx->stream), "hipMemsetAsync");
+    launch_q8_rhs_check(x, x_stride, rows, K, ctx->flag, ctx->stream);
+    HIP_TRY(hipGetLastError(), "activation check launch");
+    return read_range_flag(ctx);
+}
+
+}  // namespace
+
+int samhip_context_set_activation_check(samhip_context* ctx, int enabled) {
+    if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    ctx->check_activations = enabled != 0;
+    return SAMHIP_OK;
+}
+
 int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_tensor* x, const samhip_tensor* y) {
     if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
     if (const char* why = mul_mat_problem(w, x, y)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "mul_mat: %s", why);
     const int K = int(w->ne[0]), N = int(w->ne[1]), M = int(x->ne[1]);
     if (int rc = set_device(ctx)) return rc;
+    if (ctx->check_activations && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE) {
+        SAMHIP_NOT_WHILE_CAPTURING(ctx, "mul_mat with the activation check");
+        if (int rc = check_q8_rhs(ctx, static_cast<const float*>(x->data), int64_t(x->nb[1] / 4), M, K)) return rc;
+    }
     // tall products with a 256x256-sized weight (the fusion / decoder image
     // tokens' q, k, v, out projections) run the fused kernel: one launch
     const bool small_w = ctx->fused_skinny && int64_t(N) * K <= kFusedSmallW;
@@ -527,7 +560,8 @@ int samhip_get_rows(samhip_context* ctx, const samhip_tensor* src, const samhip_
 int samhip_quantize_rows(samhip_context* ctx, int32_t type, const float* src, size_t src_row_stride, void* dst,
                          int64_t rows, int64_t k, int32_t q8_rounding) {
     if (!ctx || !src || !dst || rows <= 0 || k <= 0) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: invalid argument");
-    if (type != T_F16 && type != T_Q8_0 && type != T_Q8_K && type != T_Q4_K && type != T_Q5_K && type != T_Q6_K)
+    if (type != T_F16 && type != T_Q8_0 && type != T_Q8_1 && type != T_Q8_K && type != T_Q4_K && type != T_Q5_K &&
+        type != T_Q6_K)
         return fail(SAMHIP_ERR_UNSUPPORTED, "quantize_rows: unsupported type %d", type);
     if (k % block_elems(type)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: k must be a multiple of %d", block_elems(type));
     if (src_row_stride < size_t(4 * k) || src_row_stride % 4 || reinterpret_cast<uintptr_t>(src) % 4)
@@ -536,18 +570,42 @@ int samhip_quantize_rows(samhip_context* ctx, int32_t type, const float* src, si
         return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: unknown Q8 rounding");
     if ((type == T_Q8_K) && reinterpret_cast<uintptr_t>(dst) % 4) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: Q8_K dst must be 4-byte aligned");
     if (rows > (int64_t(1) << 30) || k > (int64_t(1) << 24)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: too large");
-    if (type == T_F16 && reinterpret_cast<uintptr_t>(dst) % 2)
-        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: F16 dst must be 2-byte aligned");
+    if ((type == T_F16 || type == T_Q8_1) && reinterpret_cast<uintptr_t>(dst) % 2)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows: F16 and Q8_1 dst must be 2-byte aligned");
     if (int rc = set_device(ctx)) return rc;
     if (type == T_F16)
         launch_cast_f16(src, int64_t(src_row_stride / 4), int(rows), int(k), static_cast<_Float16*>(dst), ctx->stream);
     else if (type == T_Q8_0 || type == T_Q8_K)
         launch_quantize_act(type, src, int64_t(src_row_stride / 4), int(rows), int(k), dst,
                             q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->stream);
+    else if (type == T_Q8_1)
+        launch_quantize_q8_1(src, int64_t(src_row_stride / 4), int(rows), int(k), dst, ctx->stream);
     else
         launch_quantize_weights(type, src, int64_t(src_row_stride / 4), int(rows), int(k), dst, ctx->stream);
     HIP_TRY(hipGetLastError(), "quantize launch");
     return SAMHIP_OK;
+}
+
+size_t samhip_q8_1_mmq_bytes(int64_t rows, int64_t k) {
+    if (rows <= 0 || k <= 0) return 0;
+    return size_t((k + 511) / 512) * 4 * size_t(rows) * 144;
+}
+
+int samhip_quantize_rows_q8_1_mmq(samhip_context* ctx, const float* src, size_t src_row_stride, void* dst,
+                                  int64_t rows, int64_t k) {
+    if (!ctx || !src || !dst || rows <= 0 || k <= 0 || k % 32)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "native MMQ Q8 RHS needs nonempty 32-aligned rows");
+    if (src_row_stride < size_t(4 * k) || src_row_stride % 4 || reinterpret_cast<uintptr_t>(src) % 4 ||
+        reinterpret_cast<uintptr_t>(dst) % 4)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows_q8_1_mmq: invalid stride or alignment");
+    if (rows > (int64_t(1) << 24) || k > (int64_t(1) << 24))
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT, "quantize_rows_q8_1_mmq: too large");
+    SAMHIP_NOT_WHILE_CAPTURING(ctx, "quantize_rows_q8_1_mmq");
+    if (int rc = set_device(ctx)) return rc;
+    HIP_TRY(hipMemsetAsync(ctx->flag, 0, sizeof(int), ctx->stream), "hipMemsetAsync");
+    launch_quantize_q8_1_mmq(src, int64_t(src_row_stride / 4), int(rows), int(k), dst, ctx->flag, ctx->stream);
+    HIP_TRY(hipGetLastError(), "quantize_rows_q8_1_mmq launch");
+    return read_range_flag(ctx);
 }
 
 int samhip_dequantize_rows(samhip_context* ctx, int32_t type, const void* src, size_t src_row_stride, float* dst,

@@ -9,6 +9,7 @@
 //   Q4_K : f16 d @0, f16 dmin @2, u8 sc[12] @4, u8 qs[128] @16   144 B / 256
 //   Q5_K : Q4_K header, u8 qh[32] @16, u8 qs[128] @48            176 B / 256
 //   Q6_K : u8 ql[128] @0, u8 qh[64] @128, i8 sc[16] @192, f16 d @208  210 B / 256
+//   Q8_1 : f16 d @0, f16 s @2, i8 q[32] @4                       36 B / 32
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -16,7 +17,8 @@
 
 namespace samhip {
 
-enum : int { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_Q8_K = 15, T_I32 = 26 };
+enum : int { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q8_1 = 9, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_Q8_K = 15,
+              T_I32 = 26 };
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
@@ -25,11 +27,11 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __host__ __device__ constexpr int block_elems(int t) {
-    return t == T_Q8_0 ? 32 : (t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_Q8_K) ? 256 : 1;
+    return (t == T_Q8_0 || t == T_Q8_1) ? 32 : (t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_Q8_K) ? 256 : 1;
 }
 __host__ __device__ constexpr int block_bytes(int t) {
-    return t == T_Q8_0 ? 34 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : t == T_Q8_K ? 292
-         : t == T_F16 ? 2 : 4;
+    return t == T_Q8_0 ? 34 : t == T_Q8_1 ? 36 : t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210
+         : t == T_Q8_K ? 292 : t == T_F16 ? 2 : 4;
 }
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {

@@ -13,6 +13,16 @@ void launch_stage_rows(int mode, bool aligned, const float* x, int64_t x_stride,
 void launch_quantize_act(int type, const float* x, int64_t x_stride, int rows, int K, void* dst, int x86,
                          hipStream_t stream);
 
+// ggml-cuda right-operand formats: Q8_1 rows (quantize_row_q8_1_cuda) and
+// the MMQ D4 staging of Q8_0 products (quantize_mmq_q8_1_cuda; rows padded
+// to a multiple of 512 values, [kp/128][rows][144 B]).  The D4 launch and
+// the range check set *invalid for blocks outside the native activation's
+// range (non-finite, or a nonzero block maximum outside [1e-30, 1e30]).
+void launch_quantize_q8_1(const float* x, int64_t x_stride, int rows, int K, void* dst, hipStream_t stream);
+void launch_quantize_q8_1_mmq(const float* x, int64_t x_stride, int rows, int K, void* dst, int* invalid,
+                              hipStream_t stream);
+void launch_q8_rhs_check(const float* x, int64_t x_stride, int rows, int K, int* invalid, hipStream_t stream);
+
 // F32 -> F16 rows, packed (ggml_cast to F16).
 void launch_cast_f16(const float* x, int64_t x_stride, int rows, int K, _Float16* dst, hipStream_t stream);
 

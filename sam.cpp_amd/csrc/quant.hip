@@ -590,6 +590,117 @@ void launch_quantize_act(int type, const float* x, int64_t x_stride, int rows, i
                            static_cast<uint8_t*>(dst), x86);
 }
 
+// ---------------------------------------------------------------------------
+// ggml-cuda's right-operand formats and the native-activation range rule.
+// One lane per value, 32 lanes (half a wave) per 32-value block, so every
+// reduction stays inside a lane group and whole groups leave together.
+// ---------------------------------------------------------------------------
+
+// 1 when a block of F32 values is outside the native activation's range:
+// a non-finite value, or a nonzero block maximum outside [1e-30, 1e30],
+// compared as bit patterns so subnormals are not flushed
+// (cmake/patches/ggml-native-activation.patch:148-171).
+__device__ __forceinline__ bool block_out_of_range(float v) {
+    uint32_t bits = __builtin_bit_cast(uint32_t, v) & 0x7fffffffu;
+    uint32_t bad = bits >= 0x7f800000u;
+    for (int off = 16; off > 0; off >>= 1) {
+        bits = max(bits, uint32_t(__shfl_xor(int(bits), off, 32)));
+        bad |= uint32_t(__shfl_xor(int(bad), off, 32));
+    }
+    constexpr uint32_t lower = 0x0da24260u, upper = 0x7149f2cau;   // bits of 1e-30f, 1e30f
+    return bad || bits > upper || (bits != 0 && bits < lower);
+}
+
+__device__ __forceinline__ float group32_absmax(float v) {
+    float a = fabsf(v);
+    for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 32));
+    return a;
+}
+
+// quantize_q8_1 (MMVQ right operand): d = amax/127, q = roundf(x/d), half d
+// and half of the original values' sum in the 32-lane xor-butterfly order.
+__global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float* __restrict__ x, int64_t x_stride, int rows,
+                                                            int K, uint8_t* __restrict__ dst) {
+#pragma clang fp contract(off)
+    const int64_t nb = K / 32;
+    const int64_t blk = (int64_t(blockIdx.x) * 256 + threadIdx.x) >> 5;
+    const int lane = threadIdx.x & 31;
+    if (blk >= int64_t(rows) * nb) return;
+    const int64_t r = blk / nb, b = blk - r * nb;
+    const float v = x[r * x_stride + b * 32 + lane];
+    const float amax = group32_absmax(v);
+    float s = v;
+    for (int off = 16; off > 0; off >>= 1) s = s + __shfl_xor(s, off, 32);
+    const float d = amax / 127.f;
+    const float q = amax == 0.f ? 0.f : __builtin_roundf(v / d);
+    uint8_t* out = dst + blk * 36;
+    out[4 + lane] = uint8_t(int8_t(q));
+    if (lane == 0) {
+        *reinterpret_cast<uint16_t*>(out) = float_to_half_bits(d);
+        *reinterpret_cast<uint16_t*>(out + 2) = float_to_half_bits(s);
+    }
+}
+
+// quantize_mmq_q8_1, D4 layout, for Q8_0 products: rows padded with zeros to
+// kp (a multiple of 512) values, tile t of 128 values of row r at
+// dst + (t*rows + r)*144 = 4 F32 scales, then 128 codes.  d_inv = 127/amax
+// correctly rounded, q = roundf(x*d_inv), scale 1/d_inv.  Blocks outside the
+// native range set *invalid.
+__global__ __launch_bounds__(256) void quantize_q8_1_mmq_kernel(const float* __restrict__ x, int64_t x_stride,
+                                                                int rows, int K, int kp, uint8_t* __restrict__ dst,
+                                                                int* __restrict__ invalid) {
+#pragma clang fp contract(off)
+    const int64_t nb = kp / 32;
+    const int64_t blk = (int64_t(blockIdx.x) * 256 + threadIdx.x) >> 5;
+    const int lane = threadIdx.x & 31;
+    if (blk >= int64_t(rows) * nb) return;
+    const int64_t r = blk / nb, kb = blk - r * nb;
+    const int64_t k = kb * 32 + lane;
+    const float v = k < K ? x[r * x_stride + k] : 0.f;
+    if (block_out_of_range(v) && lane == 0) atomicOr(invalid, 1);
+    const float amax = group32_absmax(v);
+    float q = 0.f, d = 0.f;
+    if (amax != 0.f) {
+        const float d_inv = 127.f / amax;
+        q = __builtin_roundf(v * d_inv);
+        d = 1.f / d_inv;
+    }
+    uint8_t* out = dst + ((kb >> 2) * rows + r) * 144;
+    out[16 + 32 * (kb & 3) + lane] = uint8_t(int8_t(q));
+    if (lane == 0) *reinterpret_cast<float*>(out + 4 * (kb & 3)) = d;
+}
+
+// The range rule alone over F32 rows (mul_mat's opt-in activation check).
+__global__ __launch_bounds__(256) void q8_rhs_check_kernel(const float* __restrict__ x, int64_t x_stride, int rows,
+                                                           int K, int* __restrict__ invalid) {
+    const int64_t nb = K / 32;
+    const int64_t blk = (int64_t(blockIdx.x) * 256 + threadIdx.x) >> 5;
+    const int lane = threadIdx.x & 31;
+    if (blk >= int64_t(rows) * nb) return;
+    const int64_t r = blk / nb, b = blk - r * nb;
+    if (block_out_of_range(x[r * x_stride + b * 32 + lane]) && lane == 0) atomicOr(invalid, 1);
+}
+
+void launch_quantize_q8_1(const float* x, int64_t x_stride, int rows, int K, void* dst, hipStream_t stream) {
+    const int64_t lanes = int64_t(rows) * K;
+    hipLaunchKernelGGL(quantize_q8_1_kernel, dim3(unsigned((lanes + 255) / 256)), dim3(256), 0, stream, x, x_stride,
+                       rows, K, static_cast<uint8_t*>(dst));
+}
+
+void launch_quantize_q8_1_mmq(const float* x, int64_t x_stride, int rows, int K, void* dst, int* invalid,
+                              hipStream_t stream) {
+    const int kp = (K + 511) / 512 * 512;
+    const int64_t lanes = int64_t(rows) * kp;
+    hipLaunchKernelGGL(quantize_q8_1_mmq_kernel, dim3(unsigned((lanes + 255) / 256)), dim3(256), 0, stream, x,
+                       x_stride, rows, K, kp, static_cast<uint8_t*>(dst), invalid);
+}
+
+void launch_q8_rhs_check(const float* x, int64_t x_stride, int rows, int K, int* invalid, hipStream_t stream) {
+    const int64_t lanes = int64_t(rows) * K;
+    hipLaunchKernelGGL(q8_rhs_check_kernel, dim3(unsigned((lanes + 255) / 256)), dim3(256), 0, stream, x, x_stride,
+                       rows, K, invalid);
+}
+
 void launch_dequant_rows(int type, const void* src, int64_t src_stride, const int32_t* ids, int64_t src_rows,
                          float* dst, int64_t dst_stride, int rows, int K, int* bad_id, hipStream_t stream) {
     const int64_t threads = int64_t(rows) * (K / 32);

@@ -16,13 +16,14 @@ LIB_PATH = os.path.join(HERE, "libsamhip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "samhip.h")
 
 ABI_VERSION = 1
-F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K, I32 = 0, 1, 8, 12, 13, 14, 15, 26
+F32, F16, Q8_0, Q8_1, Q4_K, Q5_K, Q6_K, Q8_K, I32 = 0, 1, 8, 9, 12, 13, 14, 15, 26
 COMPUTE_Q8_NATIVE, COMPUTE_F16 = 0, 1
 ROUND_X86, ROUND_REF = 0, 1
 OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED, ERR_DEVICE, ERR_OUT_OF_MEMORY = 0, -1, -2, -3, -4
-BLOCK_ELEMS = {F32: 1, F16: 1, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256, I32: 1}
-BLOCK_BYTES = {F32: 4, F16: 2, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292, I32: 4}
-TYPE_NAMES = {Q8_0: "q8_0", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K", F32: "f32", F16: "f16"}
+BLOCK_ELEMS = {F32: 1, F16: 1, Q8_0: 32, Q8_1: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256, I32: 1}
+BLOCK_BYTES = {F32: 4, F16: 2, Q8_0: 34, Q8_1: 36, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292, I32: 4}
+TYPE_NAMES = {Q8_0: "q8_0", Q8_1: "q8_1", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K", F32: "f32",
+              F16: "f16"}
 
 # Every entry point the header declares, with its ctypes signature.
 _P, _I, _I32, _I64, _SZ, _U32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_uint32
@@ -100,6 +101,9 @@ SIGNATURES = {
     "samhip_mul_mat": ([_P] + [ctypes.POINTER(Tensor)] * 3, _I),
     "samhip_get_rows": ([_P] + [ctypes.POINTER(Tensor)] * 3, _I),
     "samhip_quantize_rows": ([_P, _I32, _P, _SZ, _P, _I64, _I64, _I32], _I),
+    "samhip_q8_1_mmq_bytes": ([_I64, _I64], _SZ),
+    "samhip_quantize_rows_q8_1_mmq": ([_P, _P, _SZ, _P, _I64, _I64], _I),
+    "samhip_context_set_activation_check": ([_P, _I], _I),
     "samhip_dequantize_rows": ([_P, _I32, _P, _SZ, _P, _I64, _I64], _I),
     "samhip_validate_quantized_payload": ([_I32, _I64, _I64, _P, _SZ], _I),
     "samhip_query": ([_P, ctypes.POINTER(ExecInfo)], _I),
@@ -312,6 +316,19 @@ class Context:
         dst = self.alloc(rows * row_bytes(qtype, k))
         self.quantize_rows(qtype, src.ptr, 4 * k, dst.ptr, rows, k, q8_rounding)
         return self.download(dst, (rows, row_bytes(qtype, k)), np.uint8)
+
+    def quantize_q8_1_mmq(self, x):
+        """samhip_quantize_rows_q8_1_mmq on a device copy of numpy rows x."""
+        x = np.ascontiguousarray(x, np.float32)
+        rows, k = x.shape
+        nbytes = lib().samhip_q8_1_mmq_bytes(rows, k)
+        src = self.upload(x)
+        dst = self.alloc(nbytes)
+        check(lib().samhip_quantize_rows_q8_1_mmq(self.handle, src.ptr, 4 * k, dst.ptr, rows, k))
+        return self.download(dst, (nbytes,), np.uint8)
+
+    def set_activation_check(self, enabled):
+        check(lib().samhip_context_set_activation_check(self.handle, 1 if enabled else 0))
 
     def dequantize(self, qtype, packed, k):
         packed = np.ascontiguousarray(packed, np.uint8)
