@@ -156,6 +156,20 @@ int samhip_supports_mul_mat(const samhip_tensor* w, const samhip_tensor* x, cons
  * view of a larger packed tensor, x may have a row stride above 4*K. */
 int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_tensor* x, const samhip_tensor* y);
 
+/* samhip_mul_mat without any allocation: no reference counterpart; for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same operands,
+ * kernels and results as samhip_mul_mat, but every intermediate (activation
+ * staging, decoded weights, split-K partial sums) lives in one fixed 64 MiB
+ * device array per GPU that the library holds until the process ends
+ * (enough for every SAM 3 batch-1 linear; the largest, the ViT fc2 at
+ * M = 5184, K = 4736, needs 59 MB).  A product that needs more returns
+ * INVALID_ARGUMENT.  Calls on the same GPU share that array and keep no
+ * state in it between calls: calls that overlap on one GPU (two contexts,
+ * two streams, two threads) race and must be serialized by the caller. */
+int samhip_mul_mat_noalloc(samhip_context* ctx, const samhip_tensor* w, const samhip_tensor* x,
+                           const samhip_tensor* y);
+
 /* GGML_OP_GET_ROWS: dst row i = to_float(src row ids[i]) (ggml_get_rows,
  * src/models/sam3/text_encoder.hpp:158).  src type F32/F16/Q8_0/Q4_K/Q5_K/
  * Q6_K, ids I32, dst F32.  Out-of-range ids fail with INVALID_ARGUMENT. */

@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -57,6 +58,36 @@ struct samhip_graph {
     hipGraphExec_t exec;
 };
 
+namespace {
+
+// Fixed device scratch of samhip_mul_mat_noalloc: one array per device,
+// allocated with the code object and kept until the process ends.  Host code
+// never uses the array's name as an address: each device's own address comes
+// from hipGetSymbolAddress once, with that device current, at context
+// creation.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address (looked up on its first use).
+hipError_t device_scratch(int device, void** out) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    if (!g_scratch_ptr[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[device] = p;
+    }
+    *out = g_scratch_ptr[device];
+    return hipSuccess;
+}
+
+}  // namespace
+
 struct samhip_context {
     int device = 0;
     int compute = SAMHIP_COMPUTE_Q8_NATIVE;
@@ -68,6 +99,10 @@ struct samhip_context {
     void* staging = nullptr;
     size_t staging_bytes = 0;
     int* flag = nullptr;   // device error flag (get_rows id range)
+    // this device's fixed scratch (samhip_mul_mat_noalloc); while such a call
+    // runs, `staging` points at it and `no_alloc` forbids growing it
+    void* fixed_scratch = nullptr;
+    bool no_alloc = false;
     // tall-path selection: M at or above `tall_m` uses dequant + fp16 GEMM;
     // gemm_cfg >= 0 forces one fp16 GEMM tile configuration (SAMHIP_GEMM_CONFIG)
     int cus = 256;             // compute units of the device
@@ -118,6 +153,10 @@ int set_device(samhip_context* ctx) {
 
 int ensure_staging(samhip_context* ctx, size_t bytes) {
     if (bytes <= ctx->staging_bytes) return SAMHIP_OK;
+    if (ctx->no_alloc)
+        return fail(SAMHIP_ERR_INVALID_ARGUMENT,
+                    "mul_mat_noalloc: this product needs %zu bytes of scratch; the fixed scratch holds %zu", bytes,
+                    ctx->staging_bytes);
     if (ctx->capturing)
         return fail(SAMHIP_ERR_INVALID_ARGUMENT,
                     "capture: this product needs %zu bytes of staging but %zu are reserved; run it once before "
@@ -266,6 +305,10 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
         samhip_context_destroy(ctx);
         return fail(SAMHIP_ERR_DEVICE, "HIP context initialization failed");
     }
+    if (const hipError_t e = device_scratch(o.device, &ctx->fixed_scratch); e != hipSuccess) {
+        samhip_context_destroy(ctx);
+        return fail(SAMHIP_ERR_DEVICE, "fixed scratch address of device %d: %s", o.device, hipGetErrorString(e));
+    }
     std::snprintf(ctx->info.device_name, sizeof(ctx->info.device_name), "%s (%s)", prop.name, prop.gcnArchName);
     ctx->cus = std::max(1, prop.multiProcessorCount);
     ctx->stream = ctx->own_stream;
@@ -388,6 +431,22 @@ int samhip_context_set_activation_check(samhip_context* ctx, int enabled) {
     if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
     ctx->check_activations = enabled != 0;
     return SAMHIP_OK;
+}
+
+int samhip_mul_mat_noalloc(samhip_context* ctx, const samhip_tensor* w, const samhip_tensor* x,
+                           const samhip_tensor* y) {
+    if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    if (!ctx->fixed_scratch) return fail(SAMHIP_ERR_DEVICE, "mul_mat_noalloc: no fixed scratch on this device");
+    void* const staging = ctx->staging;
+    const size_t staging_bytes = ctx->staging_bytes;
+    ctx->staging = ctx->fixed_scratch;
+    ctx->staging_bytes = kNoAllocScratchBytes;
+    ctx->no_alloc = true;
+    const int rc = samhip_mul_mat(ctx, w, x, y);
+    ctx->no_alloc = false;
+    ctx->staging = staging;
+    ctx->staging_bytes = staging_bytes;
+    return rc;
 }
 
 int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_tensor* x, const samhip_tensor* y) {

@@ -99,6 +99,7 @@ SIGNATURES = {
     "samhip_tensor_get": ([_P, _P, _P, _SZ], _I),
     "samhip_supports_mul_mat": ([ctypes.POINTER(Tensor)] * 3, _I),
     "samhip_mul_mat": ([_P] + [ctypes.POINTER(Tensor)] * 3, _I),
+    "samhip_mul_mat_noalloc": ([_P] + [ctypes.POINTER(Tensor)] * 3, _I),
     "samhip_get_rows": ([_P] + [ctypes.POINTER(Tensor)] * 3, _I),
     "samhip_quantize_rows": ([_P, _I32, _P, _SZ, _P, _I64, _I64, _I32], _I),
     "samhip_q8_1_mmq_bytes": ([_I64, _I64], _SZ),
