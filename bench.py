@@ -736,7 +736,8 @@ def encoder_measure(sh, ctx, enc, warmup, iters):
         d.attention_type = sh.F32
     by = {}
     for name, wt, m, n, k, kms in prof:
-        by.setdefault(name, []).append((m, n, k, kms))
+        # attention launches carry their key-split count (vit_attention_splitS)
+        by.setdefault("vit_attention" if name.startswith("vit_attention") else name, []).append((m, n, k, kms))
     breakdown = {name: round(sum(r[3] for r in rs), 4) for name, rs in sorted(by.items(), key=lambda t: -sum(r[3] for r in t[1]))}
     return ms, prof, breakdown
 

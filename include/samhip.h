@@ -18,8 +18,10 @@
  * src/runtime/ggml/workspace.hpp:174-177 and README.md:239-242 do.
  *
  * Threading: a context is single-threaded and stream-ordered (one HIP stream);
- * distinct contexts may be used from distinct threads.  The library never
- * keeps a caller pointer after a call returns.
+ * distinct contexts may be used from distinct threads.  Apart from the stream
+ * given to samhip_context_set_stream (used until it is replaced) and the
+ * device buffers named by captured graphs (used by every replay), the
+ * library keeps no caller pointer after a call returns.
  */
 #ifndef SAMHIP_H
 #define SAMHIP_H

@@ -113,6 +113,7 @@ struct samhip_context {
     int attn_splits = 0;        // SAMHIP_ATTN_SPLITS: key splits of the attention kernel (0: by grid size)
     int fused_max_splits = 16;  // SAMHIP_FUSED_MAX_SPLITS: cap on the fused kernel's K splits
     bool check_activations = false;   // samhip_context_set_activation_check
+    bool int8_strip = true;     // SAMHIP_INT8_STRIP=0 keeps Q8_0 products with M <= 32 on the fp16 kernels
     samhip_exec_info info{};
     // per-launch event trace (samhip_trace_begin / samhip_trace_end)
     struct TraceRecord {
@@ -318,6 +319,7 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
     ctx->strip_skinny = env_int("SAMHIP_STRIP_SKINNY", 1);
     ctx->attn_splits = std::max(0, env_int("SAMHIP_ATTN_SPLITS", 0));
     ctx->fused_max_splits = std::max(1, env_int("SAMHIP_FUSED_MAX_SPLITS", 16));
+    ctx->int8_strip = env_int("SAMHIP_INT8_STRIP", 1) != 0;
     const int cfg = env_int("SAMHIP_GEMM_CONFIG", -1);
     ctx->gemm_cfg = (cfg >= 0 && cfg < gemm_f16_config_count()) ? cfg : -1;
     *out = ctx;
@@ -407,6 +409,16 @@ int samhip_supports_mul_mat(const samhip_tensor* w, const samhip_tensor* x, cons
 
 namespace {
 
+// Trace name of an attention launch: the key-split count when it splits.
+const char* attention_name(int splits) {
+    switch (splits) {
+        case 2: return "vit_attention_split2";
+        case 3: return "vit_attention_split3";
+        case 4: return "vit_attention_split4";
+        default: return "vit_attention";
+    }
+}
+
 // Reads back the device flag a range check or D4 staging launch raised.
 int read_range_flag(samhip_context* ctx) {
     int bad = 0;
@@ -462,7 +474,27 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     // tokens' q, k, v, out projections) run the fused kernel: one launch
     const bool small_w = ctx->fused_skinny && int64_t(N) * K <= kFusedSmallW;
     const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K) && !small_w;
-    if (!tall && M <= kStripMaxM && ctx->fused_skinny && ctx->strip_skinny &&
+    if (!tall && M <= 32 && w->type == T_Q8_0 && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE && ctx->int8_strip &&
+        ctx->fused_skinny) {
+        // exact int8 block dots, one launch for K <= 1024 (the text encoder)
+        if (int rc = ensure_staging(ctx, std::max<size_t>(q8_strip_i8_part_bytes(M, N, K), 256))) return rc;
+        const char* variant = q8_strip_i8_variant();
+        int rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
+            if (!launch_q8_strip_i8(static_cast<const float*>(x->data), int64_t(x->nb[1] / 4), w->data,
+                                    int64_t(w->nb[1]), static_cast<float*>(y->data), int64_t(y->nb[1] / 4),
+                                    static_cast<float*>(ctx->staging), M, N, K,
+                                    ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->stream))
+                return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no int8 strip kernel for this shape");
+            HIP_TRY(hipGetLastError(), "int8 strip launch");
+            return SAMHIP_OK;
+        });
+        if (rc) return rc;
+        ctx->info.mul_mat_calls++;
+        ctx->info.skinny_launches++;
+        std::snprintf(ctx->info.kernel_variant, sizeof(ctx->info.kernel_variant), "%s", variant);
+        return SAMHIP_OK;
+    }
+    if (!tall && M < kStripMaxM && ctx->fused_skinny && ctx->strip_skinny &&
         (ctx->strip_skinny == 2 || strip_skinny_preferred(w->type, M, K))) {
         // one launch per product (and a reduce when K > 1024): activation
         // packing in registers, weight decode and product
@@ -863,7 +895,8 @@ int samhip_flash_attn(samhip_context* ctx, const float* q, const float* k, const
     Carve c;
     size_t off[6];
     for (size_t& o : off) o = c.take(packed);
-    const size_t att_bytes = attention_scratch_bytes(int(batches), heads, int(n), true, ctx->cus, ctx->attn_splits);
+    const int splits = attention_splits(int(batches), heads, int(n), true, ctx->cus, ctx->attn_splits);
+    const size_t att_bytes = attention_scratch_bytes(int(batches), heads, int(n), splits);
     const size_t o_att = c.take(att_bytes);
     if (int rc = ensure_work(ctx, c.used)) return rc;
     uint8_t* wb = static_cast<uint8_t*>(ctx->work);
@@ -877,9 +910,10 @@ int samhip_flash_attn(samhip_context* ctx, const float* q, const float* k, const
         return SAMHIP_OK;
     });
     if (rc) return rc;
-    return traced(ctx, "vit_attention", T_F32, batches * n, heads * 64, n, [&]() -> int {
-        launch_attention(ops, out, int64_t(heads) * 64, int(batches), heads, int(n), att_scratch, ctx->cus,
-                         ctx->attn_splits, ctx->stream);
+    return traced(ctx, attention_name(splits), T_F32, batches * n, heads * 64, n, [&]() -> int {
+        if (!launch_attention(ops, out, int64_t(heads) * 64, int(batches), heads, int(n), splits, att_scratch,
+                              att_bytes, ctx->stream))
+            return fail(SAMHIP_ERR_UNSUPPORTED, "flash_attn: no attention launch for this grid");
         HIP_TRY(hipGetLastError(), "attention launch");
         return SAMHIP_OK;
     });
@@ -911,14 +945,16 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
     if (int rc = set_device(ctx)) return rc;
 
     const int64_t T = GW * GH, per = WS > 0 ? WS * WS : T, B = T / per, np = (per + 63) / 64 * 64;
-    if (B * H * np * 64 >= (int64_t(1) << 31)) return fail(SAMHIP_ERR_UNSUPPORTED, "vit_block: grid too large");
+    if (B * H * np * 64 >= (int64_t(1) << 31) || B > 65535)
+        return fail(SAMHIP_ERR_UNSUPPORTED, "vit_block: grid too large");
     Carve c;
     const size_t o_ln = c.take(size_t(T * E) * 4), o_x1 = c.take(size_t(T * E) * 4),
                  o_h1 = c.take(size_t(T * MLP) * 4);
     const size_t packed = size_t(B * H * np * 64) * 2;
     size_t o_ops[6];
     for (int i = 0; i < (precise ? 6 : 3); ++i) o_ops[i] = c.take(packed);
-    const size_t att_bytes = attention_scratch_bytes(int(B), int(H), int(per), precise, ctx->cus, ctx->attn_splits);
+    const int splits = attention_splits(int(B), int(H), int(per), precise, ctx->cus, ctx->attn_splits);
+    const size_t att_bytes = attention_scratch_bytes(int(B), int(H), int(per), splits);
     const size_t o_att = c.take(att_bytes);
     if (int rc = ensure_work(ctx, c.used)) return rc;
     uint8_t* wb = static_cast<uint8_t*>(ctx->work);
@@ -969,9 +1005,9 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
         });
         if (rc) return rc;
     }
-    rc = traced(ctx, "vit_attention", T_F32, T, E, per, [&]() -> int {
-        launch_attention(ops, ln, E, int(B), int(H), int(per), att_scratch, ctx->cus, ctx->attn_splits,
-                         ctx->stream);
+    rc = traced(ctx, attention_name(splits), T_F32, T, E, per, [&]() -> int {
+        if (!launch_attention(ops, ln, E, int(B), int(H), int(per), splits, att_scratch, att_bytes, ctx->stream))
+            return fail(SAMHIP_ERR_UNSUPPORTED, "vit_block: no attention launch for this grid");
         HIP_TRY(hipGetLastError(), "attention launch");
         return SAMHIP_OK;
     });

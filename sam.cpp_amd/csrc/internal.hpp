@@ -135,13 +135,17 @@ void launch_zero_pad(const AttnOperands& o, int B, int H, int N, hipStream_t str
 // out row b*N + n, columns h*64.. (row stride ldo floats).  F32-accurate
 // (split operands, three products each) when o carries the lo parts.
 // softmax(Q K^T) V; when the grid is small against the CUs (SAM 3's global
-// blocks), the keys are split over up to 4 workgroups per query block whose
-// partials go through `scratch` (attention_scratch_bytes, 0 = no split) and
-// are merged in split order by a second launch.
-// force > 0 fixes the number of splits (SAMHIP_ATTN_SPLITS).
-size_t attention_scratch_bytes(int B, int H, int N, bool precise, int cus, int force);
-void launch_attention(const AttnOperands& o, float* out, int64_t ldo, int B, int H, int N, float* scratch, int cus,
-                      int force, hipStream_t stream);
+// blocks), the keys are split over S (up to 4) workgroups per query block
+// whose partials go through `scratch` (attention_scratch_bytes(.., S) bytes)
+// and are merged in split order by a second launch.  The caller picks S once
+// with attention_splits (force > 0 fixes it: SAMHIP_ATTN_SPLITS; B * S stays
+// within the grid's 65535 z limit) and sizes the scratch from the same S;
+// launch_attention returns false, launching nothing, when the scratch is
+// smaller or B * S exceeds the limit.
+int attention_splits(int B, int H, int N, bool precise, int cus, int force);
+size_t attention_scratch_bytes(int B, int H, int N, int S);
+bool launch_attention(const AttnOperands& o, float* out, int64_t ldo, int B, int H, int N, int S, float* scratch,
+                      size_t scratch_bytes, hipStream_t stream);
 // Patch convolution operands as split fp16: A [T][3*Kp] = [hi | hi | lo] of
 // the image patches, W [E][3*Kp] = [hi | lo | hi] of the kernel rows, so
 // A W^T = hi*hi + hi*lo + lo*hi (F32-accurate); Kp = 3*p*p rounded up to 128.
@@ -232,7 +236,7 @@ const char* launch_fused_skinny(int wtype, bool f16, const float* x, int64_t ldx
                                 float* y, int64_t ldy, float* part, int M, int N, int K, int x86, int max_splits,
                                 hipStream_t stream);
 
-// Strip skinny products (M <= kStripMaxM): one launch per product while
+// Strip skinny products (M < kStripMaxM): one launch per product while
 // K <= 1024 (four 256-wide chunks per workgroup), plus the split-K reduce
 // beyond; partial sums go through `part` (FusedPlan::part_bytes).
 constexpr int kStripMaxM = 256;   // in blocks of 32 activation rows
@@ -241,6 +245,18 @@ constexpr int kStripMaxM = 256;   // in blocks of 32 activation rows
 // per-lane loads and K > 1024 adds the reduce launch back.
 inline bool strip_skinny_preferred(int wtype, int M, int K) { return wtype == T_Q8_0 && K <= 1024 && M <= 32; }
 FusedPlan strip_skinny_plan(int M, int N, int K);
+// Exact int8 products of Q8_0 weights with at most 32 activation rows
+// (COMPUTE_Q8_NATIVE): one launch while K <= kI8SliceK, else slices of
+// kI8SliceK values whose partial sums go through `part`
+// (ceil(K / kI8SliceK) * M * N floats) and a reduce launch.
+constexpr int kI8SliceK = 1024;
+inline size_t q8_strip_i8_part_bytes(int M, int N, int K) {
+    const int S = (K + kI8SliceK - 1) / kI8SliceK;
+    return S > 1 ? size_t(S) * size_t(M) * size_t(N) * 4 : 0;
+}
+const char* q8_strip_i8_variant();
+const char* launch_q8_strip_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy,
+                               float* part, int M, int N, int K, int x86, hipStream_t stream);
 const char* strip_skinny_variant(int wtype);
 const char* launch_strip_skinny(int wtype, bool f16, const float* x, int64_t ldx, const void* w, int64_t w_stride,
                                 float* y, int64_t ldy, float* part, int M, int N, int K, int x86, hipStream_t stream);

@@ -505,6 +505,159 @@ __global__ __launch_bounds__(1024) void strip_skinny_kernel(const float* __restr
     if (m < M && n < N) out[int64_t(m) * ld + n] = v;
 }
 
+// ---------------------------------------------------------------------------
+// Exact int8 strip path: Q8_0 weights against at most 32 activation rows
+// (the text encoder's 32 tokens) in COMPUTE_Q8_NATIVE, i.e. ggml's CPU
+// native arithmetic on the matrix cores.  Per Q8_0 block the integer dot
+// sum_k q_w q_x comes exactly out of v_mfma_i32_32x32x32_i8 (one 32-value
+// block per instruction: the weight codes are the B operand as stored, no
+// decode), and the block adds fma(float(dot), d_w * d_x, acc) in F32 as
+// ggml's vec_dot_q8_0_q8_0 does; only the order of the block sums differs.
+// One workgroup of 16 waves per 32 weight rows and K slice of up to 1024
+// values:
+//  1. the strip's packed bytes for the slice go to LDS with coalesced dword
+//     loads (rows of an odd dword count: conflict-free reads);
+//  2. thread (m, b) packs activation row m, block b of the slice to Q8_0
+//     (ggml's from_float, x86 or reference rounding) into LDS codes and
+//     scales, so each workgroup packs its slice once, with one lane per
+//     block and no cross-lane reductions;
+//  3. wave w multiplies blocks w, w + 16 of the slice;
+//  4. the 16 partial tiles are added in LDS in wave order.
+// Slices beyond the first (K > 1024) write partial sums that
+// splitk_reduce_kernel adds in slice order.
+// ---------------------------------------------------------------------------
+constexpr int I8_XLD = kI8SliceK + 16;                                // bytes per LDS code row
+constexpr int I8_WDW = (((kI8SliceK / 32) * 34 + 2 + 3) / 4) | 1;    // dwords per LDS weight row
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+template <bool X86, bool XVEC>
+__global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restrict__ X, int64_t ldx,
+                                                           const uint8_t* __restrict__ W, int64_t w_stride,
+                                                           float* __restrict__ Y, int64_t ldy, float* __restrict__ part,
+                                                           int M, int N, int K, int RG) {
+#pragma clang fp contract(off)
+    __shared__ __attribute__((aligned(16))) int8_t Xq[32 * I8_XLD];
+    __shared__ __attribute__((aligned(16))) float Xd[kI8SliceK / 32][32];
+    __shared__ __attribute__((aligned(16))) uint32_t Ws[32 * I8_WDW];
+    __shared__ __attribute__((aligned(16))) float red[16 * 16 * 64];
+    constexpr int RI = (I8_WDW + 31) / 32;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rg = blockIdx.x % RG, sp = blockIdx.x / RG;
+    const int n0 = rg * 32, k0 = sp * kI8SliceK;
+    const int nb = min(kI8SliceK, K - k0) / 32;   // Q8_0 blocks in this slice
+
+    // 1. packed weight bytes: thread (r, c) copies dwords c, c + 32, ... of row r
+    {
+        const int r = tid >> 5, c = tid & 31;
+        const uintptr_t g = reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + r, N - 1)) * w_stride + int64_t(k0 / 32) * 34);
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(g & ~uintptr_t(3));
+        const int ndw = int(((g & 3) + 34 * nb + 3) >> 2);
+        uint32_t wr[RI];
+#pragma unroll
+        for (int i = 0; i < RI; ++i) wr[i] = c + 32 * i < ndw ? src[c + 32 * i] : 0u;
+#pragma unroll
+        for (int i = 0; i < RI; ++i)
+            if (c + 32 * i < I8_WDW) Ws[r * I8_WDW + c + 32 * i] = wr[i];
+    }
+    // 2. activation row m, block b -> Q8_0 codes and scale (zeros past M)
+    {
+        const int m = tid >> 5, b = tid & 31;
+        float v[32];
+        if (m < M && b < nb) {
+            const float* xr = X + int64_t(m) * ldx + k0 + 32 * b;
+            if (XVEC) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const floatx4 t = load4f(xr + 4 * i);
+                    v[4 * i] = t[0];
+                    v[4 * i + 1] = t[1];
+                    v[4 * i + 2] = t[2];
+                    v[4 * i + 3] = t[3];
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) v[i] = xr[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) v[i] = 0.f;
+        }
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        const float d = amax / 127.f;
+        float inv;
+        if (X86) inv = amax != 0.f ? 127.f / amax : 0.f;
+        else inv = d != 0.f ? 1.f / d : 0.f;
+        uint32_t packed[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint32_t wd = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float s = v[4 * i + j] * inv;
+                const int q = int(X86 ? __builtin_rintf(s) : __builtin_roundf(s));
+                wd |= uint32_t(q & 0xff) << (8 * j);
+            }
+            packed[i] = wd;
+        }
+        if (b < nb) {
+            u32x4* dst = reinterpret_cast<u32x4*>(&Xq[m * I8_XLD + 32 * b]);
+            dst[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
+            dst[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
+            Xd[b][m] = half_bits_to_float(float_to_half_bits(d));   // the stored fp16 scale
+        }
+    }
+    __syncthreads();
+
+    // 3. blocks wave, wave + 16 of the slice: activation row (A) and weight
+    // row (B) codes, lanes 32h.. taking bytes 16h..16h+15 of both
+    const int col = lane & 31, h = lane >> 5;
+    const int wshift = int((reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + col, N - 1)) * w_stride) + k0 / 32 * 34) & 3);
+    const uint32_t* wrow = &Ws[col * I8_WDW];
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    const i32x16 zero = {0};
+    for (int b = wave; b < nb; b += 16) {
+        const i32x4 a = *reinterpret_cast<const i32x4*>(&Xq[col * I8_XLD + 32 * b + 16 * h]);
+        // the row's bytes start at byte wshift (0 or 2) of its first dword;
+        // every read stays inside the row's dwords
+        const int sb = wshift + 34 * b, cb = sb + 2 + 16 * h;
+        const int cd = cb >> 2, cs = cb & 3;
+        const uint32_t c0 = wrow[cd], c1 = wrow[cd + 1], c2 = wrow[cd + 2], c3 = wrow[cd + 3];
+        const uint32_t c4 = cs ? wrow[cd + 4] : 0u;
+        const u32x4 wq{funnel_bytes(c1, c0, cs), funnel_bytes(c2, c1, cs), funnel_bytes(c3, c2, cs),
+                       funnel_bytes(c4, c3, cs)};
+        const float dw = half_bits_to_float((wrow[sb >> 2] >> (8 * (sb & 3))) & 0xffffu);
+        const i32x16 dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+            a, i32x4{int(wq[0]), int(wq[1]), int(wq[2]), int(wq[3])}, zero, 0, 0, 0);
+        // element r: activation row 8 (r / 4) + 4 h + r % 4, weight row col
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+            const floatx4 dx = *reinterpret_cast<const floatx4*>(&Xd[b][8 * qd + 4 * h]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[4 * qd + i] = __builtin_fmaf(dw * dx[i], float(dot[4 * qd + i]), acc[4 * qd + i]);
+        }
+    }
+    // 4. partial tiles in wave order
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
+    __syncthreads();
+    const int m = tid >> 5, n = tid & 31;
+    const int src = (4 * (m >> 3) + (m & 3)) * 64 + n + 32 * ((m >> 2) & 1);
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) v += red[w * 16 * 64 + src];
+    if (m < M && n0 + n < N) {
+        if (part) part[(int64_t(sp) * M + m) * N + n0 + n] = v;
+        else Y[int64_t(m) * ldy + n0 + n] = v;
+    }
+}
+
 template <int WT, int MODE, bool X86>
 void launch_strip_mode(bool xvec, const float* x, int64_t ldx, const uint8_t* w, int64_t w_stride, float* y,
                        int64_t ldy, float* part, int M, int N, int K, int RG, int S, hipStream_t stream) {
@@ -649,7 +802,7 @@ const char* strip_skinny_variant(int wtype) {
 
 const char* launch_strip_skinny(int wtype, bool f16, const float* x, int64_t ldx, const void* w, int64_t w_stride,
                                 float* y, int64_t ldy, float* part, int M, int N, int K, int x86, hipStream_t stream) {
-    if (M < 1 || M > kStripMaxM || N < 1 || K < 32 || K % 32) return nullptr;
+    if (M < 1 || M >= kStripMaxM || N < 1 || K < 32 || K % 32) return nullptr;
     const FusedPlan p = strip_skinny_plan(M, N, K);
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
@@ -667,6 +820,33 @@ const char* launch_strip_skinny(int wtype, bool f16, const float* x, int64_t ldx
                            M, N, p.splits);
     }
     return strip_skinny_variant(wtype);
+}
+
+const char* q8_strip_i8_variant() { return "skinny_i8mfma_q8_0"; }
+
+const char* launch_q8_strip_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy,
+                               float* part, int M, int N, int K, int x86, hipStream_t stream) {
+    if (M < 1 || M > 32 || N < 1 || K < 32 || K % 32) return nullptr;
+    const int RG = (N + 31) / 32, S = (K + kI8SliceK - 1) / kI8SliceK;
+    if (S > 1 && !part) return nullptr;
+    const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    float* pt = S > 1 ? part : nullptr;
+    const dim3 grid(unsigned(RG * S)), block(1024);
+#define SAMHIP_I8(X86V, XV) \
+    hipLaunchKernelGGL((q8_strip_i8_kernel<X86V, XV>), grid, block, 0, stream, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG)
+    if (x86) {
+        if (xvec) SAMHIP_I8(true, true); else SAMHIP_I8(true, false);
+    } else {
+        if (xvec) SAMHIP_I8(false, true); else SAMHIP_I8(false, false);
+    }
+#undef SAMHIP_I8
+    if (S > 1) {
+        const int64_t outs = int64_t(M) * N;
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(unsigned((outs + 255) / 256)), dim3(256), 0, stream, part, y, ldy,
+                           M, N, S);
+    }
+    return q8_strip_i8_variant();
 }
 
 const char* fused_skinny_variant(int wtype) {

@@ -532,16 +532,18 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(const float* __res
 // four fp16 workgroups per CU), each split keeping at least 8 key tiles.
 int attention_splits(int B, int H, int N, bool precise, int cus, int force) {
     const int np = (N + 63) / 64 * 64, nkb = np / 64;
+    // the grid's z dimension holds B * S and is limited to 65535
+    const int cap = std::max(1, std::min(4, 65535 / std::max(B, 1)));
     if (force > 0) {
         // every split keeps at least one key tile
-        int S = std::max(1, std::min(force, nkb));
+        int S = std::max(1, std::min(std::min(force, cap), nkb));
         while (S > 1 && (S - 1) * ((nkb + S - 1) / S) >= nkb) --S;
         return S;
     }
     const int64_t wgs = int64_t((np + 127) / 128) * H * B, slots = int64_t(precise ? 2 : 4) * cus;
     int best = 1;
     double best_cost = double((wgs + slots - 1) / slots);
-    for (int s = 2; s <= 4 && nkb >= 8 * s; ++s) {
+    for (int s = 2; s <= cap && nkb >= 8 * s; ++s) {
         const double cost = double((wgs * s + slots - 1) / slots) / s;
         if (cost < best_cost * 0.95) {
             best = s;
@@ -551,16 +553,16 @@ int attention_splits(int B, int H, int N, bool precise, int cus, int force) {
     return best;
 }
 
-size_t attention_scratch_bytes(int B, int H, int N, bool precise, int cus, int force) {
-    const int S = attention_splits(B, H, N, precise, cus, force);
-    return S == 1 ? 0 : size_t(S) * B * N * H * (64 + 2) * 4;
+size_t attention_scratch_bytes(int B, int H, int N, int S) {
+    return S <= 1 ? 0 : size_t(S) * B * N * H * (64 + 2) * 4;
 }
 
-void launch_attention(const AttnOperands& o, float* out, int64_t ldo, int B, int H, int N, float* scratch, int cus,
-                      int force, hipStream_t stream) {
+bool launch_attention(const AttnOperands& o, float* out, int64_t ldo, int B, int H, int N, int S, float* scratch,
+                      size_t scratch_bytes, hipStream_t stream) {
     const int np = (N + 63) / 64 * 64;
     const bool precise = o.ql && o.kl && o.vl;
-    const int S = scratch ? attention_splits(B, H, N, precise, cus, force) : 1;
+    if (S < 1 || int64_t(B) * S > 65535) return false;
+    if (S > 1 && (!scratch || scratch_bytes < attention_scratch_bytes(B, H, N, S))) return false;
     float* part_o = S > 1 ? scratch : nullptr;
     float* part_ml = S > 1 ? scratch + size_t(S) * B * N * H * 64 : nullptr;
     // 128-query workgroups: measured on the SAM 3 shapes against 64, 96 and
@@ -581,6 +583,7 @@ void launch_attention(const AttnOperands& o, float* out, int64_t ldo, int B, int
         hipLaunchKernelGGL(attention_merge_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, stream, part_o,
                            part_ml, out, ldo, B * N, H, S);
     }
+    return true;
 }
 
 void launch_patch_columns(const float* image, int img, int patch, _Float16* a, float* row_scale, int kp,

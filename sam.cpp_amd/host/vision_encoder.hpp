@@ -11,15 +11,18 @@
 #include <algorithm>
 #include <array>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace sam {
 
 // The encoder hyperparameters of a checkpoint (sam3.vision.* and
 // sam3.neck.embedding_length, src/models/sam3/weights.hpp:427-438 and
-// 595-600).  The reference accepts only SAM 3's fixed values; here any
-// encoder of the same structure loads, and every tensor's shape is checked
-// against these numbers instead.
+// 591-600).  read() is strict by default, as the reference loader is: every
+// SAM 3 image parameter must hold its fixed value and the global attention
+// blocks must be the U32 array {7, 15, 23, 31}.  read_relaxed() accepts any
+// encoder of the same structure (the reduced checkpoints of the tests) and
+// leaves the shape checks to each tensor.
 struct VisionParameters {
     int image_size = 0, patch = 0, embed = 0, blocks = 0, heads = 0, mlp = 0, window = 0, neck_dim = 0;
     std::vector<int> global_blocks;
@@ -32,7 +35,34 @@ struct VisionParameters {
         return std::find(global_blocks.begin(), global_blocks.end(), block) != global_blocks.end();
     }
 
+    // sam3_image_parameters (src/models/sam3/weights.hpp:427-439)
+    static const std::array<std::pair<const char*, uint32_t>, 22>& sam3_values() {
+        static const std::array<std::pair<const char*, uint32_t>, 22> v{{
+            {"sam3.vision.image_size", 1008}, {"sam3.vision.patch_size", 14},
+            {"sam3.vision.embedding_length", 1024}, {"sam3.vision.block_count", 32},
+            {"sam3.vision.attention.head_count", 16}, {"sam3.vision.feed_forward_length", 4736},
+            {"sam3.vision.window_size", 24}, {"sam3.text.embedding_length", 1024},
+            {"sam3.text.attention.head_count", 16}, {"sam3.text.block_count", 24},
+            {"sam3.text.context_length", 32}, {"sam3.text.vocab_size", 49408},
+            {"sam3.text.output_length", 256}, {"sam3.neck.embedding_length", 256},
+            {"sam3.fusion.block_count", 6}, {"sam3.fusion.attention.head_count", 8},
+            {"sam3.fusion.feed_forward_length", 2048}, {"sam3.decoder.block_count", 6},
+            {"sam3.decoder.attention.head_count", 8}, {"sam3.decoder.feed_forward_length", 2048},
+            {"sam3.decoder.query_count", 200}, {"sam3.geometry.block_count", 3}}};
+        return v;
+    }
+
     static VisionParameters read(const GgufReader& r) {
+        for (const auto& kv : sam3_values())
+            if (r.u32(kv.first) != kv.second)
+                throw std::runtime_error(std::string("unsupported SAM 3 image parameter: ") + kv.first);
+        VisionParameters p = read_relaxed(r);
+        const std::vector<int> expected{7, 15, 23, 31};
+        if (p.global_blocks != expected) throw std::runtime_error("unsupported SAM 3 global attention block order");
+        return p;
+    }
+
+    static VisionParameters read_relaxed(const GgufReader& r) {
         VisionParameters p;
         p.image_size = int(r.u32("sam3.vision.image_size"));
         p.patch = int(r.u32("sam3.vision.patch_size"));

@@ -11,6 +11,10 @@
 //                                  check the device bytes equal the file's and
 //                                  run each as Y = X W^T with M random rows,
 //                                  against the oracle's native product
+//   gguf_tool vision-params <file> [relaxed]
+//                                  the encoder hyperparameters as JSON, read
+//                                  strictly (the reference's fixed SAM 3
+//                                  values) or relaxed (any structure)
 //   gguf_tool encode   <file> <image.f32> <out prefix> [f32|f16]
 //                                  load vit.* / neck.det.* onto device 0, run
 //                                  the image encoder (sam.cpp_amd/host/
@@ -175,9 +179,22 @@ int gpu(const std::string& path, int64_t m) {
     return 0;
 }
 
+int vision_params(const std::string& path, bool relaxed) {
+    sam::GgufReader r(path);
+    const sam::VisionParameters p = relaxed ? sam::VisionParameters::read_relaxed(r) : sam::VisionParameters::read(r);
+    std::printf("{\"image_size\": %d, \"patch\": %d, \"embed\": %d, \"blocks\": %d, \"heads\": %d, \"mlp\": %d, "
+                "\"window\": %d, \"neck_dim\": %d, \"global_blocks\": [",
+                p.image_size, p.patch, p.embed, p.blocks, p.heads, p.mlp, p.window, p.neck_dim);
+    for (size_t i = 0; i < p.global_blocks.size(); ++i) std::printf("%s%d", i ? ", " : "", p.global_blocks[i]);
+    std::printf("]}\n");
+    return 0;
+}
+
+// The reduced test checkpoints are read relaxed; a full SAM 3 file passes
+// the strict read too.
 int encode(const std::string& path, const std::string& image_path, const std::string& prefix, bool f16) {
     sam::GgufReader r(path);
-    const sam::VisionParameters p = sam::VisionParameters::read(r);
+    const sam::VisionParameters p = sam::VisionParameters::read_relaxed(r);
     sam::HipBackend backend = sam::HipBackend::make(0, sam::HipComputeMode::Q8Native);
     sam::DeviceWeights weights(backend);
     weights.load(r, [](const sam::GgufTensorInfo& t) {
@@ -240,7 +257,7 @@ int encode(const std::string& path, const std::string& image_path, const std::st
 int main(int argc, char** argv) {
     if (argc < 3) {
         std::fprintf(stderr, "usage: gguf_tool inspect|contract|profile <file> | gpu <file> <M> | "
-                             "encode <file> <image.f32> <out prefix> [f32|f16]\n");
+                             "vision-params <file> [relaxed] | encode <file> <image.f32> <out prefix> [f32|f16]\n");
         return 2;
     }
     const std::string mode = argv[1], path = argv[2];
@@ -249,6 +266,7 @@ int main(int argc, char** argv) {
         if (mode == "contract") return contract(path);
         if (mode == "profile") return profile(path);
         if (mode == "gpu" && argc > 3) return gpu(path, std::atoll(argv[3]));
+        if (mode == "vision-params") return vision_params(path, argc > 3 && std::string(argv[3]) == "relaxed");
         if (mode == "encode" && argc > 4)
             return encode(path, argv[3], argv[4], argc > 5 && std::string(argv[5]) == "f16");
         std::fprintf(stderr, "unknown mode %s\n", mode.c_str());

@@ -451,3 +451,65 @@ def test_image_encoder_parameters_rejected(tmp_path, oracle):
     p2.write_bytes(bad)
     out = tool("encode", str(p2), str(tmp_path / "none.f32"), str(tmp_path / "o"))
     assert out.returncode == 3 and "unsupported SAM 3 image encoder parameters" in out.stdout, out.stdout
+
+
+SAM3_IMAGE_PARAMETERS = [("sam3.vision.image_size", 1008), ("sam3.vision.patch_size", 14),
+                         ("sam3.vision.embedding_length", 1024), ("sam3.vision.block_count", 32),
+                         ("sam3.vision.attention.head_count", 16), ("sam3.vision.feed_forward_length", 4736),
+                         ("sam3.vision.window_size", 24), ("sam3.text.embedding_length", 1024),
+                         ("sam3.text.attention.head_count", 16), ("sam3.text.block_count", 24),
+                         ("sam3.text.context_length", 32), ("sam3.text.vocab_size", 49408),
+                         ("sam3.text.output_length", 256), ("sam3.neck.embedding_length", 256),
+                         ("sam3.fusion.block_count", 6), ("sam3.fusion.attention.head_count", 8),
+                         ("sam3.fusion.feed_forward_length", 2048), ("sam3.decoder.block_count", 6),
+                         ("sam3.decoder.attention.head_count", 8), ("sam3.decoder.feed_forward_length", 2048),
+                         ("sam3.decoder.query_count", 200), ("sam3.geometry.block_count", 3)]
+
+
+def _params_file(tmp_path, name, values, globals_=(7, 15, 23, 31), gtype=gg.U32):
+    kv = [("general.alignment", gg.U32, 32)] + [(k, gg.U32, v) for k, v in values]
+    kv.append(("sam3.vision.global_attention_blocks", gg.ARRAY, (gtype, list(globals_))))
+    path = tmp_path / name
+    path.write_bytes(gg.gguf_bytes(kv, [("vit.ln_pre.bias", (4,), gg.GGML_F32, np.zeros(4, np.float32).tobytes())]))
+    return str(path)
+
+
+def test_vision_parameters_strict_by_default(tmp_path):
+    """The strict read mirrors the reference loader (src/models/sam3/
+    weights.hpp:591-600): the 22 fixed SAM 3 image parameters and the global
+    blocks {7, 15, 23, 31} as a U32 array; each deviation is refused with the
+    reference's message, and the relaxed read accepts the same files."""
+    good = _params_file(tmp_path, "sam3.gguf", SAM3_IMAGE_PARAMETERS)
+    out = tool("vision-params", good)
+    assert out.returncode == 0, out.stdout
+    p = json.loads(out.stdout)
+    assert (p["image_size"], p["embed"], p["blocks"], p["mlp"], p["window"], p["global_blocks"]) == \
+        (1008, 1024, 32, 4736, 24, [7, 15, 23, 31])
+    for i, (key, value) in enumerate(SAM3_IMAGE_PARAMETERS):
+        if i % 3:
+            continue   # a spread of keys across the vision, text, fusion and decoder groups
+        values = list(SAM3_IMAGE_PARAMETERS)
+        values[i] = (key, value * 2)
+        path = _params_file(tmp_path, f"bad{i}.gguf", values)
+        out = tool("vision-params", path)
+        assert out.returncode == 3 and f"unsupported SAM 3 image parameter: {key}" in out.stdout, out.stdout
+    for gl in ((7, 15, 23), (7, 15, 23, 30), (15, 7, 23, 31)):
+        path = _params_file(tmp_path, "glob.gguf", SAM3_IMAGE_PARAMETERS, gl)
+        out = tool("vision-params", path)
+        assert out.returncode == 3 and "global attention block order" in out.stdout, (gl, out.stdout)
+        relaxed = tool("vision-params", path, "relaxed")
+        assert relaxed.returncode == (0 if gl[0] < gl[1] else 3), relaxed.stdout
+    path = _params_file(tmp_path, "i32.gguf", SAM3_IMAGE_PARAMETERS, gtype=gg.I32)
+    assert tool("vision-params", path).returncode == 3
+
+
+def test_vision_parameters_reduced_checkpoint_needs_relaxed(tmp_path, oracle):
+    """The reduced encoder checkpoint (168 px, 2 blocks) is not a SAM 3 file:
+    strictly it is refused, relaxed it reads with its own structure."""
+    path, _, _ = _encoder_checkpoint(oracle, tmp_path)
+    out = tool("vision-params", path)
+    assert out.returncode == 3 and "unsupported SAM 3 image parameter" in out.stdout, out.stdout
+    out = tool("vision-params", path, "relaxed")
+    assert out.returncode == 0, out.stdout
+    p = json.loads(out.stdout)
+    assert (p["image_size"], p["blocks"], p["global_blocks"]) == (168, 2, [1])

@@ -1,0 +1,69 @@
+"""The exact int8 path for Q8_0 weights against at most 32 activation rows
+(the text encoder's products), against the oracle's native CPU path.
+
+Both sides form the same Q8_0 activation codes and exact integer block dots;
+only the F32 order in which the per-block terms d_w d_x dot are added
+differs, so the bar is the exact-code bar of the reference's dot verifier,
+max per-row relative L2 <= 2e-5 (tools/validation/verify_q8_mmq_dots.py:105),
+well inside the product tolerance of 1e-3."""
+
+import sys
+
+import numpy as np
+import pytest
+
+from tests.reference_fixtures import max_row_rel_l2, probe_rhs, probe_weights
+
+pytestmark = pytest.mark.gpu
+
+EXACT = 2e-5
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+# text encoder (in_proj, out_proj, fc1, fc2, resizer) at M = 32, ragged M and
+# N, K slices past 1024 (partial sums and the reduce launch), short K
+SHAPES = [(32, 3072, 1024), (32, 1024, 1024), (32, 4096, 1024), (32, 1024, 4096), (32, 256, 1024),
+          (1, 4096, 1024), (17, 96, 512), (31, 33, 2048), (32, 64, 32), (5, 1000, 1056)]
+
+
+@pytest.mark.parametrize("rounding", ["x86", "ref"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_int8_strip_matches_native(samhip, oracle, shape, rounding):
+    m, n, k = shape
+    say("case int8 strip", shape, rounding)
+    gmode = samhip.ROUND_X86 if rounding == "x86" else samhip.ROUND_REF
+    cmode = oracle.ROUND_X86 if rounding == "x86" else oracle.ROUND_REF
+    rng = np.random.default_rng(m * 7 + n + k)
+    w = oracle.quantize(oracle.Q8_0, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    x = (rng.standard_normal((m, k)) * np.exp(rng.uniform(-4, 4, (m, 1)))).astype(np.float32)
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE, gmode) as ctx:
+        y = ctx.matmul(samhip.Q8_0, w, x, x_row_stride=k + 3 if n % 2 else None)
+        assert ctx.query().kernel_variant == b"skinny_i8mfma_q8_0"
+        again = ctx.matmul(samhip.Q8_0, w, x)
+    ref = oracle.mul_mat_native(oracle.Q8_0, w, x, cmode)
+    err = max_row_rel_l2(y, ref)
+    say(f"  max row rel L2 {err:.2e}")
+    assert np.isfinite(y).all() and err <= EXACT
+    assert np.array_equal(y, again)                 # deterministic, strided or not
+
+
+def test_int8_strip_views_and_reference_probe(gpu_ctx, oracle, samhip):
+    """Row-offset views of a fused in-projection and the reference's probe
+    fixture (tools/benchmark/cpu_quantized_matmul.hpp:63-75) with its outlier
+    and zero activation columns."""
+    say("case int8 strip views")
+    d = 1024
+    w = oracle.quantize(oracle.Q8_0, probe_weights(d, 3 * d))
+    for scenario in ("ordinary", "outlier", "zero"):
+        x = probe_rhs(d, 32, scenario)
+        for part in range(3):
+            y = gpu_ctx.matmul(samhip.Q8_0, w, x, w_row_offset=part * d, w_rows=d)
+            ref = oracle.mul_mat_native(oracle.Q8_0, w[part * d:(part + 1) * d], x)
+            if scenario == "zero":
+                assert not y.any() and not ref.any()
+            else:
+                assert max_row_rel_l2(y, ref) <= EXACT

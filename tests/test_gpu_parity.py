@@ -336,13 +336,14 @@ def test_mul_mat_fused_in_projection_views(gpu_ctx, f16_ctx, oracle, qtype):
 
 @pytest.mark.parametrize("qtype", TYPES)
 def test_mul_mat_strip_path(gpu_ctx, samhip, oracle, monkeypatch, qtype):
-    """M <= 32 takes the strip kernel where it is preferred (Q8_0, K <= 1024;
-    SAMHIP_STRIP_SKINNY=2 forces it for every weight type and K, with a
-    split-K reduce past K = 1024): repeated calls give identical bits, and
-    the fused kernel (SAMHIP_STRIP_SKINNY=0), which forms the same fp16
-    operands, agrees to F32 summation-order rounding."""
+    """The fp16 strip kernel (SAMHIP_STRIP_SKINNY=2 forces it for every
+    weight type and M < 256, with a split-K reduce past K = 1024; Q8_0 with
+    M <= 32 reaches it only with SAMHIP_INT8_STRIP=0): repeated calls give
+    identical bits, and the fused kernel (SAMHIP_STRIP_SKINNY=0), which
+    forms the same fp16 operands, agrees to F32 summation-order rounding."""
     say("case strip path", qtype)
     rng = np.random.default_rng(45)
+    monkeypatch.setenv("SAMHIP_INT8_STRIP", "0")
     monkeypatch.setenv("SAMHIP_STRIP_SKINNY", "2")
     strip = samhip.Context(0)
     monkeypatch.setenv("SAMHIP_STRIP_SKINNY", "0")
@@ -354,10 +355,9 @@ def test_mul_mat_strip_path(gpu_ctx, samhip, oracle, monkeypatch, qtype):
             first = strip.matmul(qtype, w, x)
             assert strip.query().kernel_variant.startswith(b"skinny_strip")
             default = gpu_ctx.matmul(qtype, w, x)
-            preferred = qtype == 8 and k <= 1024 and m <= 32
-            assert gpu_ctx.query().kernel_variant.startswith(b"skinny_strip" if preferred else b"skinny_fused")
-            if preferred:
-                assert np.array_equal(first, default)
+            # Q8_0 with M <= 32 defaults to the exact int8 kernel (its own test)
+            exact = qtype == 8 and m <= 32
+            assert gpu_ctx.query().kernel_variant.startswith(b"skinny_i8mfma" if exact else b"skinny_fused")
             assert np.array_equal(first, strip.matmul(qtype, w, x))
             other = fused.matmul(qtype, w, x)
             assert fused.query().kernel_variant.startswith(b"skinny_fused")

@@ -94,6 +94,38 @@ def test_flash_attn_key_splits(samhip, oracle, monkeypatch, splits):
         ctx.close()
 
 
+@pytest.mark.parametrize("splits", [2, 3, 4])
+def test_vit_block_fp16_attention_key_splits(samhip, oracle, monkeypatch, splits):
+    """The fp16-operand attention (attention_type F16) with its keys split
+    and merged inside a block, on ragged key tiles (20x20 grid: global, 400
+    tokens = 7 tiles with a partial last one; window 10, 100 tokens = 2
+    tiles): the trace names the split count that ran, and the block matches
+    the oracle as the unsplit fp16 block does."""
+    monkeypatch.setenv("SAMHIP_ATTN_SPLITS", str(splits))
+    ctx = samhip.Context(0)
+    try:
+        for ws, tiles in ((0, 7), (10, 2)):
+            say(f"vit_block fp16 attention splits={splits} window={ws}")
+            per_w = ws if ws else 20
+            w = block_weights(oracle, 256, 640, 4, per_w * per_w, per_w, seed=61 + ws)
+            x = np.random.default_rng(62 + ws).standard_normal((400, 256)).astype(np.float32)
+            blk = samhip.VitBlock(ctx, w, 256, 4, 640, 20, 20, ws, attention_type=samhip.F16)
+            xb = ctx.upload(x)
+            ctx.trace_begin()
+            blk.forward(xb)
+            names = [r[0] for r in ctx.trace_end()]
+            got = ctx.download(xb, x.shape, np.float32)
+            blk.free()
+            want = f"vit_attention_split{min(splits, tiles)}"
+            assert want in names, names
+            ref = oracle.vit_block(w, x, 20, 20, 256, 4, 640, ws)
+            rel = row_rel(got, ref)
+            say(f"  ran {want}: max {rel.max():.3g} median {np.median(rel):.3g}")
+            assert np.isfinite(got).all() and rel.max() < 6e-3 and np.median(rel) < 4e-3
+    finally:
+        ctx.close()
+
+
 def test_flash_attn_rejects(gpu_ctx, samhip):
     x = np.zeros((64, 128), np.float32)
     with pytest.raises(samhip.SamhipError, match="head_dim"):
