@@ -239,31 +239,82 @@ def summarize_profiles(d, commands):
         f.write("\n".join(lines) + "\n")
 
 
-def cpu_baseline(plan, seconds, rows):
-    """The oracle's native-quantized CPU path (ggml-quantized-cpu-native-v1
-    arithmetic, restated in C) on `rows` activation rows of every product."""
+def cpu_info():
+    """The host CPU model, the SIMD / matrix ISA extensions relevant to
+    ggml's CPU kernels, and the thread settings (from /proc/cpuinfo and the
+    environment)."""
+    model, flags = None, set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if model is None and line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                elif not flags and line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    isa = [x for x in ("sse4_2", "avx", "avx2", "fma", "f16c", "avx_vnni", "avx512f", "avx512bw", "avx512_vnni",
+                       "avx512_bf16", "avx512_fp16", "amx_tile", "amx_int8", "amx_bf16") if x in flags]
+    return {"model": model, "isa": isa, "nproc": os.cpu_count(), "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
+def cpu_baseline(plan, rows, samples=15, warmup=3):
+    """Both CPU paths of the reference, restated in C by the oracle, on `rows`
+    activation rows of every product (BASELINE.md's protocol, after the
+    reference's probe, tools/benchmark/cpu_quantized_matmul_probe.cpp:43-67):
+      native: ggml-quantized-cpu-native-v1 (activations packed to Q8_0 / Q8_K,
+              block integer dots; src/runtime/ggml/runtime.hpp:105),
+      decode: ggml-quantized-weights-f32-v1 (weights decoded to F32 per call,
+              F32 dots; src/runtime/ggml/graph.hpp:111-139, runtime.hpp:106),
+    each at all host cores and at 4 threads (the reference's default,
+    include/sam/types.hpp:19): `warmup` untimed passes, then `samples`
+    passes alternating the two paths AB/BA; median and P95 per pass."""
     sys.path.insert(0, ROOT)
     from oracle import oracle as O
     O.lib()
-    threads = O.max_threads()
+    all_threads = O.max_threads()
     rng = np.random.default_rng(1)
     xs = {k: rng.standard_normal((rows, k)).astype(np.float32) for _, _, k, _ in plan}
     ws = {}
     for label, qt, k, n in plan:
         w = (np.random.default_rng(0).standard_normal((n, k)) * 0.02).astype(np.float32)
         ws[label] = O.quantize(qt, w, O.ROUND_REF)
-    ops, elapsed, passes = 0.0, 0.0, 0
-    while elapsed < seconds and passes < 50:
+    ops = sum(2.0 * rows * n * k for _, _, k, n in plan)
+    alg = sum(n * O.row_bytes(qt, k) + rows * k * 4 + rows * n * 4 for _, qt, k, n in plan)
+
+    def one(path, threads):
+        t0 = time.perf_counter()
         for label, qt, k, n in plan:
-            t0 = time.perf_counter()
-            O.mul_mat_native(qt, ws[label], xs[k], O.ROUND_X86, threads)
-            elapsed += time.perf_counter() - t0
-            ops += 2.0 * rows * n * k
-        passes += 1
-    return {"value": round(ops / elapsed / 1e12, 6), "unit": "TOPS", "cores": threads, "kind": "port",
-            "sample": f"{rows} of {M_TOKENS} activation rows of each of the {len(plan)} products, {passes} passes, "
-                      f"{elapsed:.1f} s; oracle/ggml_oracle.c native path (Q8_0/Q8_K activation packing + block "
-                      f"integer dots), OpenMP"}
+            if path == "native":
+                O.mul_mat_native(qt, ws[label], xs[k], O.ROUND_X86, threads)
+            else:
+                O.mul_mat_decode(qt, ws[label], xs[k], threads)
+        return time.perf_counter() - t0
+
+    paths, spent = {}, 0.0
+    for threads in sorted({all_threads, min(4, all_threads)}, reverse=True):
+        for _ in range(warmup):
+            spent += one("native", threads) + one("decode", threads)
+        t = {"native": [], "decode": []}
+        for i in range(samples):
+            for p in (("native", "decode") if i % 2 == 0 else ("decode", "native")):
+                t[p].append(one(p, threads))
+                spent += t[p][-1]
+        for p, v in t.items():
+            med, p95 = float(np.median(v)), float(np.percentile(v, 95))
+            paths[f"{p}_{threads}t"] = {"median_ms": round(med * 1e3, 3), "p95_ms": round(p95 * 1e3, 3),
+                                        "tops": round(ops / med / 1e12, 6), "gbps": round(alg / med / 1e9, 3),
+                                        "threads": threads, "samples": samples}
+    # the value: the reference's default CPU policy (F32 decode), which is also
+    # the faster of the two restated paths on these shapes
+    head = paths[f"decode_{all_threads}t"]
+    return {"value": head["tops"], "unit": "TOPS", "cores": all_threads, "kind": "port",
+            "sample": f"{rows} of {M_TOKENS} activation rows of each of the {len(plan)} products per pass; "
+                      f"{warmup} warmup + {samples} timed passes per path, AB/BA alternated, at {all_threads} and "
+                      f"4 threads ({spent:.1f} s); value = F32-decode path (the reference's default CPU policy), "
+                      f"all threads, median; oracle/ggml_oracle.c restating ggml's CPU arithmetic (ggml itself "
+                      f"is not available: its SIMD kernels are not reproduced), OpenMP",
+            "paths": paths, "host": cpu_info()}
 
 
 def stream_cpu_baseline(shape_counts, qt, seconds=10.0):
@@ -778,14 +829,118 @@ def encoder_workload(args, sh, ctx):
     return result
 
 
+def linear_set(sh, ctx, m, items, steps, warmup, seed=0):
+    """Times a set of tall products [(label, weight type, K, N)] at M = m,
+    each with its own X and Y, weights N(0, 0.02^2) and X N(0, 1): whole-step
+    TOPS (activation staging, weight decode and GEMM), per-product event
+    times, and the dominant kernel's roofline (events on its launch stream)."""
+    rng = np.random.default_rng(seed + 1)
+    ops = []
+    for label, qt, k, n in items:
+        wf = ctx.upload((np.random.default_rng(seed).standard_normal((n, k)) * 0.02).astype(np.float32))
+        wq = ctx.alloc(n * sh.row_bytes(qt, k))
+        ctx.quantize_rows(qt, wf.ptr, 4 * k, wq.ptr, n, k, sh.ROUND_REF)
+        ctx.synchronize()
+        wf.free()
+        xb = ctx.upload(rng.standard_normal((m, k)).astype(np.float32))
+        yb = ctx.alloc(m * n * 4)
+        ops.append((label, qt, k, n, sh.tensor(qt, k, n, wq.ptr), sh.tensor(sh.F32, k, m, xb.ptr),
+                    sh.tensor(sh.F32, n, m, yb.ptr), [wq, xb, yb]))
+
+    def step():
+        for _, _, _, _, w, x, y, _ in ops:
+            ctx.mul_mat(w, x, y)
+
+    for _ in range(warmup):
+        step()
+    ctx.trace_begin()
+    step()
+    prof = ctx.trace_end(capacity=4 * len(ops) + 16)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    ctx.synchronize()
+    elapsed = time.perf_counter() - t0
+    flops = sum(2.0 * m * n * k for _, _, k, n, *_ in ops)
+    per_kernel = collections.defaultdict(float)
+    for r in prof:
+        per_kernel[r[0]] += r[5]
+    dom = max(per_kernel, key=per_kernel.get)
+    recs = [r for r in prof if r[0] == dom]
+    shape = max({(r[2], r[3], r[4]) for r in recs}, key=lambda sh_: sum(r[5] for r in recs if (r[2], r[3], r[4]) == sh_))
+    sel = [r for r in recs if (r[2], r[3], r[4]) == shape]
+    ms = float(np.mean([r[5] for r in sel]))
+    mm, nn, kk = shape
+    qt = sel[0][1]
+    ach = 2.0 * mm * nn * kk / (ms * 1e-3) / 1e12
+    alg_bytes = nn * sh.row_bytes(qt, kk) + mm * kk * 4 + mm * nn * 4
+    products = []
+    for label, qt_, k, n, *_ in ops:
+        t = sum(r[5] for r in prof if r[1] == qt_ and r[3] == n and r[4] == k)
+        products.append({"product": label, "M": m, "N": n, "K": k, "ms": round(t, 5),
+                         "tops": round(2.0 * m * n * k / (t * 1e-3) / 1e12, 2) if t else None})
+    for o in ops:
+        for b in o[7]:
+            b.free()
+    return {"value": round(flops * steps / elapsed / 1e12, 3), "unit": "TOPS",
+            "ms_per_step": round(elapsed * 1e3 / steps, 4), "steps": steps, "warmup": warmup,
+            "pct_int8_peak": round(100 * flops * steps / elapsed / 1e12 / PEAK_INT8_TOPS, 2),
+            "products": products,
+            "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(ach / PEAK_FP16_TFLOPS, 4), "traffic": hbm_traffic(dom, shape), "kernel": dom,
+                         "weight_type": sh.TYPE_NAMES.get(qt, str(qt)), "shape": {"M": mm, "N": nn, "K": kk},
+                         "launch_ms": round(ms, 5), "launches": len(sel),
+                         "hbm_gbps_algorithmic": round(alg_bytes / (ms * 1e-3) / 1e9, 1)}}
+
+
+def other_configs(args, sh, ctx, ops, xbuf):
+    """The workload's other configurations, each measured in this run with
+    its own roofline: (1) the single Q8_0 ViT fc1 linear, (3) the text and
+    fusion/decoder linear streams (Q8_0 and Q4_K text), (5) the batch of 8
+    images with mixed per-module formats (vision qkv/proj Q6_K, fc1 Q5_K, fc2
+    Q8_0 at M = 41,472; its text/fusion/decoder linears are Q8_0, the streams
+    of (3))."""
+    out = {}
+    log("config 1: single Q8_0 fc1")
+    out["1_single_q8_0_fc1"] = {"workload": "ViT fc1 1024->4736, Q8_0 weights, M=5184",
+                                **linear_set(sh, ctx, M_TOKENS, [("fc1:q8_0", sh.Q8_0, 1024, 4736)],
+                                             args.steps, args.warmup)}
+    sub = argparse.Namespace(**vars(args))
+    sub.cpu_seconds = min(args.cpu_seconds, 5.0)
+    sub.steps = max(args.steps, 10)
+    for fmt in ("q8_0", "q4_k"):
+        log(f"config 3: text stream {fmt}")
+        r = text_stream(sub, sh, ctx, fmt)
+        out[f"3_text_stream_{fmt}"] = {k: r[k] for k in ("metric", "value", "unit", "ms_per_step", "roofline",
+                                                           "eager_ms_per_step", "kernel_ms_per_step", "cpu_baseline")}
+    log("config 3: fusion/decoder stream q8_0")
+    r = detector_stream(sub, sh, ctx, "q8_0")
+    out["3_detector_stream_q8_0"] = {k: r[k] for k in ("metric", "value", "unit", "ms_per_step", "tops", "roofline",
+                                                       "cpu_baseline")}
+    log("config 5: batch of 8 images, mixed formats")
+    m8 = 8 * M_TOKENS
+    out["5_batch8_mixed"] = {"workload": "8 images (M=41472): qkv 1024->3072 and proj 1024->1024 Q6_K, fc1 "
+                                         "1024->4736 Q5_K, fc2 4736->1024 Q8_0; 4 mul_mat per step",
+                             **linear_set(sh, ctx, m8, [("qkv:q6_K", sh.Q6_K, 1024, 3072),
+                                                        ("proj:q6_K", sh.Q6_K, 1024, 1024),
+                                                        ("fc1:q5_K", sh.Q5_K, 1024, 4736),
+                                                        ("fc2:q8_0", sh.Q8_0, 4736, 1024)],
+                                          max(3, args.steps // 4), 2)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--compute", choices=["native", "f16"], default="native")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--cpu-rows", type=int, default=96)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU time budget of the stream baselines")
+    ap.add_argument("--cpu-rows", type=int, default=64)
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other configurations' lines (single Q8_0 fc1, text and fusion/decoder streams, "
+                         "batch-8 mixed formats) of the headline run")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--trace", choices=["dominant", "all", "none"], default="dominant",
                     help="launches bracketed by HIP events inside the timed region")
@@ -835,10 +990,14 @@ def main():
     plan = products(sh)
 
     log("preparing inputs")
+    # every product reads its own activation rows and writes its own output,
+    # so one step touches 1.1 GB (past the 256 MB MALL) as a forward would
     rng = np.random.default_rng(1)
-    xbuf = {k: ctx.upload(rng.standard_normal((M_TOKENS, k)).astype(np.float32)) for k in sorted({p[2] for p in plan})}
+    xrows = {k: rng.standard_normal((M_TOKENS, k)).astype(np.float32) for k in sorted({p[2] for p in plan})}
+    xbuf = []     # one buffer per product (labels repeat: fc2 is Q8_0 in every profile)
     ops = []
     for label, qt, k, n in plan:
+        xbuf.append(ctx.upload(xrows[k]))
         wf = ctx.upload((np.random.default_rng(0).standard_normal((n, k)) * 0.02).astype(np.float32))
         wq = ctx.alloc(n * sh.row_bytes(qt, k))
         ctx.quantize_rows(qt, wf.ptr, 4 * k, wq.ptr, n, k, sh.ROUND_REF)
@@ -846,11 +1005,12 @@ def main():
         wf.free()
         yb = ctx.alloc(M_TOKENS * n * 4)
         w = sh.tensor(qt, k, n, wq.ptr)
-        x = sh.tensor(sh.F32, k, M_TOKENS, xbuf[k].ptr)
+        x = sh.tensor(sh.F32, k, M_TOKENS, xbuf[-1].ptr)
         y = sh.tensor(sh.F32, n, M_TOKENS, yb.ptr)
         if not sh.lib().samhip_supports_mul_mat(w, x, y):
             raise RuntimeError(f"unsupported product {label}")
         ops.append((label, qt, k, n, w, x, y, wq, yb))
+    del xrows
 
     def step():
         for _, _, _, _, w, x, y, _, _ in ops:
@@ -916,7 +1076,7 @@ def main():
     m_, n_, k_ = max(shapes, key=lambda sh_: sum(r[5] for r in launches if (r[2], r[3], r[4]) == sh_))
     same = [r[5] for r in launches if (r[2], r[3], r[4]) == (m_, n_, k_)]
     avg_ms = float(np.mean(same))
-    qt_dom = launches[0][1]
+    qt_dom = collections.Counter(r[1] for r in launches if (r[2], r[3], r[4]) == (m_, n_, k_)).most_common(1)[0][0]
     flops = 2.0 * m_ * n_ * k_
     achieved = flops / (avg_ms * 1e-3) / 1e12
     alg_bytes = n_ * k_ * 2 + m_ * k_ * 2 + m_ * n_ * 4
@@ -935,8 +1095,12 @@ def main():
         "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
         "config": {"workload": "SAM 3 ViT K-quant linear sweep (Q4_K/Q5_K/Q6_K qkv, proj, fc1; fc2 Q8_0) at "
                                "M=5184 tokens, 12 mul_mat per step",
-                   "m_tokens": M_TOKENS, "compute": "q8-native" if compute == sh.COMPUTE_Q8_NATIVE else "f16",
-                   "parallelism": "single-gpu", "activation": "F32 in HBM", "output": "F32"},
+                   "m_tokens": M_TOKENS,
+                   "compute": ("Q8_0/Q8_K activation codes (bit-exact ggml packing) x fp16(to_float(W)) on fp16 "
+                               "MFMA, F32 accumulation" if compute == sh.COMPUTE_Q8_NATIVE
+                               else "fp16(X) x fp16(to_float(W)) on fp16 MFMA, F32 accumulation"),
+                   "parallelism": "single-gpu", "activation": "F32 in HBM, one buffer per product",
+                   "output": "F32, one buffer per product"},
         "pct_int8_peak": round(100 * tops / PEAK_INT8_TOPS, 2),
         "roofline": roofline,
         "products": per_product,
@@ -947,8 +1111,9 @@ def main():
     if not args.no_encoder:
         # the metric's second figure: the Q4_K vision encoder forward, measured
         # after the sweep's timed region (its own warmup and timing)
-        for b in [o[7] for o in ops] + [o[8] for o in ops] + list(xbuf.values()):
+        for b in [o[7] for o in ops] + [o[8] for o in ops] + xbuf:
             b.free()
+        ops, xbuf = [], []
         log("building the Q4_K vision encoder")
         enc = Encoder(sh, ctx, sh.Q4_K)
         enc_ms, _, breakdown = encoder_measure(sh, ctx, enc, 3, 10)
@@ -961,9 +1126,11 @@ def main():
                       "16 heads, MLP 4736; Q4_K qkv/proj/fc1, Q8_0 fc2; SimpleFPN neck levels 0-2 (F32 columns); "
                       "random-init weights; batch 1; 3 warmup + 10 timed forwards",
             "kernel_ms_per_image": breakdown}
+    if not args.no_configs:
+        result["configs"] = other_configs(args, sh, ctx, ops, xbuf)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
-        result["cpu_baseline"] = cpu_baseline([(p[0], p[1], p[2], p[3]) for p in ops], args.cpu_seconds, args.cpu_rows)
+        result["cpu_baseline"] = cpu_baseline(plan, args.cpu_rows)
         if enc is not None:
             log("timing the encoder CPU baseline")
             result["vision_encoder"]["cpu_baseline"] = encoder_cpu_baseline(enc)

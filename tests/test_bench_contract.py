@@ -39,3 +39,17 @@ def test_detector_plan_matches_the_reference_layers():
 def test_text_stream_shapes():
     assert [s[1:] for s in bench.TEXT_SHAPES] == [(1024, 3072), (1024, 1024), (1024, 4096), (4096, 1024)]
     assert bench.TEXT_LAYERS == 24 and bench.TEXT_M == 32
+
+
+def test_cpu_baseline_protocol_on_a_small_plan():
+    """Both CPU paths at all threads and at 4, AB/BA-alternated samples with
+    median and P95, and the host's CPU model and ISA flags."""
+    plan = [("a:q8_0", 8, 64, 32), ("b:q4_K", 12, 256, 16)]
+    r = bench.cpu_baseline(plan, rows=4, samples=3, warmup=1)
+    assert r["kind"] == "port" and r["unit"] == "TOPS" and r["value"] > 0 and r["cores"] >= 1
+    threads = {p["threads"] for p in r["paths"].values()}
+    assert min(4, r["cores"]) in threads and r["cores"] in threads
+    for name, p in r["paths"].items():
+        assert name.split("_")[0] in ("native", "decode")
+        assert p["samples"] == 3 and 0 < p["median_ms"] <= p["p95_ms"]
+    assert "model" in r["host"] and isinstance(r["host"]["isa"], list)
