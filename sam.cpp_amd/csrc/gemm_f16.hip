@@ -1,18 +1,15 @@
 // fp16 x fp16 -> F32 GEMM for the tall (many-token) mul_mat shapes on gfx950:
 //   Y[m][n] = rs[m] * sum_k A[m][k] * B[n][k]
 // A = staged activations [M][K], B = weights dequantized per call to
-// fp16(ggml to_float(W)) [N][K]; both K-contiguous, K a multiple of BK.
+// fp16(ggml to_float(W)) [N][K]; both K-contiguous, K a multiple of 2*BK.
 //
 // Per workgroup a BM x BN tile, WM x WN waves, each wave a grid of 32x32
-// v_mfma_f32_32x32x16_f16 accumulators.  Two operand pipelines:
-//  * register-staged (gemm_f16_kernel): raw buffer loads whose K position is
-//    a scalar offset (rows past M or N read as zero through the buffer
-//    bounds) land in VGPRs two stages ahead and are written to a
-//    double-buffered, padded LDS tile;
-//  * direct-to-LDS (gemm_f16_dma_kernel): buffer_load_dwordx4 ... lds fills
-//    a ring of 3-4 XOR-swizzled LDS stages without a VGPR round trip.
-// Both keep one barrier per BK stage.  The epilogue goes through LDS so that
-// each lane stores 16 contiguous bytes of Y.
+// v_mfma_f32_32x32x16_f16 accumulators.  Operands go straight from HBM into
+// a ring of XOR-swizzled LDS stages (buffer_load_dwordx4 ... lds, rows past
+// M or N read as zero through the buffer bounds), one barrier per BK stage,
+// and each wave interleaves the next substep's fragment reads with the
+// current substep's MFMAs.  The epilogue goes through LDS so that each lane
+// stores 16 contiguous bytes of Y.
 #include "internal.hpp"
 #include "q8stage.hpp"
 
@@ -21,9 +18,9 @@ namespace samhip {
 namespace {
 
 constexpr int GROUP_M = 8;
-constexpr int RSRC_WORD3 = 0x00020000;   // raw buffer, 32-bit data format
+[[maybe_unused]] constexpr int RSRC_WORD3 = 0x00020000;   // raw buffer, 32-bit data format
 
-__device__ __forceinline__ void tile_order(int bid, int nblocks, int tiles_m, int tiles_n, int& tm, int& tn) {
+[[maybe_unused]] __device__ __forceinline__ void tile_order(int bid, int nblocks, int tiles_m, int tiles_n, int& tm, int& tn) {
     // Blocks are dispatched round-robin over the 8 XCDs: give XCD x a
     // contiguous run of tiles, walked in groups of GROUP_M row tiles.
     const int per = nblocks / 8, rem = nblocks % 8;
@@ -37,51 +34,14 @@ __device__ __forceinline__ void tile_order(int bid, int nblocks, int tiles_m, in
     tn = within / gm;
 }
 
-// Epilogue of a wave's (32*FM) x (32*FN) tile at (row0, col0): each 32-row
-// block goes through the wave's LDS slab (stride ES floats; accumulator
-// element r of lane l sits on row 8*(r/4) + 4*(l/32) + r%4) and leaves as
-// 16-byte row segments scaled by their row's 2^e.  (Staging the row scales
-// in LDS at kernel start measured up to 35 % slower on the long-K shapes.)
 // Epilogue flags (EPI template bits) for Epilogue fields.
 constexpr int EPI_BIAS = 1, EPI_RES = 4, EPI_REMAP = 8, EPI_PACK = 16, EPI_COLSCALE = 32, EPI_SHUFFLE = 64,
               EPI_GELU = 128, EPI_PACK_LO = 512;
 
-template <int FM, int FN, int ES>
-__device__ __forceinline__ void store_tile(floatx16 (&acc)[FM][FN], const float* row_scale, float* slab, int lane,
-                                           int row0, int col0, int M, int N, float* Y, int64_t ldy) {
-    constexpr int TN = 32 * FN, C4 = TN / 4;
-    const bool vec_ok = (ldy % 4) == 0 && (reinterpret_cast<uintptr_t>(Y) % 16) == 0;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-                slab[(8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)) * ES + 32 * j + (lane & 31)] = acc[i][j][r];
-        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the slab is written
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int e = lane; e < 32 * C4; e += 64) {
-            const int rr = e / C4, c4 = e % C4;
-            const int m = row0 + i * 32 + rr;
-            const int n = col0 + 4 * c4;
-            if (m >= M) continue;
-            const float sc = row_scale[m];
-            const floatx4 raw = *reinterpret_cast<const floatx4*>(slab + rr * ES + 4 * c4);
-            const floatx4 v{raw[0] * sc, raw[1] * sc, raw[2] * sc, raw[3] * sc};
-            float* yp = Y + int64_t(m) * ldy + n;
-            if (vec_ok && n + 3 < N) {
-                *reinterpret_cast<floatx4*>(yp) = v;
-            } else {
-                for (int q = 0; q < 4; ++q)
-                    if (n + q < N) yp[q] = v[q];
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
-    }
-}
-
-// Epilogue of the pipelined kernel: a lane always owns the same 4 columns
+// Epilogue of a wave's (32*FM) x (32*FN) tile at (row0, col0): each 32-row
+// block goes through the wave's LDS slab (stride ES floats; accumulator
+// element r of lane l sits on row 8*(r/4) + 4*(l/32) + r%4) and leaves as
+// 16-byte row segments scaled by their row's 2^e.  A lane always owns the same 4 columns
 // (64 % C4 == 0), so the bias is loaded once; each 32-row block's row
 // scales, output rows and residuals are requested before its accumulators
 // go through the slab.
@@ -219,131 +179,10 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
     }
 }
 
-template <int BM, int BN, int WM, int WN, int BK>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_f16_kernel(const _Float16* __restrict__ A, int64_t lda,
-                                                                  const float* __restrict__ row_scale,
-                                                                  const _Float16* __restrict__ B, int64_t ldb,
-                                                                  float* __restrict__ Y, int64_t ldy, int M, int N,
-                                                                  int K, int tiles_m, int tiles_n) {
-    constexpr int NT = WM * WN * 64;
-    constexpr int LS = BK + 8;                  // LDS row stride in halves
-    constexpr int CPR = BK / 8;                 // 16-byte chunks per tile row
-    constexpr int CA = BM * CPR / NT, CB = BN * CPR / NT;
-    constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
-    constexpr int ES = TN + 8;                  // epilogue LDS row stride in floats
-    static_assert(CA * NT == BM * CPR && CB * NT == BN * CPR, "tile/thread mismatch");
-    static_assert(FM * 32 == TM && FN * 32 == TN, "wave tile must be a multiple of 32");
-    static_assert(WM * WN * 32 * ES * 4 <= 2 * (BM + BN) * LS * 2, "epilogue staging must fit in LDS");
-
-    __shared__ _Float16 lds[2 * (BM + BN) * LS];
-
-    int tm, tn;
-    tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WN, wn = wave % WN;
-
-    // buffer descriptors over the whole operands; a byte offset at or past
-    // num_records reads as zero
-    const uint32_t a_bytes = uint32_t(min(int64_t(M) * lda * 2, int64_t(0x7fffffff)));
-    const uint32_t b_bytes = uint32_t(min(int64_t(N) * ldb * 2, int64_t(0x7fffffff)));
-    const __amdgpu_buffer_rsrc_t ra_desc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A), 0, a_bytes, RSRC_WORD3);
-    const __amdgpu_buffer_rsrc_t rb_desc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(B), 0, b_bytes, RSRC_WORD3);
-
-    uint32_t a_off[CA], b_off[CB];
-    int a_lds[CA], b_lds[CB];
-#pragma unroll
-    for (int i = 0; i < CA; ++i) {
-        const int c = tid + i * NT, r = c / CPR, cc = c % CPR;
-        a_off[i] = m0 + r < M ? uint32_t((int64_t(m0 + r) * lda + 8 * cc) * 2) : a_bytes;
-        a_lds[i] = r * LS + 8 * cc;
-    }
-#pragma unroll
-    for (int i = 0; i < CB; ++i) {
-        const int c = tid + i * NT, r = c / CPR, cc = c % CPR;
-        b_off[i] = n0 + r < N ? uint32_t((int64_t(n0 + r) * ldb + 8 * cc) * 2) : b_bytes;
-        b_lds[i] = r * LS + 8 * cc;
-    }
-
-    floatx16 acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-    // Two register sets: stage s+2 is requested while stage s computes and
-    // lands in LDS only after stage s+1 has computed, so every load has two
-    // compute phases to arrive.
-    u32x4 ra0[CA], rb0[CB], ra1[CA], rb1[CB];
-    const int nstages = K / BK;
-    auto gload = [&](int s, u32x4* ra, u32x4* rb) {
-        const int koff = s * BK * 2;
-#pragma unroll
-        for (int i = 0; i < CA; ++i)
-            ra[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ra_desc, int(a_off[i]), koff, 0));
-#pragma unroll
-        for (int i = 0; i < CB; ++i)
-            rb[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb_desc, int(b_off[i]), koff, 0));
-    };
-    auto lstore = [&](int buf, const u32x4* ra, const u32x4* rb) {
-        _Float16* at = lds + buf * (BM + BN) * LS;
-        _Float16* bt = at + BM * LS;
-#pragma unroll
-        for (int i = 0; i < CA; ++i) *reinterpret_cast<u32x4*>(at + a_lds[i]) = ra[i];
-#pragma unroll
-        for (int i = 0; i < CB; ++i) *reinterpret_cast<u32x4*>(bt + b_lds[i]) = rb[i];
-    };
-    const int fr = lane & 31, fk = 8 * (lane >> 5);
-    auto compute = [&](int buf) {
-        const _Float16* as = lds + buf * (BM + BN) * LS + (wm * TM + fr) * LS + fk;
-        const _Float16* bs = lds + buf * (BM + BN) * LS + BM * LS + (wn * TN + fr) * LS + fk;
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 16) {
-            half8 af[FM], bf[FN];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const half8*>(as + i * 32 * LS + kk);
-#pragma unroll
-            for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const half8*>(bs + j * 32 * LS + kk);
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-    };
-
-    gload(0, ra0, rb0);
-    if (nstages > 1) gload(1, ra1, rb1);
-    lstore(0, ra0, rb0);
-    __syncthreads();
-    const int pairs = nstages / 2;
-    for (int p = 0; p < pairs; ++p) {
-        const int s = 2 * p;
-        // stage s in LDS buffer 0; register set 1 holds stage s+1
-        if (s + 2 < nstages) gload(s + 2, ra0, rb0);
-        compute(0);
-        lstore(1, ra1, rb1);
-        __syncthreads();
-        // stage s+1 in LDS buffer 1; register set 0 holds stage s+2
-        if (s + 3 < nstages) gload(s + 3, ra1, rb1);
-        compute(1);
-        if (s + 2 < nstages) lstore(0, ra0, rb0);
-        __syncthreads();
-    }
-
-    // Epilogue, one 32-row slab of the wave tile at a time: the accumulator
-    // (lane l: column l%32, rows 8*(r/4) + 4*(l/32) + r%4) goes to a
-    // per-wave LDS slab, then each lane writes 4 consecutive floats of Y.
-    store_tile<FM, FN, ES>(acc, row_scale, reinterpret_cast<float*>(lds) + wave * 32 * ES, lane, m0 + wm * TM, n0 + wn * TN, M, N,
-                           Y, ldy);
-}
-
 // ---------------------------------------------------------------------------
-// Direct-to-LDS variant: operands go HBM -> LDS with buffer_load_dwordx4 ...
-// lds (no VGPR round trip, no ds_write), through a ring of STAGES buffers, so
-// the loads of stage s+STAGES-1 are requested while stage s computes.  One
+// LDS layout: operands go HBM -> LDS with buffer_load_dwordx4 ... lds (no
+// VGPR round trip, no ds_write), through a ring of STAGES buffers, so the
+// loads of stage s+STAGES-1 are requested while stage s computes.  One
 // wave-wide load fills 1 KB of LDS contiguously (lane l -> bytes 16l..16l+15);
 // each lane picks the global chunk that belongs at its slot, which lays every
 // tile row out with its 16-byte K chunks XOR-swizzled by the row index:
@@ -362,130 +201,8 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
 }
 
-template <int BM, int BN, int BK, int STAGES>
-__global__ __launch_bounds__(256) void gemm_f16_dma_kernel(const _Float16* __restrict__ A, int64_t lda,
-                                                           const float* __restrict__ row_scale,
-                                                           const _Float16* __restrict__ B, int64_t ldb,
-                                                           float* __restrict__ Y, int64_t ldy, int M, int N, int K,
-                                                           int tiles_m, int tiles_n) {
-#if defined(__HIP_DEVICE_COMPILE__)   // LDS-DMA builtins exist only in the device pass
-    constexpr int WM = 2, WN = 2;
-    constexpr int CPR = BK / 8, RB = BK * 2;            // chunks / bytes per tile row
-    constexpr int RPB = 64 / CPR;                       // tile rows per 1 KB wave load
-    constexpr int A_BLOCKS = BM / RPB, B_BLOCKS = BN / RPB;
-    constexpr int A_PER_WAVE = A_BLOCKS / 4, B_PER_WAVE = B_BLOCKS / 4;
-    constexpr int LOADS = A_PER_WAVE + B_PER_WAVE;      // wave loads per stage
-    constexpr int STAGE_BYTES = (BM + BN) * RB;
-    constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
-    constexpr int ES = TN + 8;
-    static_assert(A_PER_WAVE * 4 == A_BLOCKS && B_PER_WAVE * 4 == B_BLOCKS, "tile rows must split over 4 waves");
-    static_assert(STAGES >= 2 && STAGES <= 4, "ring depth");
-    static_assert(4 * 32 * ES * 4 <= STAGES * STAGE_BYTES, "epilogue staging must fit in LDS");
-
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * STAGE_BYTES];
-
-    int tm, tn;
-    tile_order(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: LDS targets stay scalar
-    const int wm = wave / WN, wn = wave % WN;
-
-    const uint32_t a_bytes = uint32_t(min(int64_t(M) * lda * 2, int64_t(0x7fffffff)));
-    const uint32_t b_bytes = uint32_t(min(int64_t(N) * ldb * 2, int64_t(0x7fffffff)));
-    const __amdgpu_buffer_rsrc_t ra_desc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A), 0, a_bytes, RSRC_WORD3);
-    const __amdgpu_buffer_rsrc_t rb_desc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(B), 0, b_bytes, RSRC_WORD3);
-
-    // global byte offset (at k = 0) of the chunk this lane fetches for each of
-    // its wave loads; past-the-end rows read as zero
-    uint32_t a_off[A_PER_WAVE], b_off[B_PER_WAVE];
-#pragma unroll
-    for (int i = 0; i < A_PER_WAVE; ++i) {
-        const int blk = wave * A_PER_WAVE + i, r = blk * RPB + lane / CPR, slot = lane % CPR;
-        const int kc = slot ^ swz<CPR>(r);
-        a_off[i] = m0 + r < M ? uint32_t((int64_t(m0 + r) * lda + 8 * kc) * 2) : a_bytes;
-    }
-#pragma unroll
-    for (int i = 0; i < B_PER_WAVE; ++i) {
-        const int blk = wave * B_PER_WAVE + i, r = blk * RPB + lane / CPR, slot = lane % CPR;
-        const int kc = slot ^ swz<CPR>(r);
-        b_off[i] = n0 + r < N ? uint32_t((int64_t(n0 + r) * ldb + 8 * kc) * 2) : b_bytes;
-    }
-    auto issue = [&](int s) {
-        uint8_t* st = lds + (s % STAGES) * STAGE_BYTES;
-        const int koff = s * RB;
-#pragma unroll
-        for (int i = 0; i < A_PER_WAVE; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ra_desc, (__attribute__((address_space(3))) void*)(st + (wave * A_PER_WAVE + i) * 1024), 16,
-                a_off[i], koff, 0, 0);
-#pragma unroll
-        for (int i = 0; i < B_PER_WAVE; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rb_desc, (__attribute__((address_space(3))) void*)(st + BM * RB + (wave * B_PER_WAVE + i) * 1024),
-                16, b_off[i], koff, 0, 0);
-    };
-
-    floatx16 acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-    const int nst = K / BK;
-    // per-lane fragment coordinates: row wm*TM + i*32 + (lane&31), chunk 2*kk + (lane>>5)
-    const int frow = lane & 31, fhalf = lane >> 5;
-    auto compute = [&](int s) {
-        const uint8_t* st = lds + (s % STAGES) * STAGE_BYTES;
-#pragma unroll
-        for (int kk = 0; kk < BK / 16; ++kk) {
-            half8 af[FM], bf[FN];
-            const int kc = 2 * kk + fhalf;
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const int r = wm * TM + i * 32 + frow;
-                af[i] = *reinterpret_cast<const half8*>(st + r * RB + 16 * (kc ^ swz<CPR>(r)));
-            }
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const int r = wn * TN + j * 32 + frow;
-                bf[j] = *reinterpret_cast<const half8*>(st + BM * RB + r * RB + 16 * (kc ^ swz<CPR>(r)));
-            }
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-    };
-
-#pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s)
-        if (s < nst) issue(s);
-    for (int s = 0; s < nst; ++s) {
-        // this wave's loads of stage s are the oldest in flight: allow the
-        // later stages' loads (up to STAGES-2 of them) to remain outstanding
-        const int later = min(STAGES - 2, nst - 1 - s);
-        if (later >= 2) wait_vmcnt<2 * LOADS>();
-        else if (later == 1) wait_vmcnt<LOADS>();
-        else wait_vmcnt<0>();
-        // every wave's stage-s data landed; stage s-1 reads are done.  A bare
-        // s_barrier (no fence) keeps the later stages' loads in flight.
-        asm volatile("s_barrier" ::: "memory");
-        if (s + STAGES - 1 < nst) issue(s + STAGES - 1);
-        compute(s);
-    }
-    __syncthreads();
-
-    store_tile<FM, FN, ES>(acc, row_scale, reinterpret_cast<float*>(lds) + wave * 32 * ES, lane, m0 + wm * TM, n0 + wn * TN, M, N,
-                           Y, ldy);
-#endif
-}
-
 // ---------------------------------------------------------------------------
-// Pipelined variant of the LDS-DMA kernel: every wave holds two sets of MFMA
+// The tall GEMM: every wave holds two sets of MFMA
 // fragments, and the ds_reads of K substep kk+1 are interleaved with the
 // MFMAs of substep kk (pinned with sched_group_barrier), so the matrix cores
 // never wait on LDS latency inside a stage.  The stage hand-over (wait for
@@ -681,8 +398,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_pipe_kernel(const _Floa
     }
     __syncthreads();
 
-    // (the prefetching epilogue measured 0.3-2 % faster than store_tile on
-    // the plain products too)
     store_tile_epi<FM, FN, ES, EPI>(acc, row_scale, reinterpret_cast<float*>(lds) + wave * 32 * ES, lane,
                                     m0 + wm * TM, n0 + wn * TN, M, N, Y, ldy, ep);
 #endif
@@ -703,24 +418,6 @@ void launch_pipe(const _Float16* a, int64_t lda, const float* rs, const _Float16
                        dim3(64 * WM * WN), pad, stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n, ep, op);
 }
 
-template <int BM, int BN, int BK, int STAGES>
-void launch_dma(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
-                int64_t ldy, int M, int N, int K, bool spread, hipStream_t stream) {
-    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    const size_t pad = spread ? spread_pad(size_t(STAGES) * (BM + BN) * BK * 2) : 0;
-    hipLaunchKernelGGL((gemm_f16_dma_kernel<BM, BN, BK, STAGES>), dim3(unsigned(tiles_m * tiles_n)), dim3(256), pad,
-                       stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n);
-}
-
-template <int BM, int BN, int WM, int WN, int BK>
-void launch_cfg(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
-                int64_t ldy, int M, int N, int K, bool spread, hipStream_t stream) {
-    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    const size_t pad = spread ? spread_pad(size_t(2) * (BM + BN) * (BK + 8) * 2) : 0;
-    hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, WM, WN, BK>), dim3(unsigned(tiles_m * tiles_n)),
-                       dim3(WM * WN * 64), pad, stream, a, lda, rs, b, ldb, y, ldy, M, N, K, tiles_m, tiles_n);
-}
-
 // Configuration-table entry point (plain epilogue).
 template <int BM, int BN, int BK, int STAGES, int WM = 2, int WN = 2>
 void launch_pipe_plain(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
@@ -732,43 +429,32 @@ struct Cfg {
     const char* name;
     void (*launch)(const _Float16*, int64_t, const float*, const _Float16*, int64_t, float*, int64_t, int, int, int,
                    bool, hipStream_t);
-    int bm, bn, bk;
+    int bm, bn, bk, wm, wn;
 };
 
-const Cfg kConfigs[] = {
-    {"gemm_f16_128x128x64_w2x2", launch_cfg<128, 128, 2, 2, 64>, 128, 128, 64},
-    {"gemm_f16_128x128x32_w2x2", launch_cfg<128, 128, 2, 2, 32>, 128, 128, 32},
-    {"gemm_f16_256x128x64_w2x2", launch_cfg<256, 128, 2, 2, 64>, 256, 128, 64},
-    {"gemm_f16_128x256x64_w2x2", launch_cfg<128, 256, 2, 2, 64>, 128, 256, 64},
-    {"gemm_f16_256x256x32_w2x2", launch_cfg<256, 256, 2, 2, 32>, 256, 256, 32},
-    {"gemm_f16_192x128x64_w2x2", launch_cfg<192, 128, 2, 2, 64>, 192, 128, 64},
-    {"gemm_f16_64x128x64_w1x2", launch_cfg<64, 128, 1, 2, 64>, 64, 128, 64},
-    {"gemm_f16dma_256x128x64_s3", launch_dma<256, 128, 64, 3>, 256, 128, 64},
-    {"gemm_f16dma_256x128x32_s3", launch_dma<256, 128, 32, 3>, 256, 128, 32},
-    {"gemm_f16dma_128x128x64_s3", launch_dma<128, 128, 64, 3>, 128, 128, 64},
-    {"gemm_f16dma_128x128x32_s4", launch_dma<128, 128, 32, 4>, 128, 128, 32},
-    {"gemm_f16dma_128x256x32_s3", launch_dma<128, 256, 32, 3>, 128, 256, 32},
-    {"gemm_f16dma_256x256x32_s3", launch_dma<256, 256, 32, 3>, 256, 256, 32},
-    {"gemm_f16pipe_256x128x32_s3", launch_pipe_plain<256, 128, 32, 3>, 256, 128, 32},
-    {"gemm_f16pipe_256x128x64_s2", launch_pipe_plain<256, 128, 64, 2>, 256, 128, 64},
-    {"gemm_f16pipe_128x256x32_s3", launch_pipe_plain<128, 256, 32, 3>, 128, 256, 32},
-    {"gemm_f16pipe_256x256x32_s3", launch_pipe_plain<256, 256, 32, 3>, 256, 256, 32},
-    {"gemm_f16pipe_128x128x32_s4", launch_pipe_plain<128, 128, 32, 4>, 128, 128, 32},
-    {"gemm_f16pipe_256x128x32_s4", launch_pipe_plain<256, 128, 32, 4>, 256, 128, 32},
-    {"gemm_f16pipe_256x256x32_s3_w2x4", launch_pipe_plain<256, 256, 32, 3, 2, 4>, 256, 256, 32},
-    {"gemm_f16pipe_256x256x64_s2_w2x4", launch_pipe_plain<256, 256, 64, 2, 2, 4>, 256, 256, 64},
-    {"gemm_f16pipe_256x128x32_s4_w4x2", launch_pipe_plain<256, 128, 32, 4, 4, 2>, 256, 128, 32},
-    {"gemm_f16pipe_256x128x64_s2_w4x2", launch_pipe_plain<256, 128, 64, 2, 4, 2>, 256, 128, 64},
-    {"gemm_f16pipe_128x256x32_s4_w2x4", launch_pipe_plain<128, 256, 32, 4, 2, 4>, 128, 256, 32},
-    {"gemm_f16pipe_256x256x32_s4_w2x4", launch_pipe_plain<256, 256, 32, 4, 2, 4>, 256, 256, 32},
-    {"gemm_f16pipe_128x128x32_s4_w2x4", launch_pipe_plain<128, 128, 32, 4, 2, 4>, 128, 128, 32},
-    {"gemm_f16pipe_256x128x64_s3_w4x2", launch_pipe_plain<256, 128, 64, 3, 4, 2>, 256, 128, 64},
-    {"gemm_f16pipe_128x128x64_s3_w2x4", launch_pipe_plain<128, 128, 64, 3, 2, 4>, 128, 128, 64},
-    {"gemm_f16pipe_128x256x64_s2_w2x4", launch_pipe_plain<128, 256, 64, 2, 2, 4>, 128, 256, 64},
-    {"gemm_f16pipe_128x128x128_s2_w2x4", launch_pipe_plain<128, 128, 128, 2, 2, 4>, 128, 128, 128},
-    {"gemm_f16pipe_192x128x64_s2_w2x4", launch_pipe_plain<192, 128, 64, 2, 2, 4>, 192, 128, 64},
-    {"gemm_f16pipe_192x128x64_s2_w2x2", launch_pipe_plain<192, 128, 64, 2, 2, 2>, 192, 128, 64},
+#define SAMHIP_CFG(BM, BN, BK, S, WM, WN)                                                            \
+    {"gemm_f16pipe_" #BM "x" #BN "x" #BK "_s" #S "_w" #WM "x" #WN, launch_pipe_plain<BM, BN, BK, S, WM, WN>, BM, \
+     BN, BK, WM, WN}
+// Every configuration runs the pipelined kernel; the ones the picks below
+// do not take stay selectable through SAMHIP_GEMM_CONFIG for tile sweeps.
+constexpr Cfg kConfigs[] = {
+    SAMHIP_CFG(256, 256, 64, 2, 2, 4),   // qkv-like grids that fill the CUs
+    SAMHIP_CFG(192, 128, 64, 2, 2, 4),   // the rest of the tall shapes
+    SAMHIP_CFG(128, 128, 64, 3, 2, 4),   // plain products with small grids
+    SAMHIP_CFG(256, 128, 64, 2, 2, 2),
+    SAMHIP_CFG(256, 128, 32, 3, 2, 2),
+    SAMHIP_CFG(128, 256, 32, 3, 2, 2),
+    SAMHIP_CFG(256, 256, 32, 3, 2, 4),
+    SAMHIP_CFG(256, 128, 64, 2, 4, 2),
+    SAMHIP_CFG(128, 256, 64, 2, 2, 4),
+    SAMHIP_CFG(128, 128, 128, 2, 2, 4),
+    SAMHIP_CFG(192, 128, 64, 2, 2, 2),
 };
+#undef SAMHIP_CFG
+constexpr int kCfgSquare = 0, kCfgWide = 1, kCfgSmall = 2;
+static_assert(kConfigs[kCfgSquare].bm == 256 && kConfigs[kCfgSquare].bn == 256 && kConfigs[kCfgWide].bm == 192 &&
+                  kConfigs[kCfgWide].bn == 128 && kConfigs[kCfgSmall].bm == 128 && kConfigs[kCfgSmall].bn == 128,
+              "the picks below name these entries");
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
 }  // namespace
@@ -800,7 +486,7 @@ bool gemm_f16_supported(int M, int N, int K, int64_t lda, int64_t ldb) {
 int gemm_f16_pick(int M, int N, int /*K*/, int cus) {
     const int64_t tiles = int64_t((M + 255) / 256) * ((N + 255) / 256);
     const int64_t waves = (tiles + cus - 1) / cus;
-    return tiles * 10 >= waves * cus * 8 ? 20 : 30;
+    return tiles * 10 >= waves * cus * 8 ? kCfgSquare : kCfgWide;
 }
 
 // Plain products (mul_mat) also take 128x128x64 tiles on 2x4 waves (three
@@ -809,14 +495,12 @@ int gemm_f16_pick(int M, int N, int /*K*/, int cus) {
 // K = 256 and 23.5 vs 29.3 us at K = 2048; N = 2048 stays 192x128 (17.3 vs
 // 22.1 us).
 int gemm_f16_pick_plain(int M, int N, int K, int cus) {
-    constexpr int kSmall = 27;
     const int64_t tiles = int64_t((M + 191) / 192) * ((N + 127) / 128);
-    if (2 * tiles <= cus && kConfigs[kSmall].bm == 128 && kConfigs[kSmall].bn == 128 && K % kConfigs[kSmall].bk == 0)
-        return kSmall;
+    if (2 * tiles <= cus && K % kConfigs[kCfgSmall].bk == 0) return kCfgSmall;
     return gemm_f16_pick(M, N, K, cus);
 }
 
-// The picked configurations (20: 256x256x64 on 2x4 waves, 30: 192x128x64 on
+// The two configurations gemm_f16_pick returns (256x256x64 and 192x128x64 on
 // 2x4 waves) with each epilogue and operand mode the encoder uses.
 template <int BM, int BN, int WM, int WN>
 bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16* b, int64_t ldb, float* y,
@@ -865,7 +549,7 @@ const char* launch_gemm_f16_epi(const _Float16* a, int64_t lda, const float* row
     const bool spread = int64_t((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) <= cus;
     if (op.mode != A_PLAIN && (op.part % (op.mode == A_CONV3 ? 128 : 64) || op.part <= 0)) return nullptr;
     if (op.mode == A_CONV3 && (op.width <= 0 || op.height <= 0 || int64_t(op.width) * op.height != M)) return nullptr;
-    const bool ok = cfg == 20
+    const bool ok = cfg == kCfgSquare
         ? launch_epi<256, 256, 2, 4>(a, lda, row_scale, b, ldb, y, ldy, M, N, K, spread, ep, op, stream)
         : launch_epi<192, 128, 2, 4>(a, lda, row_scale, b, ldb, y, ldy, M, N, K, spread, ep, op, stream);
     return ok ? c.name : nullptr;

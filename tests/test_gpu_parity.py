@@ -299,8 +299,8 @@ def test_mul_mat_skinny_shapes(gpu_ctx, f16_ctx, oracle, samhip, qtype, shape):
 @pytest.mark.parametrize("qtype", TYPES)
 def test_mul_mat_fused_split_k_deterministic(gpu_ctx, f16_ctx, oracle, samhip, qtype):
     """Few weight rows and a long K: the fused kernel splits K over 16
-    workgroups whose partials meet through the arrival counters; repeated
-    calls (counters reset by the last workgroup) give identical bits, and a
+    workgroups that write their partial sums to staging, and a second launch
+    adds them in split order; repeated calls give identical bits, and a
     row-offset view with a strided activation is covered."""
     say("case fused split-K", qtype)
     rng = np.random.default_rng(43)
