@@ -171,8 +171,9 @@ void or_rng_normal(uint64_t seed, float mean, float stddev, float* out, int64_t 
 
 /* ---- helpers ------------------------------------------------------------ */
 
-/* ggml's nearest_int: round half to even for |v| < 2^22. */
-static inline int round_even(float v) { return (int)rintf(v); }
+/* ggml's nearest_int: round half to even for |v| < 2^22; a NaN gives 0, as
+ * nearest_int's bit trick does ((0x7fc00000 & 0x7fffff) - 0x400000). */
+static inline int round_even(float v) { return isnan(v) ? 0 : (int)rintf(v); }
 
 static inline void put_f16(uint8_t* p, float v) {
     const uint16_t h = or_fp32_to_fp16(v);
@@ -214,7 +215,8 @@ static void q8_0_block(const float* x, uint8_t* out, int rounding) {
     int8_t* q = (int8_t*)(out + 2);
     for (int j = 0; j < QK8; ++j) {
         const float v = x[j] * inv;
-        q[j] = (int8_t)(rounding == OR_Q8_ROUND_X86 ? rintf(v) : roundf(v));
+        const float r = rounding == OR_Q8_ROUND_X86 ? rintf(v) : roundf(v);
+        q[j] = isnan(r) ? 0 : (int8_t)r;   /* a NaN activation packs as code 0, as Q8_K's nearest_int */
     }
 }
 

@@ -111,7 +111,8 @@ __device__ __forceinline__ void quant8_codes(const floatx8& v, int lane, float& 
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float s = v[i] * inv;
-            q[i] = X86 ? __builtin_rintf(s) : __builtin_roundf(s);
+            const float r = X86 ? __builtin_rintf(s) : __builtin_roundf(s);
+            q[i] = r == r ? r : 0.f;   // a NaN activation packs as code 0, as in ggml's integer conversion
         }
     } else {
         // Q8_K: first element of largest magnitude in the 256-value block
@@ -129,7 +130,10 @@ __device__ __forceinline__ void quant8_codes(const floatx8& v, int lane, float& 
         if (amax != 0.f) {
             const float iscale = -127.f / smax;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) q[i] = fminf(127.f, __builtin_rintf(iscale * v[i]));
+            for (int i = 0; i < 8; ++i) {
+                const float r = __builtin_rintf(iscale * v[i]);
+                q[i] = r == r ? fminf(127.f, r) : 0.f;   // NaN -> 0 (ggml nearest_int)
+            }
             d = 1.f / iscale;
         } else {
 #pragma unroll
@@ -155,6 +159,51 @@ __device__ __forceinline__ half8 quant8(const floatx8& v, int lane, float down) 
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = (_Float16)((d * q[i]) * down);
     return o;
+}
+
+// Q8_0 block: amax over 8 lanes x 4 values; returns fp16 d bits and codes.
+__device__ __forceinline__ void q8_0_codes(const floatx4& v, int x86, float& d_out, int q[4]) {
+#pragma clang fp contract(off)
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = group_max<8>(amax);
+    const float d = amax / 127.f;
+    float inv;
+    if (x86) inv = amax != 0.f ? 127.f / amax : 0.f;
+    else inv = d != 0.f ? 1.f / d : 0.f;
+    d_out = d;
+    for (int i = 0; i < 4; ++i) {
+        const float r = x86 ? __builtin_rintf(v[i] * inv) : __builtin_roundf(v[i] * inv);
+        q[i] = r == r ? int(r) : 0;   // |r| <= 127 when finite; NaN -> 0
+    }
+}
+
+// Q8_K block over the whole wave (64 lanes x 4 values = 256): ggml keeps the
+// first element of largest magnitude as the signed maximum.
+__device__ __forceinline__ void q8_k_codes(const floatx4& v, int lane, float& d_out, int q[4]) {
+#pragma clang fp contract(off)
+    float amax = 0.f, smax = 0.f;
+    int idx = 1 << 30;
+    for (int i = 0; i < 4; ++i) {
+        const float a = fabsf(v[i]);
+        if (a > amax) { amax = a; smax = v[i]; idx = 4 * lane + i; }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float oa = __shfl_xor(amax, off, 64);
+        const float os = __shfl_xor(smax, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; smax = os; idx = oi; }
+    }
+    if (amax == 0.f) {
+        d_out = 0.f;
+        for (int i = 0; i < 4; ++i) q[i] = 0;
+        return;
+    }
+    const float iscale = -127.f / smax;
+    for (int i = 0; i < 4; ++i) {
+        const float r = __builtin_rintf(iscale * v[i]);
+        q[i] = r == r ? (r < 127.f ? int(r) : 127) : 0;   // NaN -> 0 (ggml nearest_int)
+    }
+    d_out = 1.f / iscale;
 }
 
 }  // namespace samhip

@@ -214,49 +214,6 @@ __global__ __launch_bounds__(256) void prep_kernel(const float* __restrict__ x, 
     if (t < int64_t(N) * (K / 32) * 2) dequant_piece<WT>(W, w_stride, K, t, wout, ldo);
 }
 
-// Q8_0 block: amax over 8 lanes x 4 values; returns fp16 d bits and codes.
-__device__ __forceinline__ void q8_0_codes(const floatx4& v, int x86, float& d_out, int q[4]) {
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = group_max<8>(amax);
-    const float d = amax / 127.f;
-    float inv;
-    if (x86) inv = amax != 0.f ? 127.f / amax : 0.f;
-    else inv = d != 0.f ? 1.f / d : 0.f;
-    d_out = d;
-    for (int i = 0; i < 4; ++i) {
-        const float s = v[i] * inv;
-        q[i] = int(x86 ? __builtin_rintf(s) : __builtin_roundf(s));
-    }
-}
-
-// Q8_K block over the whole wave (64 lanes x 4 values = 256): ggml keeps the
-// first element of largest magnitude as the signed maximum.
-__device__ __forceinline__ void q8_k_codes(const floatx4& v, int lane, float& d_out, int q[4]) {
-    float amax = 0.f, smax = 0.f;
-    int idx = 1 << 30;
-    for (int i = 0; i < 4; ++i) {
-        const float a = fabsf(v[i]);
-        if (a > amax) { amax = a; smax = v[i]; idx = 4 * lane + i; }
-    }
-    for (int off = 32; off > 0; off >>= 1) {
-        const float oa = __shfl_xor(amax, off, 64);
-        const float os = __shfl_xor(smax, off, 64);
-        const int oi = __shfl_xor(idx, off, 64);
-        if (oa > amax || (oa == amax && oi < idx)) { amax = oa; smax = os; idx = oi; }
-    }
-    if (amax == 0.f) {
-        d_out = 0.f;
-        for (int i = 0; i < 4; ++i) q[i] = 0;
-        return;
-    }
-    const float iscale = -127.f / smax;
-    for (int i = 0; i < 4; ++i) {
-        const int t = int(__builtin_rintf(iscale * v[i]));
-        q[i] = t < 127 ? t : 127;
-    }
-    d_out = 1.f / iscale;
-}
-
 // One wave per row, 4 rows per 256-thread block.
 template <int MODE>
 __global__ __launch_bounds__(256) void stage_rows_kernel(const float* __restrict__ x, int64_t x_stride, int M, int K,
@@ -632,7 +589,8 @@ __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float* __restr
     float s = v;
     for (int off = 16; off > 0; off >>= 1) s = s + __shfl_xor(s, off, 32);
     const float d = amax / 127.f;
-    const float q = amax == 0.f ? 0.f : __builtin_roundf(v / d);
+    const float qr = amax == 0.f ? 0.f : __builtin_roundf(v / d);
+    const float q = qr == qr ? qr : 0.f;   // NaN -> code 0
     uint8_t* out = dst + blk * 36;
     out[4 + lane] = uint8_t(int8_t(q));
     if (lane == 0) {
@@ -662,7 +620,8 @@ __global__ __launch_bounds__(256) void quantize_q8_1_mmq_kernel(const float* __r
     float q = 0.f, d = 0.f;
     if (amax != 0.f) {
         const float d_inv = 127.f / amax;
-        q = __builtin_roundf(v * d_inv);
+        const float r = __builtin_roundf(v * d_inv);
+        q = r == r ? r : 0.f;   // NaN -> code 0 (such blocks also raise *invalid)
         d = 1.f / d_inv;
     }
     uint8_t* out = dst + ((kb >> 2) * rows + r) * 144;

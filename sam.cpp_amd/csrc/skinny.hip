@@ -598,7 +598,8 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float s = v[4 * i + j] * inv;
-                const int q = int(X86 ? __builtin_rintf(s) : __builtin_roundf(s));
+                const float r = X86 ? __builtin_rintf(s) : __builtin_roundf(s);
+                const int q = r == r ? int(r) : 0;   // NaN -> 0
                 wd |= uint32_t(q & 0xff) << (8 * j);
             }
             packed[i] = wd;

@@ -190,10 +190,10 @@ __global__ __launch_bounds__(256) void zero_pad_kernel(AttnOperands o, int N, in
 // computes attention in F32 (GGML_PREC_F32 on every FLASH_ATTN_EXT node,
 // src/runtime/ggml/graph.hpp:64), at three times the MFMA work.
 // ---------------------------------------------------------------------------
-constexpr int RSRC_WORD3 = 0x00020000;   // raw buffer, 32-bit data format
+[[maybe_unused]] constexpr int RSRC_WORD3 = 0x00020000;   // raw buffer, 32-bit data format
 
 // s_waitcnt vmcnt(0), expcnt/lgkmcnt left at their maximum (gfx9 encoding)
-__device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x70 | 0xF00); }
+[[maybe_unused]] __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x70 | 0xF00); }
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
@@ -202,7 +202,7 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 // (lane layout measured on gfx950).  With lane r of a group addressing
 // V[key0 + r/4][d0 + 4 (r % 4)] of a key-major tile, lane i holds
 // V[key0 + j][d0 + i], j = 0..3: four consecutive keys of one column.
-__device__ __forceinline__ half4 ds_read_tr(const uint8_t* p) {
+[[maybe_unused]] __device__ __forceinline__ half4 ds_read_tr(const uint8_t* p) {
     const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)(p));
     return __builtin_bit_cast(half4, v);
 }

@@ -234,6 +234,27 @@ def test_mul_mat_q8_0_k32(gpu_ctx, f16_ctx, oracle):
     _check_product(oracle, 8, w, x, gpu_ctx.matmul(8, w, x), f16_ctx.matmul(8, w, x))
 
 
+def test_nan_activations_pack_as_code_zero(gpu_ctx, oracle, samhip):
+    """A NaN activation packs as code 0 in Q8_0 (both roundings) and Q8_K
+    blocks, as ggml's nearest_int gives for Q8_K; the block scale comes from
+    the other values.  Wire rows are bit-exact with the oracle, and products
+    on the staged (tall) and fused (skinny) paths match its native path."""
+    say("case NaN activations")
+    rng = np.random.default_rng(61)
+    x = rng.standard_normal((300, 1024)).astype(np.float32)
+    x[3, 7] = x[40, 300] = x[299, 1023] = x[17, 511] = np.nan
+    for qtype, gpu_mode, cpu_mode in ((oracle.Q8_0, samhip.ROUND_X86, oracle.ROUND_X86),
+                                      (oracle.Q8_0, samhip.ROUND_REF, oracle.ROUND_REF),
+                                      (oracle.Q8_K, samhip.ROUND_X86, oracle.ROUND_X86)):
+        assert np.array_equal(gpu_ctx.quantize(qtype, x, gpu_mode), oracle.quantize(qtype, x, cpu_mode))
+    for qtype in (oracle.Q8_0, oracle.Q4_K):
+        w = oracle.quantize(qtype, (rng.standard_normal((256, 1024)) * 0.02).astype(np.float32))
+        for m in (300, 40):   # staging kernel + tall GEMM, fused skinny kernel
+            y = gpu_ctx.matmul(qtype, w, x[:m])
+            assert np.isfinite(y).all()
+            assert max_row_rel_l2(y, oracle.mul_mat_native(qtype, w, x[:m], oracle.ROUND_X86)) <= ROW_REL_L2
+
+
 def test_mul_mat_extreme_row_magnitudes(gpu_ctx, f16_ctx, oracle):
     """F16 mode keeps rows far outside binary16's range accurate (per-row
     power-of-two scale).  Native Q8_0 packing is ggml's: a block scale above
