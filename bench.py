@@ -25,6 +25,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 METRIC = "Q-matmul TOPS & % int8 MFMA peak; SAM3 Q4_K vision encode ms/image @1008px"
 M_TOKENS = 5184
 SHAPES = [("qkv", 1024, 3072), ("proj", 1024, 1024), ("fc1", 1024, 4736), ("fc2", 4736, 1024)]
+SWEEP_FORMATS = ("q4_K", "q5_K", "q6_K")   # weight formats of the sweep, in products() order
 PEAK_FP16_TFLOPS = 2500.0     # MI355X dense fp16 MFMA
 PEAK_INT8_TOPS = 5000.0       # MI355X dense int8 MFMA
 PEAK_HBM_GBPS = 8000.0
@@ -33,7 +34,7 @@ PEAK_HBM_GBPS = 8000.0
 # rocprofv3 commands whose CSV output summarize_profiles() reads
 PROFILE_COMMANDS = {
     "trace": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/trace -o bench -- "
-             "python3 bench.py --steps 20 --warmup 5 --no-cpu-baseline --no-encoder",
+             "python3 bench.py --steps 20 --warmup 5 --no-cpu-baseline --no-encoder --no-configs",
     "text": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/text -o bench -- "
             "python3 bench.py --workload text --steps 10 --warmup 2",
     "encoder": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/encoder -o bench -- "
@@ -41,9 +42,12 @@ PROFILE_COMMANDS = {
     "detector": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/detector -o bench -- "
                 "python3 bench.py --workload detector --steps 10 --warmup 2",
     "fetch": "rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/fetch -o bench -- "
-             "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-encoder",
+             "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-encoder --no-configs",
     "write": "rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/write -o bench -- "
-             "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-encoder",
+             "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-encoder --no-configs",
+    "pmc": "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_BUSY_CYCLES "
+           "SQ_WAIT_INST_LDS SQ_INSTS_LDS SQ_INSTS_MFMA GRBM_GUI_ACTIVE --output-format csv -d <out>/pmc -o bench -- "
+           "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-encoder --no-configs",
     "copy_fetch": "rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/copy_FETCH_SIZE -o copy -- "
                   "python3 bench.py --copy-calibration",
     "copy_write": "rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/copy_WRITE_SIZE -o copy -- "
@@ -83,21 +87,11 @@ COPY_ELEMS = 1 << 26          # F32 elements of the calibration copy (256 MiB re
 
 def kernel_symbol(variant):
     """Template symbol of a GEMM variant name, as rocprofv3 reports it demangled:
-    gemm_f16_{BM}x{BN}x{BK}_w{WM}x{WN} -> gemm_f16_kernel<BM, BN, WM, WN, BK>,
-    gemm_f16dma_{BM}x{BN}x{BK}_s{S}    -> gemm_f16_dma_kernel<BM, BN, BK, S>,
     gemm_f16pipe_{BM}x{BN}x{BK}_s{S}[_w{WM}x{WN}]
-                                       -> gemm_f16_pipe_kernel<BM, BN, BK, S, WM, WN, 0, 0> (2x2 waves by
-                                          default; plain epilogue and A operand).
+        -> gemm_f16_pipe_kernel<BM, BN, BK, S, WM, WN, 0, 0> (2x2 waves by
+           default; plain epilogue and A operand).
     Returns (symbol, threads per workgroup, BM, BN) or None."""
     import re
-    m = re.fullmatch(r"gemm_f16_(\d+)x(\d+)x(\d+)_w(\d+)x(\d+)", variant)
-    if m:
-        bm, bn, bk, wm, wn = map(int, m.groups())
-        return f"gemm_f16_kernel<{bm}, {bn}, {wm}, {wn}, {bk}>", 64 * wm * wn, bm, bn
-    m = re.fullmatch(r"gemm_f16dma_(\d+)x(\d+)x(\d+)_s(\d+)", variant)
-    if m:
-        bm, bn, bk, st = map(int, m.groups())
-        return f"gemm_f16_dma_kernel<{bm}, {bn}, {bk}, {st}>", 256, bm, bn
     m = re.fullmatch(r"gemm_f16pipe_(\d+)x(\d+)x(\d+)_s(\d+)(?:_w(\d+)x(\d+))?", variant)
     if m:
         bm, bn, bk, st = map(int, m.groups()[:4])
@@ -118,10 +112,9 @@ def hbm_traffic(variant, shape):
     grid = -(-m // bm) * -(-n // bn) * threads
     with open(TRAFFIC_FILE) as f:
         table = json.load(f)
-    for e in table["kernels"]:
-        if e["symbol"] == symbol and e["grid"] == grid:
-            return int(e["fetch_bytes"] + e["write_bytes"])
-    return None
+    hits = [e["fetch_bytes"] + e["write_bytes"] for e in table["kernels"]
+            if e["symbol"] == symbol and e["grid"] == grid and e.get("K") == shape[2]]
+    return int(np.mean(hits)) if hits else None
 
 
 def copy_calibration():
@@ -164,6 +157,40 @@ def summarize_profiles(d, commands):
         name = name.replace("void ", "", 1).replace("samhip::(anonymous namespace)::", "")
         return name.split("(")[0]
 
+    def sweep_products(rs):
+        """Dispatch id -> (product, K) for the sweep's dispatches: the sweep
+        runs first and each mul_mat launches its preparation kernels and then
+        one GEMM, in products() order, so the i-th GEMM dispatch is product
+        i mod 12 (its grid must confirm it: proj and fc2 share a kernel and a
+        grid) and a prep_kernel dispatch belongs to the GEMM that follows it.
+        Products are named `shape:format` (fc2 is Q8_0 in every format)."""
+        import re
+        order = [(f"{name}:{'q8_0' if k % 256 else fmt}", name, k, n)
+                 for fmt in SWEEP_FORMATS for name, k, n in SHAPES]
+        by_id = {}
+        for r in rs:
+            by_id[int(r["Dispatch_Id"])] = (short(r["Kernel_Name"]), int(r.get("Grid_Size") or r["Grid_Size_X"]))
+        out, pending, i = {}, [], 0
+        for did in sorted(by_id):
+            sym, grid = by_id[did]
+            if sym.startswith("prep_kernel"):
+                pending.append(did)
+                continue
+            if not sym.startswith("gemm_"):
+                continue
+            label, name, k, n = order[i % len(order)]
+            t = re.match(r"gemm_f16_pipe_kernel<(\d+), (\d+), \d+, \d+, (\d+), (\d+)", sym)
+            want = -(-M_TOKENS // int(t.group(1))) * -(-n // int(t.group(2))) * 64 * int(t.group(3)) * int(t.group(4)) \
+                if t else None
+            if want != grid:
+                break
+            for p_ in pending + [did]:
+                out[p_] = (label, k)
+            pending, i = [], i + 1
+        if i % len(order):
+            raise RuntimeError(f"{i} sweep GEMM dispatches matched: not whole steps of {len(order)}")
+        return out
+
     copy_kib = {}
     for c in ("FETCH_SIZE", "WRITE_SIZE"):
         rs = [r for r in rows(os.path.join(d, f"copy_{c}", "copy_counter_collection.csv")) if "add" in r["Kernel_Name"]]
@@ -174,16 +201,18 @@ def summarize_profiles(d, commands):
     agg = {}
     for c, sub in (("FETCH_SIZE", "fetch"), ("WRITE_SIZE", "write")):
         rs = rows(os.path.join(d, sub, "bench_counter_collection.csv"))
+        labels = sweep_products(rs)
         for r in rs:
-            key = (short(r["Kernel_Name"]), int(r["Grid_Size"]))
+            name, k = labels.get(int(r["Dispatch_Id"]), (None, None))
+            key = (short(r["Kernel_Name"]), int(r["Grid_Size"]), name, k)
             agg.setdefault(key, {}).setdefault(c, []).append(float(r["Counter_Value"]))
     kernels = []
-    for (sym, grid), v in sorted(agg.items()):
+    for (sym, grid, name, k), v in sorted(agg.items(), key=lambda t: tuple(str(x) for x in t[0])):
         if "FETCH_SIZE" not in v or "WRITE_SIZE" not in v:
             continue
         fk = float(np.mean(v["FETCH_SIZE"]))
         wk = float(np.mean(v["WRITE_SIZE"]))
-        kernels.append({"symbol": sym, "grid": grid, "dispatches": len(v["FETCH_SIZE"]),
+        kernels.append({"symbol": sym, "grid": grid, "product": name, "K": k, "dispatches": len(v["FETCH_SIZE"]),
                         "fetch_kib": round(fk, 1), "write_kib": round(wk, 1),
                         "fetch_bytes": int(fk * 1024 * fetch_factor), "write_bytes": int(wk * 1024 * write_factor)})
     table = {"fetch_factor": fetch_factor, "write_factor": write_factor, "copy_kib": copy_kib,
@@ -207,6 +236,42 @@ def summarize_profiles(d, commands):
 
     stats_table("trace", "Kernel time, SAM 3 ViT linear sweep at M=5184 (12 mul_mat per step)", commands["trace"],
                 "kernel_stats_vit_sweep_m5184.md")
+    trace_csv = os.path.join(d, "trace", "bench_kernel_trace.csv")
+    if os.path.exists(trace_csv):
+        rs = rows(trace_csv)
+        labels = sweep_products(rs)
+        per = {}
+        for r in rs:
+            did = int(r["Dispatch_Id"])
+            if did not in labels:
+                continue
+            sym = short(r["Kernel_Name"])
+            e = per.setdefault(labels[did][0], {"K": labels[did][1], "gemm": [], "prep": [], "symbol": None})
+            us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            if sym.startswith("gemm_"):
+                e["gemm"].append(us)
+                e["symbol"] = sym
+            else:
+                e["prep"].append(us)
+        nmap = dict((nm, n) for nm, _, n in SHAPES)
+        lines = ["", "Per product (same trace): every dispatch of the sweep is named by its product (each mul_mat "
+                 "launches its preparation kernel and then one GEMM, in a fixed product order that each GEMM's grid "
+                 "confirms). Means over every step of the run, warmup included.", "",
+                 "| product | M | N | K | GEMM kernel | GEMM calls | GEMM avg us | GEMM min us | GEMM TFLOP/s | prep avg us "
+                 "| linear TOPS |", "|---|---|---|---|---|---|---|---|---|---|---|"]
+        seen = set()
+        for label, _, k, n in [(f"{nm}:{'q8_0' if k_ % 256 else fmt}", nm, k_, n_)
+                               for fmt in SWEEP_FORMATS for nm, k_, n_ in SHAPES]:
+            e = per.get(label)
+            if not e or not e["gemm"] or label in seen:
+                continue
+            seen.add(label)
+            g, p_ = float(np.mean(e["gemm"])), float(np.mean(e["prep"])) if e["prep"] else 0.0
+            fl = 2.0 * M_TOKENS * n * k
+            lines.append(f"| {label} | {M_TOKENS} | {n} | {k} | `{e['symbol']}` | {len(e['gemm'])} | {g:.1f} | "
+                         f"{min(e['gemm']):.1f} | {fl / g / 1e6:.0f} | {p_:.1f} | {fl / (g + p_) / 1e6:.0f} |")
+        with open(os.path.join(ROOT, "profiles", "kernel_stats_vit_sweep_m5184.md"), "a") as f:
+            f.write("\n".join(lines) + "\n")
     stats_table("text", "Kernel time, SAM 3 text-encoder linear stream at M=32 (97 mul_mat per step, Q8_0)",
                 commands["text"], "kernel_stats_text_stream_m32_q8_0.md")
     if os.path.isdir(os.path.join(d, "detector")):
@@ -230,13 +295,58 @@ def summarize_profiles(d, commands):
              f"Calibration: a plain copy of {4 * COPY_ELEMS} bytes (read, and the same written) reads "
              f"FETCH_SIZE {copy_kib['FETCH_SIZE']:.1f} KiB and WRITE_SIZE {copy_kib['WRITE_SIZE']:.1f} KiB, so "
              f"HBM bytes = FETCH_SIZE x 1024 x {fetch_factor:.3f} + WRITE_SIZE x 1024 x {write_factor:.3f}.", "",
-             "| kernel | grid (threads) | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM MB read | HBM MB written |",
-             "|---|---|---|---|---|---|---|"]
+             "Dispatches of the sweep are named by product (M 5184; each mul_mat launches its preparation kernel "
+             "and then one GEMM, in a fixed product order that each GEMM's grid confirms); set-up kernels by "
+             "grid.", "",
+             "| kernel | grid (threads) | product | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM MB read | "
+             "HBM MB written |",
+             "|---|---|---|---|---|---|---|---|"]
+    nmap = dict((nm, n) for nm, _, n in SHAPES)
     for e in kernels:
-        lines.append(f"| `{e['symbol']}` | {e['grid']} | {e['dispatches']} | {e['fetch_kib']} | {e['write_kib']} | "
-                     f"{e['fetch_bytes'] / 1e6:.2f} | {e['write_bytes'] / 1e6:.2f} |")
+        prod = f"{e['product']} N {nmap[e['product'].split(':')[0]]} K {e['K']}" if e["product"] else ""
+        lines.append(f"| `{e['symbol']}` | {e['grid']} | {prod} | {e['dispatches']} | {e['fetch_kib']} | "
+                     f"{e['write_kib']} | {e['fetch_bytes'] / 1e6:.2f} | {e['write_bytes'] / 1e6:.2f} |")
     with open(os.path.join(ROOT, "profiles", "hbm_traffic_vit_sweep_m5184.md"), "w") as f:
         f.write("\n".join(lines) + "\n")
+
+    pmc_path = os.path.join(d, "pmc", "bench_counter_collection.csv")
+    if os.path.exists(pmc_path):
+        rs = rows(pmc_path)
+        labels = sweep_products(rs)
+        per = {}
+        for r in rs:
+            did = int(r["Dispatch_Id"])
+            if did not in labels or not short(r["Kernel_Name"]).startswith("gemm_"):
+                continue
+            e = per.setdefault(did, {"symbol": short(r["Kernel_Name"]), "grid": int(r["Grid_Size"]),
+                                     "product": labels[did],
+                                     "us": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3})
+            e[r["Counter_Name"]] = e.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        groups = {}
+        for e in per.values():
+            groups.setdefault((e["symbol"], e["grid"], e["product"]), []).append(e)
+        lines = ["# MFMA and LDS counters, SAM 3 ViT linear sweep at M=5184 (GEMM kernels)", "",
+                 "Command (from the repository root, `cd /tmp && export TMPDIR=/tmp` first):", "", "```",
+                 commands["pmc"], "```", "",
+                 "Medians per dispatch. MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 x 1024 SIMDs), "
+                 "the profiler's own MFMA-utilization expression with GRBM_GUI_ACTIVE summed over the 8 XCD "
+                 "instances; GUI_ACTIVE also counts cycles around the dispatch, so short kernels read low. LDS "
+                 "conflict = SQ_LDS_BANK_CONFLICT / (SQ_LDS_IDX_ACTIVE - SQ_LDS_BANK_CONFLICT).", "",
+                 "| kernel | grid (threads) | product | dispatches | dispatch us (under counters) | GUI_ACTIVE cycles "
+                 "per XCD | MFMA busy % | LDS bank-conflict % | SQ_INSTS_MFMA | SQ_INSTS_LDS |",
+                 "|---|---|---|---|---|---|---|---|---|---|"]
+        for (sym, grid, (name, k)), es in sorted(groups.items(), key=lambda t: t[0][2][0]):
+            def med(f):
+                return float(np.median([f(e) for e in es]))
+            gui = med(lambda e: e["GRBM_GUI_ACTIVE"] / 8)
+            busy = med(lambda e: 100 * e["SQ_VALU_MFMA_BUSY_CYCLES"] / (e["GRBM_GUI_ACTIVE"] / 8 * 1024))
+            conf = med(lambda e: 100 * e["SQ_LDS_BANK_CONFLICT"] /
+                       max(1.0, e["SQ_LDS_IDX_ACTIVE"] - e["SQ_LDS_BANK_CONFLICT"]))
+            lines.append(f"| `{sym}` | {grid} | {name} M {M_TOKENS} N {nmap[name.split(':')[0]]} K {k} | {len(es)} | "
+                         f"{med(lambda e: e['us']):.1f} | {gui:.0f} | {busy:.1f} | {conf:.1f} | "
+                         f"{med(lambda e: e['SQ_INSTS_MFMA']):.3g} | {med(lambda e: e['SQ_INSTS_LDS']):.3g} |")
+        with open(os.path.join(ROOT, "profiles", "mfma_lds_counters_vit_sweep_m5184.md"), "w") as f:
+            f.write("\n".join(lines) + "\n")
 
 
 def cpu_info():
