@@ -1043,8 +1043,8 @@ def other_configs(args, sh, ctx, ops, xbuf):
 def main():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--compute", choices=["native", "f16"], default="native")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU time budget of the stream baselines")
     ap.add_argument("--cpu-rows", type=int, default=64)
@@ -1054,6 +1054,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--trace", choices=["dominant", "all", "none"], default="dominant",
                     help="launches bracketed by HIP events inside the timed region")
+    ap.add_argument("--trace-every", type=int, default=5,
+                    help="bracket the traced launches of every N-th timed step only (1: every step)")
     ap.add_argument("--workload", choices=["vit", "text", "encoder", "detector"], default="vit",
                     help="vit: the ViT linear sweep (headline, with the encoder's ms/image beside it); text: the "
                          "M=32 text-encoder linear stream; encoder: the vision encoder forward alone")
@@ -1159,14 +1161,23 @@ def main():
                             "linear_tops": round(2.0 * M_TOKENS * n * k / (g + s + d) / 1e9, 2) if g else None})
     kernel_share = {name: round(v / sum(total.values()), 4) for name, v in sorted(total.items(), key=lambda t: -t[1])}
 
-    # timed region: events only around the dominant kernel (or none / all)
-    log(f"timing {args.steps} steps (trace: {args.trace}, dominant kernel {dominant})")
+    # timed region: events around the dominant kernel's launches (or none /
+    # all) in every trace_every-th step; each bracket adds two event records
+    # (several microseconds of GPU time), so the other steps run without
+    every = max(1, args.trace_every)
+    log(f"timing {args.steps} steps (trace: {args.trace} in every {every}. step, dominant kernel {dominant})")
     ctx.synchronize()
     if args.trace != "none":
         ctx.trace_begin(dominant if args.trace == "dominant" else None)
+        ctx.trace_pause(every > 1)
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
+    for i in range(args.steps):
+        if args.trace != "none" and every > 1 and i % every == every - 1:
+            ctx.trace_pause(False)
+            step()
+            ctx.trace_pause(True)
+        else:
+            step()
     if args.trace != "none":
         records = ctx.trace_end(capacity=4 * len(ops) * args.steps + 16)   # waits for the stream
     else:
@@ -1194,7 +1205,9 @@ def main():
                 "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": hbm_traffic(dominant, (m_, n_, k_)),
                 "kernel": dominant, "weight_type": sh.TYPE_NAMES.get(qt_dom, str(qt_dom)),
                 "shape": {"M": m_, "N": n_, "K": k_}, "launch_ms": round(avg_ms, 5),
-                "launches": len(same), "events_in": "timed region" if records else "profiling pass",
+                "launches": len(same),
+                "events_in": (f"timed region, every {every}. step" if every > 1 else "timed region") if records
+                else "profiling pass",
                 "flops_per_launch": flops, "algorithmic_bytes_per_launch": int(alg_bytes),
                 "hbm_gbps_algorithmic": round(alg_bytes / (avg_ms * 1e-3) / 1e9, 1),
                 "pct_int8_peak": round(100 * achieved / PEAK_INT8_TOPS, 2)}

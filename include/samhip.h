@@ -334,6 +334,12 @@ typedef struct samhip_kernel_record {
 } samhip_kernel_record;
 int samhip_trace_begin(samhip_context* ctx, const char* kernel_filter);
 int samhip_trace_end(samhip_context* ctx, samhip_kernel_record* records, size_t capacity, size_t* count);
+/* Pauses (paused != 0) or resumes the bracketing of an open trace without
+ * synchronizing; records already taken are kept.  Each bracket adds two
+ * event records to the stream (several microseconds of GPU time per launch),
+ * so a timed run can bracket a sample of its steps.  No reference
+ * counterpart (an observer is attached for a whole compute). */
+int samhip_trace_pause(samhip_context* ctx, int paused);
 /* --- stream capture (no reference counterpart) ----------------------------
  * For launch-bound streams of small products (the text encoder's 97 linears
  * at M = 32): the calls between capture_begin and capture_end are recorded

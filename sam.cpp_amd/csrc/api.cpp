@@ -122,7 +122,8 @@ struct samhip_context {
         int64_t m, n, k;
         hipEvent_t start, stop;
     };
-    bool tracing = false;
+    bool tracing = false;        // a trace is open (trace_begin .. trace_end)
+    bool trace_paused = false;   // open but not bracketing (samhip_trace_pause)
     // stream capture: staging buffers that captured graphs still use
     bool capturing = false;
     int live_graphs = 0;
@@ -188,8 +189,11 @@ hipEvent_t pooled_event(samhip_context* ctx) {
         ctx->event_pool.pop_back();
         return e;
     }
+    // timing only (trace_end synchronizes the stream before reading them):
+    // no system-scope fence, so recording one does not write back and
+    // invalidate the caches between the launches it brackets
     hipEvent_t e = nullptr;
-    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
     return e;
 }
 
@@ -197,7 +201,7 @@ hipEvent_t pooled_event(samhip_context* ctx) {
 template <class Body>
 int traced(samhip_context* ctx, const char* kernel, int wt, int64_t m, int64_t n, int64_t k, Body body) {
     hipEvent_t a = nullptr, b = nullptr;
-    const bool record = ctx->tracing && ctx->trace.size() < kMaxTraceRecords &&
+    const bool record = ctx->tracing && !ctx->trace_paused && ctx->trace.size() < kMaxTraceRecords &&
                         (ctx->trace_filter.empty() || std::strstr(kernel, ctx->trace_filter.c_str()) != nullptr);
     if (record) {
         a = pooled_event(ctx);
@@ -1318,6 +1322,14 @@ int samhip_trace_begin(samhip_context* ctx, const char* kernel_filter) {
     }
     ctx->trace.clear();
     ctx->tracing = true;
+    ctx->trace_paused = false;
+    return SAMHIP_OK;
+}
+
+int samhip_trace_pause(samhip_context* ctx, int paused) {
+    if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
+    if (!ctx->tracing) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "trace_pause: no trace is open");
+    ctx->trace_paused = paused != 0;
     return SAMHIP_OK;
 }
 
@@ -1325,6 +1337,7 @@ int samhip_trace_end(samhip_context* ctx, samhip_kernel_record* records, size_t 
     if (!ctx || (capacity && !records)) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "invalid trace_end argument");
     SAMHIP_NOT_WHILE_CAPTURING(ctx, "trace_end");
     ctx->tracing = false;
+    ctx->trace_paused = false;
     if (int rc = set_device(ctx)) return rc;
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     for (size_t i = 0; i < ctx->trace.size() && i < capacity; ++i) {

@@ -111,6 +111,7 @@ SIGNATURES = {
     "samhip_last_error": ([ctypes.c_char_p, _SZ], _SZ),
     "samhip_trace_begin": ([_P, ctypes.c_char_p], _I),
     "samhip_trace_end": ([_P, ctypes.POINTER(KernelRecord), _SZ, ctypes.POINTER(_SZ)], _I),
+    "samhip_trace_pause": ([_P, ctypes.c_int], _I),
     "samhip_capture_begin": ([_P], _I),
     "samhip_capture_end": ([_P, ctypes.POINTER(_P)], _I),
     "samhip_graph_launch": ([_P, _P], _I),
@@ -292,6 +293,10 @@ class Context:
     def trace_begin(self, kernel_filter=None):
         """Bracket launches (all, or those whose name contains kernel_filter) with HIP events."""
         check(lib().samhip_trace_begin(self.handle, kernel_filter.encode() if kernel_filter else None))
+
+    def trace_pause(self, paused=True):
+        """Stops (or resumes) bracketing launches of the open trace, without synchronizing."""
+        check(lib().samhip_trace_pause(self.handle, 1 if paused else 0))
 
     def trace_end(self, capacity=1 << 16):
         """Returns [(kernel, weight_type, m, n, k, ms)] of the launches since trace_begin."""

@@ -485,6 +485,32 @@ def test_exec_info_counts(gpu_ctx, samhip):
     assert info.arithmetic_profile == b"samhip-q8-native-f16mfma-v1"
 
 
+def test_trace_pause_keeps_records_and_skips_paused_launches(samhip, oracle):
+    """Launches made while the open trace is paused carry no events; the
+    records taken before and after the pause are all returned."""
+    say("case trace pause")
+    rng = np.random.default_rng(31)
+    w = oracle.quantize(oracle.Q8_0, (rng.standard_normal((256, 256)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((300, 256)).astype(np.float32)
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
+        with pytest.raises(samhip.SamhipError):
+            ctx.trace_pause()                       # no trace open
+        ctx.trace_begin()
+        ctx.matmul(samhip.Q8_0, w, x)
+        one = ctx.trace_end()                       # the launches of one call
+        ctx.trace_begin()
+        ctx.matmul(samhip.Q8_0, w, x)
+        ctx.trace_pause()
+        ctx.matmul(samhip.Q8_0, w, x)
+        ctx.matmul(samhip.Q8_0, w, x)
+        ctx.trace_pause(False)
+        y = ctx.matmul(samhip.Q8_0, w, x)
+        recs = ctx.trace_end()
+    assert one and all(r[5] > 0 for r in recs), recs
+    assert [r[0] for r in recs] == 2 * [r[0] for r in one], (one, recs)
+    assert max_row_rel_l2(y, oracle.mul_mat_native(oracle.Q8_0, w, x, oracle.ROUND_X86)) <= ROW_REL_L2
+
+
 def test_capture_replays_match_eager(samhip, oracle):
     """A captured skinny + tall pair replays bit-identically to the eager
     calls, three times, with eager work and synchronizations in between."""
