@@ -67,3 +67,50 @@ def test_int8_strip_views_and_reference_probe(gpu_ctx, oracle, samhip):
                 assert not y.any() and not ref.any()
             else:
                 assert max_row_rel_l2(y, ref) <= EXACT
+
+
+def test_int8_strip_repeats_and_replays(samhip, oracle):
+    """Products with one and with several K slices (partial sums in the
+    context's staging, added by the reduce launch) in alternating order,
+    repeated eager calls and three replays of a captured stream, with eager
+    work between them, all give the first call's bits."""
+    say("case int8 tickets")
+    rng = np.random.default_rng(77)
+    shapes = [(32, 1024, 4096), (32, 3072, 1024), (7, 100, 1056), (32, 256, 512)]
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
+        ops, bufs = [], []
+        for m, n, k in shapes:
+            w = oracle.quantize(oracle.Q8_0, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            wb, xb, yb = ctx.upload(w), ctx.upload(x), ctx.alloc(m * n * 4)
+            bufs += [wb, xb, yb]
+            ops.append((samhip.tensor(samhip.Q8_0, k, n, wb.ptr), samhip.tensor(samhip.F32, k, m, xb.ptr),
+                        samhip.tensor(samhip.F32, n, m, yb.ptr), yb, (m, n), w, x))
+        for wt, xt, yt, *_ in ops:
+            ctx.mul_mat(wt, xt, yt)
+        assert ctx.query().kernel_variant == b"skinny_i8mfma_q8_0"
+        first = [ctx.download(yb, shp, np.float32) for _, _, _, yb, shp, _, _ in ops]
+        for (_, _, _, _, _, w, x), y in zip(ops, first):
+            assert max_row_rel_l2(y, oracle.mul_mat_native(oracle.Q8_0, w, x)) <= EXACT
+        for _ in range(3):
+            for wt, xt, yt, *_ in reversed(ops):
+                ctx.mul_mat(wt, xt, yt)
+        for (_, _, _, yb, shp, _, _), y in zip(ops, first):
+            assert np.array_equal(ctx.download(yb, shp, np.float32), y)
+        ctx.capture_begin()
+        for wt, xt, yt, *_ in ops:
+            ctx.mul_mat(wt, xt, yt)
+        g = ctx.capture_end()
+        try:
+            for rep in range(3):
+                for _, _, _, yb, shp, _, _ in ops:
+                    ctx.write(yb, np.zeros(shp, np.float32))
+                wt, xt, yt = ops[1][:3]
+                ctx.mul_mat(wt, xt, yt)                 # eager work between replays
+                ctx.synchronize()
+                g.launch()
+                ctx.synchronize()
+                for (_, _, _, yb, shp, _, _), y in zip(ops, first):
+                    assert np.array_equal(ctx.download(yb, shp, np.float32), y), rep
+        finally:
+            g.destroy()
