@@ -51,9 +51,10 @@ __device__ __forceinline__ uint32_t funnel_bytes(uint32_t hi, uint32_t lo, uint3
 // dword touched holds at least one requested byte, so no load crosses into
 // memory past the requested range's last dword.
 __device__ __forceinline__ u32x4 load16_a2(const uint8_t* p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
-    const uint32_t sh = uint32_t(a & 3);
+    // the aligned address is formed from p itself (not from an integer), so
+    // the compiler keeps p's global address space: global, not flat, loads
+    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 3);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p - sh);
     const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3];
     const uint32_t w4 = sh ? q[4] : 0u;
     return u32x4{funnel_bytes(w1, w0, sh), funnel_bytes(w2, w1, sh), funnel_bytes(w3, w2, sh), funnel_bytes(w4, w3, sh)};
@@ -61,9 +62,8 @@ __device__ __forceinline__ u32x4 load16_a2(const uint8_t* p) {
 
 // 4 bytes at a 2-byte aligned address.
 __device__ __forceinline__ uint32_t load4_a2(const uint8_t* p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
-    const uint32_t sh = uint32_t(a & 3);
+    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 3);
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p - sh);
     const uint32_t w0 = q[0];
     const uint32_t w1 = sh ? q[1] : 0u;
     return funnel_bytes(w1, w0, sh);
@@ -71,9 +71,9 @@ __device__ __forceinline__ uint32_t load4_a2(const uint8_t* p) {
 
 // 2 bytes at a 2-byte aligned address.
 __device__ __forceinline__ uint32_t load2_a2(const uint8_t* p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
-    return (a & 2) ? (w >> 16) : (w & 0xffffu);
+    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 3);
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(p - sh);
+    return (sh & 2) ? (w >> 16) : (w & 0xffffu);
 }
 
 // one byte

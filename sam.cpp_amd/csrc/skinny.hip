@@ -242,9 +242,10 @@ __global__ __launch_bounds__(512) void fused_skinny_kernel(const float* __restri
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
             const int r = 16 * kh + 2 * p + h;
-            const uintptr_t g = reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + r, N - 1)) * w_stride + off);
-            const uint32_t* src = reinterpret_cast<const uint32_t*>(g & ~uintptr_t(3));
-            const int ndw = int(((g & 3) + cb + 3) >> 2);
+            const uint8_t* rowp = W + int64_t(min(n0 + r, N - 1)) * w_stride + off;
+            const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(rowp) & 3);
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(rowp - sh);
+            const int ndw = int((sh + cb + 3) >> 2);
 #pragma unroll
             for (int q = 0; q < RI; ++q) {
                 const int d = col + 32 * q;
@@ -429,9 +430,10 @@ __global__ __launch_bounds__(1024) void strip_skinny_kernel(const float* __restr
     const int64_t off = int64_t(4 * sp) * CB;   // the group's first byte in a row
     const int gb = WT == T_Q8_0 ? 34 * min(32, K / 32 - 32 * sp) : CB * min(4, nchunks - 4 * sp);
     const int wr = 2 * wave + h;                  // the row this lane copies
-    const uintptr_t g = reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + wr, N - 1)) * w_stride + off);
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(g & ~uintptr_t(3));
-    const int ndw = int(((g & 3) + gb + 3) >> 2);
+    const uint8_t* rowp = W + int64_t(min(n0 + wr, N - 1)) * w_stride + off;
+    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(rowp) & 3);
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(rowp - sh);
+    const int ndw = int((sh + gb + 3) >> 2);
     uint32_t wreg[RI];
 #pragma unroll
     for (int i = 0; i < RI; ++i) {
