@@ -552,6 +552,8 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
 
     // 1. packed weight bytes: thread (r, c) copies dwords c, c + 32, ... of row r
     {
+        // (addressed through an integer, so these are flat loads: the same
+        // reads as global loads measured ~3 % slower over the text stream)
         const int r = tid >> 5, c = tid & 31;
         const uintptr_t g = reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + r, N - 1)) * w_stride + int64_t(k0 / 32) * 34);
         const uint32_t* src = reinterpret_cast<const uint32_t*>(g & ~uintptr_t(3));
