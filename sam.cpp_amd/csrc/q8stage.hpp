@@ -56,6 +56,10 @@ __device__ __forceinline__ int row_exponent(float rowmax) {
 }
 
 __device__ __forceinline__ floatx4 load4f(const float* p) { return *reinterpret_cast<const floatx4*>(p); }
+// read-once data (activation rows being staged): a streaming load
+__device__ __forceinline__ floatx4 load4f_stream(const float* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p));
+}
 
 // Cross-lane steps on the DPP network (no LDS round trip): quad_perm swaps
 // for lane ^ 1 and lane ^ 2, row rotations by 4 and 8 within 16 lanes.

@@ -32,7 +32,7 @@ __device__ __forceinline__ void stage8_row(const float* __restrict__ x, int64_t 
     for (int c = 0; c < CH; ++c) {
         const int k = 512 * c + 8 * lane;
         if (k < K) {
-            const floatx4 lo = load4f(xr + k), hi = load4f(xr + k + 4);
+            const floatx4 lo = load4f_stream(xr + k), hi = load4f_stream(xr + k + 4);
             v[c] = floatx8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         } else {
             v[c] = floatx8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -125,7 +125,7 @@ __device__ __forceinline__ void stage8_half_row(const float* __restrict__ x, int
     for (int c = 0; c < CHH; ++c) {
         const int k = 2560 * half + 512 * c + 8 * lane;
         if (live && k < K) {
-            const floatx4 lo = load4f(xr + k), hi = load4f(xr + k + 4);
+            const floatx4 lo = load4f_stream(xr + k), hi = load4f_stream(xr + k + 4);
             v[c] = floatx8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         } else {
             v[c] = floatx8{0, 0, 0, 0, 0, 0, 0, 0};
