@@ -56,6 +56,14 @@ __device__ __forceinline__ int row_exponent(float rowmax) {
 }
 
 __device__ __forceinline__ floatx4 load4f(const float* p) { return *reinterpret_cast<const floatx4*>(p); }
+// An integral float to int32 by the hardware conversion, which gives 0 for
+// NaN (and saturates out of range); ggml's nearest_int also packs NaN as 0.
+__device__ __forceinline__ int cvt_i32_nan0(float r) {
+    int q;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(r));
+    return q;
+}
+
 // read-once data (activation rows being staged): a streaming load
 __device__ __forceinline__ floatx4 load4f_stream(const float* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p));

@@ -597,18 +597,20 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
         float inv;
         if (X86) inv = amax != 0.f ? 127.f / amax : 0.f;
         else inv = d != 0.f ? 1.f / d : 0.f;
+        // four codes per dword: the hardware conversion (NaN -> 0, which is
+        // ggml's code for a NaN activation) and two byte permutes
         uint32_t packed[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            uint32_t wd = 0;
+            uint32_t q[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float s = v[4 * i + j] * inv;
-                const float r = X86 ? __builtin_rintf(s) : __builtin_roundf(s);
-                const int q = r == r ? int(r) : 0;   // NaN -> 0
-                wd |= uint32_t(q & 0xff) << (8 * j);
+                q[j] = uint32_t(cvt_i32_nan0(X86 ? __builtin_rintf(s) : __builtin_roundf(s)));
             }
-            packed[i] = wd;
+            const uint32_t lo = __builtin_amdgcn_perm(q[1], q[0], 0x0c0c0400u);   // q0.b0, q1.b0
+            const uint32_t hi = __builtin_amdgcn_perm(q[3], q[2], 0x0c0c0400u);
+            packed[i] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
         }
         if (b < nb) {
             u32x4* dst = reinterpret_cast<u32x4*>(&Xq[m * I8_XLD + 32 * b]);

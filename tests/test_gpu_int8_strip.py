@@ -114,3 +114,28 @@ def test_int8_strip_repeats_and_replays(samhip, oracle):
                     assert np.array_equal(ctx.download(yb, shp, np.float32), y), rep
         finally:
             g.destroy()
+
+
+@pytest.mark.parametrize("rounding", ["x86", "ref"])
+def test_int8_strip_nan_activations(samhip, oracle, rounding):
+    """A NaN activation packs as code 0 (ggml's nearest_int gives 0 for NaN)
+    and leaves its block's scale to the finite values: single NaNs, a NaN
+    run across blocks and a whole NaN row, against the oracle."""
+    say("case int8 strip NaN", rounding)
+    gmode = samhip.ROUND_X86 if rounding == "x86" else samhip.ROUND_REF
+    cmode = oracle.ROUND_X86 if rounding == "x86" else oracle.ROUND_REF
+    rng = np.random.default_rng(91)
+    m, n, k = 32, 256, 1024
+    w = oracle.quantize(oracle.Q8_0, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[3, 5] = np.nan
+    x[7, 100:140] = np.nan
+    x[20, :] = np.nan
+    x[29, 31] = np.nan
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE, gmode) as ctx:
+        y = ctx.matmul(samhip.Q8_0, w, x)
+        assert ctx.query().kernel_variant == b"skinny_i8mfma_q8_0"
+    ref = oracle.mul_mat_native(oracle.Q8_0, w, x, cmode)
+    assert np.isfinite(ref).all() and np.isfinite(y).all()
+    assert not y[20].any() and not ref[20].any()
+    assert max_row_rel_l2(y, ref) <= EXACT
