@@ -769,19 +769,27 @@ const char* launch_skinny(int wtype, const _Float16* a, int64_t lda, const float
 
 namespace samhip {
 
+constexpr int kFusedRoundWGs = 256;   // workgroups of one round on MI355X (one per CU)
+
 FusedPlan fused_skinny_plan(int M, int N, int K, int max_splits) {
     FusedPlan p{};
     p.rg = (N + FROWS - 1) / FROWS;
-    // rows per block: up to 128, fewer while the grid would have fewer than
-    // 64 (row group, row block) workgroups (the decoder's 201 queries on 256
-    // weight rows: 7 blocks of 32 rows, 6.6 us per product instead of 13.5)
-    const int64_t want = M > 256 ? 256 : 64;
-    p.mt = std::min(4, (M + 31) / 32);
-    while (p.mt > 1 && int64_t(p.rg) * ((M + 32 * p.mt - 1) / (32 * p.mt)) < want) p.mt /= 2;
+    // rows per block: the fewest (32, 64 or 128) whose (row group, row
+    // block) grid still fits one round of kFusedRoundWGs workgroups, so the
+    // activation chunk is packed by as few workgroups as possible without a
+    // second round.  Measured on MI355X against the earlier rule (64 or 256
+    // workgroups wanted): the detector's 5184 image tokens on 256 x 256
+    // weights 9.3 us with 64-row blocks (162 workgroups) instead of 11.0
+    // with 32-row blocks (324: two rounds); its 201 queries on 2048 x 256
+    // weights 6.4 us with 32-row blocks (112) instead of 8.6 with 64 (64).
+    const int max_mt = std::min(4, (M + 31) / 32);
+    p.mt = 1;
+    while (p.mt < max_mt && int64_t(p.rg) * ((M + 32 * p.mt - 1) / (32 * p.mt)) > kFusedRoundWGs) p.mt *= 2;
     const int mb = (M + 32 * p.mt - 1) / (32 * p.mt);
     const int groups = p.rg * mb;
     const int nchunks = (K + CHUNK - 1) / CHUNK;
-    const int S = std::min(std::min(nchunks, std::max(1, max_splits)), std::max(1, (256 + groups - 1) / groups));
+    const int S = std::min(std::min(nchunks, std::max(1, max_splits)),
+                           std::max(1, (kFusedRoundWGs + groups - 1) / groups));
     p.cps = (nchunks + S - 1) / S;
     p.splits = (nchunks + p.cps - 1) / p.cps;
     p.part_bytes = p.splits > 1 ? size_t(p.splits) * size_t(M) * size_t(N) * 4 : 0;
