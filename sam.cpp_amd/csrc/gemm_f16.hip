@@ -17,7 +17,13 @@ namespace samhip {
 
 namespace {
 
-constexpr int GROUP_M = 8;
+// Row tiles per group of the tile order.  An XCD's run of tiles covers about
+// GROUP_M row tiles and (its tile count / GROUP_M) column tiles, whose A and
+// B panels it reads into its own L2; at M = 5184, N = 1024, K = 4736 (216
+// tiles of 192x128, 27 per XCD) 4 row tiles by ~7 column tiles read less than
+// 8 by ~4: sweep 585-588 -> 590-595 TOPS and fc2 790-794 -> 799-812 TFLOP/s
+// on one box, alternating the two libraries; the image encode unchanged.
+constexpr int GROUP_M = 4;
 [[maybe_unused]] constexpr int RSRC_WORD3 = 0x00020000;   // raw buffer, 32-bit data format
 
 [[maybe_unused]] __device__ __forceinline__ void tile_order(int bid, int nblocks, int tiles_m, int tiles_n, int& tm, int& tn) {
