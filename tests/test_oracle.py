@@ -213,7 +213,7 @@ def test_kquant_dequant_fields(oracle, kind):
     assert np.array_equal(got.reshape(-1), np.concatenate(expects))
 
 
-# ---- weight quantizers: round trip bounds ("parity unpinned" vs ggml) ------
+# ---- weight quantizers: round trip bounds (field-level pins: test_oracle_pins.py)
 
 @pytest.mark.parametrize("qtype,bound", [(8, 0.012), (12, 0.12), (13, 0.06), (14, 0.03)])
 def test_weight_quantizer_round_trip(oracle, qtype, bound):
