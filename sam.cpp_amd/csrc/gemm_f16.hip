@@ -196,9 +196,14 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
 // so that the 32 rows an MFMA fragment read touches fall in distinct banks.
 // ---------------------------------------------------------------------------
 
+// LDS has 64 banks of 4 bytes, 256 bytes across.  A tile row of CPR 16-byte
+// chunks is 16 * CPR bytes, so 16 / CPR consecutive rows share one 256-byte
+// span of banks; the XOR pattern changes every 16 / CPR rows, so the same
+// chunk of 32 consecutive rows (one fragment read) lands evenly on all
+// sixteen 16-byte bank groups.
 template <int CPR>
 __device__ __forceinline__ int swz(int r) {
-    return CPR == 8 ? ((r >> 1) & 7) : ((r >> 2) & 3);
+    return CPR == 16 ? (r & 15) : CPR == 8 ? ((r >> 1) & 7) : ((r >> 2) & 3);
 }
 
 template <int N>
