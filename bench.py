@@ -48,6 +48,9 @@ PROFILE_COMMANDS = {
     "pmc": "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_BUSY_CYCLES "
            "SQ_WAIT_INST_LDS SQ_INSTS_LDS SQ_INSTS_MFMA GRBM_GUI_ACTIVE --output-format csv -d <out>/pmc -o bench -- "
            "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-encoder --no-configs",
+    "pmc2": "rocprofv3 --pmc SQ_ACTIVE_INST_VALU SQ_INSTS_VALU TCC_HIT_sum TCC_MISS_sum TCP_TCC_READ_REQ_LATENCY_sum "
+            "TCP_TCC_READ_REQ_sum GRBM_GUI_ACTIVE --output-format csv -d <out>/pmc2 -o bench -- "
+            "python3 bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-encoder --no-configs",
     "copy_fetch": "rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/copy_FETCH_SIZE -o copy -- "
                   "python3 bench.py --copy-calibration",
     "copy_write": "rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/copy_WRITE_SIZE -o copy -- "
@@ -346,6 +349,45 @@ def summarize_profiles(d, commands):
                          f"{med(lambda e: e['us']):.1f} | {gui:.0f} | {busy:.1f} | {conf:.1f} | "
                          f"{med(lambda e: e['SQ_INSTS_MFMA']):.3g} | {med(lambda e: e['SQ_INSTS_LDS']):.3g} |")
         with open(os.path.join(ROOT, "profiles", "mfma_lds_counters_vit_sweep_m5184.md"), "w") as f:
+            f.write("\n".join(lines) + "\n")
+
+    pmc2_path = os.path.join(d, "pmc2", "bench_counter_collection.csv")
+    if os.path.exists(pmc2_path):
+        rs = rows(pmc2_path)
+        labels = sweep_products(rs)
+        per = {}
+        for r in rs:
+            did = int(r["Dispatch_Id"])
+            sym = short(r["Kernel_Name"])
+            if did not in labels or not (sym.startswith("gemm_") or sym.startswith("prep_")):
+                continue
+            e = per.setdefault(did, {"symbol": sym, "grid": int(r["Grid_Size"]), "product": labels[did],
+                                     "us": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3})
+            e[r["Counter_Name"]] = e.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        groups = {}
+        for e in per.values():
+            groups.setdefault((e["symbol"], e["grid"], e["product"]), []).append(e)
+        lines = ["# L2 and VALU counters, SAM 3 ViT linear sweep at M=5184 (preparation and GEMM kernels)", "",
+                 "Command (from the repository root, `cd /tmp && export TMPDIR=/tmp` first):", "", "```",
+                 commands["pmc2"], "```", "",
+                 "Medians per dispatch. L2 hit = TCC_HIT / (TCC_HIT + TCC_MISS) over all L2 channels. L2 read "
+                 "latency = TCP_TCC_READ_REQ_LATENCY / TCP_TCC_READ_REQ: the mean cycles a vector L1 read request "
+                 "waits for the L2 (hits and misses). VALU busy = SQ_ACTIVE_INST_VALU / (256 CUs x GRBM_GUI_ACTIVE "
+                 "/ 8), the profiler's VALU-busy expression with GRBM_GUI_ACTIVE summed over the 8 XCD instances.",
+                 "",
+                 "| kernel | grid (threads) | product | dispatches | dispatch us (under counters) | L2 hit % | "
+                 "L2 read latency (cycles) | VALU busy % | SQ_INSTS_VALU |",
+                 "|---|---|---|---|---|---|---|---|---|"]
+        for (sym, grid, (name, k)), es in sorted(groups.items(), key=lambda t: (t[0][2][0], t[0][0])):
+            def med(f):
+                return float(np.median([f(e) for e in es]))
+            hit = med(lambda e: 100 * e["TCC_HIT_sum"] / max(1.0, e["TCC_HIT_sum"] + e["TCC_MISS_sum"]))
+            lat = med(lambda e: e["TCP_TCC_READ_REQ_LATENCY_sum"] / max(1.0, e["TCP_TCC_READ_REQ_sum"]))
+            valu = med(lambda e: 100 * e["SQ_ACTIVE_INST_VALU"] / (256 * e["GRBM_GUI_ACTIVE"] / 8))
+            lines.append(f"| `{sym}` | {grid} | {name} M {M_TOKENS} N {nmap[name.split(':')[0]]} K {k} | {len(es)} | "
+                         f"{med(lambda e: e['us']):.1f} | {hit:.1f} | {lat:.0f} | {valu:.1f} | "
+                         f"{med(lambda e: e['SQ_INSTS_VALU']):.3g} |")
+        with open(os.path.join(ROOT, "profiles", "l2_valu_counters_vit_sweep_m5184.md"), "w") as f:
             f.write("\n".join(lines) + "\n")
 
 
