@@ -25,8 +25,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 //   erfc(a) = r exp(-a^2) P(r - 1),  r = 1 / (1 + 0.55 a),
 // the form of Abramowitz & Stegun 7.1.26 with a degree-7 P fitted for this
 // kernel (least squares on [0, 4] with Lawson's reweighting towards the
-// largest relative error).  Evaluated in F32 it is within 2.7e-7 of erf
-// everywhere and within a few 1e-9 for a >= 2, where 1 + erf is small.
+// largest relative error).  Evaluated in F32 (simulated with a correctly
+// rounded reciprocal and exponential; the hardware's are within 1 ulp) it is
+// within 2.7e-7 of erf everywhere and within a few 1e-9 for a >= 2, where
+// 1 + erf is small.
 // Past a = 4, 1 - erfc(a) rounds to 1, as F32 erf does.  The library erff
 // costs ~50 VALU instructions here (the wave runs both halves of its range
 // split) and made fc2's erf-GELU staging VALU-bound: 45-52 us per
