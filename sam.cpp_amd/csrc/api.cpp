@@ -478,9 +478,10 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     // tokens' q, k, v, out projections) run the fused kernel: one launch
     const bool small_w = ctx->fused_skinny && int64_t(N) * K <= kFusedSmallW;
     const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K) && !small_w;
-    if (!tall && M <= 32 && w->type == T_Q8_0 && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE && ctx->int8_strip &&
-        ctx->fused_skinny) {
-        // exact int8 block dots, one launch for K <= 1024 (the text encoder)
+    if (!tall && M < kStripMaxM && w->type == T_Q8_0 && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE &&
+        ctx->int8_strip && ctx->fused_skinny) {
+        // exact int8 block dots in blocks of 32 activation rows, one launch
+        // for K <= 1024 (the text encoder, the decoder's queries and prompt)
         if (int rc = ensure_staging(ctx, std::max<size_t>(q8_strip_i8_part_bytes(M, N, K), 256))) return rc;
         const char* variant = q8_strip_i8_variant();
         int rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {

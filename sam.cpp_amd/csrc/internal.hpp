@@ -245,7 +245,7 @@ constexpr int kStripMaxM = 256;   // in blocks of 32 activation rows
 // per-lane loads and K > 1024 adds the reduce launch back.
 inline bool strip_skinny_preferred(int wtype, int M, int K) { return wtype == T_Q8_0 && K <= 1024 && M <= 32; }
 FusedPlan strip_skinny_plan(int M, int N, int K);
-// Exact int8 products of Q8_0 weights with at most 32 activation rows
+// Exact int8 products of Q8_0 weights in blocks of 32 activation rows
 // (COMPUTE_Q8_NATIVE): one launch while K <= kI8SliceK, else slices of
 // kI8SliceK values whose partial sums go through `part`
 // (ceil(K / kI8SliceK) * M * N floats) and a reduce launch.

@@ -509,15 +509,16 @@ __global__ __launch_bounds__(1024) void strip_skinny_kernel(const float* __restr
 }
 
 // ---------------------------------------------------------------------------
-// Exact int8 strip path: Q8_0 weights against at most 32 activation rows
-// (the text encoder's 32 tokens) in COMPUTE_Q8_NATIVE, i.e. ggml's CPU
+// Exact int8 strip path: Q8_0 weights against blocks of 32 activation rows
+// (the text encoder's 32 tokens, the decoder's 201 queries) in
+// COMPUTE_Q8_NATIVE, i.e. ggml's CPU
 // native arithmetic on the matrix cores.  Per Q8_0 block the integer dot
 // sum_k q_w q_x comes exactly out of v_mfma_i32_32x32x32_i8 (one 32-value
 // block per instruction: the weight codes are the B operand as stored, no
 // decode), and the block adds fma(float(dot), d_w * d_x, acc) in F32 as
 // ggml's vec_dot_q8_0_q8_0 does; only the order of the block sums differs.
-// One workgroup of 16 waves per 32 weight rows and K slice of up to 1024
-// values:
+// One workgroup of 16 waves per 32 weight rows, 32 activation rows and K
+// slice of up to 1024 values:
 //  1. the strip's packed bytes for the slice go to LDS with coalesced dword
 //     loads (rows of an odd dword count: conflict-free reads);
 //  2. thread (m, b) packs activation row m, block b of the slice to Q8_0
@@ -538,7 +539,7 @@ template <bool X86, bool XVEC>
 __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restrict__ X, int64_t ldx,
                                                            const uint8_t* __restrict__ W, int64_t w_stride,
                                                            float* __restrict__ Y, int64_t ldy, float* __restrict__ part,
-                                                           int M, int N, int K, int RG) {
+                                                           int M, int N, int K, int RG, int S) {
 #pragma clang fp contract(off)
     __shared__ __attribute__((aligned(16))) int8_t Xq[32 * I8_XLD];
     __shared__ __attribute__((aligned(16))) float Xd[kI8SliceK / 32][32];
@@ -547,9 +548,14 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
     constexpr int RI = (I8_WDW + 31) / 32;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int rg = blockIdx.x % RG, sp = blockIdx.x / RG;
+    const int rg = blockIdx.x % RG, sp = (blockIdx.x / RG) % S, mb = blockIdx.x / (RG * S);
     const int n0 = rg * 32, k0 = sp * kI8SliceK;
     const int nb = min(kI8SliceK, K - k0) / 32;   // Q8_0 blocks in this slice
+    // this workgroup's block of 32 activation rows
+    const int m0 = mb * 32, Mall = M;
+    X += int64_t(m0) * ldx;
+    Y += int64_t(m0) * ldy;
+    M = min(M - m0, 32);
 
     // 1. packed weight bytes: thread (r, c) loads dwords c, c + 32, ... of
     // row r; the activation loads are issued before these go to LDS, so the
@@ -662,7 +668,7 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
 #pragma unroll
     for (int w = 0; w < 16; ++w) v += red[w * 16 * 64 + src];
     if (m < M && n0 + n < N) {
-        if (part) part[(int64_t(sp) * M + m) * N + n0 + n] = v;
+        if (part) part[(int64_t(sp) * Mall + m0 + m) * N + n0 + n] = v;
         else Y[int64_t(m) * ldy + n0 + n] = v;
     }
 }
@@ -843,15 +849,17 @@ const char* q8_strip_i8_variant() { return "skinny_i8mfma_q8_0"; }
 
 const char* launch_q8_strip_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy,
                                float* part, int M, int N, int K, int x86, hipStream_t stream) {
-    if (M < 1 || M > 32 || N < 1 || K < 32 || K % 32) return nullptr;
-    const int RG = (N + 31) / 32, S = (K + kI8SliceK - 1) / kI8SliceK;
+    if (M < 1 || N < 1 || K < 32 || K % 32) return nullptr;
+    const int RG = (N + 31) / 32, S = (K + kI8SliceK - 1) / kI8SliceK, MB = (M + 31) / 32;
     if (S > 1 && !part) return nullptr;
+    if (int64_t(RG) * S * MB > 0x7fffffff) return nullptr;
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     float* pt = S > 1 ? part : nullptr;
-    const dim3 grid(unsigned(RG * S)), block(1024);
-#define SAMHIP_I8(X86V, XV) \
-    hipLaunchKernelGGL((q8_strip_i8_kernel<X86V, XV>), grid, block, 0, stream, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG)
+    const dim3 grid(unsigned(RG * S * MB)), block(1024);
+#define SAMHIP_I8(X86V, XV)                                                                                    \
+    hipLaunchKernelGGL((q8_strip_i8_kernel<X86V, XV>), grid, block, 0, stream, x, ldx, wb, w_stride, y, ldy, pt, M, N, \
+                       K, RG, S)
     if (x86) {
         if (xvec) SAMHIP_I8(true, true); else SAMHIP_I8(true, false);
     } else {

@@ -1,5 +1,6 @@
-"""The exact int8 path for Q8_0 weights against at most 32 activation rows
-(the text encoder's products), against the oracle's native CPU path.
+"""The exact int8 path for Q8_0 weights against fewer than 256 activation
+rows in blocks of 32 (the text encoder's 32 tokens, the decoder's 201
+queries and 33 prompt tokens), against the oracle's native CPU path.
 
 Both sides form the same Q8_0 activation codes and exact integer block dots;
 only the F32 order in which the per-block terms d_w d_x dot are added
@@ -25,9 +26,12 @@ def say(*a):
 
 
 # text encoder (in_proj, out_proj, fc1, fc2, resizer) at M = 32, ragged M and
-# N, K slices past 1024 (partial sums and the reduce launch), short K
+# N, K slices past 1024 (partial sums and the reduce launch), short K; the
+# decoder's queries (M = 201: 256x256, FFN 256->2048 and 2048->256) and
+# prompt (M = 33), several row blocks with ragged ends
 SHAPES = [(32, 3072, 1024), (32, 1024, 1024), (32, 4096, 1024), (32, 1024, 4096), (32, 256, 1024),
-          (1, 4096, 1024), (17, 96, 512), (31, 33, 2048), (32, 64, 32), (5, 1000, 1056)]
+          (1, 4096, 1024), (17, 96, 512), (31, 33, 2048), (32, 64, 32), (5, 1000, 1056),
+          (201, 256, 256), (201, 2048, 256), (201, 256, 2048), (33, 256, 256), (255, 96, 1056), (64, 40, 64)]
 
 
 @pytest.mark.parametrize("rounding", ["x86", "ref"])

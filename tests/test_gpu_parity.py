@@ -318,21 +318,28 @@ def test_mul_mat_skinny_shapes(gpu_ctx, f16_ctx, oracle, samhip, qtype, shape):
 
 
 @pytest.mark.parametrize("qtype", TYPES)
-def test_mul_mat_fused_split_k_deterministic(gpu_ctx, f16_ctx, oracle, samhip, qtype):
+def test_mul_mat_fused_split_k_deterministic(f16_ctx, oracle, samhip, monkeypatch, qtype):
     """Few weight rows and a long K: the fused kernel splits K over 16
     workgroups that write their partial sums to staging, and a second launch
     adds them in split order; repeated calls give identical bits, and a
-    row-offset view with a strided activation is covered."""
+    row-offset view with a strided activation is covered.  (Q8_0 below 256
+    rows defaults to the int8 kernel, so its fused path is forced with
+    SAMHIP_INT8_STRIP=0.)"""
     say("case fused split-K", qtype)
     rng = np.random.default_rng(43)
     k, n, m = 4096, 96, 40
     w = oracle.quantize(qtype, (rng.standard_normal((2 * n, k)) * 0.02).astype(np.float32))
     x = rng.standard_normal((m, k)).astype(np.float32)
-    first = gpu_ctx.matmul(qtype, w, x, w_row_offset=n, w_rows=n, x_row_stride=k + 4)
-    assert gpu_ctx.query().kernel_variant.startswith(b"skinny_fused")
-    for _ in range(2):
-        again = gpu_ctx.matmul(qtype, w, x, w_row_offset=n, w_rows=n, x_row_stride=k + 4)
-        assert np.array_equal(first, again)
+    monkeypatch.setenv("SAMHIP_INT8_STRIP", "0")
+    ctx = samhip.Context(0, samhip.COMPUTE_Q8_NATIVE, samhip.ROUND_X86)
+    try:
+        first = ctx.matmul(qtype, w, x, w_row_offset=n, w_rows=n, x_row_stride=k + 4)
+        assert ctx.query().kernel_variant.startswith(b"skinny_fused")
+        for _ in range(2):
+            again = ctx.matmul(qtype, w, x, w_row_offset=n, w_rows=n, x_row_stride=k + 4)
+            assert np.array_equal(first, again)
+    finally:
+        ctx.close()
     yf = f16_ctx.matmul(qtype, w, x, w_row_offset=n, w_rows=n)
     _check_product(oracle, qtype, w[n:], x, first, yf)
 
@@ -341,8 +348,9 @@ def test_mul_mat_fused_split_k_deterministic(gpu_ctx, f16_ctx, oracle, samhip, q
 def test_mul_mat_fused_in_projection_views(gpu_ctx, f16_ctx, oracle, qtype):
     """The fusion / decoder q, k, v products: row-offset views of a fused
     [3D, D] in-projection (D = 256) against the image tokens (M = 5184, tiled
-    GEMM), the decoder queries (M = 201, fused kernel in 32-row blocks) and
-    the prompt tokens (M = 33), each compared in full."""
+    GEMM), the decoder queries (M = 201, in 32-row blocks: the int8 kernel
+    for Q8_0, the fused kernel for Q4_K) and the prompt tokens (M = 33),
+    each compared in full."""
     say("case fused in-projection views", qtype)
     rng = np.random.default_rng(46)
     d = 256
@@ -358,8 +366,8 @@ def test_mul_mat_fused_in_projection_views(gpu_ctx, f16_ctx, oracle, qtype):
 @pytest.mark.parametrize("qtype", TYPES)
 def test_mul_mat_strip_path(gpu_ctx, samhip, oracle, monkeypatch, qtype):
     """The fp16 strip kernel (SAMHIP_STRIP_SKINNY=2 forces it for every
-    weight type and M < 256, with a split-K reduce past K = 1024; Q8_0 with
-    M <= 32 reaches it only with SAMHIP_INT8_STRIP=0): repeated calls give
+    weight type and M < 256, with a split-K reduce past K = 1024; Q8_0
+    reaches it only with SAMHIP_INT8_STRIP=0): repeated calls give
     identical bits, and the fused kernel (SAMHIP_STRIP_SKINNY=0), which
     forms the same fp16 operands, agrees to F32 summation-order rounding."""
     say("case strip path", qtype)
@@ -376,8 +384,8 @@ def test_mul_mat_strip_path(gpu_ctx, samhip, oracle, monkeypatch, qtype):
             first = strip.matmul(qtype, w, x)
             assert strip.query().kernel_variant.startswith(b"skinny_strip")
             default = gpu_ctx.matmul(qtype, w, x)
-            # Q8_0 with M <= 32 defaults to the exact int8 kernel (its own test)
-            exact = qtype == 8 and m <= 32
+            # Q8_0 below 256 rows defaults to the exact int8 kernel (its own test)
+            exact = qtype == 8 and m < 256
             assert gpu_ctx.query().kernel_variant.startswith(b"skinny_i8mfma" if exact else b"skinny_fused")
             assert np.array_equal(first, strip.matmul(qtype, w, x))
             other = fused.matmul(qtype, w, x)
