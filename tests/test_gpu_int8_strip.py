@@ -31,7 +31,8 @@ def say(*a):
 # prompt (M = 33), several row blocks with ragged ends
 SHAPES = [(32, 3072, 1024), (32, 1024, 1024), (32, 4096, 1024), (32, 1024, 4096), (32, 256, 1024),
           (1, 4096, 1024), (17, 96, 512), (31, 33, 2048), (32, 64, 32), (5, 1000, 1056),
-          (201, 256, 256), (201, 2048, 256), (201, 256, 2048), (33, 256, 256), (255, 96, 1056), (64, 40, 64)]
+          (201, 256, 256), (201, 2048, 256), (201, 256, 2048), (33, 256, 256), (255, 96, 1056), (64, 40, 64),
+          (97, 33, 1024)]
 
 
 @pytest.mark.parametrize("rounding", ["x86", "ref"])
