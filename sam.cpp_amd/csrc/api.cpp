@@ -113,7 +113,8 @@ struct samhip_context {
     int attn_splits = 0;        // SAMHIP_ATTN_SPLITS: key splits of the attention kernel (0: by grid size)
     int fused_max_splits = 16;  // SAMHIP_FUSED_MAX_SPLITS: cap on the fused kernel's K splits
     bool check_activations = false;   // samhip_context_set_activation_check
-    bool int8_strip = true;     // SAMHIP_INT8_STRIP=0 keeps Q8_0 products with M <= 32 on the fp16 kernels
+    int int8_strip = 1;         // SAMHIP_INT8_STRIP: 0 keeps M < 256 products on the fp16 kernels, 2 sends every
+                                // K-quant one there too (1: where it measured faster)
     samhip_exec_info info{};
     // per-launch event trace (samhip_trace_begin / samhip_trace_end)
     struct TraceRecord {
@@ -323,7 +324,7 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
     ctx->strip_skinny = env_int("SAMHIP_STRIP_SKINNY", 1);
     ctx->attn_splits = std::max(0, env_int("SAMHIP_ATTN_SPLITS", 0));
     ctx->fused_max_splits = std::max(1, env_int("SAMHIP_FUSED_MAX_SPLITS", 16));
-    ctx->int8_strip = env_int("SAMHIP_INT8_STRIP", 1) != 0;
+    ctx->int8_strip = env_int("SAMHIP_INT8_STRIP", 1);
     const int cfg = env_int("SAMHIP_GEMM_CONFIG", -1);
     ctx->gemm_cfg = (cfg >= 0 && cfg < gemm_f16_config_count()) ? cfg : -1;
     *out = ctx;
@@ -478,18 +479,24 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     // tokens' q, k, v, out projections) run the fused kernel: one launch
     const bool small_w = ctx->fused_skinny && int64_t(N) * K <= kFusedSmallW;
     const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K) && !small_w;
-    if (!tall && M < kStripMaxM && w->type == T_Q8_0 && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE &&
+    const bool kquant = (w->type == T_Q4_K || w->type == T_Q5_K || w->type == T_Q6_K) &&
+                        (ctx->int8_strip == 2 || kq_strip_i8_preferred(M, N, K, ctx->cus));
+    if (!tall && M < kStripMaxM && (w->type == T_Q8_0 || kquant) && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE &&
         ctx->int8_strip && ctx->fused_skinny) {
         // exact int8 block dots in blocks of 32 activation rows, one launch
         // for K <= 1024 (the text encoder, the decoder's queries and prompt)
         if (int rc = ensure_staging(ctx, std::max<size_t>(q8_strip_i8_part_bytes(M, N, K), 256))) return rc;
-        const char* variant = q8_strip_i8_variant();
+        const char* variant = kquant ? kq_strip_i8_variant(w->type) : q8_strip_i8_variant();
         int rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
-            if (!launch_q8_strip_i8(static_cast<const float*>(x->data), int64_t(x->nb[1] / 4), w->data,
-                                    int64_t(w->nb[1]), static_cast<float*>(y->data), int64_t(y->nb[1] / 4),
-                                    static_cast<float*>(ctx->staging), M, N, K,
-                                    ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->stream))
-                return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no int8 strip kernel for this shape");
+            const float* xp = static_cast<const float*>(x->data);
+            float* yp = static_cast<float*>(y->data);
+            float* part = static_cast<float*>(ctx->staging);
+            const char* ok = kquant
+                ? launch_kq_strip_i8(w->type, xp, int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), yp,
+                                     int64_t(y->nb[1] / 4), part, M, N, K, ctx->stream)
+                : launch_q8_strip_i8(xp, int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), yp, int64_t(y->nb[1] / 4),
+                                     part, M, N, K, ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->stream);
+            if (!ok) return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no int8 strip kernel for this shape");
             HIP_TRY(hipGetLastError(), "int8 strip launch");
             return SAMHIP_OK;
         });

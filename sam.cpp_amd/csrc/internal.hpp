@@ -257,6 +257,21 @@ inline size_t q8_strip_i8_part_bytes(int M, int N, int K) {
 const char* q8_strip_i8_variant();
 const char* launch_q8_strip_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy,
                                float* part, int M, int N, int K, int x86, hipStream_t stream);
+// The same for Q4_K / Q5_K / Q6_K weights against Q8_K activation codes
+// (K a multiple of 256; same partial-sum buffer).  Taken by default where it
+// measured faster than the fused kernel (graph replay, one box): one
+// 256-value super-block of K and a grid of at most one workgroup per CU,
+// e.g. the decoder's M = 201 and M = 33 products on 256x256 weights (Q4_K
+// 6.8 -> 5.0 us, Q6_K 6.6 -> 5.4 us).  At K >= 1024 the Q8_K packing of four
+// super-blocks per workgroup makes it slower (Q4_K M = 32, K = 1024: 10.0
+// against 8.9 us), and so does a second round of workgroups (M = 201,
+// N = 2048, K = 256: 9.3 against 7.0 us).
+inline bool kq_strip_i8_preferred(int M, int N, int K, int cus) {
+    return K == 256 && int64_t((N + 31) / 32) * ((M + 31) / 32) <= cus;
+}
+const char* kq_strip_i8_variant(int wtype);
+const char* launch_kq_strip_i8(int wtype, const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y,
+                               int64_t ldy, float* part, int M, int N, int K, hipStream_t stream);
 const char* strip_skinny_variant(int wtype);
 const char* launch_strip_skinny(int wtype, bool f16, const float* x, int64_t ldx, const void* w, int64_t w_stride,
                                 float* y, int64_t ldy, float* part, int M, int N, int K, int x86, hipStream_t stream);

@@ -673,6 +673,207 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
     }
 }
 
+// ---------------------------------------------------------------------------
+// Exact int8 path for the K-quants: Q4_K, Q5_K and Q6_K weights against
+// Q8_K activation codes, ggml's CPU native arithmetic (vec_dot_q*_K_q8_K)
+// on the matrix cores, with the workgroup shape of the Q8_0 path (16 waves
+// per 32 weight rows, 32 activation rows and a K slice of up to 1024 values):
+//  1. the strip's packed bytes for the slice go to LDS with coalesced dword
+//     loads (rows of an odd dword count);
+//  2. each 256-value activation block of the slice is packed to Q8_K by 32
+//     lanes of 8 values (ggml's quantize_row_q8_K: the first value of
+//     largest magnitude sets iscale = -127 / max); the codes, the block's d
+//     and the code sums of every weight sub-block (32 values; 16 for Q6_K)
+//     go to LDS;
+//  3. wave w takes the slice's 32-value steps w, w + 16, ...: the integer
+//     dot of activation codes and the weight's unsigned 4/5/6-bit codes
+//     comes out of v_mfma_i32_32x32x32_i8 (for Q6_K once per 16-value half,
+//     the other half's weight codes set to zero), then in F32
+//       Q4_K, Q5_K: acc += (d sc_j) d_x dot - (dmin m_j) d_x sum(codes_j)
+//       Q6_K:       acc += (d sc) d_x (dot - 32 sum(codes))
+//     (the same integer sums ggml forms; only the order of the F32 additions
+//     differs);
+//  4. the 16 partial tiles are added in LDS in wave order.
+// Slices beyond the first (K > 1024) write partial sums that
+// splitk_reduce_kernel adds in slice order.
+// ---------------------------------------------------------------------------
+template <int WT>
+constexpr int kq_wdw() { return (((kI8SliceK / 256) * block_bytes(WT) + 2 + 3) / 4) | 1; }
+
+template <int WT, bool XVEC>
+__global__ __launch_bounds__(1024) void kq_strip_i8_kernel(const float* __restrict__ X, int64_t ldx,
+                                                           const uint8_t* __restrict__ W, int64_t w_stride,
+                                                           float* __restrict__ Y, int64_t ldy, float* __restrict__ part,
+                                                           int M, int N, int K, int RG, int S) {
+#pragma clang fp contract(off)
+    constexpr int WDW = kq_wdw<WT>();
+    constexpr int BB = block_bytes(WT);
+    constexpr int SUB = WT == T_Q6_K ? 16 : 32;     // values per weight scale
+    constexpr int SPB = 256 / SUB;                  // sub-blocks per super-block
+    constexpr int XSB = kI8SliceK / 256;            // super-blocks per full slice
+    __shared__ __attribute__((aligned(16))) int8_t Xq[32 * I8_XLD];
+    __shared__ __attribute__((aligned(16))) float Xd[XSB][32];
+    __shared__ __attribute__((aligned(16))) float Xs[XSB * SPB][32];   // code sums per sub-block and row
+    __shared__ __attribute__((aligned(16))) uint32_t Ws[32 * WDW];
+    __shared__ __attribute__((aligned(16))) float red[16 * 16 * 64];
+    constexpr int RI = (WDW + 31) / 32;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rg = blockIdx.x % RG, sp = (blockIdx.x / RG) % S, mb = blockIdx.x / (RG * S);
+    const int n0 = rg * 32, k0 = sp * kI8SliceK;
+    const int nsb = min(kI8SliceK, K - k0) / 256;   // super-blocks in this slice
+    const int m0 = mb * 32, Mall = M;
+    X += int64_t(m0) * ldx;
+    Y += int64_t(m0) * ldy;
+    M = min(M - m0, 32);
+
+    // 1. packed weight bytes: thread (r, c) loads dwords c, c + 32, ... of row r
+    const int wr_r = tid >> 5, wr_c = tid & 31;
+    uint32_t wr[RI];
+    {
+        const uint8_t* rowp = W + int64_t(min(n0 + wr_r, N - 1)) * w_stride + int64_t(k0 / 256) * BB;
+        const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(rowp) & 3);
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(rowp - sh);
+        const int ndw = int((sh + BB * nsb + 3) >> 2);
+#pragma unroll
+        for (int i = 0; i < RI; ++i) wr[i] = wr_c + 32 * i < ndw ? src[wr_c + 32 * i] : 0u;
+    }
+    // 2. activation block (row m, super-block b) by the 32 lanes of half hu
+    // of a wave, 8 values per lane: unit u = m * nsb + b = 32 pass + 2 wave + hu
+    const int hu = lane >> 5, li = lane & 31;
+    floatx8 xv[XSB];
+#pragma unroll
+    for (int p = 0; p < XSB; ++p) {
+        xv[p] = floatx8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (p < nsb) {
+            const int u = 32 * p + 2 * wave + hu, m = u / nsb, b = u - m * nsb;
+            if (m < M) {
+                const float* xr = X + int64_t(m) * ldx + k0 + 256 * b + 8 * li;
+                if (XVEC) {
+                    const floatx4 lo = load4f(xr), hi = load4f(xr + 4);
+                    xv[p] = floatx8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) xv[p][i] = xr[i];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < RI; ++i)
+        if (wr_c + 32 * i < WDW) Ws[wr_r * WDW + wr_c + 32 * i] = wr[i];
+#pragma unroll
+    for (int p = 0; p < XSB; ++p) {
+        if (p >= nsb) break;
+        const int u = 32 * p + 2 * wave + hu, m = u / nsb, b = u - m * nsb;
+        float d, q[8];
+        quant8_codes<T_Q8_K, false>(xv[p], lane, d, q);
+        int c[8], sum = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            c[i] = int(q[i]);
+            sum += c[i];
+        }
+        const uint32_t lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(uint32_t(c[3]), uint32_t(c[2]), 0x0c0c0400u),
+                                                  __builtin_amdgcn_perm(uint32_t(c[1]), uint32_t(c[0]), 0x0c0c0400u),
+                                                  0x05040100u);
+        const uint32_t hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(uint32_t(c[7]), uint32_t(c[6]), 0x0c0c0400u),
+                                                  __builtin_amdgcn_perm(uint32_t(c[5]), uint32_t(c[4]), 0x0c0c0400u),
+                                                  0x05040100u);
+        *reinterpret_cast<uint2*>(&Xq[m * I8_XLD + 256 * b + 8 * li]) = uint2{lo, hi};
+        if (li == 0) Xd[b][m] = d;
+        // code sums of the weight's sub-blocks: 4 lanes (Q4_K, Q5_K) or 2 (Q6_K)
+        sum = group_sum<SUB / 8>(sum);
+        if (li % (SUB / 8) == 0) Xs[b * SPB + li / (SUB / 8)][m] = float(sum);
+    }
+    __syncthreads();
+
+    // 3. this wave's 32-value steps; the activation rows of element r are
+    // 8 (r / 4) + 4 h + r % 4, the weight row is col
+    const int col = lane & 31, h = lane >> 5;
+    const int wshift =
+        int((reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + col, N - 1)) * w_stride) + (k0 / 256) * BB) & 3);
+    const LdsRow wrow{&Ws[col * WDW], wshift};
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    const i32x16 zero = {0};
+    const int nst = 8 * nsb;   // 32-value steps in the slice
+    for (int st = wave; st < nst; st += 16) {
+        const int b = st >> 3, jj = st & 7;
+        const i32x4 a = *reinterpret_cast<const i32x4*>(&Xq[col * I8_XLD + 32 * st + 16 * h]);
+        floatx4 dx[4];
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) dx[qd] = *reinterpret_cast<const floatx4*>(&Xd[b][8 * qd + 4 * h]);
+        WeightPiece<WT> wp;
+        wp.load(wrow, st, h);
+        if constexpr (WT == T_Q6_K) {
+            // u = low 4 | high 2 << 4 in [0, 63]; value = d sc (u - 32)
+            const int g = jj & 3;
+            const int lshift = (g >> 1) * 4, hshift = 2 * g;
+            u32x4 u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                u[i] = ((wp.ql[i] >> lshift) & 0x0f0f0f0fu) | (((wp.qh[i] >> hshift) & 0x03030303u) << 4);
+            const float d = half_bits_to_float(wp.d);
+            // the two 16-value halves' scales of this weight row
+            const int sbase = BB * b + 192 + 8 * (jj >> 2) + 2 * g;
+            const float t0 = d * float(int8_t(wrow.u8(sbase))), t1 = d * float(int8_t(wrow.u8(sbase + 1)));
+#pragma unroll
+            for (int hs = 0; hs < 2; ++hs) {
+                const i32x4 bq = h == hs ? i32x4{int(u[0]), int(u[1]), int(u[2]), int(u[3])} : i32x4{0, 0, 0, 0};
+                const i32x16 dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, zero, 0, 0, 0);
+                const float t = hs ? t1 : t0;
+#pragma unroll
+                for (int qd = 0; qd < 4; ++qd) {
+                    const floatx4 cs = *reinterpret_cast<const floatx4*>(&Xs[2 * st + hs][8 * qd + 4 * h]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float v = float(dot[4 * qd + i]) - 32.f * cs[i];   // exact integers
+                        acc[4 * qd + i] = __builtin_fmaf(t * dx[qd][i], v, acc[4 * qd + i]);
+                    }
+                }
+            }
+        } else {
+            const int shift = (jj & 1) * 4;
+            u32x4 u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                u[i] = (wp.qs[i] >> shift) & 0x0f0f0f0fu;
+                if constexpr (WT == T_Q5_K) u[i] |= ((wp.qh[i] >> jj) & 0x01010101u) << 4;
+            }
+            int sc, mn;
+            k4_scale_min(jj, wp.sc, sc, mn);
+            const float ws = half_bits_to_float(wp.hdr & 0xffffu) * float(sc);
+            const float wm = half_bits_to_float(wp.hdr >> 16) * float(mn);
+            const i32x16 dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                a, i32x4{int(u[0]), int(u[1]), int(u[2]), int(u[3])}, zero, 0, 0, 0);
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                const floatx4 cs = *reinterpret_cast<const floatx4*>(&Xs[st][8 * qd + 4 * h]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float v = __builtin_fmaf(ws * dx[qd][i], float(dot[4 * qd + i]), acc[4 * qd + i]);
+                    acc[4 * qd + i] = __builtin_fmaf(-(wm * dx[qd][i]), cs[i], v);
+                }
+            }
+        }
+    }
+    // 4. partial tiles in wave order
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
+    __syncthreads();
+    const int m = tid >> 5, n = tid & 31;
+    const int src = (4 * (m >> 3) + (m & 3)) * 64 + n + 32 * ((m >> 2) & 1);
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) v += red[w * 16 * 64 + src];
+    if (m < M && n0 + n < N) {
+        if (part) part[(int64_t(sp) * Mall + m0 + m) * N + n0 + n] = v;
+        else Y[int64_t(m) * ldy + n0 + n] = v;
+    }
+}
+
 template <int WT, int MODE, bool X86>
 void launch_strip_mode(bool xvec, const float* x, int64_t ldx, const uint8_t* w, int64_t w_stride, float* y,
                        int64_t ldy, float* part, int M, int N, int K, int RG, int S, hipStream_t stream) {
@@ -872,6 +1073,50 @@ const char* launch_q8_strip_i8(const float* x, int64_t ldx, const void* w, int64
                            M, N, S);
     }
     return q8_strip_i8_variant();
+}
+
+const char* kq_strip_i8_variant(int wtype) {
+    switch (wtype) {
+        case T_Q4_K: return "skinny_i8mfma_q4_k";
+        case T_Q5_K: return "skinny_i8mfma_q5_k";
+        case T_Q6_K: return "skinny_i8mfma_q6_k";
+        default: return nullptr;
+    }
+}
+
+template <int WT>
+void launch_kq_strip_wt(bool xvec, const float* x, int64_t ldx, const uint8_t* w, int64_t w_stride, float* y,
+                        int64_t ldy, float* part, int M, int N, int K, int RG, int S, int MB, hipStream_t stream) {
+    const dim3 grid(unsigned(RG * S * MB)), block(1024);
+    if (xvec)
+        hipLaunchKernelGGL((kq_strip_i8_kernel<WT, true>), grid, block, 0, stream, x, ldx, w, w_stride, y, ldy, part,
+                           M, N, K, RG, S);
+    else
+        hipLaunchKernelGGL((kq_strip_i8_kernel<WT, false>), grid, block, 0, stream, x, ldx, w, w_stride, y, ldy, part,
+                           M, N, K, RG, S);
+}
+
+const char* launch_kq_strip_i8(int wtype, const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y,
+                               int64_t ldy, float* part, int M, int N, int K, hipStream_t stream) {
+    if (M < 1 || N < 1 || K < 256 || K % 256) return nullptr;
+    const int RG = (N + 31) / 32, S = (K + kI8SliceK - 1) / kI8SliceK, MB = (M + 31) / 32;
+    if (S > 1 && !part) return nullptr;
+    if (int64_t(RG) * S * MB > 0x7fffffff) return nullptr;
+    const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    float* pt = S > 1 ? part : nullptr;
+    switch (wtype) {
+        case T_Q4_K: launch_kq_strip_wt<T_Q4_K>(xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, stream); break;
+        case T_Q5_K: launch_kq_strip_wt<T_Q5_K>(xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, stream); break;
+        case T_Q6_K: launch_kq_strip_wt<T_Q6_K>(xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, stream); break;
+        default: return nullptr;
+    }
+    if (S > 1) {
+        const int64_t outs = int64_t(M) * N;
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(unsigned((outs + 255) / 256)), dim3(256), 0, stream, part, y, ldy,
+                           M, N, S);
+    }
+    return kq_strip_i8_variant(wtype);
 }
 
 const char* fused_skinny_variant(int wtype) {

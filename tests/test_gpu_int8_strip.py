@@ -1,6 +1,8 @@
-"""The exact int8 path for Q8_0 weights against fewer than 256 activation
-rows in blocks of 32 (the text encoder's 32 tokens, the decoder's 201
-queries and 33 prompt tokens), against the oracle's native CPU path.
+"""The exact int8 paths for Q8_0 weights (Q8_0 activation codes) and for
+Q4_K / Q5_K / Q6_K weights (Q8_K activation codes) against fewer than 256
+activation rows in blocks of 32 (the text encoder's 32 tokens, the
+decoder's 201 queries and 33 prompt tokens), against the oracle's native
+CPU path.
 
 Both sides form the same Q8_0 activation codes and exact integer block dots;
 only the F32 order in which the per-block terms d_w d_x dot are added
@@ -144,3 +146,55 @@ def test_int8_strip_nan_activations(samhip, oracle, rounding):
     assert np.isfinite(ref).all() and np.isfinite(y).all()
     assert not y[20].any() and not ref[20].any()
     assert max_row_rel_l2(y, ref) <= EXACT
+
+
+KQ_SHAPES = [(32, 1024, 1024), (32, 1024, 4096), (32, 4096, 1024), (201, 256, 2048), (201, 2048, 256),
+             (33, 256, 256), (17, 96, 512), (255, 40, 1280), (1, 64, 256), (97, 33, 768)]
+
+
+@pytest.mark.parametrize("qtype", ["q4_K", "q5_K", "q6_K"])
+@pytest.mark.parametrize("shape", KQ_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_kquant_int8_strip_matches_native(samhip, oracle, monkeypatch, shape, qtype):
+    """K-quant weights on the int8 path (SAMHIP_INT8_STRIP=2 takes it for
+    every shape; by default only where it is faster): the 4/5/6-bit codes and
+    Q8_K activation codes meet in exact integer dots; the sub-block scales
+    and minimums are applied in F32 per sub-block, so only the order of the
+    F32 additions differs from the oracle's vec_dot (same bar as Q8_0)."""
+    m, n, k = shape
+    say("case int8 strip", qtype, shape)
+    gt = {"q4_K": samhip.Q4_K, "q5_K": samhip.Q5_K, "q6_K": samhip.Q6_K}[qtype]
+    ot = {"q4_K": oracle.Q4_K, "q5_K": oracle.Q5_K, "q6_K": oracle.Q6_K}[qtype]
+    rng = np.random.default_rng(m * 13 + n + k + gt)
+    w = oracle.quantize(ot, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    x = (rng.standard_normal((m, k)) * np.exp(rng.uniform(-4, 4, (m, 1)))).astype(np.float32)
+    if m > 3:
+        x[2, 7] = np.nan                      # packs as code 0
+        x[3, :] = 0.0                         # an all-zero row: d = 0
+    monkeypatch.setenv("SAMHIP_INT8_STRIP", "2")
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
+        y = ctx.matmul(gt, w, x, x_row_stride=k + 4 if n % 2 else None)
+        assert ctx.query().kernel_variant == ("skinny_i8mfma_" + qtype.lower()).encode()
+        again = ctx.matmul(gt, w, x)
+    ref = oracle.mul_mat_native(ot, w, x)
+    assert np.isfinite(ref).all() and np.isfinite(y).all()
+    if m > 3:
+        assert not y[3].any() and not ref[3].any()
+    err = max_row_rel_l2(y, ref)
+    say(f"  max row rel L2 {err:.2e}")
+    assert err <= EXACT
+    assert np.array_equal(y, again)
+
+
+def test_kquant_int8_default_routing(samhip, oracle):
+    """By default the K-quant int8 path takes one-super-block products whose
+    grid fits one round (the decoder's 256x256 products at M = 201 and 33);
+    longer K stays on the fused kernel."""
+    rng = np.random.default_rng(5)
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
+        for m, n, k, exact in ((201, 256, 256, True), (33, 256, 256, True), (32, 1024, 1024, False)):
+            w = oracle.quantize(oracle.Q4_K, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            y = ctx.matmul(samhip.Q4_K, w, x)
+            name = ctx.query().kernel_variant
+            assert name == (b"skinny_i8mfma_q4_k" if exact else b"skinny_fused_q4_k"), name
+            assert max_row_rel_l2(y, oracle.mul_mat_native(oracle.Q4_K, w, x)) <= (EXACT if exact else 1e-3)

@@ -348,9 +348,9 @@ def test_mul_mat_fused_split_k_deterministic(f16_ctx, oracle, samhip, monkeypatc
 def test_mul_mat_fused_in_projection_views(gpu_ctx, f16_ctx, oracle, qtype):
     """The fusion / decoder q, k, v products: row-offset views of a fused
     [3D, D] in-projection (D = 256) against the image tokens (M = 5184, tiled
-    GEMM), the decoder queries (M = 201, in 32-row blocks: the int8 kernel
-    for Q8_0, the fused kernel for Q4_K) and the prompt tokens (M = 33),
-    each compared in full."""
+    GEMM), the decoder queries (M = 201, in 32-row blocks on the int8
+    kernels: K = 256) and the prompt tokens (M = 33), each compared in
+    full."""
     say("case fused in-projection views", qtype)
     rng = np.random.default_rng(46)
     d = 256
@@ -366,8 +366,8 @@ def test_mul_mat_fused_in_projection_views(gpu_ctx, f16_ctx, oracle, qtype):
 @pytest.mark.parametrize("qtype", TYPES)
 def test_mul_mat_strip_path(gpu_ctx, samhip, oracle, monkeypatch, qtype):
     """The fp16 strip kernel (SAMHIP_STRIP_SKINNY=2 forces it for every
-    weight type and M < 256, with a split-K reduce past K = 1024; Q8_0
-    reaches it only with SAMHIP_INT8_STRIP=0): repeated calls give
+    weight type and M < 256, with a split-K reduce past K = 1024; in native
+    compute only with SAMHIP_INT8_STRIP=0): repeated calls give
     identical bits, and the fused kernel (SAMHIP_STRIP_SKINNY=0), which
     forms the same fp16 operands, agrees to F32 summation-order rounding."""
     say("case strip path", qtype)
@@ -384,9 +384,9 @@ def test_mul_mat_strip_path(gpu_ctx, samhip, oracle, monkeypatch, qtype):
             first = strip.matmul(qtype, w, x)
             assert strip.query().kernel_variant.startswith(b"skinny_strip")
             default = gpu_ctx.matmul(qtype, w, x)
-            # Q8_0 below 256 rows defaults to the exact int8 kernel (its own test)
-            exact = qtype == 8 and m < 256
-            assert gpu_ctx.query().kernel_variant.startswith(b"skinny_i8mfma" if exact else b"skinny_fused")
+            # Q8_0 below 256 rows defaults to the exact int8 kernel (its own test);
+            # these K-quant shapes (K > 256) stay on the fused kernel
+            assert gpu_ctx.query().kernel_variant.startswith(b"skinny_i8mfma" if qtype == 8 else b"skinny_fused")
             assert np.array_equal(first, strip.matmul(qtype, w, x))
             other = fused.matmul(qtype, w, x)
             assert fused.query().kernel_variant.startswith(b"skinny_fused")
