@@ -480,12 +480,14 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     const bool small_w = ctx->fused_skinny && int64_t(N) * K <= kFusedSmallW;
     const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K) && !small_w;
     const bool kquant = (w->type == T_Q4_K || w->type == T_Q5_K || w->type == T_Q6_K) &&
-                        (ctx->int8_strip == 2 || kq_strip_i8_preferred(M, N, K, ctx->cus));
+                        (ctx->int8_strip == 2 || kq_strip_i8_preferred(w->type, M, N, K, ctx->cus));
     if (!tall && M < kStripMaxM && (w->type == T_Q8_0 || kquant) && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE &&
         ctx->int8_strip && ctx->fused_skinny) {
         // exact int8 block dots in blocks of 32 activation rows, one launch
         // for K <= 1024 (the text encoder, the decoder's queries and prompt)
-        if (int rc = ensure_staging(ctx, std::max<size_t>(q8_strip_i8_part_bytes(M, N, K), 256))) return rc;
+        const int slice_sb = kq_strip_i8_slice_sb(M, N, K, ctx->cus);
+        const size_t part_bytes = kquant ? kq_strip_i8_part_bytes(M, N, K, slice_sb) : q8_strip_i8_part_bytes(M, N, K);
+        if (int rc = ensure_staging(ctx, std::max<size_t>(part_bytes, 256))) return rc;
         const char* variant = kquant ? kq_strip_i8_variant(w->type) : q8_strip_i8_variant();
         int rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
             const float* xp = static_cast<const float*>(x->data);
@@ -493,7 +495,7 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
             float* part = static_cast<float*>(ctx->staging);
             const char* ok = kquant
                 ? launch_kq_strip_i8(w->type, xp, int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), yp,
-                                     int64_t(y->nb[1] / 4), part, M, N, K, ctx->stream)
+                                     int64_t(y->nb[1] / 4), part, M, N, K, slice_sb, ctx->stream)
                 : launch_q8_strip_i8(xp, int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), yp, int64_t(y->nb[1] / 4),
                                      part, M, N, K, ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->stream);
             if (!ok) return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no int8 strip kernel for this shape");

@@ -258,20 +258,38 @@ const char* q8_strip_i8_variant();
 const char* launch_q8_strip_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy,
                                float* part, int M, int N, int K, int x86, hipStream_t stream);
 // The same for Q4_K / Q5_K / Q6_K weights against Q8_K activation codes
-// (K a multiple of 256; same partial-sum buffer).  Taken by default where it
-// measured faster than the fused kernel (graph replay, one box): one
-// 256-value super-block of K and a grid of at most one workgroup per CU,
-// e.g. the decoder's M = 201 and M = 33 products on 256x256 weights (Q4_K
-// 6.8 -> 5.0 us, Q6_K 6.6 -> 5.4 us).  At K >= 1024 the Q8_K packing of four
-// super-blocks per workgroup makes it slower (Q4_K M = 32, K = 1024: 10.0
-// against 8.9 us), and so does a second round of workgroups (M = 201,
-// N = 2048, K = 256: 9.3 against 7.0 us).
-inline bool kq_strip_i8_preferred(int M, int N, int K, int cus) {
-    return K == 256 && int64_t((N + 31) / 32) * ((M + 31) / 32) <= cus;
+// (K a multiple of 256; same partial-sum buffer, K slices of 256, 512 or 1024
+// values).  Taken by default where it measured faster than the fused kernel
+// (graph replay, one box): Q4_K and Q5_K when the grid of row groups x row
+// blocks x 1024-wide K slices fits one workgroup per CU, e.g. the text
+// encoder's M = 32 products (Q4_K K = 1024, N = 1024: 8.9 -> 7.3 us;
+// N = 4096: 9.9 -> 9.6; K = 4096: 9.9 -> 9.6) and the decoder's M = 201 and
+// M = 33 products on 256x256 weights (6.8 -> 5.0 us); Q6_K (two masked MFMAs
+// per 32 values) only when 256-wide slices fit (N = 1024, K = 1024: 8.8 ->
+// 7.7 us; with 512-wide slices N = 4096: 9.8 against 10.5 us).  A second
+// round of workgroups makes it slower (Q4_K M = 201, N = 2048, K = 256: 9.2
+// against 7.0 us).
+inline bool kq_strip_i8_preferred(int wtype, int M, int N, int K, int cus) {
+    const int slice = wtype == T_Q6_K ? 256 : kI8SliceK;
+    return int64_t((N + 31) / 32) * ((M + 31) / 32) * ((K + slice - 1) / slice) <= cus;
+}
+// Super-blocks of K per workgroup (1, 2 or 4): the fewest whose grid of row
+// groups x K slices x row blocks still fits one workgroup per CU, so a
+// workgroup's chain of loads, Q8_K packing and sub-block epilogue stays as
+// short as the chip allows; 4 when no choice fits.
+inline int kq_strip_i8_slice_sb(int M, int N, int K, int cus) {
+    const int64_t rows = int64_t((N + 31) / 32) * ((M + 31) / 32);
+    for (int sb = 1; sb < kI8SliceK / 256; sb *= 2)
+        if (rows * ((K + 256 * sb - 1) / (256 * sb)) <= cus) return sb;
+    return kI8SliceK / 256;
+}
+inline size_t kq_strip_i8_part_bytes(int M, int N, int K, int slice_sb) {
+    const int S = (K + 256 * slice_sb - 1) / (256 * slice_sb);
+    return S > 1 ? size_t(S) * size_t(M) * size_t(N) * 4 : 0;
 }
 const char* kq_strip_i8_variant(int wtype);
 const char* launch_kq_strip_i8(int wtype, const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y,
-                               int64_t ldy, float* part, int M, int N, int K, hipStream_t stream);
+                               int64_t ldy, float* part, int M, int N, int K, int slice_sb, hipStream_t stream);
 const char* strip_skinny_variant(int wtype);
 const char* launch_strip_skinny(int wtype, bool f16, const float* x, int64_t ldx, const void* w, int64_t w_stride,
                                 float* y, int64_t ldy, float* part, int M, int N, int K, int x86, hipStream_t stream);

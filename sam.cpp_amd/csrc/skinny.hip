@@ -704,7 +704,7 @@ template <int WT, bool XVEC>
 __global__ __launch_bounds__(1024) void kq_strip_i8_kernel(const float* __restrict__ X, int64_t ldx,
                                                            const uint8_t* __restrict__ W, int64_t w_stride,
                                                            float* __restrict__ Y, int64_t ldy, float* __restrict__ part,
-                                                           int M, int N, int K, int RG, int S) {
+                                                           int M, int N, int K, int RG, int S, int SK) {
 #pragma clang fp contract(off)
     constexpr int WDW = kq_wdw<WT>();
     constexpr int BB = block_bytes(WT);
@@ -720,8 +720,8 @@ __global__ __launch_bounds__(1024) void kq_strip_i8_kernel(const float* __restri
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int rg = blockIdx.x % RG, sp = (blockIdx.x / RG) % S, mb = blockIdx.x / (RG * S);
-    const int n0 = rg * 32, k0 = sp * kI8SliceK;
-    const int nsb = min(kI8SliceK, K - k0) / 256;   // super-blocks in this slice
+    const int n0 = rg * 32, k0 = sp * 256 * SK;
+    const int nsb = min(256 * SK, K - k0) / 256;    // super-blocks in this slice (SK <= XSB)
     const int m0 = mb * 32, Mall = M;
     X += int64_t(m0) * ldx;
     Y += int64_t(m0) * ldy;
@@ -1086,29 +1086,32 @@ const char* kq_strip_i8_variant(int wtype) {
 
 template <int WT>
 void launch_kq_strip_wt(bool xvec, const float* x, int64_t ldx, const uint8_t* w, int64_t w_stride, float* y,
-                        int64_t ldy, float* part, int M, int N, int K, int RG, int S, int MB, hipStream_t stream) {
+                        int64_t ldy, float* part, int M, int N, int K, int RG, int S, int MB, int SK,
+                        hipStream_t stream) {
     const dim3 grid(unsigned(RG * S * MB)), block(1024);
     if (xvec)
         hipLaunchKernelGGL((kq_strip_i8_kernel<WT, true>), grid, block, 0, stream, x, ldx, w, w_stride, y, ldy, part,
-                           M, N, K, RG, S);
+                           M, N, K, RG, S, SK);
     else
         hipLaunchKernelGGL((kq_strip_i8_kernel<WT, false>), grid, block, 0, stream, x, ldx, w, w_stride, y, ldy, part,
-                           M, N, K, RG, S);
+                           M, N, K, RG, S, SK);
 }
 
 const char* launch_kq_strip_i8(int wtype, const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y,
-                               int64_t ldy, float* part, int M, int N, int K, hipStream_t stream) {
+                               int64_t ldy, float* part, int M, int N, int K, int slice_sb, hipStream_t stream) {
     if (M < 1 || N < 1 || K < 256 || K % 256) return nullptr;
-    const int RG = (N + 31) / 32, S = (K + kI8SliceK - 1) / kI8SliceK, MB = (M + 31) / 32;
+    if (slice_sb != 1 && slice_sb != 2 && slice_sb != kI8SliceK / 256) return nullptr;
+    const int SK = slice_sb;
+    const int RG = (N + 31) / 32, S = (K + 256 * SK - 1) / (256 * SK), MB = (M + 31) / 32;
     if (S > 1 && !part) return nullptr;
     if (int64_t(RG) * S * MB > 0x7fffffff) return nullptr;
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     float* pt = S > 1 ? part : nullptr;
     switch (wtype) {
-        case T_Q4_K: launch_kq_strip_wt<T_Q4_K>(xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, stream); break;
-        case T_Q5_K: launch_kq_strip_wt<T_Q5_K>(xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, stream); break;
-        case T_Q6_K: launch_kq_strip_wt<T_Q6_K>(xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, stream); break;
+        case T_Q4_K: launch_kq_strip_wt<T_Q4_K>(xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
+        case T_Q5_K: launch_kq_strip_wt<T_Q5_K>(xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
+        case T_Q6_K: launch_kq_strip_wt<T_Q6_K>(xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
         default: return nullptr;
     }
     if (S > 1) {

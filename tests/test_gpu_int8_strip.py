@@ -186,15 +186,22 @@ def test_kquant_int8_strip_matches_native(samhip, oracle, monkeypatch, shape, qt
 
 
 def test_kquant_int8_default_routing(samhip, oracle):
-    """By default the K-quant int8 path takes one-super-block products whose
-    grid fits one round (the decoder's 256x256 products at M = 201 and 33);
-    longer K stays on the fused kernel."""
+    """By default the K-quant int8 path takes the products whose grid of
+    row groups x 32-row blocks x K slices fits one round of the chip's CUs,
+    with 1024-wide slices for Q4_K / Q5_K (the text encoder's M = 32
+    products, the decoder's 256x256 products at M = 201 and 33) and 256-wide
+    ones for Q6_K; a second round (the decoder's M = 201 FFN expansion to
+    2048) stays on the fused kernel."""
     rng = np.random.default_rng(5)
     with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
-        for m, n, k, exact in ((201, 256, 256, True), (33, 256, 256, True), (32, 1024, 1024, False)):
-            w = oracle.quantize(oracle.Q4_K, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        for qt, m, n, k, exact in ((oracle.Q4_K, 201, 256, 256, True), (oracle.Q4_K, 33, 256, 256, True),
+                                   (oracle.Q4_K, 32, 1024, 1024, True), (oracle.Q5_K, 32, 1024, 4096, True),
+                                   (oracle.Q4_K, 201, 2048, 256, False), (oracle.Q6_K, 32, 1024, 1024, True),
+                                   (oracle.Q6_K, 32, 4096, 1024, False)):
+            w = oracle.quantize(qt, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
             x = rng.standard_normal((m, k)).astype(np.float32)
-            y = ctx.matmul(samhip.Q4_K, w, x)
-            name = ctx.query().kernel_variant
-            assert name == (b"skinny_i8mfma_q4_k" if exact else b"skinny_fused_q4_k"), name
-            assert max_row_rel_l2(y, oracle.mul_mat_native(oracle.Q4_K, w, x)) <= (EXACT if exact else 1e-3)
+            y = ctx.matmul(qt, w, x)
+            name = ctx.query().kernel_variant.decode()
+            tname = {oracle.Q4_K: "q4_k", oracle.Q5_K: "q5_k", oracle.Q6_K: "q6_k"}[qt]
+            assert name == ("skinny_i8mfma_" if exact else "skinny_fused_") + tname, (name, m, n, k)
+            assert max_row_rel_l2(y, oracle.mul_mat_native(qt, w, x)) <= (EXACT if exact else 1e-3)
