@@ -485,9 +485,8 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
         ctx->int8_strip && ctx->fused_skinny) {
         // exact int8 block dots in blocks of 32 activation rows, one launch
         // for K <= 1024 (the text encoder, the decoder's queries and prompt)
-        const int slice_sb = kq_strip_i8_slice_sb(M, N, K, ctx->cus);
-        const size_t part_bytes = kquant ? kq_strip_i8_part_bytes(M, N, K, slice_sb) : q8_strip_i8_part_bytes(M, N, K);
-        if (int rc = ensure_staging(ctx, std::max<size_t>(part_bytes, 256))) return rc;
+        const int slice_sb = i8_strip_slice_sb(w->type, M, N, K, ctx->cus);
+        if (int rc = ensure_staging(ctx, std::max<size_t>(i8_strip_part_bytes(M, N, K, slice_sb), 256))) return rc;
         const char* variant = kquant ? kq_strip_i8_variant(w->type) : q8_strip_i8_variant();
         int rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
             const float* xp = static_cast<const float*>(x->data);
@@ -497,7 +496,8 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
                 ? launch_kq_strip_i8(w->type, xp, int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), yp,
                                      int64_t(y->nb[1] / 4), part, M, N, K, slice_sb, ctx->stream)
                 : launch_q8_strip_i8(xp, int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), yp, int64_t(y->nb[1] / 4),
-                                     part, M, N, K, ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->stream);
+                                     part, M, N, K, slice_sb, ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0,
+                                     ctx->stream);
             if (!ok) return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no int8 strip kernel for this shape");
             HIP_TRY(hipGetLastError(), "int8 strip launch");
             return SAMHIP_OK;

@@ -246,17 +246,32 @@ constexpr int kStripMaxM = 256;   // in blocks of 32 activation rows
 inline bool strip_skinny_preferred(int wtype, int M, int K) { return wtype == T_Q8_0 && K <= 1024 && M <= 32; }
 FusedPlan strip_skinny_plan(int M, int N, int K);
 // Exact int8 products of Q8_0 weights in blocks of 32 activation rows
-// (COMPUTE_Q8_NATIVE): one launch while K <= kI8SliceK, else slices of
-// kI8SliceK values whose partial sums go through `part`
-// (ceil(K / kI8SliceK) * M * N floats) and a reduce launch.
-constexpr int kI8SliceK = 1024;
-inline size_t q8_strip_i8_part_bytes(int M, int N, int K) {
-    const int S = (K + kI8SliceK - 1) / kI8SliceK;
+// (COMPUTE_Q8_NATIVE).  A workgroup takes a K slice of 256 * slice_sb values
+// (slice_sb 1, 2 or 4, from i8_strip_slice_sb); with more than one slice the
+// partial sums go through `part` (i8_strip_part_bytes) and a reduce launch.
+constexpr int kI8SliceK = 1024;   // widest K slice
+// 256-value units of K per workgroup (1, 2 or 4): the fewest whose grid of
+// row groups x K slices x row blocks still fits one workgroup per CU, so a
+// workgroup's chain of loads, packing and epilogue stays as short as the
+// chip allows; 4 when no choice fits.  Q8_0 packs 32-value blocks, a short
+// chain, so with K <= 1024 it keeps one slice unless 256-wide ones fit
+// (graph replay, M = 32, K = 1024: N = 1024 7.6 -> 7.1 us with four slices;
+// N = 4096 7.8 us in one slice, 8.8 in two plus the reduce launch; at
+// K = 4096, N = 1024 512-wide slices take 8.8 us against 9.9).
+inline int i8_strip_slice_sb(int wtype, int M, int N, int K, int cus) {
+    const int64_t rows = int64_t((N + 31) / 32) * ((M + 31) / 32);
+    const auto fits = [&](int sb) { return rows * ((K + 256 * sb - 1) / (256 * sb)) <= cus; };
+    if (fits(1)) return 1;
+    if (wtype == T_Q8_0 && K <= kI8SliceK) return kI8SliceK / 256;
+    return fits(2) ? 2 : kI8SliceK / 256;
+}
+inline size_t i8_strip_part_bytes(int M, int N, int K, int slice_sb) {
+    const int S = (K + 256 * slice_sb - 1) / (256 * slice_sb);
     return S > 1 ? size_t(S) * size_t(M) * size_t(N) * 4 : 0;
 }
 const char* q8_strip_i8_variant();
 const char* launch_q8_strip_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy,
-                               float* part, int M, int N, int K, int x86, hipStream_t stream);
+                               float* part, int M, int N, int K, int slice_sb, int x86, hipStream_t stream);
 // The same for Q4_K / Q5_K / Q6_K weights against Q8_K activation codes
 // (K a multiple of 256; same partial-sum buffer, K slices of 256, 512 or 1024
 // values).  Taken by default where it measured faster than the fused kernel
@@ -272,20 +287,6 @@ const char* launch_q8_strip_i8(const float* x, int64_t ldx, const void* w, int64
 inline bool kq_strip_i8_preferred(int wtype, int M, int N, int K, int cus) {
     const int slice = wtype == T_Q6_K ? 256 : kI8SliceK;
     return int64_t((N + 31) / 32) * ((M + 31) / 32) * ((K + slice - 1) / slice) <= cus;
-}
-// Super-blocks of K per workgroup (1, 2 or 4): the fewest whose grid of row
-// groups x K slices x row blocks still fits one workgroup per CU, so a
-// workgroup's chain of loads, Q8_K packing and sub-block epilogue stays as
-// short as the chip allows; 4 when no choice fits.
-inline int kq_strip_i8_slice_sb(int M, int N, int K, int cus) {
-    const int64_t rows = int64_t((N + 31) / 32) * ((M + 31) / 32);
-    for (int sb = 1; sb < kI8SliceK / 256; sb *= 2)
-        if (rows * ((K + 256 * sb - 1) / (256 * sb)) <= cus) return sb;
-    return kI8SliceK / 256;
-}
-inline size_t kq_strip_i8_part_bytes(int M, int N, int K, int slice_sb) {
-    const int S = (K + 256 * slice_sb - 1) / (256 * slice_sb);
-    return S > 1 ? size_t(S) * size_t(M) * size_t(N) * 4 : 0;
 }
 const char* kq_strip_i8_variant(int wtype);
 const char* launch_kq_strip_i8(int wtype, const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y,

@@ -539,7 +539,7 @@ template <bool X86, bool XVEC>
 __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restrict__ X, int64_t ldx,
                                                            const uint8_t* __restrict__ W, int64_t w_stride,
                                                            float* __restrict__ Y, int64_t ldy, float* __restrict__ part,
-                                                           int M, int N, int K, int RG, int S) {
+                                                           int M, int N, int K, int RG, int S, int SL) {
 #pragma clang fp contract(off)
     __shared__ __attribute__((aligned(16))) int8_t Xq[32 * I8_XLD];
     __shared__ __attribute__((aligned(16))) float Xd[kI8SliceK / 32][32];
@@ -549,8 +549,8 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int rg = blockIdx.x % RG, sp = (blockIdx.x / RG) % S, mb = blockIdx.x / (RG * S);
-    const int n0 = rg * 32, k0 = sp * kI8SliceK;
-    const int nb = min(kI8SliceK, K - k0) / 32;   // Q8_0 blocks in this slice
+    const int n0 = rg * 32, k0 = sp * SL;
+    const int nb = min(SL, K - k0) / 32;   // Q8_0 blocks in this slice (SL <= kI8SliceK)
     // this workgroup's block of 32 activation rows
     const int m0 = mb * 32, Mall = M;
     X += int64_t(m0) * ldx;
@@ -1049,9 +1049,11 @@ const char* launch_strip_skinny(int wtype, bool f16, const float* x, int64_t ldx
 const char* q8_strip_i8_variant() { return "skinny_i8mfma_q8_0"; }
 
 const char* launch_q8_strip_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy,
-                               float* part, int M, int N, int K, int x86, hipStream_t stream) {
+                               float* part, int M, int N, int K, int slice_sb, int x86, hipStream_t stream) {
     if (M < 1 || N < 1 || K < 32 || K % 32) return nullptr;
-    const int RG = (N + 31) / 32, S = (K + kI8SliceK - 1) / kI8SliceK, MB = (M + 31) / 32;
+    if (slice_sb != 1 && slice_sb != 2 && slice_sb != kI8SliceK / 256) return nullptr;
+    const int SL = 256 * slice_sb;
+    const int RG = (N + 31) / 32, S = (K + SL - 1) / SL, MB = (M + 31) / 32;
     if (S > 1 && !part) return nullptr;
     if (int64_t(RG) * S * MB > 0x7fffffff) return nullptr;
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
@@ -1060,7 +1062,7 @@ const char* launch_q8_strip_i8(const float* x, int64_t ldx, const void* w, int64
     const dim3 grid(unsigned(RG * S * MB)), block(1024);
 #define SAMHIP_I8(X86V, XV)                                                                                    \
     hipLaunchKernelGGL((q8_strip_i8_kernel<X86V, XV>), grid, block, 0, stream, x, ldx, wb, w_stride, y, ldy, pt, M, N, \
-                       K, RG, S)
+                       K, RG, S, SL)
     if (x86) {
         if (xvec) SAMHIP_I8(true, true); else SAMHIP_I8(true, false);
     } else {
