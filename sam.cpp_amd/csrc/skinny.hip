@@ -527,7 +527,8 @@ __global__ __launch_bounds__(1024) void strip_skinny_kernel(const float* __restr
 //     block and no cross-lane reductions;
 //  3. wave w multiplies blocks w, w + 16 of the slice;
 //  4. the 16 partial tiles are added in LDS in wave order.
-// Slices beyond the first (K > 1024) write partial sums that
+// The host picks the slice width SL (256, 512 or 1024 values).  With more
+// than one slice each workgroup writes its partial sums, which
 // splitk_reduce_kernel adds in slice order.
 // ---------------------------------------------------------------------------
 constexpr int I8_XLD = kI8SliceK + 16;                                // bytes per LDS code row
@@ -694,7 +695,8 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
 //     (the same integer sums ggml forms; only the order of the F32 additions
 //     differs);
 //  4. the 16 partial tiles are added in LDS in wave order.
-// Slices beyond the first (K > 1024) write partial sums that
+// The host picks the slice width (SK super-blocks of 256 values: 1, 2 or 4).
+// With more than one slice each workgroup writes its partial sums, which
 // splitk_reduce_kernel adds in slice order.
 // ---------------------------------------------------------------------------
 template <int WT>
