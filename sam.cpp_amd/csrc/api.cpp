@@ -113,8 +113,9 @@ struct samhip_context {
     int attn_splits = 0;        // SAMHIP_ATTN_SPLITS: key splits of the attention kernel (0: by grid size)
     int fused_max_splits = 16;  // SAMHIP_FUSED_MAX_SPLITS: cap on the fused kernel's K splits
     bool check_activations = false;   // samhip_context_set_activation_check
-    int int8_strip = 1;         // SAMHIP_INT8_STRIP: 0 keeps M < 256 products on the fp16 kernels, 2 sends every
-                                // K-quant one there too (1: where it measured faster)
+    int int8_strip = 1;         // SAMHIP_INT8_STRIP: 0 keeps M < 256 products on the fp16 kernels; 1 sends Q8_0
+                                // ones, and K-quant ones where that measured faster, to the int8 kernels; 2
+                                // sends every K-quant one there as well
     samhip_exec_info info{};
     // per-launch event trace (samhip_trace_begin / samhip_trace_end)
     struct TraceRecord {
@@ -483,8 +484,9 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
                         (ctx->int8_strip == 2 || kq_strip_i8_preferred(w->type, M, N, K, ctx->cus));
     if (!tall && M < kStripMaxM && (w->type == T_Q8_0 || kquant) && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE &&
         ctx->int8_strip && ctx->fused_skinny) {
-        // exact int8 block dots in blocks of 32 activation rows, one launch
-        // for K <= 1024 (the text encoder, the decoder's queries and prompt)
+        // exact int8 block dots in blocks of 32 activation rows (the text
+        // encoder, the decoder's queries and prompt); K slices of 256-1024
+        // values, and a reduce launch when there is more than one
         const int slice_sb = i8_strip_slice_sb(w->type, M, N, K, ctx->cus);
         if (int rc = ensure_staging(ctx, std::max<size_t>(i8_strip_part_bytes(M, N, K, slice_sb), 256))) return rc;
         const char* variant = kquant ? kq_strip_i8_variant(w->type) : q8_strip_i8_variant();
