@@ -34,7 +34,7 @@ def say(*a):
 SHAPES = [(32, 3072, 1024), (32, 1024, 1024), (32, 4096, 1024), (32, 1024, 4096), (32, 256, 1024),
           (1, 4096, 1024), (17, 96, 512), (31, 33, 2048), (32, 64, 32), (5, 1000, 1056),
           (201, 256, 256), (201, 2048, 256), (201, 256, 2048), (33, 256, 256), (255, 96, 1056), (64, 40, 64),
-          (97, 33, 1024)]
+          (97, 33, 1024), (3, 1, 256)]
 
 
 @pytest.mark.parametrize("rounding", ["x86", "ref"])
@@ -149,7 +149,7 @@ def test_int8_strip_nan_activations(samhip, oracle, rounding):
 
 
 KQ_SHAPES = [(32, 1024, 1024), (32, 1024, 4096), (32, 4096, 1024), (201, 256, 2048), (201, 2048, 256),
-             (33, 256, 256), (17, 96, 512), (255, 40, 1280), (1, 64, 256), (97, 33, 768)]
+             (33, 256, 256), (17, 96, 512), (255, 40, 1280), (1, 64, 256), (97, 33, 768), (3, 1, 512)]
 
 
 @pytest.mark.parametrize("qtype", ["q4_K", "q5_K", "q6_K"])

@@ -42,12 +42,15 @@ def _both(samhip, ctx, qtype, w, x, n):
     return a, b
 
 
-# (first call, second smaller call): tall GEMM path, fused skinny, strip skinny
+# (first call, second smaller call): tall GEMM path, the int8 kernels with
+# K slices (Q8_0 and K-quant), the fused skinny kernel
 PAIRS = [
     (("Q8_0", 5184, 1024, 4736), ("Q8_0", 2048, 1024, 4736)),     # ViT fc2: 59 MB of scratch, then 24 MB
     (("Q4_K", 5184, 4736, 1024), ("Q5_K", 1024, 3072, 1024)),     # ViT fc1, then a smaller qkv
     (("Q8_0", 201, 2048, 256), ("Q6_K", 33, 256, 256)),           # decoder fc1, then a prompt K/V product
     (("Q8_0", 32, 4096, 1024), ("Q8_0", 32, 1024, 4096)),         # text fc1 (strip), then fc2 (split K)
+    (("Q4_K", 32, 1024, 4096), ("Q4_K", 32, 1024, 1024)),         # text fc2: eight 512-wide K slices, then four 256-wide
+    (("Q6_K", 32, 4096, 1024), ("Q6_K", 17, 96, 512)),            # fused kernel, then int8 in two K slices
 ]
 
 
