@@ -827,6 +827,14 @@ class Encoder:
         return (2.0 * T * E * 3 * kp + sum(lin + (att_g if i in e["GLOBAL"] else att_w) for i in range(e["DEPTH"]))
                 + neck_flops(e["GRID"], E, e["NECK_MID"], e["NECK_DIM"]))
 
+    def free(self):
+        """Releases the device buffers (weights, tables, activations, levels)."""
+        for b in self.keep + [self.image, self.x] + [lv for lv in self.levels if lv is not None]:
+            b.free()
+        self.prefix.free()
+        self.neck.free()
+        self.keep, self.levels = [], []
+
     def forward(self, neck=True):
         self.prefix.forward(self.image, self.x)
         for d in self.blocks:
@@ -859,6 +867,44 @@ class Encoder:
         n_tok = e["GRID"] ** 2 if glob else e["WINDOW"] ** 2
         out["freqs"] = ctx.download(At(d.freqs_cis), (n_tok, E // e["HEADS"] // 2, 2), np.float32)
         return out
+
+
+def encoder_roofline(breakdown):
+    """Roofline of the encode's two MFMA-bound parts, from the per-image
+    kernel times of the events pass (`kernel_ms_per_image`):
+      linears: 2*M*N*K of the 32 blocks' qkv, proj, fc1 and fc2 products
+               divided by their GEMM time plus their preparation launches
+               (activation staging + weight decode, with the folded layer
+               norm / erf-GELU), against the fp16 dense peak;
+      attention: 4*N_keys*hd flops per query and head (QK^T and PV) over
+               each token's window (28 windowed blocks, 576 keys) or the
+               whole grid (4 global blocks, 5184 keys) divided by the
+               attention launches' time; at F32-accurate operands the MFMA
+               issues 3x that work (hi*hi + lo*hi + hi*lo), reported beside
+               it as `mfma_frac`."""
+    e = ENC
+    T, E, MLP = e["GRID"] ** 2, e["E"], e["MLP"]
+    n_glob = len(e["GLOBAL"])
+    lin_flops = e["DEPTH"] * 2.0 * T * E * (3 * E + E + 2 * MLP)
+    lin_names = ("vit_qkv", "vit_proj", "vit_fc1", "vit_fc2")
+    lin_ms = sum(v for k, v in breakdown.items() if k in lin_names or k.startswith("stage_"))
+    gemm_ms = sum(v for k, v in breakdown.items() if k in lin_names)
+    att_flops = ((e["DEPTH"] - n_glob) * 4.0 * T * e["WINDOW"] ** 2 * E + n_glob * 4.0 * T * T * E)
+    att_ms = breakdown.get("vit_attention", 0.0)
+    lin_ach = lin_flops / (lin_ms * 1e-3) / 1e12 if lin_ms else None
+    att_ach = att_flops / (att_ms * 1e-3) / 1e12 if att_ms else None
+    return {"bound": "mfma", "achieved": round(lin_ach, 2) if lin_ach else None, "peak": PEAK_FP16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(lin_ach / PEAK_FP16_TFLOPS, 4) if lin_ach else None, "traffic": None,
+            "kernel": "ViT linears: qkv/proj/fc1/fc2 GEMMs + their preparation launches (events, per image)",
+            "flops_per_image": lin_flops, "ms_per_image": round(lin_ms, 4),
+            "gemm_only": {"ms_per_image": round(gemm_ms, 4),
+                          "achieved": round(lin_flops / (gemm_ms * 1e-3) / 1e12, 2) if gemm_ms else None},
+            "attention": {"bound": "mfma", "achieved": round(att_ach, 2) if att_ach else None,
+                          "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                          "frac": round(att_ach / PEAK_FP16_TFLOPS, 4) if att_ach else None,
+                          "mfma_frac": round(3 * att_ach / PEAK_FP16_TFLOPS, 4) if att_ach else None,
+                          "flops_per_image": att_flops, "ms_per_image": round(att_ms, 4),
+                          "note": "F32-accurate operands: the MFMA runs 3x the algorithmic flops (mfma_frac)"}}
 
 
 def encoder_cpu_baseline(enc, seconds_cap=60.0):
@@ -904,11 +950,11 @@ def encoder_cpu_baseline(enc, seconds_cap=60.0):
                       f"oracle/vit_oracle.c (native Q8 linears, exact-softmax attention, F32 convolutions), OpenMP"}
 
 
-def encoder_measure(sh, ctx, enc, warmup, iters):
+def encoder_measure(sh, ctx, enc, warmup, iters, fp16_attention=True):
     """ms/image of the image encode (prefix + 32 blocks + neck levels 0-2,
     as the reference's image path runs it, F32-accurate attention), its
-    kernel breakdown, ms/image of the ViT alone (prefix + 32 blocks) and of
-    the encode with fp16 attention operands."""
+    kernel breakdown, ms/image of the ViT alone (prefix + 32 blocks) and,
+    with `fp16_attention`, of the encode with fp16 attention operands."""
     for _ in range(warmup):
         enc.forward()
     ctx.synchronize()
@@ -925,6 +971,9 @@ def encoder_measure(sh, ctx, enc, warmup, iters):
         enc.forward(neck=False)
     ctx.synchronize()
     enc.vit_ms = (time.perf_counter() - t0) * 1e3 / iters
+    enc.fp16_attention_ms = None
+    if not fp16_attention:
+        return ms, prof, kernel_breakdown(prof)
     # the same encode with fp16 attention operands (attention_type F16)
     for d in enc.blocks:
         d.attention_type = sh.F16
@@ -937,12 +986,16 @@ def encoder_measure(sh, ctx, enc, warmup, iters):
     enc.fp16_attention_ms = (time.perf_counter() - t0) * 1e3 / iters
     for d in enc.blocks:
         d.attention_type = sh.F32
+    return ms, prof, kernel_breakdown(prof)
+
+
+def kernel_breakdown(prof):
+    """Per-image ms by launch name from one traced forward."""
     by = {}
     for name, wt, m, n, k, kms in prof:
         # attention launches carry their key-split count (vit_attention_splitS)
         by.setdefault("vit_attention" if name.startswith("vit_attention") else name, []).append((m, n, k, kms))
-    breakdown = {name: round(sum(r[3] for r in rs), 4) for name, rs in sorted(by.items(), key=lambda t: -sum(r[3] for r in t[1]))}
-    return ms, prof, breakdown
+    return {name: round(sum(r[3] for r in rs), 4) for name, rs in sorted(by.items(), key=lambda t: -sum(r[3] for r in t[1]))}
 
 
 def encoder_workload(args, sh, ctx):
@@ -951,11 +1004,15 @@ def encoder_workload(args, sh, ctx):
     log("building the vision encoder")
     enc = Encoder(sh, ctx, qt)
     ms, prof, breakdown = encoder_measure(sh, ctx, enc, args.warmup, args.steps)
-    # dominant kernel's roofline (MFMA): the fc1 product of a block
+    # the single fc1 launch of a block, beside the encode's roofline
     fc1 = [r for r in prof if r[0] == "vit_fc1"]
     m_, n_, k_ = fc1[0][2], fc1[0][3], fc1[0][4]
     fc1_ms = float(np.mean([r[5] for r in fc1]))
     ach = 2.0 * m_ * n_ * k_ / (fc1_ms * 1e-3) / 1e12
+    roof = encoder_roofline(breakdown)
+    roof["fc1_launch"] = {"achieved": round(ach, 2), "frac": round(ach / PEAK_FP16_TFLOPS, 4),
+                          "kernel": "vit_fc1 (fp16 GEMM + bias + GELU)", "shape": {"M": m_, "N": n_, "K": k_},
+                          "launch_ms": round(fc1_ms, 5)}
     result = {
         "metric": "SAM3 vision encode ms/image @1008px", "value": round(ms, 3), "unit": "ms/image", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": False,
@@ -967,9 +1024,7 @@ def encoder_workload(args, sh, ctx):
         "tflops_effective": round(enc.flops / (ms * 1e-3) / 1e12, 2),
         "vit_ms_per_image": round(enc.vit_ms, 3),
         "fp16_attention_ms_per_image": round(enc.fp16_attention_ms, 3),
-        "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(ach / PEAK_FP16_TFLOPS, 4), "traffic": None, "kernel": "vit_fc1 (fp16 GEMM + bias + GELU)",
-                     "shape": {"M": m_, "N": n_, "K": k_}, "launch_ms": round(fc1_ms, 5)},
+        "roofline": roof,
         "kernel_ms_per_image": breakdown,
         "device": ctx.query().device_name.decode(),
     }
@@ -981,37 +1036,45 @@ def encoder_workload(args, sh, ctx):
     return result
 
 
-def linear_set(sh, ctx, m, items, steps, warmup, seed=0):
+def linear_set(sh, ctx, m, items, steps, warmup, seed=0, rotate=1):
     """Times a set of tall products [(label, weight type, K, N)] at M = m,
     each with its own X and Y, weights N(0, 0.02^2) and X N(0, 1): whole-step
     TOPS (activation staging, weight decode and GEMM), per-product event
-    times, and the dominant kernel's roofline (events on its launch stream)."""
+    times, and the dominant kernel's roofline (events on its launch stream).
+    `rotate` > 1 gives every product that many independent W / X / Y sets,
+    step i running set i % rotate, so that a set whose bytes fit the 256 MB
+    MALL is not served from it on the next step."""
     rng = np.random.default_rng(seed + 1)
-    ops = []
-    for label, qt, k, n in items:
-        wf = ctx.upload((np.random.default_rng(seed).standard_normal((n, k)) * 0.02).astype(np.float32))
-        wq = ctx.alloc(n * sh.row_bytes(qt, k))
-        ctx.quantize_rows(qt, wf.ptr, 4 * k, wq.ptr, n, k, sh.ROUND_REF)
-        ctx.synchronize()
-        wf.free()
-        xb = ctx.upload(rng.standard_normal((m, k)).astype(np.float32))
-        yb = ctx.alloc(m * n * 4)
-        ops.append((label, qt, k, n, sh.tensor(qt, k, n, wq.ptr), sh.tensor(sh.F32, k, m, xb.ptr),
-                    sh.tensor(sh.F32, n, m, yb.ptr), [wq, xb, yb]))
+    sets = []
+    for r in range(rotate):
+        ops = []
+        for label, qt, k, n in items:
+            wf = ctx.upload((np.random.default_rng(seed + 7 * r).standard_normal((n, k)) * 0.02).astype(np.float32))
+            wq = ctx.alloc(n * sh.row_bytes(qt, k))
+            ctx.quantize_rows(qt, wf.ptr, 4 * k, wq.ptr, n, k, sh.ROUND_REF)
+            ctx.synchronize()
+            wf.free()
+            xb = ctx.upload(rng.standard_normal((m, k)).astype(np.float32))
+            yb = ctx.alloc(m * n * 4)
+            ops.append((label, qt, k, n, sh.tensor(qt, k, n, wq.ptr), sh.tensor(sh.F32, k, m, xb.ptr),
+                        sh.tensor(sh.F32, n, m, yb.ptr), [wq, xb, yb]))
+        sets.append(ops)
+    ops = sets[0]
 
-    def step():
-        for _, _, _, _, w, x, y, _ in ops:
+    def step(i=0):
+        for _, _, _, _, w, x, y, _ in sets[i % rotate]:
             ctx.mul_mat(w, x, y)
 
-    for _ in range(warmup):
-        step()
+    for i in range(warmup):
+        step(i)
     ctx.trace_begin()
-    step()
-    prof = ctx.trace_end(capacity=4 * len(ops) + 16)
+    for r in range(rotate):
+        step(warmup + r)
+    prof = ctx.trace_end(capacity=4 * len(ops) * rotate + 16)
     ctx.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
+    for i in range(steps):
+        step(i)
     ctx.synchronize()
     elapsed = time.perf_counter() - t0
     flops = sum(2.0 * m * n * k for _, _, k, n, *_ in ops)
@@ -1029,14 +1092,17 @@ def linear_set(sh, ctx, m, items, steps, warmup, seed=0):
     alg_bytes = nn * sh.row_bytes(qt, kk) + mm * kk * 4 + mm * nn * 4
     products = []
     for label, qt_, k, n, *_ in ops:
-        t = sum(r[5] for r in prof if r[1] == qt_ and r[3] == n and r[4] == k)
+        t = sum(r[5] for r in prof if r[1] == qt_ and r[3] == n and r[4] == k) / rotate
         products.append({"product": label, "M": m, "N": n, "K": k, "ms": round(t, 5),
                          "tops": round(2.0 * m * n * k / (t * 1e-3) / 1e12, 2) if t else None})
-    for o in ops:
-        for b in o[7]:
-            b.free()
+    set_bytes = sum(n * sh.row_bytes(qt_, k) + m * k * 4 + m * n * 4 for _, qt_, k, n, *_ in ops)
+    for st in sets:
+        for o in st:
+            for b in o[7]:
+                b.free()
     return {"value": round(flops * steps / elapsed / 1e12, 3), "unit": "TOPS",
             "ms_per_step": round(elapsed * 1e3 / steps, 4), "steps": steps, "warmup": warmup,
+            "rotation": {"sets": rotate, "bytes_per_set": set_bytes, "bytes_rotated": set_bytes * rotate},
             "pct_int8_peak": round(100 * flops * steps / elapsed / 1e12 / PEAK_INT8_TOPS, 2),
             "products": products,
             "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
@@ -1055,9 +1121,10 @@ def other_configs(args, sh, ctx, ops, xbuf):
     of (3))."""
     out = {}
     log("config 1: single Q8_0 fc1")
-    out["1_single_q8_0_fc1"] = {"workload": "ViT fc1 1024->4736, Q8_0 weights, M=5184",
+    out["1_single_q8_0_fc1"] = {"workload": "ViT fc1 1024->4736, Q8_0 weights, M=5184; 3 W/X/Y sets rotated "
+                                            "(374 MB, past the 256 MB MALL)",
                                 **linear_set(sh, ctx, M_TOKENS, [("fc1:q8_0", sh.Q8_0, 1024, 4736)],
-                                             args.steps, args.warmup)}
+                                             args.steps, args.warmup, rotate=3)}
     sub = argparse.Namespace(**vars(args))
     sub.cpu_seconds = min(args.cpu_seconds, 5.0)
     sub.steps = max(args.steps, 10)
@@ -1290,7 +1357,19 @@ def main():
             "config": "1008x1008x3 image, 72x72 tokens, width 1024, 32 blocks (window 24, global 7/15/23/31), "
                       "16 heads, MLP 4736; Q4_K qkv/proj/fc1, Q8_0 fc2; SimpleFPN neck levels 0-2 (F32 columns); "
                       "random-init weights; batch 1; 3 warmup + 10 timed forwards",
+            "roofline": encoder_roofline(breakdown),
             "kernel_ms_per_image": breakdown}
+        # the Q8_0 variant: every linear Q8_0 (472 MB of packed weights)
+        log("building the Q8_0 vision encoder")
+        enc8 = Encoder(sh, ctx, sh.Q8_0, seed=3)
+        ms8, _, bd8 = encoder_measure(sh, ctx, enc8, 3, 10, fp16_attention=False)
+        result["vision_encoder"]["q8_0_variant"] = {
+            "ms_per_image": round(ms8, 3), "images_per_s": round(1e3 / ms8, 2),
+            "vit_ms_per_image": round(enc8.vit_ms, 3),
+            "tflops_effective": round(enc8.flops / (ms8 * 1e-3) / 1e12, 2),
+            "config": "as above with every linear (qkv/proj/fc1/fc2) Q8_0; 3 warmup + 10 timed forwards",
+            "roofline": encoder_roofline(bd8), "kernel_ms_per_image": bd8}
+        enc8.free()
     if not args.no_configs:
         result["configs"] = other_configs(args, sh, ctx, ops, xbuf)
     if not args.no_cpu_baseline:

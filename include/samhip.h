@@ -167,8 +167,13 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
  * (enough for every SAM 3 batch-1 linear; the largest, the ViT fc2 at
  * M = 5184, K = 4736, needs 59 MB).  A product that needs more returns
  * INVALID_ARGUMENT.  Calls on the same GPU share that array and keep no
- * state in it between calls: calls that overlap on one GPU (two contexts,
- * two streams, two threads) race and must be serialized by the caller. */
+ * state in it between calls.  The library orders them on the GPU: each call
+ * waits (hipStreamWaitEvent, on its context's stream) for the previous
+ * call's kernels on that GPU, whichever context, stream or host thread made
+ * it, so calls made one after another on the host run one after another on
+ * the GPU.  Calls recorded into a graph (samhip_capture_begin) are not
+ * ordered that way: replays of such a graph race with any other call on the
+ * array unless the caller orders them (same stream, or an event). */
 int samhip_mul_mat_noalloc(samhip_context* ctx, const samhip_tensor* w, const samhip_tensor* x,
                            const samhip_tensor* y);
 

@@ -216,7 +216,8 @@ static void q8_0_block(const float* x, uint8_t* out, int rounding) {
     for (int j = 0; j < QK8; ++j) {
         const float v = x[j] * inv;
         const float r = rounding == OR_Q8_ROUND_X86 ? rintf(v) : roundf(v);
-        q[j] = isnan(r) ? 0 : (int8_t)r;   /* a NaN activation packs as code 0, as Q8_K's nearest_int */
+        q[j] = isnan(r) ? 0 : (int8_t)r;   /* NaN -> code 0: Q8_K's nearest_int rule, chosen for both Q8_0
+                                              roundings (ggml's AVX2 packing would give -128 instead) */
     }
 }
 

@@ -21,6 +21,7 @@ BLOCK_BYTES = {Q8_0: 34, Q8_1: 36, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292}
 NAMES = {Q8_0: "q8_0", Q8_1: "q8_1", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K"}
 
 _lib = None
+_default_threads = None   # OpenMP's thread count when the library was loaded
 
 NECK_FIELDS = ("s0_dc1_w", "s0_dc1_b", "s0_dc2_w", "s0_dc2_b", "s0_c1_w", "s0_c1_b", "s0_c3_w", "s0_c3_b",
                "s1_dc_w", "s1_dc_b", "s1_c1_w", "s1_c1_b", "s1_c3_w", "s1_c3_b",
@@ -85,6 +86,10 @@ def lib():
         L.or_maxpool2x2.argtypes = [P, I, I, I, P]
         L.or_neck.argtypes = [ctypes.POINTER(NeckWeights), P, I, I, I, I, I, ctypes.POINTER(P), I]
         _lib = L
+        # every entry point with threads > 0 calls omp_set_num_threads, which
+        # persists: remember the process default before any call changes it
+        global _default_threads
+        _default_threads = L.or_max_threads()
     return _lib
 
 
@@ -206,7 +211,11 @@ def gemm_f64(w, x, threads=0):
 
 
 def max_threads():
-    return lib().or_max_threads()
+    """The host threads OpenMP would use by default (OMP_NUM_THREADS, else
+    every core), as read when the library was loaded, so a call made with an
+    explicit smaller count does not shrink what later callers get."""
+    lib()
+    return _default_threads
 
 
 # ---- SAM 3 vision encoder pieces (vit_oracle.c) ----------------------------

@@ -70,19 +70,36 @@ __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
-void* g_scratch_ptr[kMaxDevices] = {};
 
-// The current device's scratch address (looked up on its first use).
+// Per device: the scratch address, and what orders the calls that use it.
+// `last` is recorded on a call's stream after its kernels, and the next call
+// (on any context, any stream of that device) waits for it before its own,
+// so calls made one after another on the host also run one after another on
+// the GPU; `call` keeps two host threads from interleaving that wait/record.
+struct FixedScratch {
+    void* ptr = nullptr;
+    hipEvent_t last = nullptr;
+    std::mutex call;
+};
+FixedScratch g_fixed[kMaxDevices];
+
+// The current device's scratch (looked up on its first use, with the
+// ordering event created then; neither allocates device memory later).
 hipError_t device_scratch(int device, void** out) {
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
     if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
-    if (!g_scratch_ptr[device]) {
+    FixedScratch& f = g_fixed[device];
+    if (!f.ptr) {
         void* p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return e;
-        g_scratch_ptr[device] = p;
+        hipEvent_t ev = nullptr;
+        e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e != hipSuccess) return e;
+        f.last = ev;
+        f.ptr = p;
     }
-    *out = g_scratch_ptr[device];
+    *out = f.ptr;
     return hipSuccess;
 }
 
@@ -455,6 +472,12 @@ int samhip_mul_mat_noalloc(samhip_context* ctx, const samhip_tensor* w, const sa
                            const samhip_tensor* y) {
     if (!ctx) return fail(SAMHIP_ERR_INVALID_ARGUMENT, "null context");
     if (!ctx->fixed_scratch) return fail(SAMHIP_ERR_DEVICE, "mul_mat_noalloc: no fixed scratch on this device");
+    FixedScratch& f = g_fixed[ctx->device];
+    std::lock_guard<std::mutex> lock(f.call);
+    if (int rc = set_device(ctx)) return rc;
+    // stream order behind the previous call on this device's scratch (not
+    // while capturing: a graph's own replays are the caller's to order)
+    if (!ctx->capturing) HIP_TRY(hipStreamWaitEvent(ctx->stream, f.last, 0), "hipStreamWaitEvent");
     void* const staging = ctx->staging;
     const size_t staging_bytes = ctx->staging_bytes;
     ctx->staging = ctx->fixed_scratch;
@@ -464,6 +487,7 @@ int samhip_mul_mat_noalloc(samhip_context* ctx, const samhip_tensor* w, const sa
     ctx->no_alloc = false;
     ctx->staging = staging;
     ctx->staging_bytes = staging_bytes;
+    if (!ctx->capturing) HIP_TRY(hipEventRecord(f.last, ctx->stream), "hipEventRecord");
     return rc;
 }
 
@@ -535,7 +559,7 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     }
     if (!tall && (M <= kFusedMaxM || small_w) && ctx->fused_skinny) {
         // one launch: activation packing, weight decode and product
-        const FusedPlan plan = fused_skinny_plan(M, N, K, ctx->fused_max_splits);
+        const FusedPlan plan = fused_skinny_plan(M, N, K, ctx->fused_max_splits, ctx->cus);
         if (int rc = ensure_staging(ctx, std::max<size_t>(plan.part_bytes, 256))) return rc;
         const char* variant = fused_skinny_variant(w->type);
         if (!variant) return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no kernel for weight type %d", w->type);
@@ -544,7 +568,7 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
                                      int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), static_cast<float*>(y->data),
                                      int64_t(y->nb[1] / 4), static_cast<float*>(ctx->staging), M, N, K,
                                      ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->fused_max_splits,
-                                     ctx->stream))
+                                     ctx->cus, ctx->stream))
                 return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no fused kernel for this shape");
             HIP_TRY(hipGetLastError(), "fused skinny launch");
             return SAMHIP_OK;

@@ -230,15 +230,19 @@ struct FusedPlan {
     int mt;               // 32-row activation tiles per row block (fused kernel)
     size_t part_bytes;
 };
-FusedPlan fused_skinny_plan(int M, int N, int K, int max_splits);
+FusedPlan fused_skinny_plan(int M, int N, int K, int max_splits, int cus);
 const char* fused_skinny_variant(int wtype);
 const char* launch_fused_skinny(int wtype, bool f16, const float* x, int64_t ldx, const void* w, int64_t w_stride,
                                 float* y, int64_t ldy, float* part, int M, int N, int K, int x86, int max_splits,
-                                hipStream_t stream);
+                                int cus, hipStream_t stream);
 
 // Strip skinny products (M < kStripMaxM): one launch per product while
 // K <= 1024 (four 256-wide chunks per workgroup), plus the split-K reduce
 // beyond; partial sums go through `part` (FusedPlan::part_bytes).
+// The dispatch counts work-items in 32 bits: a grid of 1024-thread
+// workgroups may hold at most this many.
+constexpr int64_t kMaxWorkgroups1024 = int64_t(0xffffffffu) / 1024;
+
 constexpr int kStripMaxM = 256;   // in blocks of 32 activation rows
 // Where the strip kernel measured faster than the fused one: Q8_0 weights
 // with K <= 1024 (one launch).  K-quant pieces are read with scattered

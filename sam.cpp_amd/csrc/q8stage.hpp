@@ -88,7 +88,12 @@ __device__ __forceinline__ int row_exponent(float rowmax) {
 
 __device__ __forceinline__ floatx4 load4f(const float* p) { return *reinterpret_cast<const floatx4*>(p); }
 // An integral float to int32 by the hardware conversion, which gives 0 for
-// NaN (and saturates out of range); ggml's nearest_int also packs NaN as 0.
+// NaN (and saturates out of range).  NaN -> code 0 is this library's
+// contract for a NaN activation in every Q8 packing: it is what ggml's
+// nearest_int (Q8_K) and its scalar Q8_0 reference rounding give on x86,
+// but not what ggml's AVX2 Q8_0 packing gives (its saturating packs turn
+// the conversion's 0x80000000 into -128), so for the x86 rounding mode it is
+// a deliberate choice, not parity with that SIMD code.
 __device__ __forceinline__ int cvt_i32_nan0(float r) {
     int q;
     asm("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(r));
@@ -155,7 +160,7 @@ __device__ __forceinline__ void quant8_codes(const floatx8& v, int lane, float& 
         for (int i = 0; i < 8; ++i) {
             const float s = v[i] * inv;
             const float r = X86 ? __builtin_rintf(s) : __builtin_roundf(s);
-            q[i] = r == r ? r : 0.f;   // a NaN activation packs as code 0, as in ggml's integer conversion
+            q[i] = r == r ? r : 0.f;   // a NaN activation packs as code 0 (this library's contract, above)
         }
     } else {
         // Q8_K: first element of largest magnitude in the 256-value block

@@ -604,8 +604,8 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
         float inv;
         if (X86) inv = amax != 0.f ? 127.f / amax : 0.f;
         else inv = d != 0.f ? 1.f / d : 0.f;
-        // four codes per dword: the hardware conversion (NaN -> 0, which is
-        // ggml's code for a NaN activation) and two byte permutes
+        // four codes per dword: the hardware conversion (NaN -> 0, this
+        // library's code for a NaN activation) and two byte permutes
         uint32_t packed[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -978,13 +978,12 @@ const char* launch_skinny(int wtype, const _Float16* a, int64_t lda, const float
 
 namespace samhip {
 
-constexpr int kFusedRoundWGs = 256;   // workgroups of one round on MI355X (one per CU)
-
-FusedPlan fused_skinny_plan(int M, int N, int K, int max_splits) {
+FusedPlan fused_skinny_plan(int M, int N, int K, int max_splits, int cus) {
     FusedPlan p{};
     p.rg = (N + FROWS - 1) / FROWS;
-    // rows per block: the fewest (32, 64 or 128) whose (row group, row
-    // block) grid still fits one round of kFusedRoundWGs workgroups, so the
+    const int round_wgs = std::max(1, cus);   // one round: a workgroup per CU
+    // rows per block: the fewest (32, 64, 96 or 128) whose (row group, row
+    // block) grid still fits one round of workgroups, so the
     // activation chunk is packed by as few workgroups as possible without a
     // second round.  Measured on MI355X against the earlier rule (64 or 256
     // workgroups wanted): the detector's 5184 image tokens on 256 x 256
@@ -993,12 +992,13 @@ FusedPlan fused_skinny_plan(int M, int N, int K, int max_splits) {
     // weights 6.4 us with 32-row blocks (112) instead of 8.6 with 64 (64).
     const int max_mt = std::min(4, (M + 31) / 32);
     p.mt = 1;
-    while (p.mt < max_mt && int64_t(p.rg) * ((M + 32 * p.mt - 1) / (32 * p.mt)) > kFusedRoundWGs) p.mt *= 2;
+    while (p.mt < max_mt && int64_t(p.rg) * ((M + 32 * p.mt - 1) / (32 * p.mt)) > round_wgs)
+        p.mt = std::min(2 * p.mt, max_mt);
     const int mb = (M + 32 * p.mt - 1) / (32 * p.mt);
     const int groups = p.rg * mb;
     const int nchunks = (K + CHUNK - 1) / CHUNK;
     const int S = std::min(std::min(nchunks, std::max(1, max_splits)),
-                           std::max(1, (kFusedRoundWGs + groups - 1) / groups));
+                           std::max(1, (round_wgs + groups - 1) / groups));
     p.cps = (nchunks + S - 1) / S;
     p.splits = (nchunks + p.cps - 1) / p.cps;
     p.part_bytes = p.splits > 1 ? size_t(p.splits) * size_t(M) * size_t(N) * 4 : 0;
@@ -1057,7 +1057,7 @@ const char* launch_q8_strip_i8(const float* x, int64_t ldx, const void* w, int64
     const int SL = 256 * slice_sb;
     const int RG = (N + 31) / 32, S = (K + SL - 1) / SL, MB = (M + 31) / 32;
     if (S > 1 && !part) return nullptr;
-    if (int64_t(RG) * S * MB > 0x7fffffff) return nullptr;
+    if (int64_t(RG) * S * MB > kMaxWorkgroups1024) return nullptr;
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     float* pt = S > 1 ? part : nullptr;
@@ -1108,7 +1108,7 @@ const char* launch_kq_strip_i8(int wtype, const float* x, int64_t ldx, const voi
     const int SK = slice_sb;
     const int RG = (N + 31) / 32, S = (K + 256 * SK - 1) / (256 * SK), MB = (M + 31) / 32;
     if (S > 1 && !part) return nullptr;
-    if (int64_t(RG) * S * MB > 0x7fffffff) return nullptr;
+    if (int64_t(RG) * S * MB > kMaxWorkgroups1024) return nullptr;
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     float* pt = S > 1 ? part : nullptr;
@@ -1138,9 +1138,9 @@ const char* fused_skinny_variant(int wtype) {
 
 const char* launch_fused_skinny(int wtype, bool f16, const float* x, int64_t ldx, const void* w, int64_t w_stride,
                                 float* y, int64_t ldy, float* part, int M, int N, int K, int x86, int max_splits,
-                                hipStream_t stream) {
+                                int cus, hipStream_t stream) {
     if (M < 1 || (M > kFusedMaxM && int64_t(N) * K > kFusedSmallW) || N < 1 || K < 32 || K % 32) return nullptr;
-    const FusedPlan p = fused_skinny_plan(M, N, K, max_splits);
+    const FusedPlan p = fused_skinny_plan(M, N, K, max_splits, cus);
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     switch (wtype) {

@@ -487,26 +487,23 @@ inline int32_t image_modular_quantized_tensor_type(const std::string& name, cons
     return SAMHIP_TYPE_F32;
 }
 
-// Canonical, strictly ordered, nonempty CSV of modules.
+// The accepted lists are exactly the nonempty subsequences of module_order()
+// joined by commas (15 of them): the list names each module at most once, in
+// that order.  Each candidate is spelled out from a 4-bit mask and compared
+// with the whole string.
 inline std::vector<std::string> parse_image_quantization_modules(const std::string& csv) {
     if (csv.empty()) throw std::runtime_error("schema-4 quantization module list is empty");
-    std::vector<std::string> out;
-    int previous = -1;
-    std::size_t begin = 0;
-    while (true) {
-        const std::size_t comma = csv.find(',', begin);
-        const std::string token = csv.substr(begin, comma == std::string::npos ? std::string::npos : comma - begin);
-        int index = -1;
-        for (int i = 0; i < 4; ++i)
-            if (token == module_order()[i]) index = i;
-        if (index <= previous)
-            throw std::runtime_error("schema-4 quantization modules must be a nonempty canonical CSV list");
-        previous = index;
-        out.push_back(token);
-        if (comma == std::string::npos) break;
-        begin = comma + 1;
+    for (unsigned mask = 1; mask < 16; ++mask) {
+        std::vector<std::string> picked;
+        std::string spelled;
+        for (unsigned i = 0; i < 4; ++i) {
+            if (!((mask >> i) & 1u)) continue;
+            picked.emplace_back(module_order()[i]);
+            spelled += (spelled.empty() ? "" : ",") + picked.back();
+        }
+        if (spelled == csv) return picked;
     }
-    return out;
+    throw std::runtime_error("schema-4 quantization modules must be a nonempty canonical CSV list");
 }
 
 }  // namespace policy

@@ -178,6 +178,15 @@ void test_policy() {
     CHECK(throws<std::runtime_error>([] { parse_image_quantization_modules("text,vision"); }, "canonical"));
     CHECK(throws<std::runtime_error>([] { parse_image_quantization_modules("vision,vision"); }, "canonical"));
     CHECK(throws<std::runtime_error>([] { parse_image_quantization_modules("vision,"); }, "canonical"));
+    CHECK(throws<std::runtime_error>([] { parse_image_quantization_modules(",vision"); }, "canonical"));
+    CHECK(throws<std::runtime_error>([] { parse_image_quantization_modules("vision,,text"); }, "canonical"));
+    CHECK(throws<std::runtime_error>([] { parse_image_quantization_modules("Vision"); }, "canonical"));
+    CHECK(throws<std::runtime_error>([] { parse_image_quantization_modules("vision text"); }, "canonical"));
+    CHECK(throws<std::runtime_error>([] { parse_image_quantization_modules("decoder,fusion"); }, "canonical"));
+    CHECK(parse_image_quantization_modules("vision,text,fusion,decoder") ==
+          (std::vector<std::string>{"vision", "text", "fusion", "decoder"}));
+    CHECK(parse_image_quantization_modules("decoder") == (std::vector<std::string>{"decoder"}));
+    CHECK(parse_image_quantization_modules("text,decoder") == (std::vector<std::string>{"text", "decoder"}));
 }
 
 void test_status_mapping_without_device() {

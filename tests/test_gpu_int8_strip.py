@@ -125,7 +125,8 @@ def test_int8_strip_repeats_and_replays(samhip, oracle):
 
 @pytest.mark.parametrize("rounding", ["x86", "ref"])
 def test_int8_strip_nan_activations(samhip, oracle, rounding):
-    """A NaN activation packs as code 0 (ggml's nearest_int gives 0 for NaN)
+    """A NaN activation packs as code 0 (the library's contract, as ggml's
+    nearest_int gives; not ggml's AVX2 Q8_0 packing, which would give -128)
     and leaves its block's scale to the finite values: single NaNs, a NaN
     run across blocks and a whole NaN row, against the oracle."""
     say("case int8 strip NaN", rounding)

@@ -236,7 +236,8 @@ def test_mul_mat_q8_0_k32(gpu_ctx, f16_ctx, oracle):
 
 def test_nan_activations_pack_as_code_zero(gpu_ctx, oracle, samhip):
     """A NaN activation packs as code 0 in Q8_0 (both roundings) and Q8_K
-    blocks, as ggml's nearest_int gives for Q8_K; the block scale comes from
+    blocks (the library's contract, as ggml's nearest_int gives for Q8_K; not
+    parity with ggml's AVX2 Q8_0 packing); the block scale comes from
     the other values.  Wire rows are bit-exact with the oracle, and products
     on the staged (tall) and fused (skinny) paths match its native path."""
     say("case NaN activations")
@@ -287,6 +288,23 @@ def test_mul_mat_tall_path_tails(gpu_ctx, f16_ctx, oracle, qtype):
         yn = gpu_ctx.matmul(qtype, w, x, w_row_offset=off, w_rows=131, x_row_stride=stride)
         yf = f16_ctx.matmul(qtype, w, x, w_row_offset=off, w_rows=131, x_row_stride=stride)
         _check_product(oracle, qtype, w[off:off + 131], x, yn, yf)
+
+
+@pytest.mark.parametrize("k", [800, 1056])
+def test_mul_mat_tall_k_not_multiple_of_128(gpu_ctx, f16_ctx, oracle, k):
+    """M >= 256 with K % 128 != 0 (only Q8_0 rows can be that wide: the
+    K-quants need K % 256 == 0): the pipelined GEMM does not take it, so the
+    staged activations meet gemm_kernel, which decodes the packed weight
+    while staging it into LDS.  M and N tails, fully compared."""
+    say("case mul_mat tall fallback", k)
+    rng = np.random.default_rng(31 + k)
+    w = oracle.quantize(oracle.Q8_0, (rng.standard_normal((259, k)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((300, k)).astype(np.float32)
+    yn = gpu_ctx.matmul(8, w, x)
+    assert gpu_ctx.query().kernel_variant == b"gemm_f16mfma_128x128x32_q8_0"
+    yf = f16_ctx.matmul(8, w, x)
+    assert f16_ctx.query().kernel_variant == b"gemm_f16mfma_128x128x32_q8_0"
+    _check_product(oracle, 8, w, x, yn, yf, DECODED_TOL)
 
 
 SKINNY_CASES = [(1, 96, 256), (32, 257, 1024), (33, 300, 512), (64, 64, 256), (65, 33, 256), (201, 256, 512),

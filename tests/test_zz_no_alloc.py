@@ -80,3 +80,40 @@ def test_noalloc_rejects_products_beyond_the_scratch(samhip, oracle):
         assert rc == samhip.ERR_INVALID_ARGUMENT
         assert "scratch" in samhip.last_error()
         assert (ctx.download(yb, (m, n), np.float32) == 3.0).all()
+
+
+def test_noalloc_calls_from_two_contexts_run_in_order(samhip, oracle):
+    """Two contexts (two streams) on one thread call the no-allocation entry
+    point back to back with no synchronization between: the second call's
+    staging would overwrite the first one's in the shared array if they
+    overlapped on the GPU.  The library's per-device event puts them in
+    order, so both match their own samhip_mul_mat results bit for bit."""
+    cases = [("Q8_0", 5184, 1024, 4736), ("Q4_K", 5184, 4736, 1024), ("Q8_0", 2048, 3072, 1024)]
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE, samhip.ROUND_X86) as ca, \
+            samhip.Context(0, samhip.COMPUTE_Q8_NATIVE, samhip.ROUND_X86) as cb:
+        runs = []
+        for i, (tname, m, n, k) in enumerate(cases):
+            ctx = (ca, cb)[i % 2]
+            qtype = getattr(samhip, tname)
+            w, x = _case(oracle, 500 + i, qtype, m, n, k)
+            wb, xb = ctx.upload(w), ctx.upload(x)
+            ya, yb = ctx.alloc(m * n * 4), ctx.alloc(m * n * 4)
+            W = samhip.tensor(qtype, k, n, wb.ptr)
+            X = samhip.tensor(samhip.F32, k, m, xb.ptr)
+            Ya, Yb = samhip.tensor(samhip.F32, n, m, ya.ptr), samhip.tensor(samhip.F32, n, m, yb.ptr)
+            ctx.mul_mat(W, X, Ya)
+            ctx.synchronize()
+            runs.append((ctx, W, X, Ya, Yb, (wb, xb, ya, yb), m, n))
+        for rep in range(2):
+            say("case noalloc two contexts, pass", rep)
+            for ctx, W, X, _, Yb, _, _, _ in (runs if rep == 0 else runs[::-1]):
+                samhip.check(samhip.lib().samhip_mul_mat_noalloc(ctx.handle, ctypes.byref(W), ctypes.byref(X),
+                                                                 ctypes.byref(Yb)))
+            for ctx, _, _, _, _, bufs, m, n in runs:
+                a = ctx.download(bufs[2], (m, n), np.float32)
+                b = ctx.download(bufs[3], (m, n), np.float32)
+                assert np.isfinite(a).all()
+                assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        for run in runs:
+            for buf in run[5]:
+                buf.free()
