@@ -130,6 +130,7 @@ struct samhip_context {
     int attn_splits = 0;        // SAMHIP_ATTN_SPLITS: key splits of the attention kernel (0: by grid size)
     int fused_max_splits = 16;  // SAMHIP_FUSED_MAX_SPLITS: cap on the fused kernel's K splits
     bool check_activations = false;   // samhip_context_set_activation_check
+    bool tall_small = true;     // SAMHIP_TALL_SMALL=0 keeps M >= 256 products with small Q8_0 weights on the fused kernel
     int int8_strip = 1;         // SAMHIP_INT8_STRIP: 0 keeps M < 256 products on the fp16 kernels; 1 sends Q8_0
                                 // ones, and K-quant ones where that measured faster, to the int8 kernels; 2
                                 // sends every K-quant one there as well
@@ -343,6 +344,7 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
     ctx->attn_splits = std::max(0, env_int("SAMHIP_ATTN_SPLITS", 0));
     ctx->fused_max_splits = std::max(1, env_int("SAMHIP_FUSED_MAX_SPLITS", 16));
     ctx->int8_strip = env_int("SAMHIP_INT8_STRIP", 1);
+    ctx->tall_small = env_int("SAMHIP_TALL_SMALL", 1) != 0;
     const int cfg = env_int("SAMHIP_GEMM_CONFIG", -1);
     ctx->gemm_cfg = (cfg >= 0 && cfg < gemm_f16_config_count()) ? cfg : -1;
     *out = ctx;
@@ -506,6 +508,25 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K) && !small_w;
     const bool kquant = (w->type == T_Q4_K || w->type == T_Q5_K || w->type == T_Q6_K) &&
                         (ctx->int8_strip == 2 || kq_strip_i8_preferred(w->type, M, N, K, ctx->cus));
+    if (small_w && M >= kStripMaxM && w->type == T_Q8_0 && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE &&
+        ctx->tall_small && tall_small_i8_supported(M, N, K, w->data, int64_t(w->nb[1]))) {
+        // many rows against a weight that fits in LDS: exact int8, one
+        // workgroup per CU, no staging
+        const char* variant = tall_small_i8_variant();
+        int rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
+            if (!launch_tall_small_i8(static_cast<const float*>(x->data), int64_t(x->nb[1] / 4), w->data,
+                                      int64_t(w->nb[1]), static_cast<float*>(y->data), int64_t(y->nb[1] / 4), M, N, K,
+                                      ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->cus, ctx->stream))
+                return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no small-weight kernel for this shape");
+            HIP_TRY(hipGetLastError(), "small-weight launch");
+            return SAMHIP_OK;
+        });
+        if (rc) return rc;
+        ctx->info.mul_mat_calls++;
+        ctx->info.skinny_launches++;
+        std::snprintf(ctx->info.kernel_variant, sizeof(ctx->info.kernel_variant), "%s", variant);
+        return SAMHIP_OK;
+    }
     if (!tall && M < kStripMaxM && (w->type == T_Q8_0 || kquant) && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE &&
         ctx->int8_strip && ctx->fused_skinny) {
         // exact int8 block dots in blocks of 32 activation rows (the text

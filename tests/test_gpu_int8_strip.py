@@ -206,3 +206,47 @@ def test_kquant_int8_default_routing(samhip, oracle):
             tname = {oracle.Q4_K: "q4_k", oracle.Q5_K: "q5_k", oracle.Q6_K: "q6_k"}[qt]
             assert name == ("skinny_i8mfma_" if exact else "skinny_fused_") + tname, (name, m, n, k)
             assert max_row_rel_l2(y, oracle.mul_mat_native(qt, w, x)) <= (EXACT if exact else 1e-3)
+
+
+# many activation rows against a Q8_0 weight that fits in LDS (N, K <= 256):
+# the fusion encoder's and decoder's image tokens (M = 5184) on 256x256
+# weights, a batch of 8 images (several 32-row steps per workgroup), ragged
+# M, N and K, short rows, an unaligned activation stride
+TALL_SMALL = [(5184, 256, 256), (41472, 256, 256), (300, 100, 224), (1000, 256, 32), (257, 33, 64),
+              (4097, 255, 256), (5184, 64, 128)]
+
+
+@pytest.mark.parametrize("rounding", ["x86", "ref"])
+@pytest.mark.parametrize("shape", TALL_SMALL, ids=lambda s: "x".join(map(str, s)))
+def test_tall_small_weight_int8_matches_native(samhip, oracle, shape, rounding):
+    m, n, k = shape
+    say("case tall small-weight int8", shape, rounding)
+    gmode = samhip.ROUND_X86 if rounding == "x86" else samhip.ROUND_REF
+    cmode = oracle.ROUND_X86 if rounding == "x86" else oracle.ROUND_REF
+    rng = np.random.default_rng(m + 3 * n + k)
+    w = oracle.quantize(oracle.Q8_0, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    x = (rng.standard_normal((m, k)) * np.exp(rng.uniform(-4, 4, (m, 1)))).astype(np.float32)
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE, gmode) as ctx:
+        y = ctx.matmul(samhip.Q8_0, w, x, x_row_stride=k + 1 if m % 2 else None)
+        assert ctx.query().kernel_variant == b"tall_small_i8mfma_q8_0"
+        again = ctx.matmul(samhip.Q8_0, w, x)
+    ref = oracle.mul_mat_native(oracle.Q8_0, w, x, cmode)
+    err = max_row_rel_l2(y, ref)
+    say(f"  max row rel L2 {err:.2e}")
+    assert np.isfinite(y).all() and err <= EXACT
+    assert np.array_equal(y, again)
+
+
+def test_tall_small_weight_views_of_in_projection(samhip, oracle):
+    """q / k / v as row-offset views of a fused [3 x 256, 256] in-projection
+    (fusion_encoder.hpp:63-137), each against the oracle on its rows."""
+    say("case tall small-weight views")
+    rng = np.random.default_rng(91)
+    w = oracle.quantize(oracle.Q8_0, (rng.standard_normal((768, 256)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((5184, 256)).astype(np.float32)
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE, samhip.ROUND_X86) as ctx:
+        for s in range(3):
+            y = ctx.matmul(samhip.Q8_0, w, x, w_row_offset=256 * s, w_rows=256)
+            assert ctx.query().kernel_variant == b"tall_small_i8mfma_q8_0"
+            ref = oracle.mul_mat_native(oracle.Q8_0, w[256 * s:256 * (s + 1)], x, oracle.ROUND_X86)
+            assert max_row_rel_l2(y, ref) <= EXACT
