@@ -244,10 +244,10 @@ const char* launch_fused_skinny(int wtype, bool f16, const float* x, int64_t ldx
 constexpr int64_t kMaxWorkgroups1024 = int64_t(0xffffffffu) / 1024;
 
 // Many activation rows against a Q8_0 weight that fits in LDS whole (the
-// fusion / decoder image-token projections): exact int8, one workgroup per
-// CU with an even run of rows.  The packed rows must be contiguous
-// (w_stride = row bytes) and 16-byte aligned.
-constexpr int kTallSmallMaxN = 256, kTallSmallMaxK = 256;
+// fusion / decoder image-token projections, K = 256, N <= 256): exact int8,
+// one workgroup per CU with an even run of rows.  The packed rows must be
+// contiguous (w_stride = row bytes) and 16-byte aligned.
+constexpr int kTallSmallMaxN = 256, kTallSmallK = 256;
 bool tall_small_i8_supported(int M, int N, int K, const void* w, int64_t w_stride);
 const char* tall_small_i8_variant();
 const char* launch_tall_small_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy,

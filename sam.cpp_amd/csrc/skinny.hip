@@ -675,92 +675,86 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
 }
 
 // ---------------------------------------------------------------------------
-// Many activation rows against a small Q8_0 weight (N <= 256, K <= 256: the
+// Many activation rows against a small Q8_0 weight (N <= 256, K = 256: the
 // fusion encoder's and decoder's image-token projections, M = 5184), exact
 // int8 as the strip kernel but shaped for a weight that fits in LDS whole:
 //  1. one workgroup per CU, each with an even run of rows (M / grid: 20 or
 //     21 of 5184), so every CU streams the same number of activation bytes;
-//  2. per 32 rows of the run, two threads per 32-value block load its
-//     values (requested first: they come from HBM), then the packed weight
-//     (N rows of K/32 34-byte blocks, at most 68 KB) goes to LDS once by
-//     direct-to-LDS loads, 1 KB per wave instruction, while the threads pack
-//     their values to Q8_0 codes and the block's fp16 scale (ggml's
-//     from_float, bit-exact; the block maximum meets on the lane pair);
-//  3. wave w takes column tiles w (and w + 8) of 32 weight rows: every
-//     32-value block's v_mfma_i32_32x32x32_i8 is issued before the first
-//     epilogue, then acc = fma(d_w d_x, dot, acc) in K order (ggml's
-//     vec_dot_q8_0_q8_0 order of the block sums), and the 32x32 tile goes
-//     straight from the accumulators to Y (a store covers two 128-byte row
-//     segments; stores past the run or past N are dropped by the bounds of
-//     a buffer clipped to the run).
+//  2. waves 0-3 load the run's next 32 activation rows (a 32-value block per
+//     thread) and pack them to Q8_0 codes and the block's fp16 scale (ggml's
+//     from_float, bit-exact); meanwhile waves 4-7 bring 64 weight rows each
+//     into LDS by direct-to-LDS loads (1 KB per wave instruction; a row is
+//     272 bytes, so a wave's rows are 17 whole KB) and each lane re-lays its
+//     row in place: the 32 codes of every block 16-byte aligned (a block is
+//     34 bytes, so its codes sit 2 bytes off a dword in the packed row) and
+//     the scales as floats, so every MFMA operand is one 16-byte LDS read;
+//  3. wave w takes column tile w of 32 weight rows: all 8 blocks'
+//     v_mfma_i32_32x32x32_i8 are issued before the first epilogue, then
+//     acc = fma(d_w d_x, dot, acc) in K order (ggml's vec_dot_q8_0_q8_0
+//     order of the block sums), and the 32x32 tile goes straight from the
+//     accumulators to Y (a store covers two 128-byte row segments; stores
+//     past the rows or past N are dropped by the bounds of a buffer clipped
+//     to the rows).
 // Timed with per-wave stamps on MI355X at M = 5184, N = K = 256: 9.7 us per
-// launch with 4 waves and one MFMA at a time, 7.3 us with this shape.
+// launch with 4 waves reading the packed rows and one MFMA at a time, 8.2
+// with 8 waves, 6.6 with the weight re-laid by a separate pass.
 // ---------------------------------------------------------------------------
-constexpr int TS_WBYTES = kTallSmallMaxN * (kTallSmallMaxK / 32) * 34;   // 69632
-constexpr int TS_XLD = kTallSmallMaxK + 16;                              // bytes per LDS code row
-constexpr int TS_NB = kTallSmallMaxK / 32;                               // blocks per row, at most
+constexpr int TS_RB = (kTallSmallK / 32) * 34;          // 272 bytes per packed row
+constexpr int TS_XLD = kTallSmallK + 16;                 // bytes per LDS code row
+constexpr int TS_NB = kTallSmallK / 32;                  // 8 blocks per row
+static_assert(TS_RB % 16 == 0 && 64 * TS_RB % 1024 == 0, "64 packed rows are whole KB of 16-byte aligned rows");
 
 template <bool X86, bool XVEC>
 __global__ __launch_bounds__(512) void tall_small_i8_kernel(const float* __restrict__ X, int64_t ldx,
                                                             const uint8_t* __restrict__ W, float* __restrict__ Y,
-                                                            int64_t ldy, int M, int N, int K) {
+                                                            int64_t ldy, int M, int N) {
 #pragma clang fp contract(off)
-    __shared__ __attribute__((aligned(16))) uint8_t Wl[TS_WBYTES + 16];
+    __shared__ __attribute__((aligned(16))) uint8_t Wl[kTallSmallMaxN * TS_RB];   // packed, then re-laid rows
+    __shared__ __attribute__((aligned(16))) float Wd[TS_NB][kTallSmallMaxN];      // weight block scales
     __shared__ __attribute__((aligned(16))) int8_t Xq[32 * TS_XLD];
     __shared__ __attribute__((aligned(16))) float Xd[TS_NB][32];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nb = K / 32, rb = 34 * nb, wbytes = N * rb;
     const int G = gridDim.x, g = blockIdx.x;
     const int r_begin = int(int64_t(M) * g / G), r_end = int(int64_t(M) * (g + 1) / G);
     const int col = lane & 31, h = lane >> 5;
-    const int ntile = (N + 31) / 32;
-    // quantizer role: row m of the 32, block b, half hf of the block
-    const int qm = tid >> 4, qb = (tid >> 1) & 7, hf = tid & 1;
-    const uint32_t* wdw = reinterpret_cast<const uint32_t*>(Wl);
+    const int n = wave * 32 + col;          // this lane's weight row in the products
+    const int nr = min(n, N - 1);
     for (int rt = r_begin; rt < r_end; rt += 32) {
         const int rows = min(32, r_end - rt);
-        float v[16];
-        if (qm < rows && qb < nb) {
-            const float* xr = X + int64_t(rt + qm) * ldx + 32 * qb + 16 * hf;
-            if (XVEC) {
+        if (wave < 4) {
+            // activation row qm, block qb -> Q8_0 codes and scale (zeros past the rows)
+            const int qm = tid >> 3, qb = tid & 7;
+            float v[32];
+            if (qm < rows) {
+                const float* xr = X + int64_t(rt + qm) * ldx + 32 * qb;
+                if (XVEC) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const floatx4 t = load4f(xr + 4 * i);
-                    v[4 * i] = t[0];
-                    v[4 * i + 1] = t[1];
-                    v[4 * i + 2] = t[2];
-                    v[4 * i + 3] = t[3];
+                    for (int i = 0; i < 8; ++i) {
+                        const floatx4 t = load4f(xr + 4 * i);
+                        v[4 * i] = t[0];
+                        v[4 * i + 1] = t[1];
+                        v[4 * i + 2] = t[2];
+                        v[4 * i + 3] = t[3];
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 32; ++i) v[i] = xr[i];
                 }
             } else {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) v[i] = xr[i];
+                for (int i = 0; i < 32; ++i) v[i] = 0.f;
             }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = 0.f;
-        }
-        if (rt == r_begin) {
-            // the packed weight into LDS (requests past wbytes read as zero)
-            const __amdgpu_buffer_rsrc_t wd =
-                __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), 0, uint32_t(wbytes), 0x00020000);
-            const int chunks = (wbytes + 1023) / 1024;
-            for (int c = wave; c < chunks; c += 8)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(wd, (__attribute__((address_space(3))) void*)(Wl + c * 1024),
-                                                         16, uint32_t(c * 1024 + 16 * lane), 0, 0, 0);
-        }
-        {
             float amax = 0.f;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
-            amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+            for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
             const float d = amax / 127.f;
             float inv;
             if (X86) inv = amax != 0.f ? 127.f / amax : 0.f;
             else inv = d != 0.f ? 1.f / d : 0.f;
-            uint32_t packed[4];
+            uint32_t packed[8];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < 8; ++i) {
                 uint32_t q[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -771,37 +765,61 @@ __global__ __launch_bounds__(512) void tall_small_i8_kernel(const float* __restr
                 const uint32_t hi = __builtin_amdgcn_perm(q[3], q[2], 0x0c0c0400u);
                 packed[i] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
             }
-            if (qb < nb) {
-                *reinterpret_cast<u32x4*>(&Xq[qm * TS_XLD + 32 * qb + 16 * hf]) =
-                    u32x4{packed[0], packed[1], packed[2], packed[3]};
-                if (hf == 0) Xd[qb][qm] = half_bits_to_float(float_to_half_bits(d));   // the stored fp16 scale
+            u32x4* dst = reinterpret_cast<u32x4*>(&Xq[qm * TS_XLD + 32 * qb]);
+            dst[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
+            dst[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
+            Xd[qb][qm] = half_bits_to_float(float_to_half_bits(d));   // the stored fp16 scale
+        } else if (rt == r_begin) {
+            // weight rows 64 v .. 64 v + 63 (requests past N rows read as zero)
+            const int v = wave - 4, wrow = 64 * v + lane;
+            const __amdgpu_buffer_rsrc_t wd =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), 0, uint32_t(N * TS_RB), 0x00020000);
+#pragma unroll
+            for (int c = 0; c < 64 * TS_RB / 1024; ++c)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    wd, (__attribute__((address_space(3))) void*)(Wl + 64 * v * TS_RB + c * 1024), 16,
+                    uint32_t(64 * v * TS_RB + c * 1024 + 16 * lane), 0, 0, 0);
+            __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's rows have landed
+            __builtin_amdgcn_wave_barrier();
+            if (wrow < N) {
+                // the lane's packed row in registers, then its blocks' codes
+                // back 16-byte aligned (block b at byte 32 b) and the scales out
+                uint32_t rw[TS_RB / 4 + 1];
+#pragma unroll
+                for (int i = 0; i < TS_RB / 16; ++i) {
+                    const u32x4 t = *reinterpret_cast<const u32x4*>(Wl + wrow * TS_RB + 16 * i);
+                    rw[4 * i] = t[0];
+                    rw[4 * i + 1] = t[1];
+                    rw[4 * i + 2] = t[2];
+                    rw[4 * i + 3] = t[3];
+                }
+                rw[TS_RB / 4] = 0u;
+#pragma unroll
+                for (int b = 0; b < TS_NB; ++b) {
+                    const int sb = 34 * b, cb = sb + 2, cd = cb >> 2, cs = cb & 3;
+                    Wd[b][wrow] = half_bits_to_float((rw[sb >> 2] >> (8 * (sb & 3))) & 0xffffu);
+                    const u32x4 lo{funnel_bytes(rw[cd + 1], rw[cd], cs), funnel_bytes(rw[cd + 2], rw[cd + 1], cs),
+                                   funnel_bytes(rw[cd + 3], rw[cd + 2], cs), funnel_bytes(rw[cd + 4], rw[cd + 3], cs)};
+                    const u32x4 hi{funnel_bytes(rw[cd + 5], rw[cd + 4], cs), funnel_bytes(rw[cd + 6], rw[cd + 5], cs),
+                                   funnel_bytes(rw[cd + 7], rw[cd + 6], cs), funnel_bytes(rw[cd + 8], rw[cd + 7], cs)};
+                    u32x4* dst = reinterpret_cast<u32x4*>(Wl + wrow * TS_RB + 32 * b);
+                    dst[0] = lo;
+                    dst[1] = hi;
+                }
             }
         }
-        if (rt == r_begin) __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): the weight has landed in LDS
         __syncthreads();
-        // output rows of this step: a buffer clipped to them
-        const __amdgpu_buffer_rsrc_t yd =
-            __builtin_amdgcn_make_buffer_rsrc(Y + int64_t(rt) * ldy, 0, uint32_t(((rows - 1) * ldy + N) * 4), 0x00020000);
-        for (int ct = wave; ct < ntile; ct += 8) {
-            const int n = ct * 32 + col;
-            const int nr = min(n, N - 1);
+        // column tile `wave` of 32 weight rows against the 32 activation rows
+        if (wave * 32 < N) {
+            const __amdgpu_buffer_rsrc_t yd = __builtin_amdgcn_make_buffer_rsrc(
+                Y + int64_t(rt) * ldy, 0, uint32_t(((rows - 1) * ldy + N) * 4), 0x00020000);
             const i32x16 zero = {0};
             i32x16 dots[TS_NB];
-            float dws[TS_NB];
 #pragma unroll
             for (int b = 0; b < TS_NB; ++b) {
-                if (b < nb) {
-                    const i32x4 a = *reinterpret_cast<const i32x4*>(&Xq[col * TS_XLD + 32 * b + 16 * h]);
-                    const int sb = nr * rb + 34 * b, cb = sb + 2 + 16 * h;
-                    const int cd = cb >> 2, cs = cb & 3;
-                    const uint32_t c0 = wdw[cd], c1 = wdw[cd + 1], c2 = wdw[cd + 2], c3 = wdw[cd + 3];
-                    const uint32_t c4 = cs ? wdw[cd + 4] : 0u;
-                    const u32x4 wq{funnel_bytes(c1, c0, cs), funnel_bytes(c2, c1, cs), funnel_bytes(c3, c2, cs),
-                                   funnel_bytes(c4, c3, cs)};
-                    dws[b] = half_bits_to_float((wdw[sb >> 2] >> (8 * (sb & 3))) & 0xffffu);
-                    dots[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
-                        a, i32x4{int(wq[0]), int(wq[1]), int(wq[2]), int(wq[3])}, zero, 0, 0, 0);
-                }
+                const i32x4 a = *reinterpret_cast<const i32x4*>(&Xq[col * TS_XLD + 32 * b + 16 * h]);
+                const i32x4 w = *reinterpret_cast<const i32x4*>(Wl + nr * TS_RB + 32 * b + 16 * h);
+                dots[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, w, zero, 0, 0, 0);
             }
             // element r: activation row 8 (r / 4) + 4 h + r % 4, weight row n
             floatx16 acc;
@@ -809,14 +827,13 @@ __global__ __launch_bounds__(512) void tall_small_i8_kernel(const float* __restr
             for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 #pragma unroll
             for (int b = 0; b < TS_NB; ++b) {
-                if (b < nb) {
+                const float dw = Wd[b][nr];
 #pragma unroll
-                    for (int qd = 0; qd < 4; ++qd) {
-                        const floatx4 dx = *reinterpret_cast<const floatx4*>(&Xd[b][8 * qd + 4 * h]);
+                for (int qd = 0; qd < 4; ++qd) {
+                    const floatx4 dx = *reinterpret_cast<const floatx4*>(&Xd[b][8 * qd + 4 * h]);
 #pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            acc[4 * qd + i] = __builtin_fmaf(dws[b] * dx[i], float(dots[b][4 * qd + i]), acc[4 * qd + i]);
-                    }
+                    for (int i = 0; i < 4; ++i)
+                        acc[4 * qd + i] = __builtin_fmaf(dw * dx[i], float(dots[b][4 * qd + i]), acc[4 * qd + i]);
                 }
             }
             const uint32_t base = n < N ? uint32_t(4 * h * ldy + n) * 4 : 0x80000000u;
@@ -1286,21 +1303,21 @@ const char* launch_kq_strip_i8(int wtype, const float* x, int64_t ldx, const voi
 const char* tall_small_i8_variant() { return "tall_small_i8mfma_q8_0"; }
 
 bool tall_small_i8_supported(int M, int N, int K, const void* w, int64_t w_stride) {
-    return M >= 1 && N >= 1 && N <= kTallSmallMaxN && K >= 32 && K <= kTallSmallMaxK && K % 32 == 0 &&
-           w_stride == int64_t(K / 32) * 34 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+    return M >= 1 && N >= 1 && N <= kTallSmallMaxN && K == kTallSmallK && w_stride == TS_RB &&
+           reinterpret_cast<uintptr_t>(w) % 16 == 0;
 }
 
 const char* launch_tall_small_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy,
                                  int M, int N, int K, int x86, int cus, hipStream_t stream) {
     if (!tall_small_i8_supported(M, N, K, w, w_stride)) return nullptr;
+    if (int64_t(M) * ldy * 4 > 0x7fffffff) return nullptr;   // 32-bit output offsets
     // one workgroup per CU, each with an even run of rows (at least 16)
     const int grid = std::max(1, std::min(cus, (M + 15) / 16));
-    if (int64_t(M) * ldy * 4 > 0x7fffffff) return nullptr;   // 32-bit output offsets
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
 #define SAMHIP_TS(X86V, XV)                                                                                          \
     hipLaunchKernelGGL((tall_small_i8_kernel<X86V, XV>), dim3(unsigned(grid)), dim3(512), 0, stream, x, ldx, wb, y, \
-                       ldy, M, N, K)
+                       ldy, M, N)
     if (x86) {
         if (xvec) SAMHIP_TS(true, true); else SAMHIP_TS(true, false);
     } else {

@@ -208,12 +208,12 @@ def test_kquant_int8_default_routing(samhip, oracle):
             assert max_row_rel_l2(y, oracle.mul_mat_native(qt, w, x)) <= (EXACT if exact else 1e-3)
 
 
-# many activation rows against a Q8_0 weight that fits in LDS (N, K <= 256):
-# the fusion encoder's and decoder's image tokens (M = 5184) on 256x256
-# weights, a batch of 8 images (several 32-row steps per workgroup), ragged
-# M, N and K, short rows, an unaligned activation stride
-TALL_SMALL = [(5184, 256, 256), (41472, 256, 256), (300, 100, 224), (1000, 256, 32), (257, 33, 64),
-              (4097, 255, 256), (5184, 64, 128)]
+# many activation rows against a Q8_0 weight that fits in LDS (K = 256,
+# N <= 256): the fusion encoder's and decoder's image tokens (M = 5184) on
+# 256x256 weights, a batch of 8 images (several 32-row steps per
+# workgroup), ragged M and N, an unaligned activation stride
+TALL_SMALL = [(5184, 256, 256), (41472, 256, 256), (300, 100, 256), (1000, 255, 256), (257, 33, 256),
+              (4097, 17, 256), (5184, 64, 256), (256, 200, 256)]
 
 
 @pytest.mark.parametrize("rounding", ["x86", "ref"])
@@ -235,6 +235,19 @@ def test_tall_small_weight_int8_matches_native(samhip, oracle, shape, rounding):
     say(f"  max row rel L2 {err:.2e}")
     assert np.isfinite(y).all() and err <= EXACT
     assert np.array_equal(y, again)
+
+
+def test_tall_small_weight_other_widths_take_the_fused_kernel(samhip, oracle):
+    """K other than 256 keeps the fused kernel (the small-weight kernel holds
+    256-value rows only)."""
+    rng = np.random.default_rng(92)
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE, samhip.ROUND_X86) as ctx:
+        for n, k in ((100, 224), (256, 128)):
+            w = oracle.quantize(oracle.Q8_0, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+            x = rng.standard_normal((1000, k)).astype(np.float32)
+            y = ctx.matmul(samhip.Q8_0, w, x)
+            assert ctx.query().kernel_variant.startswith(b"skinny_fused")
+            assert max_row_rel_l2(y, oracle.mul_mat_native(oracle.Q8_0, w, x, oracle.ROUND_X86)) <= 1e-3
 
 
 def test_tall_small_weight_views_of_in_projection(samhip, oracle):
