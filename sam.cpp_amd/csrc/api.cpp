@@ -130,6 +130,7 @@ struct samhip_context {
     int attn_splits = 0;        // SAMHIP_ATTN_SPLITS: key splits of the attention kernel (0: by grid size)
     int fused_max_splits = 16;  // SAMHIP_FUSED_MAX_SPLITS: cap on the fused kernel's K splits
     bool check_activations = false;   // samhip_context_set_activation_check
+    bool tall_int8 = false;     // SAMHIP_TALL_INT8=1: tall Q8_0 products on the exact int8 GEMM
     bool tall_small = true;     // SAMHIP_TALL_SMALL=0 keeps M >= 256 products with small Q8_0 weights on the fused kernel
     int int8_strip = 1;         // SAMHIP_INT8_STRIP: 0 keeps M < 256 products on the fp16 kernels; 1 sends Q8_0
                                 // ones, and K-quant ones where that measured faster, to the int8 kernels; 2
@@ -345,6 +346,7 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
     ctx->fused_max_splits = std::max(1, env_int("SAMHIP_FUSED_MAX_SPLITS", 16));
     ctx->int8_strip = env_int("SAMHIP_INT8_STRIP", 1);
     ctx->tall_small = env_int("SAMHIP_TALL_SMALL", 1) != 0;
+    ctx->tall_int8 = env_int("SAMHIP_TALL_INT8", 0) != 0;
     const int cfg = env_int("SAMHIP_GEMM_CONFIG", -1);
     ctx->gemm_cfg = (cfg >= 0 && cfg < gemm_f16_config_count()) ? cfg : -1;
     *out = ctx;
@@ -597,6 +599,29 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
         if (rc) return rc;
         ctx->info.mul_mat_calls++;
         ctx->info.skinny_launches++;
+        std::snprintf(ctx->info.kernel_variant, sizeof(ctx->info.kernel_variant), "%s", variant);
+        return SAMHIP_OK;
+    }
+    if (M >= ctx->tall_m && !small_w && w->type == T_Q8_0 && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE &&
+        ctx->tall_int8 && gemm_i8_supported(M, N, K)) {
+        // exact: int8 codes and F32 block scales for both operands, int8 MFMA
+        if (int rc = ensure_staging(ctx, gemm_i8_staging_bytes(M, N, K))) return rc;
+        const char* variant = gemm_i8_variant();
+        int rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
+            const char* prep = nullptr;
+            if (!launch_gemm_i8(static_cast<const float*>(x->data), int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]),
+                                static_cast<float*>(y->data), int64_t(y->nb[1] / 4), M, N, K,
+                                ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->staging, ctx->stream, &prep))
+                return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no int8 GEMM for this shape");
+            HIP_TRY(hipGetLastError(), "int8 GEMM launch");
+            return SAMHIP_OK;
+        });
+        if (rc) return rc;
+        ctx->info.mul_mat_calls++;
+        ctx->info.activation_launches++;
+        ctx->info.gemm_launches++;
+        ctx->info.activation_payload_peak_bytes =
+            std::max<uint64_t>(ctx->info.activation_payload_peak_bytes, uint64_t(M) * K + uint64_t(M) * (K / 32) * 4);
         std::snprintf(ctx->info.kernel_variant, sizeof(ctx->info.kernel_variant), "%s", variant);
         return SAMHIP_OK;
     }

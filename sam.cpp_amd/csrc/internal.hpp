@@ -253,6 +253,17 @@ const char* tall_small_i8_variant();
 const char* launch_tall_small_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy,
                                  int M, int N, int K, int x86, int cus, hipStream_t stream);
 
+// Exact tall products for Q8_0 weights (gemm_i8.hip): activations and the
+// weight split per call into int8 codes and F32 block scales (staging of
+// gemm_i8_staging_bytes), then an int8-MFMA GEMM with ggml's per-block
+// scaling in K order.  K a multiple of 64.  Returns the GEMM's name and the
+// staging launch's name in *prep_name.
+bool gemm_i8_supported(int M, int N, int K);
+size_t gemm_i8_staging_bytes(int M, int N, int K);
+const char* gemm_i8_variant();
+const char* launch_gemm_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy, int M,
+                           int N, int K, int x86, void* staging, hipStream_t stream, const char** prep_name);
+
 constexpr int kStripMaxM = 256;   // in blocks of 32 activation rows
 // Where the strip kernel measured faster than the fused one: Q8_0 weights
 // with K <= 1024 (one launch).  K-quant pieces are read with scattered

@@ -263,3 +263,51 @@ def test_tall_small_weight_views_of_in_projection(samhip, oracle):
             assert ctx.query().kernel_variant == b"tall_small_i8mfma_q8_0"
             ref = oracle.mul_mat_native(oracle.Q8_0, w[256 * s:256 * (s + 1)], x, oracle.ROUND_X86)
             assert max_row_rel_l2(y, ref) <= EXACT
+
+
+# the exact int8 GEMM for tall Q8_0 products (SAMHIP_TALL_INT8=1): ViT fc2
+# (K = 4736) and fc1 (config 1) on sampled rows, ragged M and N, a strided
+# activation, a row-offset view, both roundings
+TALL_I8 = [(5184, 1024, 4736), (5184, 4736, 1024), (300, 257, 1024), (1000, 96, 4736), (257, 1000, 128),
+           (700, 3072, 64)]
+
+
+@pytest.mark.parametrize("rounding", ["x86", "ref"])
+@pytest.mark.parametrize("shape", TALL_I8, ids=lambda s: "x".join(map(str, s)))
+def test_tall_int8_gemm_matches_native(samhip, oracle, monkeypatch, shape, rounding):
+    m, n, k = shape
+    say("case tall int8 gemm", shape, rounding)
+    gmode = samhip.ROUND_X86 if rounding == "x86" else samhip.ROUND_REF
+    cmode = oracle.ROUND_X86 if rounding == "x86" else oracle.ROUND_REF
+    rng = np.random.default_rng(m + n + 7 * k)
+    w = oracle.quantize(oracle.Q8_0, (rng.standard_normal((n + 5, k)) * 0.02).astype(np.float32))
+    x = (rng.standard_normal((m, k)) * np.exp(rng.uniform(-4, 4, (m, 1)))).astype(np.float32)
+    monkeypatch.setenv("SAMHIP_TALL_INT8", "1")
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE, gmode) as ctx:
+        y = ctx.matmul(samhip.Q8_0, w, x, w_row_offset=5, w_rows=n, x_row_stride=k + 4 if m % 2 else None)
+        assert ctx.query().kernel_variant == b"gemm_i8mfma_q8_0_128x128x64"
+        again = ctx.matmul(samhip.Q8_0, w, x, w_row_offset=5, w_rows=n)
+    rows = np.arange(m) if m * n * k <= 2 ** 31 else np.unique(np.concatenate(
+        [np.arange(8), np.arange(m - 8, m), rng.choice(m, 32, replace=False)]))
+    ref = oracle.mul_mat_native(oracle.Q8_0, w[5:5 + n], x[rows], cmode)
+    err = max_row_rel_l2(y[rows], ref)
+    say(f"  max row rel L2 {err:.2e} over {len(rows)} rows")
+    assert np.isfinite(y).all() and err <= EXACT
+    assert np.array_equal(y, again)
+
+
+def test_tall_int8_gemm_nan_and_zero_rows(samhip, oracle, monkeypatch):
+    """A NaN activation packs as code 0 and zero rows give zero outputs, as
+    the oracle's native path does."""
+    say("case tall int8 gemm NaN")
+    rng = np.random.default_rng(95)
+    w = oracle.quantize(oracle.Q8_0, (rng.standard_normal((256, 1024)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((300, 1024)).astype(np.float32)
+    x[3, 7] = x[40, 300] = x[299, 1023] = np.nan
+    x[10] = 0.0
+    monkeypatch.setenv("SAMHIP_TALL_INT8", "1")
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE, samhip.ROUND_X86) as ctx:
+        y = ctx.matmul(samhip.Q8_0, w, x)
+        assert ctx.query().kernel_variant == b"gemm_i8mfma_q8_0_128x128x64"
+    assert np.isfinite(y).all() and not y[10].any()
+    assert max_row_rel_l2(y, oracle.mul_mat_native(oracle.Q8_0, w, x, oracle.ROUND_X86)) <= EXACT
