@@ -1165,9 +1165,11 @@ def main():
                     help="launches bracketed by HIP events inside the timed region")
     ap.add_argument("--trace-every", type=int, default=5,
                     help="bracket the traced launches of every N-th timed step only (1: every step)")
-    ap.add_argument("--workload", choices=["vit", "text", "encoder", "detector"], default="vit",
+    ap.add_argument("--workload", choices=["vit", "text", "encoder", "detector", "linear"], default="vit",
                     help="vit: the ViT linear sweep (headline, with the encoder's ms/image beside it); text: the "
-                         "M=32 text-encoder linear stream; encoder: the vision encoder forward alone")
+                         "M=32 text-encoder linear stream; encoder: the vision encoder forward alone; linear: the "
+                         "four ViT linears at M=5184 in one weight format (--format, default q8_0), 3 rotated "
+                         "W/X/Y sets")
     ap.add_argument("--format", choices=["q8_0", "q4_k", "q5_k", "q6_k"], default=None,
                     help="weight format of the text stream (default q8_0) or of the encoder's K-quant linears "
                          "(default q4_k)")
@@ -1205,6 +1207,21 @@ def main():
     if args.workload == "encoder":
         args.format = args.format or "q4_k"
         result = encoder_workload(args, sh, ctx)
+        ctx.close()
+        print(json.dumps(result), flush=True)
+        return
+    if args.workload == "linear":
+        fmt = args.format or "q8_0"
+        qt = {"q4_k": sh.Q4_K, "q5_k": sh.Q5_K, "q6_k": sh.Q6_K, "q8_0": sh.Q8_0}[fmt]
+        items = [(f"{name}:{fmt}", qt if k % 256 == 0 or qt == sh.Q8_0 else sh.Q8_0, k, n) for name, k, n in SHAPES]
+        r = linear_set(sh, ctx, M_TOKENS, items, args.steps, args.warmup, rotate=3)
+        result = {"metric": f"ViT linears at M={M_TOKENS}, {fmt} (fc2 Q8_0), TOPS", "value": r["value"], "unit": "TOPS",
+                  "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_per_step"],
+                  "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+                  "data": "synthetic", "config": {"workload": f"qkv, proj, fc1, fc2 at M={M_TOKENS}, 3 rotated sets",
+                                                   "tall_int8": os.environ.get("SAMHIP_TALL_INT8", "0")},
+                  "roofline": r["roofline"], "products": r["products"], "rotation": r["rotation"],
+                  "device": ctx.query().device_name.decode()}
         ctx.close()
         print(json.dumps(result), flush=True)
         return

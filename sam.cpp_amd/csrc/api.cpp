@@ -131,6 +131,7 @@ struct samhip_context {
     int fused_max_splits = 16;  // SAMHIP_FUSED_MAX_SPLITS: cap on the fused kernel's K splits
     bool check_activations = false;   // samhip_context_set_activation_check
     bool tall_int8 = false;     // SAMHIP_TALL_INT8=1: tall Q8_0 products on the exact int8 GEMM
+    bool tall_decode = false;   // SAMHIP_TALL_DECODE=1: tall products on the in-loader weight-decode GEMM
     bool tall_small = true;     // SAMHIP_TALL_SMALL=0 keeps M >= 256 products with small Q8_0 weights on the fused kernel
     int int8_strip = 1;         // SAMHIP_INT8_STRIP: 0 keeps M < 256 products on the fp16 kernels; 1 sends Q8_0
                                 // ones, and K-quant ones where that measured faster, to the int8 kernels; 2
@@ -347,6 +348,7 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
     ctx->int8_strip = env_int("SAMHIP_INT8_STRIP", 1);
     ctx->tall_small = env_int("SAMHIP_TALL_SMALL", 1) != 0;
     ctx->tall_int8 = env_int("SAMHIP_TALL_INT8", 0) != 0;
+    ctx->tall_decode = env_int("SAMHIP_TALL_DECODE", 0) != 0;
     const int cfg = env_int("SAMHIP_GEMM_CONFIG", -1);
     ctx->gemm_cfg = (cfg >= 0 && cfg < gemm_f16_config_count()) ? cfg : -1;
     *out = ctx;
@@ -507,7 +509,10 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     // tall products with a 256x256-sized weight (the fusion / decoder image
     // tokens' q, k, v, out projections) run the fused kernel: one launch
     const bool small_w = ctx->fused_skinny && int64_t(N) * K <= kFusedSmallW;
-    const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K) && !small_w;
+    // SAMHIP_TALL_DECODE=1 sends the tall products to the GEMM that decodes
+    // the packed weight while staging it into LDS (gemm_kernel, one pass over
+    // the weight) instead of weight decode in the preparation + fp16 GEMM
+    const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K) && !small_w && !ctx->tall_decode;
     const bool kquant = (w->type == T_Q4_K || w->type == T_Q5_K || w->type == T_Q6_K) &&
                         (ctx->int8_strip == 2 || kq_strip_i8_preferred(w->type, M, N, K, ctx->cus));
     if (small_w && M >= kStripMaxM && w->type == T_Q8_0 && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE &&
