@@ -25,6 +25,8 @@ namespace samhip {
 namespace {
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float wave_sum(float v) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -279,6 +281,8 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
 #pragma unroll
     for (int r = 0; r < 16; ++r) o0[r] = o1[r] = 0.f;
     float mrun = -__builtin_inff(), lsum = 0.f;
+    float one = 1.0f;
+    asm("" : "+s"(one));   // 1.0 the compiler cannot see (the P split below)
     const int nkb = Np / 64, per_split = (nkb + S - 1) / S;
     const int kb0 = sp * per_split, kb1 = min(nkb, kb0 + per_split);
 
@@ -320,10 +324,13 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
                 if (key + 32 >= N) s1[r] = -__builtin_inff();
             }
         }
+        // the tile's largest score per query: IEEE maximum (v_maximum3_f32,
+        // a NaN score gives a NaN row either way), where fmaxf would first
+        // quiet every MFMA result with a separate v_max
         float mx = -__builtin_inff();
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        for (int r = 0; r < 16; ++r) mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(s0[r], s1[r]));
+        mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 32, 64));
         // Lazy rescaling: the exponent base mrun only moves when a score
         // exceeds it by more than 8 / log2(e), so the weights stay below 2^8
         // (fp16 keeps its full relative precision there) and most tiles skip
@@ -348,18 +355,26 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
             ps += s0[r] + s1[r];
         }
         lsum = lsum + ps;
+        // P in fp16: hi = fp16(p) two at a time (v_cvt_pk_f16_f32) and, at
+        // LEVEL 2, lo = fp16(p - hi) (exact difference, one rounding) by
+        // v_fma_mixlo/mixhi_f16 reading hi's halves: fma(p, one, -hi) with
+        // `one` opaque to the compiler, which would otherwise fold the fma
+        // into a subtraction and convert hi back to F32 separately
         half8 pf[PV][4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            pf[0][0][j] = (_Float16)s0[j];
-            pf[0][1][j] = (_Float16)s0[8 + j];
-            pf[0][2][j] = (_Float16)s1[j];
-            pf[0][3][j] = (_Float16)s1[8 + j];
-            if (PRECISE_PV) {
-                pf[PV - 1][0][j] = (_Float16)(s0[j] - (float)pf[0][0][j]);
-                pf[PV - 1][1][j] = (_Float16)(s0[8 + j] - (float)pf[0][1][j]);
-                pf[PV - 1][2][j] = (_Float16)(s1[j] - (float)pf[0][2][j]);
-                pf[PV - 1][3][j] = (_Float16)(s1[8 + j] - (float)pf[0][3][j]);
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                const float2_t p{t < 2 ? s0[8 * t + j] : s1[8 * (t - 2) + j],
+                                 t < 2 ? s0[8 * t + j + 1] : s1[8 * (t - 2) + j + 1]};
+                const half2_t hi = __builtin_convertvector(p, half2_t);
+                pf[0][t][j] = hi[0];
+                pf[0][t][j + 1] = hi[1];
+                if (PRECISE_PV) {
+                    const float2_t hf = __builtin_convertvector(hi, float2_t);
+                    pf[PV - 1][t][j] = (_Float16)__builtin_fmaf(p[0], one, -hf[0]);
+                    pf[PV - 1][t][j + 1] = (_Float16)__builtin_fmaf(p[1], one, -hf[1]);
+                }
             }
         }
         // V^T fragments of part p for 16-key step u (lane: dim l%32 of each
@@ -567,7 +582,9 @@ bool launch_attention(const AttnOperands& o, float* out, int64_t ldo, int B, int
     float* part_ml = S > 1 ? scratch + size_t(S) * B * N * H * 64 : nullptr;
     // 128-query workgroups: measured on the SAM 3 shapes against 64, 96 and
     // 192 (windowed 34 / 42 / 35 / 41 us, global 206 / 294 / 213 / 267 us;
-    // 96 tiles 576 and 5184 queries exactly and still loses)
+    // 96 and 192 tile 576 and 5184 queries exactly and still lose; 192 again
+    // at 151 VGPRs, three waves per SIMD: windowed 54.7 against 52.2 us,
+    // global 389 against 333 us)
     const dim3 grid(unsigned((np + 127) / 128), unsigned(H), unsigned(B * S));
     // (splitting the scores alone, level 1, measured 6e-4 relative error per
     // output row at 2.8 ms per SAM 3 image against 5e-6 at 3.9 ms for level 2
