@@ -210,6 +210,9 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 }
 constexpr float LOG2E = 1.44269504088896340736f;
 
+// slot permutation of a V tile row (the attention kernel's LDS layout)
+__device__ __forceinline__ int v_swizzle(int r) { return 2 * (r & 3) + ((r >> 2) & 1); }
+
 // LEVEL 0: fp16 operands; 1: split scores; 2: split scores and output.
 template <int QW, int LEVEL>   // waves per workgroup (32 queries each), precision level
 __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, float* __restrict__ out, int64_t ldo,
@@ -242,8 +245,12 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
 
     // K and V tiles go straight from HBM into LDS (buffer_load ... lds): a
     // tile's 512 16-byte chunks, two per lane; the chunk landing in slot c of
-    // row r is the row's chunk c ^ (r & 7), so that the fragment reads of 32
-    // rows at one column spread over the banks.
+    // row r is the row's chunk c ^ swz(r).  K: swz(r) = r & 7, so that the
+    // 16-byte fragment reads of 8 rows at one column hit 8 different slots.
+    // V: its transposed reads take 32 bytes (a slot pair) from each of 4
+    // consecutive rows per 16 lanes, so swz(r) = 2 (r & 3) + ((r >> 2) & 1)
+    // puts those 4 rows' pairs in 4 different pairs of slots (with r & 7 two
+    // rows shared a pair: a 2-way bank conflict on every V read).
     const uint32_t bytes = uint32_t(Np) * 128;
     __amdgpu_buffer_rsrc_t kr[P], vr[PV];
 #pragma unroll
@@ -254,11 +261,12 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
     for (int p = 0; p < PV; ++p)
         vr[p] = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>((p ? op.vl : op.v) + bh * Np * 64), 0, bytes,
                                                   RSRC_WORD3);
-    uint32_t goff[2];
+    uint32_t goff[2], gofv[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int id = wave * 128 + i * 64 + lane, r = id >> 3, c = id & 7;
         goff[i] = uint32_t(r * 128 + ((c ^ (r & 7)) << 4));
+        gofv[i] = uint32_t(r * 128 + ((c ^ v_swizzle(r)) << 4));
     }
     auto issue = [&](int kb, int buf) {
         const int koff = kb * TB;
@@ -273,7 +281,7 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
             for (int p = 0; p < PV; ++p)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
                     vr[p], (__attribute__((address_space(3))) void*)(vtile[p][buf] + (wave * 128 + i * 64) * 16), 16,
-                    goff[i], koff, 0, 0);
+                    gofv[i], koff, 0, 0);
         }
     };
 
@@ -382,7 +390,7 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
         // read transposed out of the key-major tile
         auto vfrag = [&](int p, int u, half8& a0, half8& a1) {
             const int row = 32 * (u >> 1) + 16 * (u & 1) + 4 * hh + ((lane & 15) >> 2);
-            const int cg = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1), sw = row & 7;   // rows row, row + 8 alike
+            const int cg = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1), sw = v_swizzle(row);   // row + 8 alike
             const uint8_t* at = vtile[p][buf] + row * 128 + 8 * (lane & 1);
             const half4 a_lo0 = ds_read_tr(at + ((cg ^ sw) << 4));
             const half4 a_hi0 = ds_read_tr(at + 8 * 128 + ((cg ^ sw) << 4));
