@@ -132,6 +132,31 @@ def copy_calibration():
                       "check": float(y[-1].item())}), flush=True)
 
 
+def blas_calibration(iters=20):
+    """hipBLASLt (torch.mm with an F32 output dtype) on fp16 operands at the
+    four ViT product shapes (M = 5184), Y = A B^T with B row-major [N][K] as
+    the staged weights are: the vendor library's time for the same operand
+    formats and output type as this library's tall GEMM."""
+    import torch
+    out = {}
+    for name, k, n in SHAPES:
+        a = torch.randn(M_TOKENS, k, device="cuda", dtype=torch.float16)
+        b = torch.randn(n, k, device="cuda", dtype=torch.float16)
+        for _ in range(5):
+            torch.mm(a, b.t(), out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(iters):
+            torch.mm(a, b.t(), out_dtype=torch.float32)
+        e.record()
+        torch.cuda.synchronize()
+        us = s.elapsed_time(e) / iters * 1e3
+        out[name] = {"M": M_TOKENS, "N": n, "K": k, "us": round(us, 1),
+                     "tflops": round(2.0 * M_TOKENS * n * k / (us * 1e-6) / 1e12, 1)}
+    print(json.dumps({"hipblaslt_f16_f32out": out}), flush=True)
+
+
 def summarize_profiles(d, commands):
     """Writes the committed text summaries from a rocprofv3 output folder
     `d` holding trace/, fetch/, write/, copy_FETCH_SIZE/ and copy_WRITE_SIZE/
@@ -1176,11 +1201,16 @@ def main():
     ap.add_argument("--no-encoder", action="store_true", help="skip the vision-encoder measurement of the headline run")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the plain copy used to scale HBM traffic counters")
+    ap.add_argument("--blas-calibration", action="store_true",
+                    help="time hipBLASLt (torch.mm, fp16 operands, F32 output) at the four ViT shapes and exit")
     ap.add_argument("--summarize-profiles", metavar="DIR",
                     help="write profiles/ summaries from rocprofv3 CSV output in DIR and exit")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.blas_calibration:
+        blas_calibration()
         return
     if args.summarize_profiles:
         summarize_profiles(args.summarize_profiles, PROFILE_COMMANDS)
