@@ -25,6 +25,7 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __host__ __device__ constexpr int block_elems(int t) {
     return (t == T_Q8_0 || t == T_Q8_1) ? 32 : (t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_Q8_K) ? 256 : 1;

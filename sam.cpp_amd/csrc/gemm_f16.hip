@@ -79,10 +79,23 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
         for (int q = 0; q < 4; ++q) cs[q] = (full || n + q < N) ? ep.col_scale[n + q] : 0.f;
     const float inv_sw = (EPI & EPI_SHUFFLE) ? 1.0f / float(ep.shuffle_w) : 0.f;
     // packed outputs: the wave's 64-aligned column block lies in one part and
-    // one head (embed is a multiple of 64)
-    const int part = (EPI & EPI_PACK) ? n / ep.embed : 0;
+    // one head (embed is a multiple of 64), so the part and its output
+    // arrays are the same for every lane; element offsets are 32-bit (the
+    // host keeps each part's array below 2^31 elements)
+    const int part = (EPI & EPI_PACK) ? __builtin_amdgcn_readfirstlane(col0 / ep.embed) : 0;
     const float inv_per = (EPI & EPI_PACK) ? 1.0f / float(ep.per) : 0.f;
     const int head_off = (EPI & EPI_PACK) ? ((n - part * ep.embed) >> 6) * ep.np * 64 + (n & 63) : 0;
+    _Float16* const pk_hi = (EPI & EPI_PACK) ? (part == 0 ? ep.pack[0] : part == 1 ? ep.pack[1] : ep.pack[2]) : nullptr;
+    _Float16* const pk_lo =
+        (EPI & EPI_PACK_LO) ? (part == 0 ? ep.pack_lo[0] : part == 1 ? ep.pack_lo[1] : ep.pack_lo[2]) : nullptr;
+    const __amdgpu_buffer_rsrc_t pk_rsrc = __builtin_amdgcn_make_buffer_rsrc(pk_hi, 0, 0x7fffffff, RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t pk_lo_rsrc = __builtin_amdgcn_make_buffer_rsrc(pk_lo, 0, 0x7fffffff, RSRC_WORD3);
+    const bool rope = (EPI & EPI_PACK) && part < 2 && ep.freqs;
+    // 1.0 the compiler cannot see: fma(v, one, -hi) stays one v_fma_mix
+    // (v - hi is exact in F32, rounded once to fp16) instead of a conversion
+    // of hi back to F32 and a subtraction
+    float one = 1.0f;
+    if (EPI & EPI_PACK_LO) asm("" : "+s"(one));
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
         float sc[IT];
@@ -95,14 +108,21 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
             const bool live = m < M;
             sc[t] = live ? row_scale[m] : 0.f;
             if (EPI & EPI_PACK) {
-                // window = m / per by a float reciprocal and one correction
+                // window = m / per by a float reciprocal and one correction;
+                // every factor is below 2^24 (24-bit multiplies)
                 int w = int(float(m) * inv_per);
-                w += (w + 1) * ep.per <= m;
-                w -= w * ep.per > m;
-                const int tok = live ? m - w * ep.per : 0;
-                dst[t] = (int64_t(w) * ep.heads * ep.np + tok) * 64;
-                if (part < 2 && ep.freqs)
-                    fq[t] = *reinterpret_cast<const floatx4*>(ep.freqs + (int64_t(tok) * 32 + ((n & 63) >> 1)) * 2);
+                int wp = int(__umul24(unsigned(w), unsigned(ep.per)));
+                if (wp + ep.per <= m) {
+                    ++w;
+                    wp += ep.per;
+                }
+                if (wp > m) {
+                    --w;
+                    wp -= ep.per;
+                }
+                const int tok = live ? m - wp : 0;
+                dst[t] = (int(__umul24(__umul24(unsigned(w), unsigned(ep.heads)), unsigned(ep.np))) + tok) * 64;
+                if (rope) fq[t] = *reinterpret_cast<const floatx4*>(ep.freqs + (tok * 32 + ((n & 63) >> 1)) * 2);
             } else if (EPI & EPI_SHUFFLE) {
                 // input pixel (x, y) = (m % shuffle_w, m / shuffle_w) by a float
                 // reciprocal and one correction
@@ -144,15 +164,22 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
             floatx4 v;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                float u = raw[q] * sc[t];
-                if (EPI & EPI_COLSCALE) u = u * cs[q];
-                if (EPI & EPI_BIAS) u = u + bias[q];
+                // the row scale is a power of two, so raw * sc is exact and
+                // fma(raw, sc, bias) rounds as the product and the sum do
+                float u;
+                if ((EPI & EPI_BIAS) && !(EPI & EPI_COLSCALE)) {
+                    u = __builtin_fmaf(raw[q], sc[t], bias[q]);
+                } else {
+                    u = raw[q] * sc[t];
+                    if (EPI & EPI_COLSCALE) u = u * cs[q];
+                    if (EPI & EPI_BIAS) u = u + bias[q];
+                }
                 if (EPI & EPI_GELU) u = gelu_erf(u);
                 if (EPI & EPI_RES) u = res[t][q] + u;
                 v[q] = u;
             }
             if (EPI & EPI_PACK) {
-                if (part < 2 && ep.freqs) {
+                if (rope) {
 #pragma unroll
                     for (int p2 = 0; p2 < 2; ++p2) {
                         const float re = v[2 * p2], im = v[2 * p2 + 1], c = fq[t][2 * p2], s = fq[t][2 * p2 + 1];
@@ -165,12 +192,17 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
 #pragma unroll
                     for (int q = 0; q < 4; ++q) v[q] = v[q] * ep.q_scale;
                 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-                const half4_t hv{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-                *reinterpret_cast<half4_t*>(ep.pack[part] + dst[t] + head_off) = hv;
-                if ((EPI & EPI_PACK_LO) && ep.pack_lo[part])
-                    *reinterpret_cast<half4_t*>(ep.pack_lo[part] + dst[t] + head_off) =
-                        half4_t{(_Float16)(v[0] - (float)hv[0]), (_Float16)(v[1] - (float)hv[1]),
-                                (_Float16)(v[2] - (float)hv[2]), (_Float16)(v[3] - (float)hv[3])};
+                const half4_t hv = __builtin_convertvector(v, half4_t);
+                // 8-byte stores at 32-bit byte offsets from the part's array
+                const uint32_t off = uint32_t(head_off + int(dst[t])) * 2;
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, hv), pk_rsrc, off, 0, 0);
+                if ((EPI & EPI_PACK_LO) && pk_lo) {
+                    const half4_t lv{(_Float16)__builtin_fmaf(v[0], one, -(float)hv[0]),
+                                     (_Float16)__builtin_fmaf(v[1], one, -(float)hv[1]),
+                                     (_Float16)__builtin_fmaf(v[2], one, -(float)hv[2]),
+                                     (_Float16)__builtin_fmaf(v[3], one, -(float)hv[3])};
+                    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, lv), pk_lo_rsrc, off, 0, 0);
+                }
                 continue;
             }
             float* yp = Y + dst[t] * ldy + ycol;
