@@ -196,6 +196,11 @@ __global__ __launch_bounds__(256) void zero_pad_kernel(AttnOperands o, int N, in
 
 // s_waitcnt vmcnt(0), expcnt/lgkmcnt left at their maximum (gfx9 encoding)
 [[maybe_unused]] __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x70 | 0xF00); }
+// s_waitcnt vmcnt(N), expcnt/lgkmcnt left at their maximum (gfx9 encoding)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
@@ -225,8 +230,12 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
     constexpr int PV = PRECISE_PV ? 2 : 1;      // parts of V
     static_assert(QW == 4, "the tile loads assume 4 waves");
     constexpr int TB = 64 * 128;   // bytes of one 64-key tile of one part
+    // K tiles are double-buffered; with split V (LEVEL 2) the V tiles have a
+    // single buffer, reloaded once every wave is past the tile's products, so
+    // a workgroup takes 48 KB of LDS and three fit on a CU (two with 64 KB)
+    constexpr int VB = PRECISE_PV ? 1 : 2;
     __shared__ __attribute__((aligned(1024))) uint8_t ktile[P][2][TB];
-    __shared__ __attribute__((aligned(1024))) uint8_t vtile[PV][2][TB];
+    __shared__ __attribute__((aligned(1024))) uint8_t vtile[PV][VB][TB];
     // grid z = window x key split: split sp takes key tiles [kb0, kb1)
     const int h = blockIdx.y, b = blockIdx.z / S, sp = blockIdx.z - b * S;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -268,21 +277,25 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
         goff[i] = uint32_t(r * 128 + ((c ^ (r & 7)) << 4));
         gofv[i] = uint32_t(r * 128 + ((c ^ v_swizzle(r)) << 4));
     }
-    auto issue = [&](int kb, int buf) {
+    auto issue_k = [&](int kb, int buf) {   // 2 P loads per lane
         const int koff = kb * TB;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int p = 0; p < P; ++p)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
                     kr[p], (__attribute__((address_space(3))) void*)(ktile[p][buf] + (wave * 128 + i * 64) * 16), 16,
                     goff[i], koff, 0, 0);
+    };
+    auto issue_v = [&](int kb, int buf) {
+        const int koff = kb * TB;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int p = 0; p < PV; ++p)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
                     vr[p], (__attribute__((address_space(3))) void*)(vtile[p][buf] + (wave * 128 + i * 64) * 16), 16,
                     gofv[i], koff, 0, 0);
-        }
     };
 
     floatx16 o0, o1;
@@ -294,12 +307,16 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
     const int nkb = Np / 64, per_split = (nkb + S - 1) / S;
     const int kb0 = sp * per_split, kb1 = min(nkb, kb0 + per_split);
 
-    issue(kb0, 0);
+    issue_k(kb0, 0);
+    issue_v(kb0, 0);
     wait_vmcnt0();
     __syncthreads();
     for (int kb = kb0; kb < kb1; ++kb) {
-        const int buf = (kb - kb0) & 1;
-        if (kb + 1 < kb1) issue(kb + 1, buf ^ 1);   // that buffer's reads ended at the last barrier
+        const int buf = (kb - kb0) & 1, vbuf = VB == 2 ? buf : 0;
+        if (kb + 1 < kb1) {   // that buffer's reads ended at the last barrier
+            issue_k(kb + 1, buf ^ 1);
+            if (VB == 2) issue_v(kb + 1, buf ^ 1);
+        }
         floatx16 s0, s1;
 #pragma unroll
         for (int r = 0; r < 16; ++r) s0[r] = s1[r] = 0.f;
@@ -391,7 +408,7 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
         auto vfrag = [&](int p, int u, half8& a0, half8& a1) {
             const int row = 32 * (u >> 1) + 16 * (u & 1) + 4 * hh + ((lane & 15) >> 2);
             const int cg = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1), sw = v_swizzle(row);   // row + 8 alike
-            const uint8_t* at = vtile[p][buf] + row * 128 + 8 * (lane & 1);
+            const uint8_t* at = vtile[p][vbuf] + row * 128 + 8 * (lane & 1);
             const half4 a_lo0 = ds_read_tr(at + ((cg ^ sw) << 4));
             const half4 a_hi0 = ds_read_tr(at + 8 * 128 + ((cg ^ sw) << 4));
             const half4 a_lo1 = ds_read_tr(at + (((cg + 4) ^ sw) << 4));
@@ -399,6 +416,14 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
             a0 = __builtin_shufflevector(a_lo0, a_hi0, 0, 1, 2, 3, 4, 5, 6, 7);
             a1 = __builtin_shufflevector(a_lo1, a_hi1, 0, 1, 2, 3, 4, 5, 6, 7);
         };
+        if (VB == 1 && kb > kb0) {
+            // V(kb), requested after the last barrier and before K(kb + 1):
+            // this lane's part has landed once at most K(kb + 1)'s 2 P loads
+            // are outstanding, every lane's after the barrier
+            if (kb + 1 < kb1) wait_vmcnt<2 * P>();
+            else wait_vmcnt0();
+            __syncthreads();
+        }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             half8 a0, a1;
@@ -417,6 +442,7 @@ __global__ __launch_bounds__(64 * QW) void attention_kernel(AttnOperands op, flo
         if (kb + 1 < kb1) {
             wait_vmcnt0();   // this wave's loads of the next tile landed
             __syncthreads();
+            if (VB == 1) issue_v(kb + 1, 0);   // every wave is past V(kb)
         }
     }
     const float ltot = lsum + __shfl_xor(lsum, 32, 64);
@@ -550,9 +576,8 @@ __global__ __launch_bounds__(256) void attention_merge_kernel(const float* __res
         floatx4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
 }
 
-// Key splits for a grid of `wgs` workgroups: the S in 1..4 that needs the
-// fewest rounds of resident workgroups per unit of work (two F32-accurate or
-// four fp16 workgroups per CU), each split keeping at least 8 key tiles.
+// Key splits for a grid of `wgs` workgroups: the S in 1..4 with the lowest
+// cost below, each split keeping at least 8 key tiles.
 int attention_splits(int B, int H, int N, bool precise, int cus, int force) {
     const int np = (N + 63) / 64 * 64, nkb = np / 64;
     // the grid's z dimension holds B * S and is limited to 65535
@@ -563,7 +588,12 @@ int attention_splits(int B, int H, int N, bool precise, int cus, int force) {
         while (S > 1 && (S - 1) * ((nkb + S - 1) / S) >= nkb) --S;
         return S;
     }
-    const int64_t wgs = int64_t((np + 127) / 128) * H * B, slots = int64_t(precise ? 2 : 4) * cus;
+    // fp16 operands: cost = rounds of resident workgroups (four per CU) per
+    // unit of work.  F32-accurate: three fit a CU and share its matrix cores,
+    // so the cost is the most workgroups any CU runs per unit of work (SAM 3
+    // global block, 656 workgroups of 81 key tiles: 3 splits 317 us, 4 324,
+    // 2 335, whole 326 us)
+    const int64_t wgs = int64_t((np + 127) / 128) * H * B, slots = precise ? int64_t(cus) : int64_t(4) * cus;
     int best = 1;
     double best_cost = double((wgs + slots - 1) / slots);
     for (int s = 2; s <= cap && nkb >= 8 * s; ++s) {
