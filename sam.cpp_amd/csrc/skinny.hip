@@ -571,59 +571,54 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
 #pragma unroll
         for (int i = 0; i < RI; ++i) wr[i] = wr_c + 32 * i < ndw ? src[wr_c + 32 * i] : 0u;
     }
-    // 2. activation row m, block b -> Q8_0 codes and scale (zeros past M)
+    // 2. activation rows -> Q8_0 codes and scales: wave w takes rows 2 w and
+    // 2 w + 1 of the block, in SL / 256 passes of 512 values; lane l holds 8
+    // consecutive values and lanes 4g..4g+3 one 32-value block (its maximum
+    // over the quad by DPP), so a 16-byte load instruction touches 16 cache
+    // lines instead of the 64 of a lane per block
     {
-        const int m = tid >> 5, b = tid & 31;
-        float v[32];
-        if (m < M && b < nb) {
-            const float* xr = X + int64_t(m) * ldx + k0 + 32 * b;
-            if (XVEC) {
+        const int passes = SL / 256;
+        floatx8 v[kI8SliceK / 256];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const floatx4 t = load4f(xr + 4 * i);
-                    v[4 * i] = t[0];
-                    v[4 * i + 1] = t[1];
-                    v[4 * i + 2] = t[2];
-                    v[4 * i + 3] = t[3];
+        for (int p = 0; p < kI8SliceK / 256; ++p) {
+            if (p >= passes) break;
+            const int e = 512 * p + 8 * lane, pr = e >= SL, kl = e - pr * SL, m = 2 * wave + pr;
+            if (m < M && kl < 32 * nb) {
+                const float* xr = X + int64_t(m) * ldx + k0 + kl;
+                if (XVEC) {
+                    const floatx4 a = load4f(xr), c = load4f(xr + 4);
+                    v[p] = floatx8{a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[p][i] = xr[i];
                 }
             } else {
 #pragma unroll
-                for (int i = 0; i < 32; ++i) v[i] = xr[i];
+                for (int i = 0; i < 8; ++i) v[p][i] = 0.f;
             }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 32; ++i) v[i] = 0.f;
         }
 #pragma unroll
         for (int i = 0; i < RI; ++i)
             if (wr_c + 32 * i < I8_WDW) Ws[wr_r * I8_WDW + wr_c + 32 * i] = wr[i];
-        float amax = 0.f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-        const float d = amax / 127.f;
-        float inv;
-        if (X86) inv = amax != 0.f ? 127.f / amax : 0.f;
-        else inv = d != 0.f ? 1.f / d : 0.f;
-        // four codes per dword: the hardware conversion (NaN -> 0, this
-        // library's code for a NaN activation) and two byte permutes
-        uint32_t packed[8];
+        for (int p = 0; p < kI8SliceK / 256; ++p) {
+            if (p >= passes) break;
+            const int e = 512 * p + 8 * lane, pr = e >= SL, kl = e - pr * SL, m = 2 * wave + pr;
+            // ggml's from_float on the block (x86 or reference rounding; NaN
+            // -> code 0, this library's contract), the stored fp16 scale
+            float d, q[8];
+            quant8_codes<T_Q8_0, X86>(v[p], lane, d, q);
+            uint32_t c[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            uint32_t q[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float s = v[4 * i + j] * inv;
-                q[j] = uint32_t(cvt_i32_nan0(X86 ? __builtin_rintf(s) : __builtin_roundf(s)));
+            for (int i = 0; i < 8; ++i) c[i] = uint32_t(int(q[i]));
+            const uint32_t lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(c[3], c[2], 0x0c0c0400u),
+                                                      __builtin_amdgcn_perm(c[1], c[0], 0x0c0c0400u), 0x05040100u);
+            const uint32_t hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(c[7], c[6], 0x0c0c0400u),
+                                                      __builtin_amdgcn_perm(c[5], c[4], 0x0c0c0400u), 0x05040100u);
+            if (kl < 32 * nb) {
+                *reinterpret_cast<u32x2*>(&Xq[m * I8_XLD + kl]) = u32x2{lo, hi};
+                if ((lane & 3) == 0) Xd[kl >> 5][m] = d;
             }
-            const uint32_t lo = __builtin_amdgcn_perm(q[1], q[0], 0x0c0c0400u);   // q0.b0, q1.b0
-            const uint32_t hi = __builtin_amdgcn_perm(q[3], q[2], 0x0c0c0400u);
-            packed[i] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
-        }
-        if (b < nb) {
-            u32x4* dst = reinterpret_cast<u32x4*>(&Xq[m * I8_XLD + 32 * b]);
-            dst[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
-            dst[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
-            Xd[b][m] = half_bits_to_float(float_to_half_bits(d));   // the stored fp16 scale
         }
     }
     __syncthreads();
