@@ -492,11 +492,14 @@ constexpr Cfg kConfigs[] = {
     SAMHIP_CFG(128, 256, 64, 2, 2, 4),
     SAMHIP_CFG(128, 128, 128, 2, 2, 4),
     SAMHIP_CFG(192, 128, 64, 2, 2, 2),
+    SAMHIP_CFG(64, 128, 64, 3, 2, 4),
+    SAMHIP_CFG(128, 64, 64, 3, 4, 2),
 };
 #undef SAMHIP_CFG
-constexpr int kCfgSquare = 0, kCfgWide = 1, kCfgSmall = 2;
+constexpr int kCfgSquare = 0, kCfgWide = 1, kCfgSmall = 2, kCfgTiny = 11;
 static_assert(kConfigs[kCfgSquare].bm == 256 && kConfigs[kCfgSquare].bn == 256 && kConfigs[kCfgWide].bm == 192 &&
-                  kConfigs[kCfgWide].bn == 128 && kConfigs[kCfgSmall].bm == 128 && kConfigs[kCfgSmall].bn == 128,
+                  kConfigs[kCfgWide].bn == 128 && kConfigs[kCfgSmall].bm == 128 && kConfigs[kCfgSmall].bn == 128 &&
+                  kConfigs[kCfgTiny].bm == 64 && kConfigs[kCfgTiny].bn == 128,
               "the picks below name these entries");
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -537,8 +540,16 @@ int gemm_f16_pick(int M, int N, int /*K*/, int cus) {
 // N = 256 (the fusion / decoder image-token products) 9.5 vs 10.9 us at
 // K = 256 and 23.5 vs 29.3 us at K = 2048; N = 2048 stays 192x128 (17.3 vs
 // 22.1 us).
+//
+// 64x128 tiles (2x4 waves of 32x32) where even 128x128 tiles would leave
+// half the CUs idle, and for K of at most 256 (four stages, too few to
+// amortize a large tile's prologue and epilogue): M = 5184, N = 256,
+// K = 2048 (the fusion encoder's FFN output product) 21.7 -> 17.1 us;
+// N = 2048, K = 256 (its FFN input) 19.7 -> 18.7 us against 192x128.
 int gemm_f16_pick_plain(int M, int N, int K, int cus) {
     const int64_t tiles = int64_t((M + 191) / 192) * ((N + 127) / 128);
+    const int64_t small = int64_t((M + 127) / 128) * ((N + 127) / 128);
+    if (K <= 256 || (2 * tiles <= cus && 2 * small <= cus)) return kCfgTiny;
     if (2 * tiles <= cus && K % kConfigs[kCfgSmall].bk == 0) return kCfgSmall;
     return gemm_f16_pick(M, N, K, cus);
 }
