@@ -132,7 +132,7 @@ struct samhip_context {
     bool check_activations = false;   // samhip_context_set_activation_check
     bool tall_int8 = false;     // SAMHIP_TALL_INT8=1: tall Q8_0 products on the exact int8 GEMM
     bool tall_decode = false;   // SAMHIP_TALL_DECODE=1: tall products on the in-loader weight-decode GEMM
-    bool tall_small = true;     // SAMHIP_TALL_SMALL=0 keeps M >= 256 products with small Q8_0 weights on the fused kernel
+    bool tall_small = true;     // SAMHIP_TALL_SMALL=0 keeps M >= 256 products with small weights on the fused kernel
     int int8_strip = 1;         // SAMHIP_INT8_STRIP: 0 keeps M < 256 products on the fp16 kernels; 1 sends Q8_0
                                 // ones, and K-quant ones where that measured faster, to the int8 kernels; 2
                                 // sends every K-quant one there as well
@@ -515,16 +515,24 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K) && !small_w && !ctx->tall_decode;
     const bool kquant = (w->type == T_Q4_K || w->type == T_Q5_K || w->type == T_Q6_K) &&
                         (ctx->int8_strip == 2 || kq_strip_i8_preferred(w->type, M, N, K, ctx->cus));
-    if (small_w && M >= kStripMaxM && w->type == T_Q8_0 && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE &&
-        ctx->tall_small && tall_small_i8_supported(M, N, K, w->data, int64_t(w->nb[1]))) {
+    const bool tall_small_q8 = w->type == T_Q8_0 && tall_small_i8_supported(M, N, K, w->data, int64_t(w->nb[1]));
+    const bool tall_small_kq = tall_small_kq_i8_supported(w->type, M, N, K, w->data, int64_t(w->nb[1]));
+    if (small_w && M >= kStripMaxM && (tall_small_q8 || tall_small_kq) && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE &&
+        ctx->tall_small) {
         // many rows against a weight that fits in LDS: exact int8, one
         // workgroup per CU, no staging
-        const char* variant = tall_small_i8_variant();
+        const char* variant = tall_small_q8 ? tall_small_i8_variant() : tall_small_kq_i8_variant(w->type);
         int rc = traced(ctx, variant, w->type, M, N, K, [&]() -> int {
-            if (!launch_tall_small_i8(static_cast<const float*>(x->data), int64_t(x->nb[1] / 4), w->data,
-                                      int64_t(w->nb[1]), static_cast<float*>(y->data), int64_t(y->nb[1] / 4), M, N, K,
-                                      ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->cus, ctx->stream))
-                return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no small-weight kernel for this shape");
+            const float* xp = static_cast<const float*>(x->data);
+            float* yp = static_cast<float*>(y->data);
+            const char* ok =
+                tall_small_q8
+                    ? launch_tall_small_i8(xp, int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), yp,
+                                           int64_t(y->nb[1] / 4), M, N, K,
+                                           ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0, ctx->cus, ctx->stream)
+                    : launch_tall_small_kq_i8(w->type, xp, int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), yp,
+                                              int64_t(y->nb[1] / 4), M, N, K, ctx->cus, ctx->stream);
+            if (!ok) return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no small-weight kernel for this shape");
             HIP_TRY(hipGetLastError(), "small-weight launch");
             return SAMHIP_OK;
         });

@@ -252,6 +252,12 @@ bool tall_small_i8_supported(int M, int N, int K, const void* w, int64_t w_strid
 const char* tall_small_i8_variant();
 const char* launch_tall_small_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy,
                                  int M, int N, int K, int x86, int cus, hipStream_t stream);
+// The same for Q4_K / Q5_K / Q6_K weights (one super-block per row), with
+// ggml's native arithmetic (Q8_K activation codes, exact integer sums).
+bool tall_small_kq_i8_supported(int wtype, int M, int N, int K, const void* w, int64_t w_stride);
+const char* tall_small_kq_i8_variant(int wtype);
+const char* launch_tall_small_kq_i8(int wtype, const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y,
+                                    int64_t ldy, int M, int N, int K, int cus, hipStream_t stream);
 
 // Exact tall products for Q8_0 weights (gemm_i8.hip): activations and the
 // weight split per call into int8 codes and F32 block scales (staging of

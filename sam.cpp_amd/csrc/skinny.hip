@@ -844,6 +844,278 @@ __global__ __launch_bounds__(512) void tall_small_i8_kernel(const float* __restr
 }
 
 // ---------------------------------------------------------------------------
+// The same shape for K-quant weights (Q4_K, Q5_K, Q6_K; K = 256, one
+// super-block per row), with ggml's CPU native arithmetic reproduced
+// exactly: each activation row is packed to Q8_K (quantize_row_q8_K, one
+// F32 scale d_x), and for weight row n
+//   Q4_K, Q5_K:  y = (d d_x) isum - (dmin d_x) msum,
+//                isum = sum_j sc_j dot_j,  msum = sum_j m_j xs_j,
+//   Q6_K:        y = (d d_x) isum,
+//                isum = sum_s sc_s (dot_s - 32 xs_s),
+// with the integer sums of vec_dot_q4_K/q5_K/q6_K_q8_K exact in int32
+// (dot_j: the codes' dot over sub-block j, v_mfma_i32_32x32x32_i8; xs_j:
+// the activation codes' sum over the sub-block; the F32 steps in ggml's
+// order), so the result equals the CPU path's.
+//  1. waves 4-7 copy the packed weight into LDS (direct-to-LDS loads, each
+//     wave the whole KBs that cover its 64 rows) and each lane decodes one
+//     row: its codes (0..15, 0..31 or 0..63) 16-byte aligned, its sub-block
+//     scales (and Q4_K/Q5_K mins) as int8 rows, d (and dmin) as floats;
+//     meanwhile waves 0-3 pack the next 32 activation rows to Q8_K codes,
+//     d_x and the sub-block code sums, split as xs = 64 xh + xl (xl in
+//     [0, 63], xh in [-64, 63]) so that sum_j m_j xs_j and sum_s sc_s xs_s
+//     are two more int8 MFMAs against the mins (scales) as the B operand;
+//  2. wave w takes column tile w of 32 weight rows: the sub-block dots,
+//     isum by 24-bit integer multiply-adds in sub-block order, then the F32
+//     steps and the stores.
+// ---------------------------------------------------------------------------
+template <int WT>
+constexpr int tskq_pack_bytes() { return kTallSmallMaxN * block_bytes(WT) + 1024; }
+
+template <int WT, bool XVEC>
+__global__ __launch_bounds__(512) void tall_small_kq_i8_kernel(const float* __restrict__ X, int64_t ldx,
+                                                               const uint8_t* __restrict__ W, float* __restrict__ Y,
+                                                               int64_t ldy, int M, int N) {
+#pragma clang fp contract(off)
+    constexpr int BB = block_bytes(WT);
+    constexpr bool Q6 = WT == T_Q6_K;
+    constexpr int NS = Q6 ? 16 : 8;                 // weight sub-blocks per row (16 or 32 values)
+    __shared__ __attribute__((aligned(16))) uint8_t Wp[tskq_pack_bytes<WT>()];   // packed rows as stored
+    __shared__ __attribute__((aligned(16))) uint8_t Wl[kTallSmallMaxN * TS_XLD]; // codes, 16-byte aligned rows
+    __shared__ __attribute__((aligned(16))) int8_t Wsc[kTallSmallMaxN * 32];    // sub-block scales (zero padded)
+    __shared__ __attribute__((aligned(16))) int8_t Wm[Q6 ? 16 : kTallSmallMaxN * 32];   // Q4_K/Q5_K mins
+    __shared__ __attribute__((aligned(16))) float Wd[kTallSmallMaxN], Wdm[kTallSmallMaxN];
+    __shared__ __attribute__((aligned(16))) int8_t Xq[32 * TS_XLD];
+    __shared__ __attribute__((aligned(16))) int8_t Xsl[32 * 32], Xsh[32 * 32];
+    __shared__ __attribute__((aligned(16))) float Xd[32];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = gridDim.x, g = blockIdx.x;
+    const int r_begin = int(int64_t(M) * g / G), r_end = int(int64_t(M) * (g + 1) / G);
+    const int col = lane & 31, h = lane >> 5;
+    const int n = wave * 32 + col;          // this lane's weight row in the products
+    const int nr = min(n, N - 1);
+    for (int rt = r_begin; rt < r_end; rt += 32) {
+        const int rows = min(32, r_end - rt);
+        if (wave < 4) {
+            // pass p: activation row 8 p + tid / 32, values 8 li .. 8 li + 7
+            // (32 lanes per Q8_K block: the row's 256 values)
+            const int li = tid & 31;
+            floatx8 v[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int m = 8 * p + (tid >> 5);
+                v[p] = floatx8{0, 0, 0, 0, 0, 0, 0, 0};
+                if (m < rows) {
+                    const float* xr = X + int64_t(rt + m) * ldx + 8 * li;
+                    if (XVEC) {
+                        const floatx4 a = load4f(xr), c = load4f(xr + 4);
+                        v[p] = floatx8{a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) v[p][i] = xr[i];
+                    }
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int m = 8 * p + (tid >> 5);
+                float d, q[8];
+                quant8_codes<T_Q8_K, false>(v[p], lane, d, q);
+                int c[8], sum = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    c[i] = int(q[i]);
+                    sum += c[i];
+                }
+                const uint32_t lo = __builtin_amdgcn_perm(
+                    __builtin_amdgcn_perm(uint32_t(c[3]), uint32_t(c[2]), 0x0c0c0400u),
+                    __builtin_amdgcn_perm(uint32_t(c[1]), uint32_t(c[0]), 0x0c0c0400u), 0x05040100u);
+                const uint32_t hi = __builtin_amdgcn_perm(
+                    __builtin_amdgcn_perm(uint32_t(c[7]), uint32_t(c[6]), 0x0c0c0400u),
+                    __builtin_amdgcn_perm(uint32_t(c[5]), uint32_t(c[4]), 0x0c0c0400u), 0x05040100u);
+                *reinterpret_cast<u32x2*>(&Xq[m * TS_XLD + 8 * li]) = u32x2{lo, hi};
+                if (li == 0) Xd[m] = d;
+                // code sum of the weight's sub-block: 4 lanes (32 values) or 2 (16)
+                const int xs = group_sum<Q6 ? 2 : 4>(sum);
+                const int sj = Q6 ? li >> 1 : li >> 2;   // sub-block of this lane
+                const int xh = xs >> 6, xl = xs - 64 * xh;
+                if ((li & (Q6 ? 1 : 3)) == 0) {
+                    Xsl[m * 32 + sj] = int8_t(xl);
+                    Xsh[m * 32 + sj] = int8_t(xh);
+                }
+                if (li >= NS) {   // the K padding of the sum operands
+                    Xsl[m * 32 + li] = 0;
+                    Xsh[m * 32 + li] = 0;
+                }
+            }
+        } else if (rt == r_begin) {
+            // the packed bytes of rows 64 v .. 64 v + 63, whole KBs from the
+            // first (requests past the N rows read as zero)
+            const int v = wave - 4, wrow = 64 * v + lane;
+            constexpr int CH = (64 * BB + 1023) / 1024;
+            const __amdgpu_buffer_rsrc_t wd =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), 0, uint32_t(N * BB), 0x00020000);
+#pragma unroll
+            for (int c = 0; c < CH; ++c)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    wd, (__attribute__((address_space(3))) void*)(Wp + 64 * v * BB + c * 1024), 16,
+                    uint32_t(64 * v * BB + c * 1024 + 16 * lane), 0, 0, 0);
+            __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's rows have landed
+            __builtin_amdgcn_wave_barrier();
+            if (wrow < N) {
+                if constexpr (BB % 16 != 0) {
+                    // the buffer's range check zeroes a dword that crosses its
+                    // end (N odd for the 210-byte Q6_K rows): the last row
+                    // takes its bytes past the last whole 16 from memory
+                    if (wrow == N - 1)
+                        for (int o = (N * BB) & ~15; o < N * BB; o += 2)
+                            *reinterpret_cast<uint16_t*>(Wp + o) = *reinterpret_cast<const uint16_t*>(W + o);
+                }
+                // the lane's packed row in registers (as dwords from its
+                // 2-byte aligned start), then its decode
+                const uint8_t* rp = Wp + wrow * BB;
+                const uint32_t* rd = reinterpret_cast<const uint32_t*>(rp - (reinterpret_cast<uintptr_t>(rp) & 3));
+                const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(rp) & 3);
+                constexpr int ND = (BB + 3) / 4 + 1;
+                uint32_t rw[ND];
+#pragma unroll
+                for (int i = 0; i < ND; ++i) rw[i] = rd[i];
+                auto word = [&](int o) -> uint32_t {   // bytes o .. o + 3 of the row, o a multiple of 4
+                    return funnel_bytes(rw[(o >> 2) + 1], rw[o >> 2], (sh + uint32_t(o)) & 3u);
+                };
+                uint32_t* dst = reinterpret_cast<uint32_t*>(Wl + wrow * TS_XLD);
+                if constexpr (Q6) {
+                    // value e = 128 hf + 32 gq + l: low = nibble gq / 2 of ql[64 hf + 32 (gq & 1) + l],
+                    // high = bits 2 gq of qh[32 hf + l]
+#pragma unroll
+                    for (int st = 0; st < 8; ++st) {
+                        const int hf = st >> 2, gq = st & 3;
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) {
+                            const uint32_t ql = word(64 * hf + 32 * (gq & 1) + 4 * t);
+                            const uint32_t qh = word(128 + 32 * hf + 4 * t);
+                            dst[8 * st + t] =
+                                ((ql >> (4 * (gq >> 1))) & 0x0f0f0f0fu) | (((qh >> (2 * gq)) & 0x03030303u) << 4);
+                        }
+                    }
+                    const uint32_t s0 = word(192), s1 = word(196), s2 = word(200), s3 = word(204);
+                    uint32_t* sd = reinterpret_cast<uint32_t*>(Wsc + wrow * 32);
+                    sd[0] = s0; sd[1] = s1; sd[2] = s2; sd[3] = s3;
+                    sd[4] = sd[5] = sd[6] = sd[7] = 0u;
+                    Wd[wrow] = half_bits_to_float(word(208) & 0xffffu);
+                } else {
+                    // Q4_K: d @0, dmin @2, scales @4, qs @16; Q5_K: qh @16, qs @48
+                    constexpr int QS = WT == T_Q5_K ? 48 : 16;
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) {
+                            uint32_t u = (word(QS + 32 * (jj >> 1) + 4 * t) >> (4 * (jj & 1))) & 0x0f0f0f0fu;
+                            if constexpr (WT == T_Q5_K) u |= ((word(16 + 4 * t) >> jj) & 0x01010101u) << 4;
+                            dst[8 * jj + t] = u;
+                        }
+                    }
+                    const uint32_t scw[3] = {word(4), word(8), word(12)};
+                    uint32_t scp[2] = {0u, 0u}, mnp[2] = {0u, 0u};
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        int sc, mn;
+                        k4_scale_min(jj, scw, sc, mn);
+                        scp[jj >> 2] |= uint32_t(sc) << (8 * (jj & 3));
+                        mnp[jj >> 2] |= uint32_t(mn) << (8 * (jj & 3));
+                    }
+                    uint32_t* sd = reinterpret_cast<uint32_t*>(Wsc + wrow * 32);
+                    uint32_t* md = reinterpret_cast<uint32_t*>(Wm + wrow * 32);
+                    sd[0] = scp[0]; sd[1] = scp[1];
+                    md[0] = mnp[0]; md[1] = mnp[1];
+#pragma unroll
+                    for (int i = 2; i < 8; ++i) sd[i] = md[i] = 0u;
+                    const uint32_t hdr = word(0);
+                    Wd[wrow] = half_bits_to_float(hdr & 0xffffu);
+                    Wdm[wrow] = half_bits_to_float(hdr >> 16);
+                }
+            }
+        }
+        __syncthreads();
+        // column tile `wave` of 32 weight rows against the 32 activation rows
+        if (wave * 32 < N) {
+            const __amdgpu_buffer_rsrc_t yd = __builtin_amdgcn_make_buffer_rsrc(
+                Y + int64_t(rt) * ldy, 0, uint32_t(((rows - 1) * ldy + N) * 4), 0x00020000);
+            const i32x16 zero = {0};
+            // this lane's weight row: sub-block scales (unsigned 6-bit, or
+            // int8 for Q6_K) in sub-block order
+            const i32x4 scv = *reinterpret_cast<const i32x4*>(&Wsc[nr * 32]);
+            auto sc_of = [&](int j) -> int {
+                const uint32_t b = (uint32_t(scv[j >> 2]) >> (8 * (j & 3))) & 0xffu;
+                return Q6 ? int(int8_t(b)) : int(b);
+            };
+            // the activation code sums against the mins (Q4_K/Q5_K) or the
+            // scales (Q6_K): exact, as 64 xh + xl
+            const i32x4 bsum_b = *reinterpret_cast<const i32x4*>(Q6 ? &Wsc[nr * 32 + 16 * h] : &Wm[nr * 32 + 16 * h]);
+            const i32x16 cl = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                *reinterpret_cast<const i32x4*>(&Xsl[col * 32 + 16 * h]), bsum_b, zero, 0, 0, 0);
+            const i32x16 ch = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                *reinterpret_cast<const i32x4*>(&Xsh[col * 32 + 16 * h]), bsum_b, zero, 0, 0, 0);
+            i32x16 isum = zero;
+            // sub-block dots four steps at a time, isum in sub-block order
+#pragma unroll
+            for (int q4 = 0; q4 < 2; ++q4) {
+                i32x16 dots[4][Q6 ? 2 : 1];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int st = 4 * q4 + k;
+                    const i32x4 a = *reinterpret_cast<const i32x4*>(&Xq[col * TS_XLD + 32 * st + 16 * h]);
+                    const i32x4 w = *reinterpret_cast<const i32x4*>(&Wl[nr * TS_XLD + 32 * st + 16 * h]);
+                    if constexpr (Q6) {
+                        // each 16-value half against its own scale: the other
+                        // half's weight codes zeroed
+#pragma unroll
+                        for (int hs = 0; hs < 2; ++hs)
+                            dots[k][hs] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, h == hs ? w : i32x4{0, 0, 0, 0}, zero,
+                                                                                0, 0, 0);
+                    } else {
+                        dots[k][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, w, zero, 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int st = 4 * q4 + k;
+#pragma unroll
+                    for (int hs = 0; hs < (Q6 ? 2 : 1); ++hs) {
+                        const int scj = sc_of(Q6 ? 2 * st + hs : st);
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) isum[r] = __mul24(scj, dots[k][hs][r]) + isum[r];
+                    }
+                }
+            }
+            const float dw = Wd[nr];
+            const float dmw = Q6 ? 0.f : Wdm[nr];
+            const uint32_t base = n < N ? uint32_t(4 * h * ldy + n) * 4 : 0x80000000u;
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                const floatx4 dx = *reinterpret_cast<const floatx4*>(&Xd[8 * qd + 4 * h]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 4 * qd + i;
+                    const int xsum = __mul24(64, ch[r]) + cl[r];   // sum over sub-blocks of (mins|scales) x code sums
+                    float y;
+                    if constexpr (Q6) {
+                        const int is = isum[r] - 32 * xsum;
+                        y = 0.f + (dw * dx[i]) * float(is);
+                    } else {
+                        y = 0.f + (dw * dx[i]) * float(isum[r]);
+                        y = y - (dmw * dx[i]) * float(xsum);
+                    }
+                    const uint32_t dr = uint32_t(8 * (r >> 2) + (r & 3));
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), yd, base + dr * uint32_t(ldy) * 4, 0, 0);
+                }
+            }
+        }
+        __syncthreads();   // the codes are read before the next rows overwrite them
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Exact int8 path for the K-quants: Q4_K, Q5_K and Q6_K weights against
 // Q8_K activation codes, ggml's CPU native arithmetic (vec_dot_q*_K_q8_K)
 // on the matrix cores, with the workgroup shape of the Q8_0 path (16 waves
@@ -1297,6 +1569,47 @@ const char* launch_kq_strip_i8(int wtype, const float* x, int64_t ldx, const voi
 
 const char* tall_small_i8_variant() { return "tall_small_i8mfma_q8_0"; }
 
+bool tall_small_kq_i8_supported(int wtype, int M, int N, int K, const void* w, int64_t w_stride) {
+    return (wtype == T_Q4_K || wtype == T_Q5_K || wtype == T_Q6_K) && M >= 1 && N >= 1 && N <= kTallSmallMaxN &&
+           K == kTallSmallK && w_stride == block_bytes(wtype) && reinterpret_cast<uintptr_t>(w) % 16 == 0;
+}
+
+const char* tall_small_kq_i8_variant(int wtype) {
+    switch (wtype) {
+        case T_Q4_K: return "tall_small_i8mfma_q4_k";
+        case T_Q5_K: return "tall_small_i8mfma_q5_k";
+        case T_Q6_K: return "tall_small_i8mfma_q6_k";
+        default: return nullptr;
+    }
+}
+
+const char* launch_tall_small_kq_i8(int wtype, const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y,
+                                    int64_t ldy, int M, int N, int K, int cus, hipStream_t stream) {
+    if (!tall_small_kq_i8_supported(wtype, M, N, K, w, w_stride)) return nullptr;
+    // 32-bit output offsets, also for the dropped stores of a partial 32-row tile
+    if ((int64_t(std::max(M, 32)) * ldy + N) * 4 > 0x7fffffff) return nullptr;
+    const int grid = std::max(1, std::min(cus, (M + 15) / 16));
+    const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+#define SAMHIP_TSK(WT)                                                                                          \
+    do {                                                                                                        \
+        if (xvec)                                                                                               \
+            hipLaunchKernelGGL((tall_small_kq_i8_kernel<WT, true>), dim3(unsigned(grid)), dim3(512), 0, stream, x, \
+                               ldx, wb, y, ldy, M, N);                                                          \
+        else                                                                                                    \
+            hipLaunchKernelGGL((tall_small_kq_i8_kernel<WT, false>), dim3(unsigned(grid)), dim3(512), 0, stream, x, \
+                               ldx, wb, y, ldy, M, N);                                                          \
+    } while (0)
+    switch (wtype) {
+        case T_Q4_K: SAMHIP_TSK(T_Q4_K); break;
+        case T_Q5_K: SAMHIP_TSK(T_Q5_K); break;
+        case T_Q6_K: SAMHIP_TSK(T_Q6_K); break;
+        default: return nullptr;
+    }
+#undef SAMHIP_TSK
+    return tall_small_kq_i8_variant(wtype);
+}
+
 bool tall_small_i8_supported(int M, int N, int K, const void* w, int64_t w_stride) {
     return M >= 1 && N >= 1 && N <= kTallSmallMaxN && K == kTallSmallK && w_stride == TS_RB &&
            reinterpret_cast<uintptr_t>(w) % 16 == 0;
@@ -1305,7 +1618,8 @@ bool tall_small_i8_supported(int M, int N, int K, const void* w, int64_t w_strid
 const char* launch_tall_small_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy,
                                  int M, int N, int K, int x86, int cus, hipStream_t stream) {
     if (!tall_small_i8_supported(M, N, K, w, w_stride)) return nullptr;
-    if (int64_t(M) * ldy * 4 > 0x7fffffff) return nullptr;   // 32-bit output offsets
+    // 32-bit output offsets, also for the dropped stores of a partial 32-row tile
+    if ((int64_t(std::max(M, 32)) * ldy + N) * 4 > 0x7fffffff) return nullptr;
     // one workgroup per CU, each with an even run of rows (at least 16)
     const int grid = std::max(1, std::min(cus, (M + 15) / 16));
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;

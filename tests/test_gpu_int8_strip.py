@@ -265,6 +265,53 @@ def test_tall_small_weight_views_of_in_projection(samhip, oracle):
             assert max_row_rel_l2(y, ref) <= EXACT
 
 
+# the same shapes on K-quant weights: one 256-value super-block per row, the
+# activations packed to Q8_K, ggml's integer dot of codes and scales
+@pytest.mark.parametrize("qtype", ["Q4_K", "Q5_K", "Q6_K"])
+@pytest.mark.parametrize("shape", TALL_SMALL, ids=lambda s: "x".join(map(str, s)))
+def test_tall_small_kquant_int8_matches_native(samhip, oracle, shape, qtype):
+    m, n, k = shape
+    say("case tall small-weight kquant int8", shape, qtype)
+    gt, ot = getattr(samhip, qtype), getattr(oracle, qtype)
+    rng = np.random.default_rng(m + 5 * n + k + len(qtype) + ord(qtype[1]))
+    w = oracle.quantize(ot, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    x = (rng.standard_normal((m, k)) * np.exp(rng.uniform(-4, 4, (m, 1)))).astype(np.float32)
+    x[2, 7] = np.nan                          # packs as code 0
+    x[3, :] = 0.0                             # an all-zero row: d = 0
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
+        y = ctx.matmul(gt, w, x, x_row_stride=k + 1 if m % 2 else None)
+        assert ctx.query().kernel_variant == ("tall_small_i8mfma_" + qtype.lower()).encode()
+        again = ctx.matmul(gt, w, x)
+    ref = oracle.mul_mat_native(ot, w, x)
+    assert np.isfinite(ref).all() and np.isfinite(y).all()
+    assert not y[3].any() and not ref[3].any()
+    err = max_row_rel_l2(y, ref)
+    say(f"  max row rel L2 {err:.2e}")
+    assert err <= EXACT
+    assert np.array_equal(y, again)
+
+
+def test_tall_small_kquant_views_and_switch(samhip, oracle, monkeypatch):
+    """Row-offset views of a [768, 256] Q4_K weight take the small-weight
+    kernel; SAMHIP_TALL_SMALL=0 puts the same products back on the fused
+    kernel."""
+    say("case tall small-weight kquant views")
+    rng = np.random.default_rng(93)
+    w = oracle.quantize(oracle.Q4_K, (rng.standard_normal((768, 256)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((5184, 256)).astype(np.float32)
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
+        for s in range(3):
+            y = ctx.matmul(samhip.Q4_K, w, x, w_row_offset=256 * s, w_rows=256)
+            assert ctx.query().kernel_variant == b"tall_small_i8mfma_q4_k"
+            ref = oracle.mul_mat_native(oracle.Q4_K, w[256 * s:256 * (s + 1)], x)
+            assert max_row_rel_l2(y, ref) <= EXACT
+    monkeypatch.setenv("SAMHIP_TALL_SMALL", "0")
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
+        y = ctx.matmul(samhip.Q4_K, w, x, w_rows=256)
+        assert ctx.query().kernel_variant == b"skinny_fused_q4_k"
+        assert max_row_rel_l2(y, oracle.mul_mat_native(oracle.Q4_K, w[:256], x)) <= 1e-3
+
+
 # the exact int8 GEMM for tall Q8_0 products (SAMHIP_TALL_INT8=1): ViT fc2
 # (K = 4736) and fc1 (config 1) on sampled rows, ragged M and N, a strided
 # activation, a row-offset view, both roundings

@@ -366,9 +366,9 @@ def test_mul_mat_fused_split_k_deterministic(f16_ctx, oracle, samhip, monkeypatc
 def test_mul_mat_fused_in_projection_views(gpu_ctx, f16_ctx, oracle, qtype):
     """The fusion / decoder q, k, v products: row-offset views of a fused
     [3D, D] in-projection (D = 256) against the image tokens (M = 5184: the
-    small-weight int8 kernel for Q8_0, the fused kernel for Q4_K), the decoder queries (M = 201, in 32-row blocks on the int8
-    kernels: K = 256) and the prompt tokens (M = 33), each compared in
-    full."""
+    small-weight int8 kernels), the decoder queries (M = 201, in 32-row
+    blocks on the int8 kernels: K = 256) and the prompt tokens (M = 33),
+    each compared in full."""
     say("case fused in-projection views", qtype)
     rng = np.random.default_rng(46)
     d = 256
