@@ -1140,7 +1140,7 @@ def linear_set(sh, ctx, m, items, steps, warmup, seed=0, rotate=1):
 def other_configs(args, sh, ctx, ops, xbuf):
     """The workload's other configurations, each measured in this run with
     its own roofline: (1) the single Q8_0 ViT fc1 linear, (3) the text and
-    fusion/decoder linear streams (Q8_0 and Q4_K text), (5) the batch of 8
+    fusion/decoder linear streams (Q8_0 and Q4_K each), (5) the batch of 8
     images with mixed per-module formats (vision qkv/proj Q6_K, fc1 Q5_K, fc2
     Q8_0 at M = 41,472; its text/fusion/decoder linears are Q8_0, the streams
     of (3))."""
@@ -1158,10 +1158,11 @@ def other_configs(args, sh, ctx, ops, xbuf):
         r = text_stream(sub, sh, ctx, fmt)
         out[f"3_text_stream_{fmt}"] = {k: r[k] for k in ("metric", "value", "unit", "ms_per_step", "roofline",
                                                            "eager_ms_per_step", "kernel_ms_per_step", "cpu_baseline")}
-    log("config 3: fusion/decoder stream q8_0")
-    r = detector_stream(sub, sh, ctx, "q8_0")
-    out["3_detector_stream_q8_0"] = {k: r[k] for k in ("metric", "value", "unit", "ms_per_step", "tops", "roofline",
-                                                       "cpu_baseline")}
+    for fmt in ("q8_0", "q4_k"):
+        log(f"config 3: fusion/decoder stream {fmt}")
+        r = detector_stream(sub, sh, ctx, fmt)
+        out[f"3_detector_stream_{fmt}"] = {k: r[k] for k in ("metric", "value", "unit", "ms_per_step", "tops",
+                                                               "roofline", "cpu_baseline")}
     log("config 5: batch of 8 images, mixed formats")
     m8 = 8 * M_TOKENS
     out["5_batch8_mixed"] = {"workload": "8 images (M=41472): qkv 1024->3072 and proj 1024->1024 Q6_K, fc1 "
