@@ -507,7 +507,8 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
         if (int rc = check_q8_rhs(ctx, static_cast<const float*>(x->data), int64_t(x->nb[1] / 4), M, K)) return rc;
     }
     // tall products with a 256x256-sized weight (the fusion / decoder image
-    // tokens' q, k, v, out projections) run the fused kernel: one launch
+    // tokens' q, k, v, out projections) take one launch: the small-weight
+    // int8 kernels in native compute, the fused kernel otherwise
     const bool small_w = ctx->fused_skinny && int64_t(N) * K <= kFusedSmallW;
     // SAMHIP_TALL_DECODE=1 sends the tall products to the GEMM that decodes
     // the packed weight while staging it into LDS (gemm_kernel, one pass over
