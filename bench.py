@@ -34,7 +34,7 @@ PEAK_HBM_GBPS = 8000.0
 # rocprofv3 commands whose CSV output summarize_profiles() reads
 PROFILE_COMMANDS = {
     "trace": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/trace -o bench -- "
-             "python3 bench.py --steps 20 --warmup 5 --no-cpu-baseline --no-encoder --no-configs",
+             "python3 bench.py --steps 50 --warmup 5 --no-cpu-baseline --no-encoder --no-configs",
     "text": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/text -o bench -- "
             "python3 bench.py --workload text --steps 10 --warmup 2",
     "encoder": "rocprofv3 --kernel-trace --stats --output-format csv -d <out>/encoder -o bench -- "
@@ -253,11 +253,20 @@ def summarize_profiles(d, commands):
         path = os.path.join(d, sub, "bench_kernel_stats.csv")
         if not os.path.exists(path):
             return
+        # medians per kernel symbol from the same run's dispatch trace
+        durations = {}
+        trace = os.path.join(d, sub, "bench_kernel_trace.csv")
+        if os.path.exists(trace):
+            for r in rows(trace):
+                durations.setdefault(short(r["Kernel_Name"]), []).append(
+                    (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
         lines = [f"# {title}", "", "Command (from the repository root, `cd /tmp && export TMPDIR=/tmp` first):", "",
                  "```", command, "```", ""] + ([note, ""] if note else []) + [
-                 "| kernel | calls | avg us | min us | max us | share % |", "|---|---|---|---|---|---|"]
+                 "| kernel | calls | median us | avg us | min us | max us | share % |", "|---|---|---|---|---|---|---|"]
         for r in rows(path):
-            lines.append(f"| `{short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+            ds = durations.get(short(r["Name"]))
+            med = f"{float(np.median(ds)):.1f}" if ds else "-"
+            lines.append(f"| `{short(r['Name'])}` | {r['Calls']} | {med} | {float(r['AverageNs']) / 1e3:.1f} | "
                          f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f} |")
         with open(os.path.join(ROOT, "profiles", out_name), "w") as f:
             f.write("\n".join(lines) + "\n")
@@ -284,9 +293,10 @@ def summarize_profiles(d, commands):
         nmap = dict((nm, n) for nm, _, n in SHAPES)
         lines = ["", "Per product (same trace): every dispatch of the sweep is named by its product (each mul_mat "
                  "launches its preparation kernel and then one GEMM, in a fixed product order that each GEMM's grid "
-                 "confirms). Means over every step of the run, warmup included.", "",
-                 "| product | M | N | K | GEMM kernel | GEMM calls | GEMM avg us | GEMM min us | GEMM TFLOP/s | prep avg us "
-                 "| linear TOPS |", "|---|---|---|---|---|---|---|---|---|---|---|"]
+                 "confirms). Medians and means over every step of the run, warmup included; the rates use the "
+                 "medians.", "",
+                 "| product | M | N | K | GEMM kernel | GEMM calls | GEMM median us | GEMM avg us | GEMM min us | "
+                 "GEMM TFLOP/s | prep median us | linear TOPS |", "|---|---|---|---|---|---|---|---|---|---|---|---|"]
         seen = set()
         for label, _, k, n in [(f"{nm}:{'q8_0' if k_ % 256 else fmt}", nm, k_, n_)
                                for fmt in SWEEP_FORMATS for nm, k_, n_ in SHAPES]:
@@ -294,10 +304,11 @@ def summarize_profiles(d, commands):
             if not e or not e["gemm"] or label in seen:
                 continue
             seen.add(label)
-            g, p_ = float(np.mean(e["gemm"])), float(np.mean(e["prep"])) if e["prep"] else 0.0
+            g, p_ = float(np.median(e["gemm"])), float(np.median(e["prep"])) if e["prep"] else 0.0
             fl = 2.0 * M_TOKENS * n * k
             lines.append(f"| {label} | {M_TOKENS} | {n} | {k} | `{e['symbol']}` | {len(e['gemm'])} | {g:.1f} | "
-                         f"{min(e['gemm']):.1f} | {fl / g / 1e6:.0f} | {p_:.1f} | {fl / (g + p_) / 1e6:.0f} |")
+                         f"{float(np.mean(e['gemm'])):.1f} | {min(e['gemm']):.1f} | {fl / g / 1e6:.0f} | {p_:.1f} | "
+                         f"{fl / (g + p_) / 1e6:.0f} |")
         with open(os.path.join(ROOT, "profiles", "kernel_stats_vit_sweep_m5184.md"), "a") as f:
             f.write("\n".join(lines) + "\n")
     stats_table("text", "Kernel time, SAM 3 text-encoder linear stream at M=32 (97 mul_mat per step, Q8_0)",
