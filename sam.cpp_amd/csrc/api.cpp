@@ -136,6 +136,9 @@ struct samhip_context {
     int int8_strip = 1;         // SAMHIP_INT8_STRIP: 0 keeps M < 256 products on the fp16 kernels; 1 sends Q8_0
                                 // ones, and K-quant ones where that measured faster, to the int8 kernels; 2
                                 // sends every K-quant one there as well
+    int strip_rows = 0;         // SAMHIP_I8_STRIP_ROWS: weight rows per workgroup of the Q8_0 int8 kernel,
+                                // 32 or 64 (64 only for K slices of at most 256 values); 0: 64 where that
+                                // brings the grid into one round
     samhip_exec_info info{};
     // per-launch event trace (samhip_trace_begin / samhip_trace_end)
     struct TraceRecord {
@@ -346,6 +349,7 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
     ctx->attn_splits = std::max(0, env_int("SAMHIP_ATTN_SPLITS", 0));
     ctx->fused_max_splits = std::max(1, env_int("SAMHIP_FUSED_MAX_SPLITS", 16));
     ctx->int8_strip = env_int("SAMHIP_INT8_STRIP", 1);
+    ctx->strip_rows = env_int("SAMHIP_I8_STRIP_ROWS", 0);
     ctx->tall_small = env_int("SAMHIP_TALL_SMALL", 1) != 0;
     ctx->tall_int8 = env_int("SAMHIP_TALL_INT8", 0) != 0;
     ctx->tall_decode = env_int("SAMHIP_TALL_DECODE", 0) != 0;
@@ -560,6 +564,9 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
                                      int64_t(y->nb[1] / 4), part, M, N, K, slice_sb, ctx->stream)
                 : launch_q8_strip_i8(xp, int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), yp, int64_t(y->nb[1] / 4),
                                      part, M, N, K, slice_sb, ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0,
+                                     ctx->strip_rows == 64 ||
+                                         (ctx->strip_rows != 32 &&
+                                          i8_strip_two_tiles_preferred(M, N, K, slice_sb, ctx->cus)),
                                      ctx->stream);
             if (!ok) return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no int8 strip kernel for this shape");
             HIP_TRY(hipGetLastError(), "int8 strip launch");

@@ -301,8 +301,22 @@ inline size_t i8_strip_part_bytes(int M, int N, int K, int slice_sb) {
     return S > 1 ? size_t(S) * size_t(M) * size_t(N) * 4 : 0;
 }
 const char* q8_strip_i8_variant();
+// two_tiles: 64 weight rows per workgroup when a K slice holds at most 256
+// values (two 32-row column tiles; the same bits as 32 rows per workgroup).
+// Taken where 32-row workgroups need a second round of the chip and 64-row
+// ones fit one (the decoder's M = 201 FFN expansion, 256 -> 2048: 448
+// workgroups become 224).  In the streams' replayed graphs, with each
+// product's weight read cold, it measured slower where both fit one round
+// (M = 201, 256x256: 0.241 -> 0.252 ms per step; text out_proj, four
+// 256-wide slices: text stream 476 -> 472 GB/s).
+inline bool i8_strip_two_tiles_preferred(int M, int N, int K, int slice_sb, int cus) {
+    if (slice_sb != 1 && K > 256) return false;
+    const int64_t blocks = int64_t((M + 31) / 32) * ((K + 256 * slice_sb - 1) / (256 * slice_sb));
+    return blocks * ((N + 31) / 32) > cus && blocks * ((N + 63) / 64) <= cus;
+}
 const char* launch_q8_strip_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy,
-                               float* part, int M, int N, int K, int slice_sb, int x86, hipStream_t stream);
+                               float* part, int M, int N, int K, int slice_sb, int x86, bool two_tiles,
+                               hipStream_t stream);
 // The same for Q4_K / Q5_K / Q6_K weights against Q8_K activation codes
 // (K a multiple of 256; same partial-sum buffer, K slices of 256, 512 or 1024
 // values).  Taken by default where it measured faster than the fused kernel

@@ -517,7 +517,8 @@ __global__ __launch_bounds__(1024) void strip_skinny_kernel(const float* __restr
 // block per instruction: the weight codes are the B operand as stored, no
 // decode), and the block adds fma(float(dot), d_w * d_x, acc) in F32 as
 // ggml's vec_dot_q8_0_q8_0 does; only the order of the block sums differs.
-// One workgroup of 16 waves per 32 weight rows, 32 activation rows and K
+// One workgroup of 16 waves per 32 weight rows (CT = 1) or, for slices of
+// at most 256 values, per 64 weight rows (CT = 2), 32 activation rows and K
 // slice of up to 1024 values:
 //  1. the strip's packed bytes for the slice go to LDS with coalesced dword
 //     loads (rows of an odd dword count: conflict-free reads);
@@ -525,32 +526,45 @@ __global__ __launch_bounds__(1024) void strip_skinny_kernel(const float* __restr
 //     (ggml's from_float, x86 or reference rounding) into LDS codes and
 //     scales, so each workgroup packs its slice once, with one lane per
 //     block and no cross-lane reductions;
-//  3. wave w multiplies blocks w, w + 16 of the slice;
-//  4. the 16 partial tiles are added in LDS in wave order.
+//  3. CT = 1: wave w multiplies blocks w, w + 16 of the slice; CT = 2: wave
+//     w multiplies block w % 8 of column tile w / 8, so all 16 waves have a
+//     block and the activation slice is packed once per 64 weight rows;
+//  4. each column tile's partial tiles are added in LDS in wave order.
 // The host picks the slice width SL (256, 512 or 1024 values).  With more
 // than one slice each workgroup writes its partial sums, which
-// splitk_reduce_kernel adds in slice order.
+// splitk_reduce_kernel adds in slice order.  Timed back to back on MI355X
+// with the weight warm in L2: CT = 2 takes 3.85 against 7.3 us per launch at
+// M = 201, N = 2048, K = 256 (224 workgroups in one round instead of 448 in
+// two) and 3.6 against 4.2 us at M = 201 and 33 with N = K = 256; in the
+// streams, with each product's weight read cold, only the first gained, so
+// the host takes CT = 2 where it brings the grid into one round.  Both
+// forms give the same bits.
 // ---------------------------------------------------------------------------
 constexpr int I8_XLD = kI8SliceK + 16;                                // bytes per LDS code row
 constexpr int I8_WDW = (((kI8SliceK / 32) * 34 + 2 + 3) / 4) | 1;    // dwords per LDS weight row
+constexpr int I8_WDW256 = ((8 * 34 + 2 + 3) / 4) | 1;                 // the same for slices of 256 values
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
-template <bool X86, bool XVEC>
+template <bool X86, bool XVEC, int CT>
 __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restrict__ X, int64_t ldx,
                                                            const uint8_t* __restrict__ W, int64_t w_stride,
                                                            float* __restrict__ Y, int64_t ldy, float* __restrict__ part,
                                                            int M, int N, int K, int RG, int S, int SL) {
 #pragma clang fp contract(off)
+    static_assert(CT == 1 || CT == 2, "one or two column tiles");
+    constexpr int WP = CT == 2 ? I8_WDW256 : I8_WDW;   // dword pitch of an LDS weight row
+    constexpr int TPR = 32 / CT;                        // threads per weight row in the load
+    static_assert(32 * CT * WP <= 32 * I8_WDW, "the weight rows fit the LDS strip");
     __shared__ __attribute__((aligned(16))) int8_t Xq[32 * I8_XLD];
     __shared__ __attribute__((aligned(16))) float Xd[kI8SliceK / 32][32];
     __shared__ __attribute__((aligned(16))) uint32_t Ws[32 * I8_WDW];
     __shared__ __attribute__((aligned(16))) float red[16 * 16 * 64];
-    constexpr int RI = (I8_WDW + 31) / 32;
+    constexpr int RI = (WP + TPR - 1) / TPR;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int rg = blockIdx.x % RG, sp = (blockIdx.x / RG) % S, mb = blockIdx.x / (RG * S);
-    const int n0 = rg * 32, k0 = sp * SL;
+    const int n0 = rg * 32 * CT, k0 = sp * SL;
     const int nb = min(SL, K - k0) / 32;   // Q8_0 blocks in this slice (SL <= kI8SliceK)
     // this workgroup's block of 32 activation rows
     const int m0 = mb * 32, Mall = M;
@@ -561,15 +575,15 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
     // 1. packed weight bytes: thread (r, c) loads dwords c, c + 32, ... of
     // row r; the activation loads are issued before these go to LDS, so the
     // two latencies overlap (7.57 against 7.88 us per K = 1024 product)
-    const int wr_r = tid >> 5, wr_c = tid & 31;
+    const int wr_r = tid / TPR, wr_c = tid % TPR;
     uint32_t wr[RI];
     {
         const uint8_t* rowp = W + int64_t(min(n0 + wr_r, N - 1)) * w_stride + int64_t(k0 / 32) * 34;
         const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(rowp) & 3);
         const uint32_t* src = reinterpret_cast<const uint32_t*>(rowp - sh);
-        const int ndw = int((sh + 34 * nb + 3) >> 2);
+        const int ndw = int((sh + 34 * nb + 3) >> 2);   // <= WP (CT = 2: nb <= 8)
 #pragma unroll
-        for (int i = 0; i < RI; ++i) wr[i] = wr_c + 32 * i < ndw ? src[wr_c + 32 * i] : 0u;
+        for (int i = 0; i < RI; ++i) wr[i] = wr_c + TPR * i < ndw ? src[wr_c + TPR * i] : 0u;
     }
     // 2. activation rows -> Q8_0 codes and scales: wave w takes rows 2 w and
     // 2 w + 1 of the block, in SL / 256 passes of 512 values; lane l holds 8
@@ -599,7 +613,7 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
         }
 #pragma unroll
         for (int i = 0; i < RI; ++i)
-            if (wr_c + 32 * i < I8_WDW) Ws[wr_r * I8_WDW + wr_c + 32 * i] = wr[i];
+            if (wr_c + TPR * i < WP) Ws[wr_r * WP + wr_c + TPR * i] = wr[i];
 #pragma unroll
         for (int p = 0; p < kI8SliceK / 256; ++p) {
             if (p >= passes) break;
@@ -623,16 +637,19 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
     }
     __syncthreads();
 
-    // 3. blocks wave, wave + 16 of the slice: activation row (A) and weight
-    // row (B) codes, lanes 32h.. taking bytes 16h..16h+15 of both
+    // 3. blocks wave, wave + 16 of the slice (CT = 2: block wave % 8 of
+    // column tile wave / 8): activation row (A) and weight row (B) codes,
+    // lanes 32h.. taking bytes 16h..16h+15 of both
     const int col = lane & 31, h = lane >> 5;
-    const int wshift = int((reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + col, N - 1)) * w_stride) + k0 / 32 * 34) & 3);
-    const uint32_t* wrow = &Ws[col * I8_WDW];
+    const int tile = CT == 2 ? wave >> 3 : 0;
+    const int wn = n0 + 32 * tile + col;
+    const int wshift = int((reinterpret_cast<uintptr_t>(W + int64_t(min(wn, N - 1)) * w_stride) + k0 / 32 * 34) & 3);
+    const uint32_t* wrow = &Ws[(32 * tile + col) * WP];
     floatx16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
     const i32x16 zero = {0};
-    for (int b = wave; b < nb; b += 16) {
+    for (int b = CT == 2 ? wave & 7 : wave; b < nb; b += 16 / CT) {
         const i32x4 a = *reinterpret_cast<const i32x4*>(&Xq[col * I8_XLD + 32 * b + 16 * h]);
         // the row's bytes start at byte wshift (0 or 2) of its first dword;
         // every read stays inside the row's dwords
@@ -654,18 +671,22 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
                 acc[4 * qd + i] = __builtin_fmaf(dw * dx[i], float(dot[4 * qd + i]), acc[4 * qd + i]);
         }
     }
-    // 4. partial tiles in wave order
+    // 4. partial tiles in wave order, per column tile
 #pragma unroll
     for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
     __syncthreads();
     const int m = tid >> 5, n = tid & 31;
     const int src = (4 * (m >> 3) + (m & 3)) * 64 + n + 32 * ((m >> 2) & 1);
-    float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < 16; ++w) v += red[w * 16 * 64 + src];
-    if (m < M && n0 + n < N) {
-        if (part) part[(int64_t(sp) * Mall + m0 + m) * N + n0 + n] = v;
-        else Y[int64_t(m) * ldy + n0 + n] = v;
+    for (int t = 0; t < CT; ++t) {
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < 16 / CT; ++w) v += red[(t * (16 / CT) + w) * 16 * 64 + src];
+        const int nn = n0 + 32 * t + n;
+        if (m < M && nn < N) {
+            if (part) part[(int64_t(sp) * Mall + m0 + m) * N + nn] = v;
+            else Y[int64_t(m) * ldy + nn] = v;
+        }
     }
 }
 
@@ -1492,25 +1513,34 @@ const char* launch_strip_skinny(int wtype, bool f16, const float* x, int64_t ldx
 const char* q8_strip_i8_variant() { return "skinny_i8mfma_q8_0"; }
 
 const char* launch_q8_strip_i8(const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y, int64_t ldy,
-                               float* part, int M, int N, int K, int slice_sb, int x86, hipStream_t stream) {
+                               float* part, int M, int N, int K, int slice_sb, int x86, bool two_tiles,
+                               hipStream_t stream) {
     if (M < 1 || N < 1 || K < 32 || K % 32) return nullptr;
     if (slice_sb != 1 && slice_sb != 2 && slice_sb != kI8SliceK / 256) return nullptr;
     const int SL = 256 * slice_sb;
-    const int RG = (N + 31) / 32, S = (K + SL - 1) / SL, MB = (M + 31) / 32;
+    // two column tiles per workgroup when a slice holds at most 256 values
+    const int CT = (SL == 256 || K <= 256) && two_tiles ? 2 : 1;
+    const int RG = (N + 32 * CT - 1) / (32 * CT), S = (K + SL - 1) / SL, MB = (M + 31) / 32;
     if (S > 1 && !part) return nullptr;
     if (int64_t(RG) * S * MB > kMaxWorkgroups1024) return nullptr;
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     float* pt = S > 1 ? part : nullptr;
     const dim3 grid(unsigned(RG * S * MB)), block(1024);
-#define SAMHIP_I8(X86V, XV)                                                                                    \
-    hipLaunchKernelGGL((q8_strip_i8_kernel<X86V, XV>), grid, block, 0, stream, x, ldx, wb, w_stride, y, ldy, pt, M, N, \
-                       K, RG, S, SL)
+#define SAMHIP_I8(X86V, XV, CTV)                                                                                   \
+    hipLaunchKernelGGL((q8_strip_i8_kernel<X86V, XV, CTV>), grid, block, 0, stream, x, ldx, wb, w_stride, y, ldy, pt, \
+                       M, N, K, RG, S, SL)
+#define SAMHIP_I8_CT(X86V, XV)                              \
+    do {                                                    \
+        if (CT == 2) SAMHIP_I8(X86V, XV, 2);                \
+        else SAMHIP_I8(X86V, XV, 1);                        \
+    } while (0)
     if (x86) {
-        if (xvec) SAMHIP_I8(true, true); else SAMHIP_I8(true, false);
+        if (xvec) SAMHIP_I8_CT(true, true); else SAMHIP_I8_CT(true, false);
     } else {
-        if (xvec) SAMHIP_I8(false, true); else SAMHIP_I8(false, false);
+        if (xvec) SAMHIP_I8_CT(false, true); else SAMHIP_I8_CT(false, false);
     }
+#undef SAMHIP_I8_CT
 #undef SAMHIP_I8
     if (S > 1) {
         const int64_t outs = int64_t(M) * N;

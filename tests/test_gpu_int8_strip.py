@@ -58,6 +58,38 @@ def test_int8_strip_matches_native(samhip, oracle, shape, rounding):
     assert np.array_equal(y, again)                 # deterministic, strided or not
 
 
+def test_int8_strip_two_column_tiles_same_bits(samhip, oracle, monkeypatch):
+    """SAMHIP_I8_STRIP_ROWS=64 runs 64 weight rows per workgroup (two 32-row
+    column tiles, all 16 waves busy) wherever the K slice holds at most 256
+    values, =32 keeps 32 rows, and the default takes 64 only where that
+    brings the grid into one round (M = 201, N = 2048, K = 256).  All give
+    the same bits: K = 256 products with one and several row blocks, ragged
+    N (one row, 33 rows: the second tile partly or wholly past N), K = 64,
+    and 256-wide slices of K = 1024 with the reduce launch."""
+    say("case int8 strip two column tiles")
+    rng = np.random.default_rng(78)
+    shapes = [(201, 256, 256), (201, 2048, 256), (33, 256, 256), (3, 1, 256), (17, 33, 256), (64, 40, 64),
+              (32, 1024, 1024), (97, 33, 1024)]
+    cases = []
+    for m, n, k in shapes:
+        w = oracle.quantize(oracle.Q8_0, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        x = (rng.standard_normal((m, k)) * np.exp(rng.uniform(-4, 4, (m, 1)))).astype(np.float32)
+        cases.append((w, x))
+    outs = {}
+    for rows in ("64", "32", None):
+        if rows:
+            monkeypatch.setenv("SAMHIP_I8_STRIP_ROWS", rows)
+        else:
+            monkeypatch.delenv("SAMHIP_I8_STRIP_ROWS", raising=False)
+        with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
+            outs[rows] = [ctx.matmul(samhip.Q8_0, w, x) for w, x in cases]
+            assert ctx.query().kernel_variant == b"skinny_i8mfma_q8_0"
+    for i, ((w, x), shp) in enumerate(zip(cases, shapes)):
+        assert np.array_equal(outs["64"][i], outs["32"][i]), shp
+        assert np.array_equal(outs[None][i], outs["32"][i]), shp
+        assert max_row_rel_l2(outs["64"][i], oracle.mul_mat_native(oracle.Q8_0, w, x)) <= EXACT, shp
+
+
 def test_int8_strip_views_and_reference_probe(gpu_ctx, oracle, samhip):
     """Row-offset views of a fused in-projection and the reference's probe
     fixture (tools/benchmark/cpu_quantized_matmul.hpp:63-75) with its outlier
