@@ -136,7 +136,7 @@ struct samhip_context {
     int int8_strip = 1;         // SAMHIP_INT8_STRIP: 0 keeps M < 256 products on the fp16 kernels; 1 sends Q8_0
                                 // ones, and K-quant ones where that measured faster, to the int8 kernels; 2
                                 // sends every K-quant one there as well
-    int strip_rows = 0;         // SAMHIP_I8_STRIP_ROWS: weight rows per workgroup of the Q8_0 int8 kernel,
+    int strip_rows = 0;         // SAMHIP_I8_STRIP_ROWS: weight rows per workgroup of the int8 strip kernels,
                                 // 32 or 64 (64 only for K slices of at most 256 values); 0: 64 where that
                                 // brings the grid into one round
     samhip_exec_info info{};
@@ -519,7 +519,7 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
     // the weight) instead of weight decode in the preparation + fp16 GEMM
     const bool tall = M >= ctx->tall_m && gemm_f16_supported(M, N, K, K, K) && !small_w && !ctx->tall_decode;
     const bool kquant = (w->type == T_Q4_K || w->type == T_Q5_K || w->type == T_Q6_K) &&
-                        (ctx->int8_strip == 2 || kq_strip_i8_preferred(w->type, M, N, K, ctx->cus));
+                        (ctx->int8_strip == 2 || kq_strip_i8_preferred(w->type, M, N, K, ctx->cus, ctx->strip_rows != 32));
     const bool tall_small_q8 = w->type == T_Q8_0 && tall_small_i8_supported(M, N, K, w->data, int64_t(w->nb[1]));
     const bool tall_small_kq = tall_small_kq_i8_supported(w->type, M, N, K, w->data, int64_t(w->nb[1]));
     if (small_w && M >= kStripMaxM && (tall_small_q8 || tall_small_kq) && ctx->compute == SAMHIP_COMPUTE_Q8_NATIVE &&
@@ -559,15 +559,14 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
             const float* xp = static_cast<const float*>(x->data);
             float* yp = static_cast<float*>(y->data);
             float* part = static_cast<float*>(ctx->staging);
+            const bool two_tiles = ctx->strip_rows == 64 ||
+                                   (ctx->strip_rows != 32 && i8_strip_two_tiles_preferred(M, N, K, slice_sb, ctx->cus));
             const char* ok = kquant
                 ? launch_kq_strip_i8(w->type, xp, int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), yp,
-                                     int64_t(y->nb[1] / 4), part, M, N, K, slice_sb, ctx->stream)
+                                     int64_t(y->nb[1] / 4), part, M, N, K, slice_sb, two_tiles, ctx->stream)
                 : launch_q8_strip_i8(xp, int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), yp, int64_t(y->nb[1] / 4),
                                      part, M, N, K, slice_sb, ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0,
-                                     ctx->strip_rows == 64 ||
-                                         (ctx->strip_rows != 32 &&
-                                          i8_strip_two_tiles_preferred(M, N, K, slice_sb, ctx->cus)),
-                                     ctx->stream);
+                                     two_tiles, ctx->stream);
             if (!ok) return fail(SAMHIP_ERR_UNSUPPORTED, "mul_mat: no int8 strip kernel for this shape");
             HIP_TRY(hipGetLastError(), "int8 strip launch");
             return SAMHIP_OK;

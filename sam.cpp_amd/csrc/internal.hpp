@@ -329,13 +329,20 @@ const char* launch_q8_strip_i8(const float* x, int64_t ldx, const void* w, int64
 // 7.7 us; with 512-wide slices N = 4096: 9.8 against 10.5 us).  A second
 // round of workgroups makes it slower (Q4_K M = 201, N = 2048, K = 256: 9.2
 // against 7.0 us).
-inline bool kq_strip_i8_preferred(int wtype, int M, int N, int K, int cus) {
+// With K = 256 it also takes the products that fit one round only with 64
+// weight rows per workgroup (the decoder's M = 201 FFN expansion, 256 ->
+// 2048), two_tiles below.
+inline bool kq_strip_i8_preferred(int wtype, int M, int N, int K, int cus, bool allow_two_tiles = true) {
     const int slice = wtype == T_Q6_K ? 256 : kI8SliceK;
-    return int64_t((N + 31) / 32) * ((M + 31) / 32) * ((K + slice - 1) / slice) <= cus;
+    return int64_t((N + 31) / 32) * ((M + 31) / 32) * ((K + slice - 1) / slice) <= cus ||
+           (allow_two_tiles && K == 256 && i8_strip_two_tiles_preferred(M, N, K, 1, cus));
 }
 const char* kq_strip_i8_variant(int wtype);
+// two_tiles: 64 weight rows per workgroup when a K slice holds one
+// super-block (two 32-row column tiles; the same bits as 32 rows)
 const char* launch_kq_strip_i8(int wtype, const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y,
-                               int64_t ldy, float* part, int M, int N, int K, int slice_sb, hipStream_t stream);
+                               int64_t ldy, float* part, int M, int N, int K, int slice_sb, bool two_tiles,
+                               hipStream_t stream);
 const char* strip_skinny_variant(int wtype);
 const char* launch_strip_skinny(int wtype, bool f16, const float* x, int64_t ldx, const void* w, int64_t w_stride,
                                 float* y, int64_t ldy, float* part, int M, int N, int K, int x86, hipStream_t stream);

@@ -1159,18 +1159,25 @@ __global__ __launch_bounds__(512) void tall_small_kq_i8_kernel(const float* __re
 //  4. the 16 partial tiles are added in LDS in wave order.
 // The host picks the slice width (SK super-blocks of 256 values: 1, 2 or 4).
 // With more than one slice each workgroup writes its partial sums, which
-// splitk_reduce_kernel adds in slice order.
+// splitk_reduce_kernel adds in slice order.  With slices of one super-block
+// a workgroup can take 64 weight rows instead (CT = 2, as in the Q8_0
+// kernel: wave w takes step w % 8 of column tile w / 8).
 // ---------------------------------------------------------------------------
 template <int WT>
 constexpr int kq_wdw() { return (((kI8SliceK / 256) * block_bytes(WT) + 2 + 3) / 4) | 1; }
+template <int WT>
+constexpr int kq_wdw1() { return ((block_bytes(WT) + 2 + 3) / 4) | 1; }   // one super-block
 
-template <int WT, bool XVEC>
+template <int WT, bool XVEC, int CT>
 __global__ __launch_bounds__(1024) void kq_strip_i8_kernel(const float* __restrict__ X, int64_t ldx,
                                                            const uint8_t* __restrict__ W, int64_t w_stride,
                                                            float* __restrict__ Y, int64_t ldy, float* __restrict__ part,
                                                            int M, int N, int K, int RG, int S, int SK) {
 #pragma clang fp contract(off)
-    constexpr int WDW = kq_wdw<WT>();
+    static_assert(CT == 1 || CT == 2, "one or two column tiles");
+    constexpr int WDW = CT == 2 ? kq_wdw1<WT>() : kq_wdw<WT>();   // dword pitch of an LDS weight row
+    constexpr int TPR = 32 / CT;                                  // threads per weight row in the load
+    static_assert(32 * CT * WDW <= 32 * kq_wdw<WT>(), "the weight rows fit the LDS strip");
     constexpr int BB = block_bytes(WT);
     constexpr int SUB = WT == T_Q6_K ? 16 : 32;     // values per weight scale
     constexpr int SPB = 256 / SUB;                  // sub-blocks per super-block
@@ -1178,21 +1185,21 @@ __global__ __launch_bounds__(1024) void kq_strip_i8_kernel(const float* __restri
     __shared__ __attribute__((aligned(16))) int8_t Xq[32 * I8_XLD];
     __shared__ __attribute__((aligned(16))) float Xd[XSB][32];
     __shared__ __attribute__((aligned(16))) float Xs[XSB * SPB][32];   // code sums per sub-block and row
-    __shared__ __attribute__((aligned(16))) uint32_t Ws[32 * WDW];
+    __shared__ __attribute__((aligned(16))) uint32_t Ws[32 * kq_wdw<WT>()];
     __shared__ __attribute__((aligned(16))) float red[16 * 16 * 64];
-    constexpr int RI = (WDW + 31) / 32;
+    constexpr int RI = (WDW + TPR - 1) / TPR;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int rg = blockIdx.x % RG, sp = (blockIdx.x / RG) % S, mb = blockIdx.x / (RG * S);
-    const int n0 = rg * 32, k0 = sp * 256 * SK;
-    const int nsb = min(256 * SK, K - k0) / 256;    // super-blocks in this slice (SK <= XSB)
+    const int n0 = rg * 32 * CT, k0 = sp * 256 * SK;
+    const int nsb = min(256 * SK, K - k0) / 256;    // super-blocks in this slice (SK <= XSB; CT = 2: 1)
     const int m0 = mb * 32, Mall = M;
     X += int64_t(m0) * ldx;
     Y += int64_t(m0) * ldy;
     M = min(M - m0, 32);
 
-    // 1. packed weight bytes: thread (r, c) loads dwords c, c + 32, ... of row r
-    const int wr_r = tid >> 5, wr_c = tid & 31;
+    // 1. packed weight bytes: thread (r, c) loads dwords c, c + TPR, ... of row r
+    const int wr_r = tid / TPR, wr_c = tid % TPR;
     uint32_t wr[RI];
     {
         const uint8_t* rowp = W + int64_t(min(n0 + wr_r, N - 1)) * w_stride + int64_t(k0 / 256) * BB;
@@ -1200,7 +1207,7 @@ __global__ __launch_bounds__(1024) void kq_strip_i8_kernel(const float* __restri
         const uint32_t* src = reinterpret_cast<const uint32_t*>(rowp - sh);
         const int ndw = int((sh + BB * nsb + 3) >> 2);
 #pragma unroll
-        for (int i = 0; i < RI; ++i) wr[i] = wr_c + 32 * i < ndw ? src[wr_c + 32 * i] : 0u;
+        for (int i = 0; i < RI; ++i) wr[i] = wr_c + TPR * i < ndw ? src[wr_c + TPR * i] : 0u;
     }
     // 2. activation block (row m, super-block b) by the 32 lanes of half hu
     // of a wave, 8 values per lane: unit u = m * nsb + b = 32 pass + 2 wave + hu
@@ -1225,7 +1232,7 @@ __global__ __launch_bounds__(1024) void kq_strip_i8_kernel(const float* __restri
     }
 #pragma unroll
     for (int i = 0; i < RI; ++i)
-        if (wr_c + 32 * i < WDW) Ws[wr_r * WDW + wr_c + 32 * i] = wr[i];
+        if (wr_c + TPR * i < WDW) Ws[wr_r * WDW + wr_c + TPR * i] = wr[i];
 #pragma unroll
     for (int p = 0; p < XSB; ++p) {
         if (p >= nsb) break;
@@ -1252,18 +1259,21 @@ __global__ __launch_bounds__(1024) void kq_strip_i8_kernel(const float* __restri
     }
     __syncthreads();
 
-    // 3. this wave's 32-value steps; the activation rows of element r are
-    // 8 (r / 4) + 4 h + r % 4, the weight row is col
+    // 3. this wave's 32-value steps (CT = 2: step wave % 8 of column tile
+    // wave / 8); the activation rows of element r are 8 (r / 4) + 4 h + r % 4,
+    // the weight row is the tile's row col
     const int col = lane & 31, h = lane >> 5;
-    const int wshift =
-        int((reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + col, N - 1)) * w_stride) + (k0 / 256) * BB) & 3);
-    const LdsRow wrow{&Ws[col * WDW], wshift};
+    const int tile = CT == 2 ? wave >> 3 : 0;
+    const int wshift = int((reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + 32 * tile + col, N - 1)) * w_stride) +
+                            (k0 / 256) * BB) &
+                           3);
+    const LdsRow wrow{&Ws[(32 * tile + col) * WDW], wshift};
     floatx16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
     const i32x16 zero = {0};
     const int nst = 8 * nsb;   // 32-value steps in the slice
-    for (int st = wave; st < nst; st += 16) {
+    for (int st = CT == 2 ? wave & 7 : wave; st < nst; st += 16 / CT) {
         const int b = st >> 3, jj = st & 7;
         const i32x4 a = *reinterpret_cast<const i32x4*>(&Xq[col * I8_XLD + 32 * st + 16 * h]);
         floatx4 dx[4];
@@ -1323,18 +1333,22 @@ __global__ __launch_bounds__(1024) void kq_strip_i8_kernel(const float* __restri
             }
         }
     }
-    // 4. partial tiles in wave order
+    // 4. partial tiles in wave order, per column tile
 #pragma unroll
     for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
     __syncthreads();
     const int m = tid >> 5, n = tid & 31;
     const int src = (4 * (m >> 3) + (m & 3)) * 64 + n + 32 * ((m >> 2) & 1);
-    float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < 16; ++w) v += red[w * 16 * 64 + src];
-    if (m < M && n0 + n < N) {
-        if (part) part[(int64_t(sp) * Mall + m0 + m) * N + n0 + n] = v;
-        else Y[int64_t(m) * ldy + n0 + n] = v;
+    for (int t = 0; t < CT; ++t) {
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < 16 / CT; ++w) v += red[(t * (16 / CT) + w) * 16 * 64 + src];
+        const int nn = n0 + 32 * t + n;
+        if (m < M && nn < N) {
+            if (part) part[(int64_t(sp) * Mall + m0 + m) * N + nn] = v;
+            else Y[int64_t(m) * ldy + nn] = v;
+        }
     }
 }
 
@@ -1560,33 +1574,39 @@ const char* kq_strip_i8_variant(int wtype) {
 }
 
 template <int WT>
-void launch_kq_strip_wt(bool xvec, const float* x, int64_t ldx, const uint8_t* w, int64_t w_stride, float* y,
+void launch_kq_strip_wt(bool xvec, int CT, const float* x, int64_t ldx, const uint8_t* w, int64_t w_stride, float* y,
                         int64_t ldy, float* part, int M, int N, int K, int RG, int S, int MB, int SK,
                         hipStream_t stream) {
     const dim3 grid(unsigned(RG * S * MB)), block(1024);
-    if (xvec)
-        hipLaunchKernelGGL((kq_strip_i8_kernel<WT, true>), grid, block, 0, stream, x, ldx, w, w_stride, y, ldy, part,
-                           M, N, K, RG, S, SK);
-    else
-        hipLaunchKernelGGL((kq_strip_i8_kernel<WT, false>), grid, block, 0, stream, x, ldx, w, w_stride, y, ldy, part,
-                           M, N, K, RG, S, SK);
+#define SAMHIP_KQ(XV, CTV)                                                                                          \
+    hipLaunchKernelGGL((kq_strip_i8_kernel<WT, XV, CTV>), grid, block, 0, stream, x, ldx, w, w_stride, y, ldy, part, \
+                       M, N, K, RG, S, SK)
+    if (xvec) {
+        if (CT == 2) SAMHIP_KQ(true, 2); else SAMHIP_KQ(true, 1);
+    } else {
+        if (CT == 2) SAMHIP_KQ(false, 2); else SAMHIP_KQ(false, 1);
+    }
+#undef SAMHIP_KQ
 }
 
 const char* launch_kq_strip_i8(int wtype, const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y,
-                               int64_t ldy, float* part, int M, int N, int K, int slice_sb, hipStream_t stream) {
+                               int64_t ldy, float* part, int M, int N, int K, int slice_sb, bool two_tiles,
+                               hipStream_t stream) {
     if (M < 1 || N < 1 || K < 256 || K % 256) return nullptr;
     if (slice_sb != 1 && slice_sb != 2 && slice_sb != kI8SliceK / 256) return nullptr;
     const int SK = slice_sb;
-    const int RG = (N + 31) / 32, S = (K + 256 * SK - 1) / (256 * SK), MB = (M + 31) / 32;
+    // two column tiles per workgroup when a slice holds one super-block
+    const int CT = (SK == 1 || K == 256) && two_tiles ? 2 : 1;
+    const int RG = (N + 32 * CT - 1) / (32 * CT), S = (K + 256 * SK - 1) / (256 * SK), MB = (M + 31) / 32;
     if (S > 1 && !part) return nullptr;
     if (int64_t(RG) * S * MB > kMaxWorkgroups1024) return nullptr;
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     float* pt = S > 1 ? part : nullptr;
     switch (wtype) {
-        case T_Q4_K: launch_kq_strip_wt<T_Q4_K>(xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
-        case T_Q5_K: launch_kq_strip_wt<T_Q5_K>(xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
-        case T_Q6_K: launch_kq_strip_wt<T_Q6_K>(xvec, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
+        case T_Q4_K: launch_kq_strip_wt<T_Q4_K>(xvec, CT, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
+        case T_Q5_K: launch_kq_strip_wt<T_Q5_K>(xvec, CT, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
+        case T_Q6_K: launch_kq_strip_wt<T_Q6_K>(xvec, CT, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
         default: return nullptr;
     }
     if (S > 1) {

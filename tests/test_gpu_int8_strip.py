@@ -223,14 +223,16 @@ def test_kquant_int8_default_routing(samhip, oracle):
     row groups x 32-row blocks x K slices fits one round of the chip's CUs,
     with 1024-wide slices for Q4_K / Q5_K (the text encoder's M = 32
     products, the decoder's 256x256 products at M = 201 and 33) and 256-wide
-    ones for Q6_K; a second round (the decoder's M = 201 FFN expansion to
-    2048) stays on the fused kernel."""
+    ones for Q6_K, and with K = 256 those that fit one round with 64 weight
+    rows per workgroup (the decoder's M = 201 FFN expansion to 2048); the
+    rest (M = 201, N = 4096, K = 256; Q6_K M = 32, N = 4096, K = 1024) stays
+    on the fused kernel."""
     rng = np.random.default_rng(5)
     with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
         for qt, m, n, k, exact in ((oracle.Q4_K, 201, 256, 256, True), (oracle.Q4_K, 33, 256, 256, True),
                                    (oracle.Q4_K, 32, 1024, 1024, True), (oracle.Q5_K, 32, 1024, 4096, True),
-                                   (oracle.Q4_K, 201, 2048, 256, False), (oracle.Q6_K, 32, 1024, 1024, True),
-                                   (oracle.Q6_K, 32, 4096, 1024, False)):
+                                   (oracle.Q4_K, 201, 2048, 256, True), (oracle.Q4_K, 201, 4096, 256, False),
+                                   (oracle.Q6_K, 32, 1024, 1024, True), (oracle.Q6_K, 32, 4096, 1024, False)):
             w = oracle.quantize(qt, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
             x = rng.standard_normal((m, k)).astype(np.float32)
             y = ctx.matmul(qt, w, x)
@@ -238,6 +240,36 @@ def test_kquant_int8_default_routing(samhip, oracle):
             tname = {oracle.Q4_K: "q4_k", oracle.Q5_K: "q5_k", oracle.Q6_K: "q6_k"}[qt]
             assert name == ("skinny_i8mfma_" if exact else "skinny_fused_") + tname, (name, m, n, k)
             assert max_row_rel_l2(y, oracle.mul_mat_native(qt, w, x)) <= (EXACT if exact else 1e-3)
+
+
+@pytest.mark.parametrize("qtype", ["q4_K", "q5_K", "q6_K"])
+def test_kquant_int8_strip_two_column_tiles_same_bits(samhip, oracle, monkeypatch, qtype):
+    """The K-quant int8 kernel with 64 weight rows per workgroup
+    (SAMHIP_I8_STRIP_ROWS=64, slices of one super-block) gives the bits of
+    32 rows (=32): one and several row blocks, ragged N, and 256-wide slices
+    of K = 1024 with the reduce launch (SAMHIP_INT8_STRIP=2 keeps every
+    product on the int8 kernel)."""
+    say("case kquant int8 strip two column tiles", qtype)
+    qt = {"q4_K": oracle.Q4_K, "q5_K": oracle.Q5_K, "q6_K": oracle.Q6_K}[qtype]
+    gt = {"q4_K": samhip.Q4_K, "q5_K": samhip.Q5_K, "q6_K": samhip.Q6_K}[qtype]
+    rng = np.random.default_rng(79)
+    shapes = [(201, 256, 256), (201, 2048, 256), (33, 256, 256), (3, 1, 256), (17, 33, 256), (32, 1024, 1024),
+              (97, 33, 1024)]
+    cases = []
+    for m, n, k in shapes:
+        w = oracle.quantize(qt, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        x = (rng.standard_normal((m, k)) * np.exp(rng.uniform(-4, 4, (m, 1)))).astype(np.float32)
+        cases.append((w, x))
+    monkeypatch.setenv("SAMHIP_INT8_STRIP", "2")
+    outs = {}
+    for rows in ("64", "32"):
+        monkeypatch.setenv("SAMHIP_I8_STRIP_ROWS", rows)
+        with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
+            outs[rows] = [ctx.matmul(gt, w, x) for w, x in cases]
+            assert ctx.query().kernel_variant == ("skinny_i8mfma_" + qtype.lower()).encode()
+    for i, ((w, x), shp) in enumerate(zip(cases, shapes)):
+        assert np.array_equal(outs["64"][i], outs["32"][i]), shp
+        assert max_row_rel_l2(outs["64"][i], oracle.mul_mat_native(qt, w, x)) <= EXACT, shp
 
 
 # many activation rows against a Q8_0 weight that fits in LDS (K = 256,
