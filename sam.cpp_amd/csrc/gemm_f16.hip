@@ -275,7 +275,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_pipe_kernel(const _Floa
     constexpr int NF = FM * FN;
     constexpr int ES = TN + 8;
     static_assert(A_PER_WAVE * NW == A_BLOCKS && B_PER_WAVE * NW == B_BLOCKS, "tile rows must split over the waves");
-    static_assert(STAGES >= 2 && STAGES <= 4, "ring depth");
+    static_assert(STAGES >= 2 && STAGES <= 6, "ring depth");
     static_assert(KK % 2 == 0, "fragment double buffer alternates per substep");
     static_assert(NW * 32 * ES * 4 <= STAGES * STAGE_BYTES, "epilogue staging must fit in LDS");
 
@@ -387,7 +387,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_f16_pipe_kernel(const _Floa
     auto enter = [&](int t) {
         const int later = min(STAGES - 2, nst - 1 - t);
         __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
-        if (later >= 2) wait_vmcnt<2 * LOADS>();
+        if (later >= 4) wait_vmcnt<4 * LOADS>();
+        else if (later == 3) wait_vmcnt<3 * LOADS>();
+        else if (later == 2) wait_vmcnt<2 * LOADS>();
         else if (later == 1) wait_vmcnt<LOADS>();
         else wait_vmcnt<0>();
         asm volatile("s_barrier" ::: "memory");
@@ -494,12 +496,14 @@ constexpr Cfg kConfigs[] = {
     SAMHIP_CFG(192, 128, 64, 2, 2, 2),
     SAMHIP_CFG(64, 128, 64, 3, 2, 4),
     SAMHIP_CFG(128, 64, 64, 3, 4, 2),
+    SAMHIP_CFG(64, 128, 64, 4, 2, 4),
 };
 #undef SAMHIP_CFG
-constexpr int kCfgSquare = 0, kCfgWide = 1, kCfgSmall = 2, kCfgTiny = 11;
+constexpr int kCfgSquare = 0, kCfgWide = 1, kCfgSmall = 2, kCfgTiny = 11, kCfgTinyDeep = 13;
 static_assert(kConfigs[kCfgSquare].bm == 256 && kConfigs[kCfgSquare].bn == 256 && kConfigs[kCfgWide].bm == 192 &&
                   kConfigs[kCfgWide].bn == 128 && kConfigs[kCfgSmall].bm == 128 && kConfigs[kCfgSmall].bn == 128 &&
-                  kConfigs[kCfgTiny].bm == 64 && kConfigs[kCfgTiny].bn == 128,
+                  kConfigs[kCfgTiny].bm == 64 && kConfigs[kCfgTiny].bn == 128 && kConfigs[kCfgTinyDeep].bm == 64 &&
+                  kConfigs[kCfgTinyDeep].bn == 128,
               "the picks below name these entries");
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -546,9 +550,16 @@ int gemm_f16_pick(int M, int N, int /*K*/, int cus) {
 // amortize a large tile's prologue and epilogue): M = 5184, N = 256,
 // K = 2048 (the fusion encoder's FFN output product) 21.7 -> 17.1 us;
 // N = 2048, K = 256 (its FFN input) 19.7 -> 18.7 us against 192x128.
+// When those tiles take one workgroup per CU anyway and K is long, a
+// four-deep ring (96 KB of LDS): the FFN output product 17.1 -> 16.3 us
+// (five and six stages 18.5 and 17.9; 64x64 tiles on 2x2 waves 18.4, 17.1
+// with four stages); at K = 256 the deep ring's second workgroup per CU is
+// missed (18.7 -> 24.8 us).
 int gemm_f16_pick_plain(int M, int N, int K, int cus) {
     const int64_t tiles = int64_t((M + 191) / 192) * ((N + 127) / 128);
     const int64_t small = int64_t((M + 127) / 128) * ((N + 127) / 128);
+    const int64_t tiny = int64_t((M + 63) / 64) * ((N + 127) / 128);
+    if (K >= 1024 && tiny <= cus && 2 * small <= cus && K % kConfigs[kCfgTinyDeep].bk == 0) return kCfgTinyDeep;
     if (K <= 256 || (2 * tiles <= cus && 2 * small <= cus)) return kCfgTiny;
     if (2 * tiles <= cus && K % kConfigs[kCfgSmall].bk == 0) return kCfgSmall;
     return gemm_f16_pick(M, N, K, cus);
