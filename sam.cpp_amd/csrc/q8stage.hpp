@@ -172,9 +172,11 @@ __device__ __forceinline__ void quant8_codes(const floatx8& v, int lane, float& 
             const float t = fabsf(v[i]);
             if (t > la) { la = t; ls = v[i]; li = base + i; }
         }
+        // its sign rides in the low bit of the index minimum (the value at
+        // the first maximum is +-amax), so no lane-to-lane read is needed
         const float amax = max32_lanes(la);
-        const int idx = min32_lanes(la == amax ? li : (1 << 20));
-        const float smax = __shfl(ls, (lane & 32) + ((idx >> 3) & 31), 64);
+        const int key = min32_lanes(la == amax ? 2 * li + int(__float_as_uint(ls) >> 31) : (1 << 20));
+        const float smax = (key & 1) ? -amax : amax;
         if (amax != 0.f) {
             const float iscale = -127.f / smax;
 #pragma unroll
