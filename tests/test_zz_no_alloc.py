@@ -43,8 +43,11 @@ def _both(samhip, ctx, qtype, w, x, n):
 
 
 # (first call, second smaller call): tall GEMM path, the int8 kernels with
-# K slices (Q8_0 and K-quant), the fused skinny kernel
+# K slices (Q8_0 and K-quant, 32 and 64 weight rows per workgroup), the
+# small-weight int8 kernels, the fused skinny kernel
 PAIRS = [
+    (("Q4_K", 5184, 256, 256), ("Q6_K", 1000, 255, 256)),         # small-weight K-quant kernel, twice
+    (("Q4_K", 201, 2048, 256), ("Q8_0", 300, 100, 256)),          # K-quant strip, 64-row workgroups; small-weight Q8_0
     (("Q8_0", 5184, 1024, 4736), ("Q8_0", 2048, 1024, 4736)),     # ViT fc2: 59 MB of scratch, then 24 MB
     (("Q4_K", 5184, 4736, 1024), ("Q5_K", 1024, 3072, 1024)),     # ViT fc1, then a smaller qkv
     (("Q8_0", 201, 2048, 256), ("Q6_K", 33, 256, 256)),           # decoder fc1, then a prompt K/V product
