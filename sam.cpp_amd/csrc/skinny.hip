@@ -1152,7 +1152,7 @@ __global__ __launch_bounds__(512) void tall_small_kq_i8_kernel(const float* __re
 //     dot of activation codes and the weight's unsigned 4/5/6-bit codes
 //     comes out of v_mfma_i32_32x32x32_i8 (for Q6_K once per 16-value half,
 //     the other half's weight codes set to zero), then in F32
-//       Q4_K, Q5_K: acc += (d sc_j) d_x dot - (dmin m_j) d_x sum(codes_j)
+//       Q4_K, Q5_K: acc += d_x ((d sc_j) dot - (dmin m_j) sum(codes_j))
 //       Q6_K:       acc += (d sc) d_x (dot - 32 sum(codes))
 //     (the same integer sums ggml forms; only the order of the F32 additions
 //     differs);
@@ -1322,13 +1322,14 @@ __global__ __launch_bounds__(1024) void kq_strip_i8_kernel(const float* __restri
             const float wm = half_bits_to_float(wp.hdr >> 16) * float(mn);
             const i32x16 dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(
                 a, i32x4{int(u[0]), int(u[1]), int(u[2]), int(u[3])}, zero, 0, 0, 0);
+            // acc += d_x (ws dot - wm csum): four VALU operations per element
 #pragma unroll
             for (int qd = 0; qd < 4; ++qd) {
                 const floatx4 cs = *reinterpret_cast<const floatx4*>(&Xs[st][8 * qd + 4 * h]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    float v = __builtin_fmaf(ws * dx[qd][i], float(dot[4 * qd + i]), acc[4 * qd + i]);
-                    acc[4 * qd + i] = __builtin_fmaf(-(wm * dx[qd][i]), cs[i], v);
+                    const float t = __builtin_fmaf(-wm, cs[i], ws * float(dot[4 * qd + i]));
+                    acc[4 * qd + i] = __builtin_fmaf(dx[qd][i], t, acc[4 * qd + i]);
                 }
             }
         }
