@@ -448,8 +448,8 @@ def cpu_info():
 
 def cpu_baseline(plan, rows, samples=15, warmup=3):
     """Both CPU paths of the reference, restated in C by the oracle, on `rows`
-    activation rows of every product (BASELINE.md's protocol, after the
-    reference's probe, tools/benchmark/cpu_quantized_matmul_probe.cpp:43-67):
+    activation rows of every product (the protocol of the reference's probe,
+    tools/benchmark/cpu_quantized_matmul_probe.cpp:43-67):
       native: ggml-quantized-cpu-native-v1 (activations packed to Q8_0 / Q8_K,
               block integer dots; src/runtime/ggml/runtime.hpp:105),
       decode: ggml-quantized-weights-f32-v1 (weights decoded to F32 per call,
