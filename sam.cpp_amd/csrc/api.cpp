@@ -136,6 +136,9 @@ struct samhip_context {
     int int8_strip = 1;         // SAMHIP_INT8_STRIP: 0 keeps M < 256 products on the fp16 kernels; 1 sends Q8_0
                                 // ones, and K-quant ones where that measured faster, to the int8 kernels; 2
                                 // sends every K-quant one there as well
+    bool kq_isum = false;       // SAMHIP_KQ_ISUM=1: the K-quant int8 strip kernel in its integer form (per
+                                // super-block integer sums, ggml's F32 steps in K order: the oracle's bits with
+                                // one K slice; measured 5 % slower on the Q4_K text stream)
     int strip_rows = 0;         // SAMHIP_I8_STRIP_ROWS: weight rows per workgroup of the int8 strip kernels,
                                 // 32 or 64 (64 only for K slices of at most 256 values); 0: 64 where that
                                 // brings the grid into one round
@@ -350,6 +353,7 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
     ctx->fused_max_splits = std::max(1, env_int("SAMHIP_FUSED_MAX_SPLITS", 16));
     ctx->int8_strip = env_int("SAMHIP_INT8_STRIP", 1);
     ctx->strip_rows = env_int("SAMHIP_I8_STRIP_ROWS", 0);
+    ctx->kq_isum = env_int("SAMHIP_KQ_ISUM", 0) != 0;
     ctx->tall_small = env_int("SAMHIP_TALL_SMALL", 1) != 0;
     ctx->tall_int8 = env_int("SAMHIP_TALL_INT8", 0) != 0;
     ctx->tall_decode = env_int("SAMHIP_TALL_DECODE", 0) != 0;
@@ -563,7 +567,8 @@ int samhip_mul_mat(samhip_context* ctx, const samhip_tensor* w, const samhip_ten
                                    (ctx->strip_rows != 32 && i8_strip_two_tiles_preferred(M, N, K, slice_sb, ctx->cus));
             const char* ok = kquant
                 ? launch_kq_strip_i8(w->type, xp, int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), yp,
-                                     int64_t(y->nb[1] / 4), part, M, N, K, slice_sb, two_tiles, ctx->stream)
+                                     int64_t(y->nb[1] / 4), part, M, N, K, slice_sb, two_tiles, ctx->kq_isum,
+                                     ctx->stream)
                 : launch_q8_strip_i8(xp, int64_t(x->nb[1] / 4), w->data, int64_t(w->nb[1]), yp, int64_t(y->nb[1] / 4),
                                      part, M, N, K, slice_sb, ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0,
                                      two_tiles, ctx->stream);

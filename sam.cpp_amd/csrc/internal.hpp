@@ -339,9 +339,11 @@ inline bool kq_strip_i8_preferred(int wtype, int M, int N, int K, int cus, bool 
 }
 const char* kq_strip_i8_variant(int wtype);
 // two_tiles: 64 weight rows per workgroup when a K slice holds one
-// super-block (two 32-row column tiles; the same bits as 32 rows)
+// super-block (two 32-row column tiles; the same bits as 32 rows).  isum:
+// the integer form (per super-block integer sums, then ggml's F32 steps in
+// K order: with one K slice the oracle's bits); otherwise F32 per sub-block.
 const char* launch_kq_strip_i8(int wtype, const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y,
-                               int64_t ldy, float* part, int M, int N, int K, int slice_sb, bool two_tiles,
+                               int64_t ldy, float* part, int M, int N, int K, int slice_sb, bool two_tiles, bool isum,
                                hipStream_t stream);
 const char* strip_skinny_variant(int wtype);
 const char* launch_strip_skinny(int wtype, bool f16, const float* x, int64_t ldx, const void* w, int64_t w_stride,

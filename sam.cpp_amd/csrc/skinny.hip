@@ -1353,6 +1353,235 @@ __global__ __launch_bounds__(1024) void kq_strip_i8_kernel(const float* __restri
     }
 }
 
+template <int WT, bool XVEC, int CT>
+__global__ __launch_bounds__(1024) void kq_strip_isum_kernel(const float* __restrict__ X, int64_t ldx,
+                                                           const uint8_t* __restrict__ W, int64_t w_stride,
+                                                           float* __restrict__ Y, int64_t ldy, float* __restrict__ part,
+                                                           int M, int N, int K, int RG, int S, int SK) {
+#pragma clang fp contract(off)
+    static_assert(CT == 1 || CT == 2, "one or two column tiles");
+    constexpr int WDW = CT == 2 ? kq_wdw1<WT>() : kq_wdw<WT>();   // dword pitch of an LDS weight row
+    constexpr int TPR = 32 / CT;                                  // threads per weight row in the load
+    static_assert(32 * CT * WDW <= 32 * kq_wdw<WT>(), "the weight rows fit the LDS strip");
+    constexpr int BB = block_bytes(WT);
+    constexpr int SUB = WT == T_Q6_K ? 16 : 32;     // values per weight scale
+    constexpr int SPB = 256 / SUB;                  // sub-blocks per super-block
+    constexpr int XSB = kI8SliceK / 256;            // super-blocks per full slice
+    __shared__ __attribute__((aligned(16))) int8_t Xq[32 * I8_XLD];
+    __shared__ __attribute__((aligned(16))) float Xd[XSB][32];
+    // code sums per (super-block, row, sub-block) as xs = 64 xh + xl, the
+    // K axis of the sum products padded to 32 with zeros
+    __shared__ __attribute__((aligned(16))) int8_t Xsl[XSB][32][32], Xsh[XSB][32][32];
+    __shared__ __attribute__((aligned(16))) uint32_t Ws[32 * kq_wdw<WT>()];
+    __shared__ __attribute__((aligned(16))) int red[16 * 16 * 64];           // integer partial tiles
+    __shared__ __attribute__((aligned(16))) int Mst[XSB][16 * 64];           // sum products per super-block
+    __shared__ __attribute__((aligned(16))) float Dw[XSB][32], Dmw[XSB][32]; // d, dmin per weight row
+    constexpr int RI = (WDW + TPR - 1) / TPR;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rg = blockIdx.x % RG, sp = (blockIdx.x / RG) % S, mb = blockIdx.x / (RG * S);
+    const int n0 = rg * 32 * CT, k0 = sp * 256 * SK;
+    const int nsb = min(256 * SK, K - k0) / 256;    // super-blocks in this slice (SK <= XSB; CT = 2: 1)
+    const int m0 = mb * 32, Mall = M;
+    X += int64_t(m0) * ldx;
+    Y += int64_t(m0) * ldy;
+    M = min(M - m0, 32);
+
+    // 1. packed weight bytes: thread (r, c) loads dwords c, c + TPR, ... of row r
+    const int wr_r = tid / TPR, wr_c = tid % TPR;
+    uint32_t wr[RI];
+    {
+        const uint8_t* rowp = W + int64_t(min(n0 + wr_r, N - 1)) * w_stride + int64_t(k0 / 256) * BB;
+        const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(rowp) & 3);
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(rowp - sh);
+        const int ndw = int((sh + BB * nsb + 3) >> 2);
+#pragma unroll
+        for (int i = 0; i < RI; ++i) wr[i] = wr_c + TPR * i < ndw ? src[wr_c + TPR * i] : 0u;
+    }
+    // 2. activation block (row m, super-block b) by the 32 lanes of half hu
+    // of a wave, 8 values per lane: unit u = m * nsb + b = 32 pass + 2 wave + hu
+    const int hu = lane >> 5, li = lane & 31;
+    floatx8 xv[XSB];
+#pragma unroll
+    for (int p = 0; p < XSB; ++p) {
+        xv[p] = floatx8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (p < nsb) {
+            const int u = 32 * p + 2 * wave + hu, m = u / nsb, b = u - m * nsb;
+            if (m < M) {
+                const float* xr = X + int64_t(m) * ldx + k0 + 256 * b + 8 * li;
+                if (XVEC) {
+                    const floatx4 lo = load4f(xr), hi = load4f(xr + 4);
+                    xv[p] = floatx8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) xv[p][i] = xr[i];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < RI; ++i)
+        if (wr_c + TPR * i < WDW) Ws[wr_r * WDW + wr_c + TPR * i] = wr[i];
+#pragma unroll
+    for (int p = 0; p < XSB; ++p) {
+        if (p >= nsb) break;
+        const int u = 32 * p + 2 * wave + hu, m = u / nsb, b = u - m * nsb;
+        float d, q[8];
+        quant8_codes<T_Q8_K, false>(xv[p], lane, d, q);
+        int c[8], sum = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            c[i] = int(q[i]);
+            sum += c[i];
+        }
+        const uint32_t lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(uint32_t(c[3]), uint32_t(c[2]), 0x0c0c0400u),
+                                                  __builtin_amdgcn_perm(uint32_t(c[1]), uint32_t(c[0]), 0x0c0c0400u),
+                                                  0x05040100u);
+        const uint32_t hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(uint32_t(c[7]), uint32_t(c[6]), 0x0c0c0400u),
+                                                  __builtin_amdgcn_perm(uint32_t(c[5]), uint32_t(c[4]), 0x0c0c0400u),
+                                                  0x05040100u);
+        *reinterpret_cast<uint2*>(&Xq[m * I8_XLD + 256 * b + 8 * li]) = uint2{lo, hi};
+        if (li == 0) Xd[b][m] = d;
+        // code sums of the weight's sub-blocks: 4 lanes (Q4_K, Q5_K) or 2 (Q6_K)
+        const int xs = group_sum<SUB / 8>(sum);
+        const int xh = xs >> 6, xl = xs - 64 * xh;   // xl in [0, 63], xh in [-64, 63]
+        if (li % (SUB / 8) == 0) {
+            Xsl[b][m][li / (SUB / 8)] = int8_t(xl);
+            Xsh[b][m][li / (SUB / 8)] = int8_t(xh);
+        }
+        if (li >= SPB) {   // the K padding
+            Xsl[b][m][li] = 0;
+            Xsh[b][m][li] = 0;
+        }
+    }
+    __syncthreads();
+
+    // 3. wave w takes steps st0 .. st0 + spw - 1 of one super-block (CT = 2:
+    // step w % 8 of column tile w / 8) and sums sc_j dot_j in integers; the
+    // wave that takes a super-block's first step also forms that super-block's
+    // sum products sum_j c_j xs_j (c_j the mins, Q6_K the scales) by two int8
+    // MFMAs, and its d (and dmin); the activation rows of element r are
+    // 8 (r / 4) + 4 h + r % 4, the weight row is the tile's row col
+    const int col = lane & 31, h = lane >> 5;
+    const int tile = CT == 2 ? wave >> 3 : 0;
+    const int wt = CT == 2 ? wave & 7 : wave;            // wave within its column tile
+    const int nst = 8 * nsb;                             // 32-value steps in the slice
+    const int spw = CT == 2 ? 1 : (nst + 15) / 16;       // steps per wave: 1 or 2 (a divisor of 8)
+    const int st0 = wt * spw;
+    const int wshift = int((reinterpret_cast<uintptr_t>(W + int64_t(min(n0 + 32 * tile + col, N - 1)) * w_stride) +
+                            (k0 / 256) * BB) &
+                           3);
+    const LdsRow wrow{&Ws[(32 * tile + col) * WDW], wshift};
+    const i32x16 zero = {0};
+    i32x16 isum = zero;
+    if (st0 < nst) {
+        for (int st = st0; st < st0 + spw; ++st) {
+            const int b = st >> 3, jj = st & 7;
+            const i32x4 a = *reinterpret_cast<const i32x4*>(&Xq[col * I8_XLD + 32 * st + 16 * h]);
+            WeightPiece<WT> wp;
+            wp.load(wrow, st, h);
+            if constexpr (WT == T_Q6_K) {
+                // unsigned codes u = low 4 | high 2 << 4 in [0, 63]; value u - 32
+                const int g = jj & 3;
+                const int lshift = (g >> 1) * 4, hshift = 2 * g;
+                u32x4 u;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    u[i] = ((wp.ql[i] >> lshift) & 0x0f0f0f0fu) | (((wp.qh[i] >> hshift) & 0x03030303u) << 4);
+                const int sbase = BB * b + 192 + 8 * (jj >> 2) + 2 * g;
+#pragma unroll
+                for (int hs = 0; hs < 2; ++hs) {
+                    const i32x4 bq = h == hs ? i32x4{int(u[0]), int(u[1]), int(u[2]), int(u[3])} : i32x4{0, 0, 0, 0};
+                    const i32x16 dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, zero, 0, 0, 0);
+                    const int sc = int(int8_t(wrow.u8(sbase + hs)));
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) isum[r] = __mul24(sc, dot[r]) + isum[r];
+                }
+            } else {
+                const int shift = (jj & 1) * 4;
+                u32x4 u;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    u[i] = (wp.qs[i] >> shift) & 0x0f0f0f0fu;
+                    if constexpr (WT == T_Q5_K) u[i] |= ((wp.qh[i] >> jj) & 0x01010101u) << 4;
+                }
+                int sc, mn;
+                k4_scale_min(jj, wp.sc, sc, mn);
+                const i32x16 dot = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                    a, i32x4{int(u[0]), int(u[1]), int(u[2]), int(u[3])}, zero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) isum[r] = __mul24(sc, dot[r]) + isum[r];
+            }
+        }
+        if ((st0 & 7) == 0) {
+            // this super-block's sum products for the tile and its d (dmin)
+            const int b = st0 >> 3, slot = CT == 2 ? tile : b;
+            uint32_t c0 = 0u, c1 = 0u, c2 = 0u, c3 = 0u;   // c_j as int8, j = 0 .. SPB - 1 (lanes h = 0)
+            float dw, dmw = 0.f;
+            if constexpr (WT == T_Q6_K) {
+                const u32x4 scs = wrow.u128(BB * b + 192);
+                c0 = scs[0]; c1 = scs[1]; c2 = scs[2]; c3 = scs[3];
+                dw = half_bits_to_float(wrow.u16(BB * b + 208));
+            } else {
+                const uint32_t scw[3] = {wrow.u32(BB * b + 4), wrow.u32(BB * b + 8), wrow.u32(BB * b + 12)};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    int sc, mn;
+                    k4_scale_min(j, scw, sc, mn);
+                    if (j < 4) c0 |= uint32_t(mn) << (8 * j);
+                    else c1 |= uint32_t(mn) << (8 * (j - 4));
+                }
+                const uint32_t hdr = wrow.u32(BB * b);
+                dw = half_bits_to_float(hdr & 0xffffu);
+                dmw = half_bits_to_float(hdr >> 16);
+            }
+            const i32x4 cb = h == 0 ? i32x4{int(c0), int(c1), int(c2), int(c3)} : i32x4{0, 0, 0, 0};
+            const i32x16 ml = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                *reinterpret_cast<const i32x4*>(&Xsl[b][col][16 * h]), cb, zero, 0, 0, 0);
+            const i32x16 mh = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                *reinterpret_cast<const i32x4*>(&Xsh[b][col][16 * h]), cb, zero, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) Mst[slot][r * 64 + lane] = __mul24(64, mh[r]) + ml[r];
+            if (h == 0) {
+                Dw[slot][col] = dw;
+                Dmw[slot][col] = dmw;
+            }
+        }
+    }
+    // 4. per column tile and super-block (in K order): the waves' integer
+    // partials added, then ggml's F32 steps
+    //   Q4_K, Q5_K: y += (d d_x) isum;  y -= (dmin d_x) msum
+    //   Q6_K:       y += (d d_x) (isum - 32 sum_s sc_s xs_s)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = isum[r];
+    __syncthreads();
+    const int m = tid >> 5, n = tid & 31;
+    const int src = (4 * (m >> 3) + (m & 3)) * 64 + n + 32 * ((m >> 2) & 1);
+    const int wpb = 8 / spw;   // waves per super-block
+#pragma unroll
+    for (int t = 0; t < CT; ++t) {
+        float v = 0.f;
+        for (int b = 0; b < nsb; ++b) {
+            const int slot = CT == 2 ? t : b, w0 = CT == 2 ? 8 * t : b * wpb;
+            int is = 0;
+            for (int w = 0; w < wpb; ++w) is += red[((w0 + w) * 16) * 64 + src];
+            const int ms = Mst[slot][src];
+            const float dx = Xd[b][m];
+            if constexpr (WT == T_Q6_K) {
+                v = v + (Dw[slot][n] * dx) * float(is - 32 * ms);
+            } else {
+                v = v + (Dw[slot][n] * dx) * float(is);
+                v = v - (Dmw[slot][n] * dx) * float(ms);
+            }
+        }
+        const int nn = n0 + 32 * t + n;
+        if (m < M && nn < N) {
+            if (part) part[(int64_t(sp) * Mall + m0 + m) * N + nn] = v;
+            else Y[int64_t(m) * ldy + nn] = v;
+        }
+    }
+}
+
 template <int WT, int MODE, bool X86>
 void launch_strip_mode(bool xvec, const float* x, int64_t ldx, const uint8_t* w, int64_t w_stride, float* y,
                        int64_t ldy, float* part, int M, int N, int K, int RG, int S, hipStream_t stream) {
@@ -1575,23 +1804,29 @@ const char* kq_strip_i8_variant(int wtype) {
 }
 
 template <int WT>
-void launch_kq_strip_wt(bool xvec, int CT, const float* x, int64_t ldx, const uint8_t* w, int64_t w_stride, float* y,
-                        int64_t ldy, float* part, int M, int N, int K, int RG, int S, int MB, int SK,
+void launch_kq_strip_wt(bool xvec, int CT, bool isum, const float* x, int64_t ldx, const uint8_t* w, int64_t w_stride,
+                        float* y, int64_t ldy, float* part, int M, int N, int K, int RG, int S, int MB, int SK,
                         hipStream_t stream) {
     const dim3 grid(unsigned(RG * S * MB)), block(1024);
-#define SAMHIP_KQ(XV, CTV)                                                                                          \
-    hipLaunchKernelGGL((kq_strip_i8_kernel<WT, XV, CTV>), grid, block, 0, stream, x, ldx, w, w_stride, y, ldy, part, \
-                       M, N, K, RG, S, SK)
-    if (xvec) {
-        if (CT == 2) SAMHIP_KQ(true, 2); else SAMHIP_KQ(true, 1);
-    } else {
-        if (CT == 2) SAMHIP_KQ(false, 2); else SAMHIP_KQ(false, 1);
-    }
+#define SAMHIP_KQ(KERN, XV, CTV)                                                                              \
+    hipLaunchKernelGGL((KERN<WT, XV, CTV>), grid, block, 0, stream, x, ldx, w, w_stride, y, ldy, part, M, N, K, RG, \
+                       S, SK)
+#define SAMHIP_KQ_CT(KERN)                                                                       \
+    do {                                                                                         \
+        if (xvec) {                                                                              \
+            if (CT == 2) SAMHIP_KQ(KERN, true, 2); else SAMHIP_KQ(KERN, true, 1);                \
+        } else {                                                                                 \
+            if (CT == 2) SAMHIP_KQ(KERN, false, 2); else SAMHIP_KQ(KERN, false, 1);              \
+        }                                                                                        \
+    } while (0)
+    if (isum) SAMHIP_KQ_CT(kq_strip_isum_kernel);
+    else SAMHIP_KQ_CT(kq_strip_i8_kernel);
+#undef SAMHIP_KQ_CT
 #undef SAMHIP_KQ
 }
 
 const char* launch_kq_strip_i8(int wtype, const float* x, int64_t ldx, const void* w, int64_t w_stride, float* y,
-                               int64_t ldy, float* part, int M, int N, int K, int slice_sb, bool two_tiles,
+                               int64_t ldy, float* part, int M, int N, int K, int slice_sb, bool two_tiles, bool isum,
                                hipStream_t stream) {
     if (M < 1 || N < 1 || K < 256 || K % 256) return nullptr;
     if (slice_sb != 1 && slice_sb != 2 && slice_sb != kI8SliceK / 256) return nullptr;
@@ -1605,9 +1840,9 @@ const char* launch_kq_strip_i8(int wtype, const float* x, int64_t ldx, const voi
     const uint8_t* wb = static_cast<const uint8_t*>(w);
     float* pt = S > 1 ? part : nullptr;
     switch (wtype) {
-        case T_Q4_K: launch_kq_strip_wt<T_Q4_K>(xvec, CT, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
-        case T_Q5_K: launch_kq_strip_wt<T_Q5_K>(xvec, CT, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
-        case T_Q6_K: launch_kq_strip_wt<T_Q6_K>(xvec, CT, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
+        case T_Q4_K: launch_kq_strip_wt<T_Q4_K>(xvec, CT, isum, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
+        case T_Q5_K: launch_kq_strip_wt<T_Q5_K>(xvec, CT, isum, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
+        case T_Q6_K: launch_kq_strip_wt<T_Q6_K>(xvec, CT, isum, x, ldx, wb, w_stride, y, ldy, pt, M, N, K, RG, S, MB, SK, stream); break;
         default: return nullptr;
     }
     if (S > 1) {

@@ -185,14 +185,17 @@ KQ_SHAPES = [(32, 1024, 1024), (32, 1024, 4096), (32, 4096, 1024), (201, 256, 20
              (33, 256, 256), (17, 96, 512), (255, 40, 1280), (1, 64, 256), (97, 33, 768), (3, 1, 512)]
 
 
+@pytest.mark.parametrize("form", ["f32", "isum"])
 @pytest.mark.parametrize("qtype", ["q4_K", "q5_K", "q6_K"])
 @pytest.mark.parametrize("shape", KQ_SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_kquant_int8_strip_matches_native(samhip, oracle, monkeypatch, shape, qtype):
+def test_kquant_int8_strip_matches_native(samhip, oracle, monkeypatch, shape, qtype, form):
     """K-quant weights on the int8 path (SAMHIP_INT8_STRIP=2 takes it for
     every shape; by default only where it is faster): the 4/5/6-bit codes and
     Q8_K activation codes meet in exact integer dots; the sub-block scales
-    and minimums are applied in F32 per sub-block, so only the order of the
-    F32 additions differs from the oracle's vec_dot (same bar as Q8_0)."""
+    and minimums are applied in F32 per sub-block (form f32, the default) or
+    in integers per super-block (form isum, SAMHIP_KQ_ISUM=1), so only the
+    order of the F32 additions differs from the oracle's vec_dot (same bar
+    as Q8_0; K slices past the first, K = 768 in three, among them)."""
     m, n, k = shape
     say("case int8 strip", qtype, shape)
     gt = {"q4_K": samhip.Q4_K, "q5_K": samhip.Q5_K, "q6_K": samhip.Q6_K}[qtype]
@@ -203,6 +206,7 @@ def test_kquant_int8_strip_matches_native(samhip, oracle, monkeypatch, shape, qt
     if m > 3:
         x[2, 7] = np.nan                      # packs as code 0
         x[3, :] = 0.0                         # an all-zero row: d = 0
+    monkeypatch.setenv("SAMHIP_KQ_ISUM", "1" if form == "isum" else "0")
     monkeypatch.setenv("SAMHIP_INT8_STRIP", "2")
     with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
         y = ctx.matmul(gt, w, x, x_row_stride=k + 4 if n % 2 else None)
@@ -240,6 +244,35 @@ def test_kquant_int8_default_routing(samhip, oracle):
             tname = {oracle.Q4_K: "q4_k", oracle.Q5_K: "q5_k", oracle.Q6_K: "q6_k"}[qt]
             assert name == ("skinny_i8mfma_" if exact else "skinny_fused_") + tname, (name, m, n, k)
             assert max_row_rel_l2(y, oracle.mul_mat_native(qt, w, x)) <= (EXACT if exact else 1e-3)
+
+
+@pytest.mark.parametrize("qtype", ["q4_K", "q5_K", "q6_K"])
+def test_kquant_int8_strip_one_slice_bit_equal(samhip, oracle, monkeypatch, qtype):
+    """In its integer form (SAMHIP_KQ_ISUM=1) the K-quant int8 kernel sums
+    each super-block's sc_j dot_j and c_j xs_j in integers and then takes
+    ggml's F32 steps per super-block in K order, the oracle's arithmetic:
+    with the whole K in one slice the bits agree (K = 256 with one and
+    several row blocks, ragged N, 64 weight rows per workgroup at N = 2048;
+    K = 1024 in one 1024-wide slice at N = 8192; a NaN activation and an
+    all-zero row)."""
+    say("case kquant int8 strip bit-equal", qtype)
+    qt = {"q4_K": oracle.Q4_K, "q5_K": oracle.Q5_K, "q6_K": oracle.Q6_K}[qtype]
+    gt = {"q4_K": samhip.Q4_K, "q5_K": samhip.Q5_K, "q6_K": samhip.Q6_K}[qtype]
+    rng = np.random.default_rng(80)
+    monkeypatch.setenv("SAMHIP_INT8_STRIP", "2")
+    monkeypatch.setenv("SAMHIP_KQ_ISUM", "1")
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
+        for m, n, k in ((201, 256, 256), (33, 256, 256), (3, 1, 256), (17, 33, 256), (201, 2048, 256),
+                        (32, 8192, 1024)):
+            w = oracle.quantize(qt, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+            x = (rng.standard_normal((m, k)) * np.exp(rng.uniform(-4, 4, (m, 1)))).astype(np.float32)
+            if m > 3:
+                x[2, 7] = np.nan
+                x[3, :] = 0.0
+            y = ctx.matmul(gt, w, x, x_row_stride=k + 4 if n % 2 else None)
+            assert ctx.query().kernel_variant == ("skinny_i8mfma_" + qtype.lower()).encode()
+            ref = oracle.mul_mat_native(qt, w, x)
+            assert np.array_equal(y, ref), (m, n, k, max_row_rel_l2(y, ref))
 
 
 @pytest.mark.parametrize("qtype", ["q4_K", "q5_K", "q6_K"])
