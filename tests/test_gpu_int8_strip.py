@@ -155,6 +155,52 @@ def test_int8_strip_repeats_and_replays(samhip, oracle):
             g.destroy()
 
 
+def test_small_weight_and_kquant_kernels_in_graph_replays(samhip, oracle):
+    """The small-weight kernels (Q8_0 and Q4_K), the K-quant strip kernel
+    (one and several K slices) and the 64-row Q8_0 strip workgroups,
+    captured as one stream and replayed three times with eager work between
+    the replays: every replay gives the eager call's bits."""
+    say("case graph replays of the int8 kernels")
+    rng = np.random.default_rng(81)
+    cases = [(samhip.Q8_0, oracle.Q8_0, 5184, 256, 256), (samhip.Q4_K, oracle.Q4_K, 1000, 200, 256),
+             (samhip.Q4_K, oracle.Q4_K, 32, 1024, 1024), (samhip.Q6_K, oracle.Q6_K, 33, 256, 256),
+             (samhip.Q8_0, oracle.Q8_0, 201, 2048, 256)]
+    with samhip.Context(0, samhip.COMPUTE_Q8_NATIVE) as ctx:
+        ops = []
+        for gt, ot, m, n, k in cases:
+            w = oracle.quantize(ot, (rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+            x = rng.standard_normal((m, k)).astype(np.float32)
+            wb, xb, yb = ctx.upload(w), ctx.upload(x), ctx.alloc(m * n * 4)
+            ops.append((samhip.tensor(gt, k, n, wb.ptr), samhip.tensor(samhip.F32, k, m, xb.ptr),
+                        samhip.tensor(samhip.F32, n, m, yb.ptr), (wb, xb, yb), (m, n), w, x, ot))
+        first = []
+        for wt, xt, yt, bufs, shp, w, x, ot in ops:
+            ctx.mul_mat(wt, xt, yt)
+            y = ctx.download(bufs[2], shp, np.float32)
+            assert max_row_rel_l2(y, oracle.mul_mat_native(ot, w, x)) <= EXACT
+            first.append(y)
+        ctx.capture_begin()
+        for wt, xt, yt, *_ in ops:
+            ctx.mul_mat(wt, xt, yt)
+        g = ctx.capture_end()
+        try:
+            for rep in range(3):
+                for _, _, _, bufs, shp, *_ in ops:
+                    ctx.write(bufs[2], np.zeros(shp, np.float32))
+                wt, xt, yt = ops[2][:3]
+                ctx.mul_mat(wt, xt, yt)                 # eager work between replays
+                ctx.synchronize()
+                g.launch()
+                ctx.synchronize()
+                for (_, _, _, bufs, shp, *_), y in zip(ops, first):
+                    assert np.array_equal(ctx.download(bufs[2], shp, np.float32), y), (rep, shp)
+        finally:
+            g.destroy()
+        for *_, bufs, _, _, _, _ in ops:
+            for b in bufs:
+                b.free()
+
+
 @pytest.mark.parametrize("rounding", ["x86", "ref"])
 def test_int8_strip_nan_activations(samhip, oracle, rounding):
     """A NaN activation packs as code 0 (the library's contract, as ggml's
