@@ -720,7 +720,7 @@ constexpr int TS_XLD = kTallSmallK + 16;                 // bytes per LDS code r
 constexpr int TS_NB = kTallSmallK / 32;                  // 8 blocks per row
 static_assert(TS_RB % 16 == 0 && 64 * TS_RB % 1024 == 0, "64 packed rows are whole KB of 16-byte aligned rows");
 
-template <bool X86, bool XVEC>
+template <bool X86, bool XVEC, int NQD>
 __global__ __launch_bounds__(512) void tall_small_i8_kernel(const float* __restrict__ X, int64_t ldx,
                                                             const uint8_t* __restrict__ W, float* __restrict__ Y,
                                                             int64_t ldy, int M, int N) {
@@ -837,7 +837,9 @@ __global__ __launch_bounds__(512) void tall_small_i8_kernel(const float* __restr
                 const i32x4 w = *reinterpret_cast<const i32x4*>(Wl + nr * TS_RB + 32 * b + 16 * h);
                 dots[b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, w, zero, 0, 0, 0);
             }
-            // element r: activation row 8 (r / 4) + 4 h + r % 4, weight row n
+            // element r: activation row 8 (r / 4) + 4 h + r % 4, weight row n;
+            // the host takes NQD = 3 when no run has more than 24 rows, so the
+            // last group of 8 rows is neither scaled nor stored
             floatx16 acc;
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[r] = 0.f;
@@ -845,7 +847,7 @@ __global__ __launch_bounds__(512) void tall_small_i8_kernel(const float* __restr
             for (int b = 0; b < TS_NB; ++b) {
                 const float dw = Wd[b][nr];
 #pragma unroll
-                for (int qd = 0; qd < 4; ++qd) {
+                for (int qd = 0; qd < NQD; ++qd) {
                     const floatx4 dx = *reinterpret_cast<const floatx4*>(&Xd[b][8 * qd + 4 * h]);
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
@@ -854,7 +856,7 @@ __global__ __launch_bounds__(512) void tall_small_i8_kernel(const float* __restr
             }
             const uint32_t base = n < N ? uint32_t(4 * h * ldy + n) * 4 : 0x80000000u;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
+            for (int r = 0; r < 4 * NQD; ++r) {
                 const float val = acc[r];
                 const uint32_t dr = uint32_t(8 * (r >> 2) + (r & 3));
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), yd, base + dr * uint32_t(ldy) * 4, 0, 0);
@@ -892,7 +894,7 @@ __global__ __launch_bounds__(512) void tall_small_i8_kernel(const float* __restr
 template <int WT>
 constexpr int tskq_pack_bytes() { return kTallSmallMaxN * block_bytes(WT) + 1024; }
 
-template <int WT, bool XVEC>
+template <int WT, bool XVEC, int NQD>
 __global__ __launch_bounds__(512) void tall_small_kq_i8_kernel(const float* __restrict__ X, int64_t ldx,
                                                                const uint8_t* __restrict__ W, float* __restrict__ Y,
                                                                int64_t ldy, int M, int N) {
@@ -1112,8 +1114,9 @@ __global__ __launch_bounds__(512) void tall_small_kq_i8_kernel(const float* __re
             const float dw = Wd[nr];
             const float dmw = Q6 ? 0.f : Wdm[nr];
             const uint32_t base = n < N ? uint32_t(4 * h * ldy + n) * 4 : 0x80000000u;
+            // NQD = 3 (no run past 24 rows): the tile's last 8 rows are not stored
 #pragma unroll
-            for (int qd = 0; qd < 4; ++qd) {
+            for (int qd = 0; qd < NQD; ++qd) {
                 const floatx4 dx = *reinterpret_cast<const floatx4*>(&Xd[8 * qd + 4 * h]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -1877,14 +1880,20 @@ const char* launch_tall_small_kq_i8(int wtype, const float* x, int64_t ldx, cons
     const int grid = std::max(1, std::min(cus, (M + 15) / 16));
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
+    // no run past 24 rows: the epilogue skips the tile's last 8 rows
+    const bool short_runs = (M + grid - 1) / grid <= 24;
+#define SAMHIP_TSK1(WT, XV)                                                                                      \
+    do {                                                                                                        \
+        if (short_runs)                                                                                         \
+            hipLaunchKernelGGL((tall_small_kq_i8_kernel<WT, XV, 3>), dim3(unsigned(grid)), dim3(512), 0, stream, \
+                               x, ldx, wb, y, ldy, M, N);                                                       \
+        else                                                                                                    \
+            hipLaunchKernelGGL((tall_small_kq_i8_kernel<WT, XV, 4>), dim3(unsigned(grid)), dim3(512), 0, stream, \
+                               x, ldx, wb, y, ldy, M, N);                                                       \
+    } while (0)
 #define SAMHIP_TSK(WT)                                                                                          \
     do {                                                                                                        \
-        if (xvec)                                                                                               \
-            hipLaunchKernelGGL((tall_small_kq_i8_kernel<WT, true>), dim3(unsigned(grid)), dim3(512), 0, stream, x, \
-                               ldx, wb, y, ldy, M, N);                                                          \
-        else                                                                                                    \
-            hipLaunchKernelGGL((tall_small_kq_i8_kernel<WT, false>), dim3(unsigned(grid)), dim3(512), 0, stream, x, \
-                               ldx, wb, y, ldy, M, N);                                                          \
+        if (xvec) SAMHIP_TSK1(WT, true); else SAMHIP_TSK1(WT, false);                                           \
     } while (0)
     switch (wtype) {
         case T_Q4_K: SAMHIP_TSK(T_Q4_K); break;
@@ -1893,6 +1902,7 @@ const char* launch_tall_small_kq_i8(int wtype, const float* x, int64_t ldx, cons
         default: return nullptr;
     }
 #undef SAMHIP_TSK
+#undef SAMHIP_TSK1
     return tall_small_kq_i8_variant(wtype);
 }
 
@@ -1910,9 +1920,17 @@ const char* launch_tall_small_i8(const float* x, int64_t ldx, const void* w, int
     const int grid = std::max(1, std::min(cus, (M + 15) / 16));
     const bool xvec = reinterpret_cast<uintptr_t>(x) % 16 == 0 && ldx % 4 == 0;
     const uint8_t* wb = static_cast<const uint8_t*>(w);
+    // no run past 24 rows: the epilogue skips the tile's last 8 rows
+    const bool short_runs = (M + grid - 1) / grid <= 24;
 #define SAMHIP_TS(X86V, XV)                                                                                          \
-    hipLaunchKernelGGL((tall_small_i8_kernel<X86V, XV>), dim3(unsigned(grid)), dim3(512), 0, stream, x, ldx, wb, y, \
-                       ldy, M, N)
+    do {                                                                                                             \
+        if (short_runs)                                                                                              \
+            hipLaunchKernelGGL((tall_small_i8_kernel<X86V, XV, 3>), dim3(unsigned(grid)), dim3(512), 0, stream, x, ldx, \
+                               wb, y, ldy, M, N);                                                                    \
+        else                                                                                                         \
+            hipLaunchKernelGGL((tall_small_i8_kernel<X86V, XV, 4>), dim3(unsigned(grid)), dim3(512), 0, stream, x, ldx, \
+                               wb, y, ldy, M, N);                                                                    \
+    } while (0)
     if (x86) {
         if (xvec) SAMHIP_TS(true, true); else SAMHIP_TS(true, false);
     } else {
