@@ -142,6 +142,9 @@ struct samhip_context {
     int strip_rows = 0;         // SAMHIP_I8_STRIP_ROWS: weight rows per workgroup of the int8 strip kernels,
                                 // 32 or 64 (64 only for K slices of at most 256 values); 0: 64 where that
                                 // brings the grid into one round
+    bool vit_fc1_codes = false; // SAMHIP_VIT_FC1_CODES=1: with a Q8_0 fc2, an encoder block's fc1 epilogue
+                                // applies the erf-GELU and writes fc2's Q8_0 codes (same bits; measured no
+                                // faster: the GEMM gains the GELU's VALU work, the staging loses the F32 reads)
     samhip_exec_info info{};
     // per-launch event trace (samhip_trace_begin / samhip_trace_end)
     struct TraceRecord {
@@ -354,6 +357,7 @@ int samhip_context_create(const samhip_options* options, samhip_context** out) {
     ctx->int8_strip = env_int("SAMHIP_INT8_STRIP", 1);
     ctx->strip_rows = env_int("SAMHIP_I8_STRIP_ROWS", 0);
     ctx->kq_isum = env_int("SAMHIP_KQ_ISUM", 0) != 0;
+    ctx->vit_fc1_codes = env_int("SAMHIP_VIT_FC1_CODES", 0) != 0;
     ctx->tall_small = env_int("SAMHIP_TALL_SMALL", 1) != 0;
     ctx->tall_int8 = env_int("SAMHIP_TALL_INT8", 0) != 0;
     ctx->tall_decode = env_int("SAMHIP_TALL_DECODE", 0) != 0;
@@ -913,11 +917,19 @@ int ensure_row_map(samhip_context* ctx, int gw, int gh, int ws) {
     return SAMHIP_OK;
 }
 
-// Tall product through staging (with the producing node folded in, `pre`)
-// + weight decode + the fp16 GEMM with an epilogue; x rows are K contiguous
-// floats (16-byte aligned), y rows ldy.
+// Activation rows as Q8_0 codes [M][ld] and F32 block maxima [M][ld / 32]
+// (what Epilogue::q8 writes).
+struct CodeRows {
+    const int8_t* codes = nullptr;
+    const float* amax = nullptr;
+    int64_t ld = 0;
+};
+
+// Tall product through staging (with the producing node folded in, `pre`;
+// or from Q8_0 code rows, `in`) + weight decode + the fp16 GEMM with an
+// epilogue; x rows are K contiguous floats (16-byte aligned), y rows ldy.
 int linear(samhip_context* ctx, const samhip_tensor& w, const float* x, int M, float* y, int64_t ldy,
-           const Epilogue& ep, const char* what, const RowPre& pre = RowPre{}) {
+           const Epilogue& ep, const char* what, const RowPre& pre = RowPre{}, const CodeRows* in = nullptr) {
     const int K = int(w.ne[0]), N = int(w.ne[1]);
     auto align256 = [](size_t v) { return (v + 255) & ~size_t(255); };
     const size_t rs_offset = align256(size_t(M) * size_t(K) * 2);
@@ -929,10 +941,12 @@ int linear(samhip_context* ctx, const samhip_tensor& w, const float* x, int M, f
     _Float16* wh = reinterpret_cast<_Float16*>(base + w_offset);
     const int mode = ctx->compute == SAMHIP_COMPUTE_F16 ? T_F16 : vec_dot_type(w.type);
     const int x86 = ctx->q8_rounding == SAMHIP_Q8_ROUND_X86 ? 1 : 0;
-    int rc = traced(ctx, prep_name(mode), w.type, M, N, K, [&]() -> int {
-        if (!launch_prep(mode, w.type, x, K, M, K, a, K, rs, x86, w.data, int64_t(w.nb[1]), N, wh, K, ctx->stream,
-                         pre))
-            return fail(SAMHIP_ERR_UNSUPPORTED, "%s: no staging kernel for K = %d", what, K);
+    int rc = traced(ctx, in ? "stage_codes_q8_0" : prep_name(mode), w.type, M, N, K, [&]() -> int {
+        const bool ok = in ? launch_prep_codes(in->codes, in->amax, in->ld, M, K, a, K, rs, w.type, w.data,
+                                               int64_t(w.nb[1]), N, wh, K, ctx->stream)
+                           : launch_prep(mode, w.type, x, K, M, K, a, K, rs, x86, w.data, int64_t(w.nb[1]), N, wh, K,
+                                         ctx->stream, pre);
+        if (!ok) return fail(SAMHIP_ERR_UNSUPPORTED, "%s: no staging kernel for K = %d", what, K);
         HIP_TRY(hipGetLastError(), "staging and weight decode launch");
         return SAMHIP_OK;
     });
@@ -1137,12 +1151,30 @@ int samhip_vit_block(samhip_context* ctx, const samhip_vit_block_desc* d, float*
     ln2.ws = 0;
     Epilogue e_fc1;
     e_fc1.bias = d->fc1_b;
-    if ((rc = linear(ctx, d->fc1_w, x1, iT, h1, MLP, e_fc1, "vit_fc1", ln2))) return rc;
-    RowPre gelu;
-    gelu.kind = PRE_GELU;
     Epilogue e_fc2;
     e_fc2.bias = d->fc2_b;
     e_fc2.res = x1;
+    // Opt-in: with a Q8_0 fc2 in native compute, fc1's epilogue applies the
+    // erf-GELU and packs fc2's Q8_0 blocks itself (codes and F32 block
+    // maxima, 1.125 bytes per value in h1's space instead of 4), and fc2's
+    // staging expands them: the same operand bits as staging the F32 rows.
+    if (ctx->vit_fc1_codes && d->fc2_w.type == T_Q8_0 && ctx->compute != SAMHIP_COMPUTE_F16 && MLP % 32 == 0) {
+        CodeRows rows;
+        rows.codes = reinterpret_cast<const int8_t*>(h1);
+        rows.amax = reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(h1) +
+                                                   ((size_t(T * MLP) + 255) & ~size_t(255)));
+        rows.ld = MLP;
+        e_fc1.gelu = true;
+        e_fc1.q8 = const_cast<int8_t*>(rows.codes);
+        e_fc1.q8_amax = const_cast<float*>(rows.amax);
+        e_fc1.q8_ld = MLP;
+        e_fc1.q8_x86 = ctx->q8_rounding == SAMHIP_Q8_ROUND_X86;
+        if ((rc = linear(ctx, d->fc1_w, x1, iT, nullptr, MLP, e_fc1, "vit_fc1", ln2))) return rc;
+        return linear(ctx, d->fc2_w, nullptr, iT, x, E, e_fc2, "vit_fc2", RowPre{}, &rows);
+    }
+    if ((rc = linear(ctx, d->fc1_w, x1, iT, h1, MLP, e_fc1, "vit_fc1", ln2))) return rc;
+    RowPre gelu;
+    gelu.kind = PRE_GELU;
     return linear(ctx, d->fc2_w, h1, iT, x, E, e_fc2, "vit_fc2", gelu);
 }
 

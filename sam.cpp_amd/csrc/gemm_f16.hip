@@ -42,7 +42,7 @@ constexpr int GROUP_M = 4;
 
 // Epilogue flags (EPI template bits) for Epilogue fields.
 constexpr int EPI_BIAS = 1, EPI_RES = 4, EPI_REMAP = 8, EPI_PACK = 16, EPI_COLSCALE = 32, EPI_SHUFFLE = 64,
-              EPI_GELU = 128, EPI_PACK_LO = 512;
+              EPI_GELU = 128, EPI_Q8 = 256, EPI_PACK_LO = 512;
 
 // Epilogue of a wave's (32*FM) x (32*FN) tile at (row0, col0): each 32-row
 // block goes through the wave's LDS slab (stride ES floats; accumulator
@@ -177,6 +177,31 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
                 if (EPI & EPI_GELU) u = gelu_erf(u);
                 if (EPI & EPI_RES) u = res[t][q] + u;
                 v[q] = u;
+            }
+            if constexpr ((EPI & EPI_Q8) != 0) {
+                // Q8_0 packing of the row's 32-column block, held by the 8
+                // lanes c4 = 8g .. 8g + 7 (C4 is a multiple of 8, col0 of 32):
+                // ggml's from_float on these F32 values (x86 scale 127/amax
+                // with ties to even, or the reference 1/d with ties away;
+                // NaN packs as code 0); the block maximum leaves in F32
+                float amax = 0.f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) amax = fmaxf(amax, fabsf(v[q]));
+                amax = group_max<8>(amax);
+                const float dd = amax / 127.f;
+                float inv;
+                if (ep.q8_x86) inv = amax != 0.f ? 127.f / amax : 0.f;
+                else inv = dd != 0.f ? 1.f / dd : 0.f;
+                uint32_t word = 0;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float sq = v[q] * inv;
+                    const float r = ep.q8_x86 ? __builtin_rintf(sq) : __builtin_roundf(sq);
+                    word |= (uint32_t(r == r ? int(r) : 0) & 0xffu) << (8 * q);
+                }
+                *reinterpret_cast<uint32_t*>(ep.q8 + dst[t] * ep.q8_ld + n) = word;
+                if ((c4 & 7) == 0) ep.q8_amax[dst[t] * (ep.q8_ld >> 5) + (n >> 5)] = amax;
+                continue;
             }
             if (EPI & EPI_PACK) {
                 if (rope) {
@@ -574,7 +599,7 @@ bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16*
     const int flags = (ep.bias ? EPI_BIAS : 0) | (ep.res ? EPI_RES : 0) | (ep.row_map ? EPI_REMAP : 0) |
                       (ep.pack[0] ? EPI_PACK : 0) | (ep.col_scale ? EPI_COLSCALE : 0) |
                       (ep.shuffle_c > 0 ? EPI_SHUFFLE : 0) | (ep.gelu ? EPI_GELU : 0) |
-                      (ep.pack_lo[0] ? EPI_PACK_LO : 0);
+                      (ep.pack_lo[0] ? EPI_PACK_LO : 0) | (ep.q8 ? EPI_Q8 : 0);
 #define SAMHIP_EPI(E, AMODE)                                                                                     \
     launch_pipe<BM, BN, 64, 2, WM, WN, E, AMODE>(a, lda, rs, b, ldb, y, ldy, M, N, K, spread, stream, ep, op); \
     return true;
@@ -588,6 +613,7 @@ bool launch_epi(const _Float16* a, int64_t lda, const float* rs, const _Float16*
             case EPI_BIAS | EPI_PACK | EPI_PACK_LO: SAMHIP_EPI(EPI_BIAS | EPI_PACK | EPI_PACK_LO, A_PLAIN)
             case EPI_BIAS | EPI_RES | EPI_REMAP: SAMHIP_EPI(EPI_BIAS | EPI_RES | EPI_REMAP, A_PLAIN)
             case BC: SAMHIP_EPI(BC, A_PLAIN)
+            case EPI_BIAS | EPI_GELU | EPI_Q8: SAMHIP_EPI(EPI_BIAS | EPI_GELU | EPI_Q8, A_PLAIN)
             default: return false;
         }
     }

@@ -87,6 +87,15 @@ struct Epilogue {
     // is indexed by c.
     int shuffle_w = 0, shuffle_c = 0;
     bool gelu = false;   // ggml_gelu_erf after the bias
+    // Q8_0 blocks instead of Y (with bias and gelu: an encoder block's fc1,
+    // whose output only feeds fc2's Q8_0 packing): the 32 values of row m,
+    // columns 32b .. 32b + 31 leave as their ggml Q8_0 codes
+    // q8[m * q8_ld + 32b ..] and their F32 maximum magnitude
+    // q8_amax[m * (q8_ld / 32) + b]; N and q8_ld are multiples of 32.
+    int8_t* q8 = nullptr;
+    float* q8_amax = nullptr;
+    int64_t q8_ld = 0;
+    bool q8_x86 = true;   // x86 rounding (127/amax, ties to even) or ggml's reference (1/d, ties away)
 };
 // How the A tile loader reads row m, logical column k (K columns) of A:
 //   A_PLAIN : A[m][k] (lda halves per row);
@@ -203,6 +212,13 @@ struct RowPre {
 bool launch_prep(int mode, int wtype, const float* x, int64_t x_stride, int M, int K, _Float16* a, int64_t lda,
                  float* row_scale, int x86, const void* w, int64_t w_stride, int N, _Float16* wout, int64_t ldo,
                  hipStream_t stream, const RowPre& pre = RowPre{});
+// The same for a Q8_0 weight whose activation rows arrive as Q8_0 codes
+// [M][ldc] and F32 block maxima [M][ldc / 32] (Epilogue::q8): the fp16
+// operand and row scales launch_prep gives for the F32 rows these codes
+// pack; false when not applicable.
+bool launch_prep_codes(const int8_t* codes, const float* amax, int64_t ldc, int M, int K, _Float16* a, int64_t lda,
+                       float* row_scale, int wtype, const void* w, int64_t w_stride, int N, _Float16* wout,
+                       int64_t ldo, hipStream_t stream);
 
 // Kernel variant name for a weight type, or nullptr when unsupported.
 const char* gemm_variant(int wtype);

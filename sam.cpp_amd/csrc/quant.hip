@@ -408,6 +408,51 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __rest
     }
 }
 
+// Staging of a product whose activation rows arrive as Q8_0 codes and F32
+// block maxima (Epilogue::q8 of the producing GEMM): the fp16 operand and
+// row scale that staging the F32 rows gives, bit for bit, since the row
+// maximum is the largest block maximum, the block scale fp16(amax / 127) and
+// each value fp16((d * q) * 2^-e).  One wave per row, four rows per
+// workgroup; lane l takes values 8l .. 8l + 7 of each 512-value chunk.  The
+// workgroups past stage_blocks decode the weight as prep_kernel's do.
+template <int WT>
+__global__ __launch_bounds__(256) void prep_codes_kernel(const int8_t* __restrict__ codes,
+                                                         const float* __restrict__ amax, int64_t ldc, int M, int K,
+                                                         _Float16* __restrict__ a, int64_t lda,
+                                                         float* __restrict__ row_scale, int stage_blocks,
+                                                         const uint8_t* __restrict__ W, int64_t w_stride, int N,
+                                                         _Float16* __restrict__ wout, int64_t ldo) {
+#pragma clang fp contract(off)
+    if (int(blockIdx.x) < stage_blocks) {
+        const int lane = threadIdx.x & 63;
+        const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+        if (m >= M) return;
+        const float* am = amax + int64_t(m) * (ldc >> 5);
+        float rmax = 0.f;
+        for (int b = lane; b < K / 32; b += 64) rmax = fmaxf(rmax, am[b]);
+        rmax = wave_max(rmax);
+        const int e = row_exponent(rmax);
+        const float down = exp2i(-e);
+        if (lane == 0) row_scale[m] = exp2i(e);
+        const int8_t* cr = codes + int64_t(m) * ldc;
+        _Float16* ar = a + int64_t(m) * lda;
+        for (int k = 8 * lane; k < K; k += 512) {
+            const u32x2 w = *reinterpret_cast<const u32x2*>(cr + k);
+            const float d = half_bits_to_float(float_to_half_bits(am[k >> 5] / 127.f));
+            half8 o;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int q = int(int8_t(uint8_t(w[i >> 2] >> (8 * (i & 3)))));
+                o[i] = (_Float16)((d * float(q)) * down);
+            }
+            *reinterpret_cast<half8*>(ar + k) = o;
+        }
+        return;
+    }
+    const int64_t t = int64_t(blockIdx.x - stage_blocks) * 256 + threadIdx.x;
+    if (t < int64_t(N) * (K / 32) * 2) dequant_piece<WT>(W, w_stride, K, t, wout, ldo);
+}
+
 }  // namespace
 
 void launch_dequant_w_f16(int wtype, const void* w, int64_t w_stride, int N, int K, _Float16* out, int64_t ldo,
@@ -477,6 +522,21 @@ bool launch_prep(int mode, int wtype, const float* x, int64_t x_stride, int M, i
     }
 #undef SAMHIP_PREP_CH
 #undef SAMHIP_PREP
+    return true;
+}
+
+bool launch_prep_codes(const int8_t* codes, const float* amax, int64_t ldc, int M, int K, _Float16* a, int64_t lda,
+                       float* row_scale, int wtype, const void* w, int64_t w_stride, int N, _Float16* wout,
+                       int64_t ldo, hipStream_t stream) {
+    // 8-byte code loads and 16-byte operand stores
+    if (wtype != T_Q8_0 || M < 1 || N < 1 || K < 32 || K % 32 || ldc % 32 || K > ldc || lda % 8 ||
+        reinterpret_cast<uintptr_t>(codes) % 8 || reinterpret_cast<uintptr_t>(amax) % 4 ||
+        reinterpret_cast<uintptr_t>(a) % 16)
+        return false;
+    const int sb = (M + 3) / 4;
+    const int64_t db = (int64_t(N) * (K / 32) * 2 + 255) / 256;
+    hipLaunchKernelGGL(prep_codes_kernel<T_Q8_0>, dim3(unsigned(sb + db)), dim3(256), 0, stream, codes, amax, ldc, M,
+                       K, a, lda, row_scale, sb, static_cast<const uint8_t*>(w), w_stride, N, wout, ldo);
     return true;
 }
 

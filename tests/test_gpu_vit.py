@@ -259,6 +259,76 @@ def test_vit_block_is_deterministic(gpu_ctx, oracle, samhip):
     assert np.array_equal(outs[0], outs[1])
 
 
+def _block_run(ctx, samhip, w, x, E, heads, mlp, grid, ws):
+    blk = samhip.VitBlock(ctx, w, E, heads, mlp, grid, grid, ws)
+    xb = ctx.upload(x)
+    ctx.trace_begin()
+    blk.forward(xb)
+    names = [r[0] for r in ctx.trace_end()]
+    got = ctx.download(xb, x.shape, np.float32)
+    blk.free()
+    return got, names
+
+
+@pytest.mark.parametrize("rounding", ["x86", "ref"])
+@pytest.mark.parametrize("case", ["72x72_window24", "72x72_global", "16x16_wide_range"])
+def test_vit_block_fc1_codes_same_bits(samhip, oracle, monkeypatch, rounding, case):
+    """SAMHIP_VIT_FC1_CODES=1: with a Q8_0 fc2 in native compute, fc1's
+    epilogue applies the erf-GELU and writes fc2's Q8_0 codes and F32 block
+    maxima, and fc2's staging expands them (stage_codes_q8_0).  The block
+    output must have the bits of the default path, which writes fc1's F32
+    rows and packs them in fc2's staging, in both Q8_0 roundings: full SAM 3
+    blocks, and a reduced block whose fc1 bias spreads the rows over ~5
+    decades with one all-zero 32-column block (amax 0, codes 0)."""
+    rnd = samhip.ROUND_X86 if rounding == "x86" else samhip.ROUND_REF
+    if case.startswith("72x72"):
+        grid, E, heads, mlp, ws = 72, 1024, 16, 4736, (24 if case.endswith("24") else 0)
+    else:
+        grid, E, heads, mlp, ws = 16, 256, 4, 640, 8
+    per_w = ws if ws else grid
+    w = block_weights(oracle, E, mlp, heads, per_w * per_w, per_w, seed=71 + ws)
+    assert w["fc2_type"] == oracle.Q8_0
+    if case == "16x16_wide_range":
+        w["fc1_b"] = (w["fc1_b"] * np.where(np.arange(mlp) % 7 == 0, 4e3, 1.0)).astype(np.float32)
+        fc1 = w["fc1_w"].reshape(mlp, -1).copy()
+        fc1[64:96] = 0   # all-zero packed rows decode to 0
+        w["fc1_w"] = fc1
+        w["fc1_b"][64:96] = 0.0
+    x = np.random.default_rng(72 + ws).standard_normal((grid * grid, E)).astype(np.float32)
+    say(f"vit_block fc1 codes {case} rounding={rounding}")
+    monkeypatch.setenv("SAMHIP_VIT_FC1_CODES", "1")
+    ctx = samhip.Context(0, samhip.COMPUTE_Q8_NATIVE, rnd)
+    try:
+        got, names = _block_run(ctx, samhip, w, x, E, heads, mlp, grid, ws)
+    finally:
+        ctx.close()
+    monkeypatch.delenv("SAMHIP_VIT_FC1_CODES")
+    ctx = samhip.Context(0, samhip.COMPUTE_Q8_NATIVE, rnd)
+    try:
+        want, names_f32 = _block_run(ctx, samhip, w, x, E, heads, mlp, grid, ws)
+    finally:
+        ctx.close()
+    assert "stage_codes_q8_0" in names and "stage_codes_q8_0" not in names_f32, (names, names_f32)
+    assert np.isfinite(got).all()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_vit_block_kquant_fc2_keeps_f32_rows(samhip, oracle, monkeypatch):
+    """Even with SAMHIP_VIT_FC1_CODES=1, a K-quant fc2 packs Q8_K blocks of
+    256 values, which no fc1 tile holds: fc1 writes F32 rows and fc2's
+    staging packs them."""
+    t = dict(qkv=oracle.Q4_K, proj=oracle.Q4_K, fc1=oracle.Q4_K, fc2=oracle.Q6_K)
+    w = block_weights(oracle, 256, 768, 4, 64, 8, seed=75, types=t)
+    x = np.random.default_rng(76).standard_normal((256, 256)).astype(np.float32)
+    monkeypatch.setenv("SAMHIP_VIT_FC1_CODES", "1")
+    ctx = samhip.Context(0)
+    try:
+        _, names = _block_run(ctx, samhip, w, x, 256, 4, 768, 16, 8)
+    finally:
+        ctx.close()
+    assert "stage_codes_q8_0" not in names and "stage_dequant_q8_k" in names, names
+
+
 def test_vit_block_rejects(gpu_ctx, oracle, samhip):
     w = block_weights(oracle, 256, 640, 4, 64, 8, seed=51)
     x = gpu_ctx.upload(np.zeros((256, 256), np.float32))
