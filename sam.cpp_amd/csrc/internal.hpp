@@ -117,7 +117,8 @@ struct AOperand {
 // Same product as launch_gemm_f16 with the shape's picked configuration and
 // the epilogue; returns the configuration's name, or nullptr for an
 // epilogue / operand combination without a kernel (plain A with: bias;
-// bias + res; bias + res + row_map; bias + pack; bias + col_scale; or none;
+// bias + res; bias + res + row_map; bias + pack; bias + col_scale;
+// bias + gelu + q8; or none;
 // repeated A with bias + col_scale (+ shuffle (+ gelu)); gathered A with
 // bias + col_scale are built).
 const char* launch_gemm_f16_epi(const _Float16* a, int64_t lda, const float* row_scale, const _Float16* b,
