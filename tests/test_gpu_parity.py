@@ -479,7 +479,10 @@ VIT = {"qkv": (1024, 3072), "proj": (1024, 1024), "fc1": (1024, 4736), "fc2": (4
 
 @pytest.mark.parametrize("name", list(VIT))
 @pytest.mark.parametrize("qtype", TYPES)
-def test_mul_mat_vit_shapes_sampled_rows(gpu_ctx, f16_ctx, oracle, samhip, name, qtype):
+def test_mul_mat_vit_shapes_all_rows(gpu_ctx, f16_ctx, oracle, samhip, name, qtype):
+    """Every one of the 5184 rows of each ViT product against the oracle
+    (native Q8 path and F32-decode path; the oracle's OpenMP C runs a
+    product in well under a second on the host cores)."""
     k, n = VIT[name]
     if k % samhip.BLOCK_ELEMS[qtype]:
         pytest.skip("4736-wide rows are stored as Q8_0 (src/models/sam3/weights.hpp:159-160)")
@@ -489,12 +492,11 @@ def test_mul_mat_vit_shapes_sampled_rows(gpu_ctx, f16_ctx, oracle, samhip, name,
     x = rng.standard_normal((m, k)).astype(np.float32)
     w = gpu_ctx.quantize(qtype, (np.random.default_rng(0).standard_normal((n, k)) * 0.02).astype(np.float32),
                          samhip.ROUND_REF)
-    rows = np.unique(np.concatenate([np.arange(0, m, 97), [m - 1]]))
     yn = gpu_ctx.matmul(qtype, w, x)
-    r1 = max_row_rel_l2(yn[rows], oracle.mul_mat_native(qtype, w, x[rows]))
+    r1 = max_row_rel_l2(yn, oracle.mul_mat_native(qtype, w, x))
     del yn
     yf = f16_ctx.matmul(qtype, w, x)
-    r2 = max_row_rel_l2(yf[rows], oracle.mul_mat_decode(qtype, w, x[rows]))
+    r2 = max_row_rel_l2(yf, oracle.mul_mat_decode(qtype, w, x))
     say("  row rel L2 native", r1, "f16", r2)
     assert r1 <= ROW_REL_L2 and r2 <= ROW_REL_L2
     # size-independent property: linearity in X, exact for a power of two
