@@ -603,7 +603,7 @@ def test_mul_mat_batch8_mixed_formats(gpu_ctx, oracle, samhip):
     """One forward's worth of products with the format switching per module:
     vision qkv/proj Q6_K, fc1 Q5_K, fc2 Q8_0 (4736-wide rows cannot hold
     K-quant super-blocks, src/models/sam3/weights.hpp:159-160), text and
-    decoder linears Q8_0, interleaved on one context.  Sampled rows against
+    decoder linears Q8_0, interleaved on one context.  Every row against
     the oracle's native path (1e-3), and every image's rows bit-identical to
     the same image run alone (the products are row-independent)."""
     m1, batch = 5184, 8
@@ -616,8 +616,7 @@ def test_mul_mat_batch8_mixed_formats(gpu_ctx, oracle, samhip):
                              samhip.ROUND_REF)
         x = np.random.default_rng(20 + i).standard_normal((m, k)).astype(np.float32)
         y = gpu_ctx.matmul(qtype, w, x)
-        rows = np.unique(np.concatenate([np.arange(0, m, 331), [m - 1]]))
-        r = max_row_rel_l2(y[rows], oracle.mul_mat_native(qtype, w, x[rows]))
+        r = max_row_rel_l2(y, oracle.mul_mat_native(qtype, w, x))
         say("  row rel L2", r)
         assert r <= ROW_REL_L2, name
         if m == m1 * batch:
