@@ -639,6 +639,10 @@ const char* launch_gemm_f16_epi(const _Float16* a, int64_t lda, const float* row
     const Cfg& c = kConfigs[cfg];
     const bool spread = int64_t((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) <= cus;
     if (op.mode != A_PLAIN && (op.part % (op.mode == A_CONV3 ? 128 : 64) || op.part <= 0)) return nullptr;
+    // Q8_0 blocks: whole 32-column blocks, 4-byte aligned code rows
+    if (ep.q8 && (N % 32 || ep.q8_ld % 32 || ep.q8_ld < N || !ep.q8_amax ||
+                  reinterpret_cast<uintptr_t>(ep.q8) % 4 || reinterpret_cast<uintptr_t>(ep.q8_amax) % 4))
+        return nullptr;
     if (op.mode == A_CONV3 && (op.width <= 0 || op.height <= 0 || int64_t(op.width) * op.height != M)) return nullptr;
     const bool ok = cfg == kCfgSquare
         ? launch_epi<256, 256, 2, 4>(a, lda, row_scale, b, ldb, y, ldy, M, N, K, spread, ep, op, stream)
