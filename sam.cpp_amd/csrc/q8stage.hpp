@@ -193,8 +193,12 @@ __device__ __forceinline__ void quant8_codes(const floatx8& v, int lane, float& 
 }
 
 // The fp16 MFMA operand of the same 8 activations:
-//   Q8 modes: fp16(d * q * down);  F16 mode: fp16(x * down)
-// with `down` = 2^-e.
+//   Q8 modes: fp16(q * (d * down));  F16 mode: fp16(x * down)
+// with `down` = 2^-e.  d * down is d scaled by a power of two, so
+// q * (d * down) is fl(d * q) * down whenever d * q is a normal float (a
+// subnormal d * q is below 2^-126, and such a value times down is below
+// fp16's range unless the row maximum is below ~2^-87, where this form
+// keeps more bits).
 template <int MODE, bool X86>
 __device__ __forceinline__ half8 quant8(const floatx8& v, int lane, float down) {
 #pragma clang fp contract(off)
@@ -206,8 +210,9 @@ __device__ __forceinline__ half8 quant8(const floatx8& v, int lane, float down) 
     }
     float d, q[8];
     quant8_codes<MODE, X86>(v, lane, d, q);
+    const float dd = d * down;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = (_Float16)((d * q[i]) * down);
+    for (int i = 0; i < 8; ++i) o[i] = (_Float16)(q[i] * dd);
     return o;
 }
 

@@ -247,7 +247,8 @@ __global__ __launch_bounds__(256) void stage_rows_kernel(const float* __restrict
             } else {
                 q8_k_codes(v, lane, d, q);
             }
-            for (int i = 0; i < 4; ++i) out[i] = (_Float16)((d * (float)q[i]) * down);
+            const float dd = d * down;
+            for (int i = 0; i < 4; ++i) out[i] = (_Float16)((float)q[i] * dd);
         }
         typedef _Float16 half4 __attribute__((ext_vector_type(4)));
         *reinterpret_cast<half4*>(ar + k) = half4{out[0], out[1], out[2], out[3]};
@@ -294,8 +295,9 @@ __global__ __launch_bounds__(256) void stage_rows_unaligned_kernel(const float* 
         } else if (MODE == T_Q8_K) {
             q8_k_codes(v, lane, d, q);
         }
+        const float dd = d * down;
         for (int i = 0; i < 4; ++i)
-            ar[k + i] = MODE == T_F16 ? (_Float16)(v[i] * down) : (_Float16)((d * (float)q[i]) * down);
+            ar[k + i] = MODE == T_F16 ? (_Float16)(v[i] * down) : (_Float16)((float)q[i] * dd);
     }
 }
 
@@ -412,7 +414,7 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __rest
 // block maxima (Epilogue::q8 of the producing GEMM): the fp16 operand and
 // row scale that staging the F32 rows gives, bit for bit, since the row
 // maximum is the largest block maximum, the block scale fp16(amax / 127) and
-// each value fp16((d * q) * 2^-e).  One wave per row, four rows per
+// each value fp16(q * (d * 2^-e)).  One wave per row, four rows per
 // workgroup; lane l takes values 8l .. 8l + 7 of each 512-value chunk.  The
 // workgroups past stage_blocks decode the weight as prep_kernel's do.
 template <int WT>
@@ -438,12 +440,12 @@ __global__ __launch_bounds__(256) void prep_codes_kernel(const int8_t* __restric
         _Float16* ar = a + int64_t(m) * lda;
         for (int k = 8 * lane; k < K; k += 512) {
             const u32x2 w = *reinterpret_cast<const u32x2*>(cr + k);
-            const float d = half_bits_to_float(float_to_half_bits(am[k >> 5] / 127.f));
+            const float dd = half_bits_to_float(float_to_half_bits(am[k >> 5] / 127.f)) * down;
             half8 o;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int q = int(int8_t(uint8_t(w[i >> 2] >> (8 * (i & 3)))));
-                o[i] = (_Float16)((d * float(q)) * down);
+                o[i] = (_Float16)(float(q) * dd);
             }
             *reinterpret_cast<half8*>(ar + k) = o;
         }
