@@ -179,10 +179,13 @@ __device__ __forceinline__ void quant8_codes(const floatx8& v, int lane, float& 
         const float smax = (key & 1) ? -amax : amax;
         if (amax != 0.f) {
             const float iscale = -127.f / smax;
+            // ggml clamps the code to 127; with |v| <= amax = |smax| the
+            // product is at most 127 (1 + 2^-23), which rounds to 127, so
+            // the clamp never acts (a non-finite amax makes the product NaN)
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float r = __builtin_rintf(iscale * v[i]);
-                q[i] = r == r ? fminf(127.f, r) : 0.f;   // NaN -> 0 (ggml nearest_int)
+                q[i] = r == r ? r : 0.f;   // NaN -> 0 (ggml nearest_int)
             }
             d = 1.f / iscale;
         } else {

@@ -55,14 +55,25 @@ __device__ __forceinline__ void stage8_row(const float* __restrict__ x, int64_t 
             for (int i = 0; i < 8; ++i) s += v[c][i];
         const float mean = wave_sum(s) / float(K);
         float s2 = 0.f;
+        if (K == 512 * CH) {   // every lane's values lie in the row
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const bool live = 512 * c + 8 * lane < K;
+            for (int c = 0; c < CH; ++c)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float d = live ? v[c][i] - mean : 0.f;
-                v[c][i] = d;
-                s2 += d * d;
+                for (int i = 0; i < 8; ++i) {
+                    const float d = v[c][i] - mean;
+                    v[c][i] = d;
+                    s2 += d * d;
+                }
+        } else {
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const bool live = 512 * c + 8 * lane < K;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float d = live ? v[c][i] - mean : 0.f;
+                    v[c][i] = d;
+                    s2 += d * d;
+                }
             }
         }
         const float variance = wave_sum(s2) / float(K);
