@@ -135,33 +135,29 @@ __device__ __forceinline__ int min32_lanes(int v) {
 }
 typedef float floatx8 __attribute__((ext_vector_type(8)));
 
-// The Q8 block codes of 8 consecutive activations held by each lane; lanes
-// 4g..4g+3 hold one Q8_0 block, lanes 32h..32h+31 one Q8_K block.  Every
-// lane of the wave must call it (cross-lane reductions); lanes past the
-// row's end hold zeros.  d is the block's decoded scale (the stored fp16 for
-// Q8_0), q[i] the integer codes in [-127, 127].  X86 selects the Q8_0
-// rounding of ggml's x86-64 from_float (scale 127/amax, ties to even) over
-// the reference quantize_row_q8_0_ref (scale 1/d, ties away from zero).
+// The Q8 block packing of 8 consecutive activations held by each lane;
+// lanes 4g..4g+3 hold one Q8_0 block, lanes 32h..32h+31 one Q8_K block.
+// Every lane of the wave must call these (cross-lane reductions); lanes past
+// the row's end hold zeros.  quant8_scale gives the block's decoded scale d
+// (the stored fp16 for Q8_0) and the multiplier that takes a value to its
+// unrounded code; quant8_codes and quant8_icodes give the codes in
+// [-127, 127] as floats or as ints.  X86 selects the Q8_0 rounding of
+// ggml's x86-64 from_float (scale 127/amax, ties to even) over the reference
+// quantize_row_q8_0_ref (scale 1/d, ties away from zero).
 template <int MODE, bool X86>
-__device__ __forceinline__ void quant8_codes(const floatx8& v, int lane, float& d, float (&q)[8]) {
+__device__ __forceinline__ void quant8_scale(const floatx8& v, int lane, float& d, float& mul) {
 #pragma clang fp contract(off)
     d = 0.f;
+    mul = 0.f;
     if (MODE == T_Q8_0) {
         float amax = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
         amax = max4_lanes(amax);
         const float dd = amax / 127.f;
-        float inv;
-        if (X86) inv = amax != 0.f ? 127.f / amax : 0.f;
-        else inv = dd != 0.f ? 1.f / dd : 0.f;
+        if (X86) mul = amax != 0.f ? 127.f / amax : 0.f;
+        else mul = dd != 0.f ? 1.f / dd : 0.f;
         d = half_bits_to_float(float_to_half_bits(dd));   // stored fp16 scale
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float s = v[i] * inv;
-            const float r = X86 ? __builtin_rintf(s) : __builtin_roundf(s);
-            q[i] = r == r ? r : 0.f;   // a NaN activation packs as code 0 (this library's contract, above)
-        }
     } else {
         // Q8_K: first element of largest magnitude in the 256-value block
         const int base = 8 * (lane & 31);
@@ -178,21 +174,42 @@ __device__ __forceinline__ void quant8_codes(const floatx8& v, int lane, float& 
         const int key = min32_lanes(la == amax ? 2 * li + int(__float_as_uint(ls) >> 31) : (1 << 20));
         const float smax = (key & 1) ? -amax : amax;
         if (amax != 0.f) {
-            const float iscale = -127.f / smax;
             // ggml clamps the code to 127; with |v| <= amax = |smax| the
             // product is at most 127 (1 + 2^-23), which rounds to 127, so
             // the clamp never acts (a non-finite amax makes the product NaN)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float r = __builtin_rintf(iscale * v[i]);
-                q[i] = r == r ? r : 0.f;   // NaN -> 0 (ggml nearest_int)
-            }
-            d = 1.f / iscale;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) q[i] = 0.f;
+            mul = -127.f / smax;
+            d = 1.f / mul;
         }
     }
+}
+
+// The rounding of a scaled value to its code.
+template <int MODE, bool X86>
+__device__ __forceinline__ float quant8_round(float s) {
+    return (MODE == T_Q8_0 && !X86) ? __builtin_roundf(s) : __builtin_rintf(s);
+}
+
+template <int MODE, bool X86>
+__device__ __forceinline__ void quant8_codes(const floatx8& v, int lane, float& d, float (&q)[8]) {
+#pragma clang fp contract(off)
+    float mul;
+    quant8_scale<MODE, X86>(v, lane, d, mul);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float r = quant8_round<MODE, X86>(v[i] * mul);
+        q[i] = r == r ? r : 0.f;   // a NaN activation packs as code 0 (this library's contract, above)
+    }
+}
+
+// The same codes as integers (the int8 kernels): the conversion itself
+// takes a NaN to 0.
+template <int MODE, bool X86>
+__device__ __forceinline__ void quant8_icodes(const floatx8& v, int lane, float& d, int (&c)[8]) {
+#pragma clang fp contract(off)
+    float mul;
+    quant8_scale<MODE, X86>(v, lane, d, mul);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = cvt_i32_nan0(quant8_round<MODE, X86>(v[i] * mul));
 }
 
 // The fp16 MFMA operand of the same 8 activations:

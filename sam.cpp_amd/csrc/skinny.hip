@@ -620,11 +620,12 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
             const int e = 512 * p + 8 * lane, pr = e >= SL, kl = e - pr * SL, m = 2 * wave + pr;
             // ggml's from_float on the block (x86 or reference rounding; NaN
             // -> code 0, this library's contract), the stored fp16 scale
-            float d, q[8];
-            quant8_codes<T_Q8_0, X86>(v[p], lane, d, q);
+            float d;
+            int ci[8];
+            quant8_icodes<T_Q8_0, X86>(v[p], lane, d, ci);
             uint32_t c[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) c[i] = uint32_t(int(q[i]));
+            for (int i = 0; i < 8; ++i) c[i] = uint32_t(ci[i]);
             const uint32_t lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(c[3], c[2], 0x0c0c0400u),
                                                       __builtin_amdgcn_perm(c[1], c[0], 0x0c0c0400u), 0x05040100u);
             const uint32_t hi = __builtin_amdgcn_perm(__builtin_amdgcn_perm(c[7], c[6], 0x0c0c0400u),
@@ -942,14 +943,11 @@ __global__ __launch_bounds__(512) void tall_small_kq_i8_kernel(const float* __re
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
                 const int m = 8 * p + (tid >> 5);
-                float d, q[8];
-                quant8_codes<T_Q8_K, false>(v[p], lane, d, q);
+                float d;
                 int c[8], sum = 0;
+                quant8_icodes<T_Q8_K, false>(v[p], lane, d, c);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    c[i] = int(q[i]);
-                    sum += c[i];
-                }
+                for (int i = 0; i < 8; ++i) sum += c[i];
                 const uint32_t lo = __builtin_amdgcn_perm(
                     __builtin_amdgcn_perm(uint32_t(c[3]), uint32_t(c[2]), 0x0c0c0400u),
                     __builtin_amdgcn_perm(uint32_t(c[1]), uint32_t(c[0]), 0x0c0c0400u), 0x05040100u);
@@ -1240,14 +1238,11 @@ __global__ __launch_bounds__(1024) void kq_strip_i8_kernel(const float* __restri
     for (int p = 0; p < XSB; ++p) {
         if (p >= nsb) break;
         const int u = 32 * p + 2 * wave + hu, m = u / nsb, b = u - m * nsb;
-        float d, q[8];
-        quant8_codes<T_Q8_K, false>(xv[p], lane, d, q);
+        float d;
         int c[8], sum = 0;
+        quant8_icodes<T_Q8_K, false>(xv[p], lane, d, c);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            c[i] = int(q[i]);
-            sum += c[i];
-        }
+        for (int i = 0; i < 8; ++i) sum += c[i];
         const uint32_t lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(uint32_t(c[3]), uint32_t(c[2]), 0x0c0c0400u),
                                                   __builtin_amdgcn_perm(uint32_t(c[1]), uint32_t(c[0]), 0x0c0c0400u),
                                                   0x05040100u);
@@ -1429,14 +1424,11 @@ __global__ __launch_bounds__(1024) void kq_strip_isum_kernel(const float* __rest
     for (int p = 0; p < XSB; ++p) {
         if (p >= nsb) break;
         const int u = 32 * p + 2 * wave + hu, m = u / nsb, b = u - m * nsb;
-        float d, q[8];
-        quant8_codes<T_Q8_K, false>(xv[p], lane, d, q);
+        float d;
         int c[8], sum = 0;
+        quant8_icodes<T_Q8_K, false>(xv[p], lane, d, c);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            c[i] = int(q[i]);
-            sum += c[i];
-        }
+        for (int i = 0; i < 8; ++i) sum += c[i];
         const uint32_t lo = __builtin_amdgcn_perm(__builtin_amdgcn_perm(uint32_t(c[3]), uint32_t(c[2]), 0x0c0c0400u),
                                                   __builtin_amdgcn_perm(uint32_t(c[1]), uint32_t(c[0]), 0x0c0c0400u),
                                                   0x05040100u);
