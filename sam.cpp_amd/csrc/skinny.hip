@@ -765,7 +765,7 @@ __global__ __launch_bounds__(512) void tall_small_i8_kernel(const float* __restr
             float amax = 0.f;
 #pragma unroll
             for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-            const float d = amax / 127.f;
+            const float d = div127(amax);
             float inv;
             if (X86) inv = amax != 0.f ? 127.f / amax : 0.f;
             else inv = d != 0.f ? 1.f / d : 0.f;
