@@ -232,7 +232,7 @@ __device__ __forceinline__ void store_tile_epi(floatx16 (&acc)[FM][FN], const fl
             }
             float* yp = Y + dst[t] * ldy + ycol;
             if (vec_ok && full) {
-                *reinterpret_cast<floatx4*>(yp) = v;
+                __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(yp));
             } else {
                 for (int q = 0; q < 4; ++q)
                     if (n + q < N) yp[q] = v[q];
