@@ -686,7 +686,7 @@ __global__ __launch_bounds__(1024) void q8_strip_i8_kernel(const float* __restri
         const int nn = n0 + 32 * t + n;
         if (m < M && nn < N) {
             if (part) part[(int64_t(sp) * Mall + m0 + m) * N + nn] = v;
-            else Y[int64_t(m) * ldy + nn] = v;
+            else __builtin_nontemporal_store(v, Y + int64_t(m) * ldy + nn);
         }
     }
 }
@@ -860,7 +860,7 @@ __global__ __launch_bounds__(512) void tall_small_i8_kernel(const float* __restr
             for (int r = 0; r < 4 * NQD; ++r) {
                 const float val = acc[r];
                 const uint32_t dr = uint32_t(8 * (r >> 2) + (r & 3));
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), yd, base + dr * uint32_t(ldy) * 4, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), yd, base + dr * uint32_t(ldy) * 4, 0, 2);
             }
         }
         __syncthreads();   // the codes are read before the next rows overwrite them
@@ -1129,7 +1129,7 @@ __global__ __launch_bounds__(512) void tall_small_kq_i8_kernel(const float* __re
                         y = y - (dmw * dx[i]) * float(xsum);
                     }
                     const uint32_t dr = uint32_t(8 * (r >> 2) + (r & 3));
-                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), yd, base + dr * uint32_t(ldy) * 4, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), yd, base + dr * uint32_t(ldy) * 4, 0, 2);
                 }
             }
         }
@@ -1346,7 +1346,7 @@ __global__ __launch_bounds__(1024) void kq_strip_i8_kernel(const float* __restri
         const int nn = n0 + 32 * t + n;
         if (m < M && nn < N) {
             if (part) part[(int64_t(sp) * Mall + m0 + m) * N + nn] = v;
-            else Y[int64_t(m) * ldy + nn] = v;
+            else __builtin_nontemporal_store(v, Y + int64_t(m) * ldy + nn);
         }
     }
 }
@@ -1572,7 +1572,7 @@ __global__ __launch_bounds__(1024) void kq_strip_isum_kernel(const float* __rest
         const int nn = n0 + 32 * t + n;
         if (m < M && nn < N) {
             if (part) part[(int64_t(sp) * Mall + m0 + m) * N + nn] = v;
-            else Y[int64_t(m) * ldy + nn] = v;
+            else __builtin_nontemporal_store(v, Y + int64_t(m) * ldy + nn);
         }
     }
 }
